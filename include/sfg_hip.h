@@ -1,0 +1,251 @@
+/*
+ * sfg_hip.h -- C ABI of the MI355X (gfx950) execution backend for SchedForge's
+ * compiled decoder layer.  Library: schedforge_amd/lib/libsfg_hip.so.
+ *
+ * Conventions (after the reference's only C ABI, `schedforge_matmul_v1`,
+ * src/llvm_backend.cpp:39-40, 62-64, and its metadata symbol, 622-643):
+ *   - versioned `_v1` names, int64_t sizes, raw device pointers, no C++ types;
+ *   - every entry point returns 0 on success, SFG_ERR_* otherwise, and never
+ *     throws.  Codes below 16 are configuration / shape / guard violations
+ *     (the reference throws std::invalid_argument for these); codes from 16 up
+ *     are device or resource failures (the reference's std::runtime_error).
+ *     sfg_hip_last_error() returns this thread's message for the last failure;
+ *   - `stream` is a hipStream_t passed as void* (NULL = default stream); kernels
+ *     are enqueued asynchronously on it.  Calls sharing a stream must be
+ *     serialised by the caller; independent calls may run on different streams;
+ *   - the library allocates no device memory: callers pass workspaces sized by
+ *     the *_workspace_v1 queries.
+ *
+ * Device layouts (all row-major):
+ *   activations   [rows][H] fp32 (residual stream) / bf16 (GEMM operands)
+ *   weights       [N][K] -- output channel major, K contiguous.  The reference
+ *                 keeps [K][N] fp32 (decoder_compiler.h:34-49) and packs
+ *                 Wq|Wk|Wv and Wg|Wu by columns (decoder_compiler.cpp:535-552);
+ *                 sfg_hip_pack_weight_v1 produces the transposed packed form.
+ *                 int8 weights are [N][K] with per-channel fp32 scales, exactly
+ *                 the reference's QuantizedMatMulWeights (next_milestones.h:52-56).
+ *   paged KV      [page][Hkv][page_tokens][D] bf16, one page table row per
+ *                 sequence [B][pages_per_seq] int32.
+ */
+#ifndef SFG_HIP_H
+#define SFG_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SFG_HIP_ABI_VERSION 1
+
+enum sfg_status {
+    SFG_OK = 0,
+    SFG_ERR_INVALID_CONFIG = 1, /* decoder_compiler.cpp:26-39 validate()            */
+    SFG_ERR_SHAPE = 2,          /* shape / layout mismatch (attention_compiler.cpp:31-41) */
+    SFG_ERR_GUARD = 3,          /* compiled guard violated (context > capacity, page id) */
+    SFG_ERR_UNSUPPORTED = 4,    /* configuration valid but not lowered on gfx950  */
+    SFG_ERR_ABI = 5,            /* descriptor ABI version mismatch               */
+    SFG_ERR_DEVICE = 16,        /* HIP runtime error                             */
+    SFG_ERR_WORKSPACE = 17      /* workspace too small                           */
+};
+
+enum sfg_dtype { SFG_F32 = 0, SFG_BF16 = 1, SFG_I8 = 2 };
+
+enum sfg_epilogue {
+    SFG_EPI_NONE = 0,      /* C = A B                                             */
+    SFG_EPI_RESIDUAL = 1,  /* C = A B + R  (R fp32 [M][N]); decoder_compiler.cpp:256,277 */
+    SFG_EPI_SWIGLU = 2,    /* B is [2N][K]: rows [0,N) gate, [N,2N) up;
+                              C = silu(A Bg) * (A Bu); decoder_compiler.cpp:183-194 */
+    SFG_EPI_GLU_SILU_UP = 3 /* MoE form: C = (A B1) * silu(A B3), B = [W1 ; W3];
+                              moe_compiler.cpp:143-149                          */
+};
+
+/* ---------------- library identity ---------------- */
+int sfg_hip_abi_version(void);
+const char* sfg_hip_metadata_v1(void);
+const char* sfg_hip_last_error(void);
+int sfg_hip_device_info_v1(int device, int* cu_count, int* xcd_count, int64_t* hbm_bytes);
+
+/* ---------------- constant packing (DecoderCompiler::compile constant
+ * specialisation, decoder_compiler.cpp:535-552; quantize_matmul_weights,
+ * next_milestones.cpp:611-637) ---------------- */
+
+/* src fp32 [K][N] (ld_src >= N) -> dst [N][K] in dtype (SFG_F32 or SFG_BF16). */
+int sfg_hip_pack_weight_v1(const float* src, int64_t k, int64_t n, int64_t ld_src, void* dst,
+                           int dst_dtype, void* stream);
+/* src fp32 [K][N] -> int8 [N][K] + scales[N]: s = max|w|/127 (1 if zero),
+ * q = clamp(round-half-away(w/s), -127, 127). */
+int sfg_hip_quantize_weight_v1(const float* src, int64_t k, int64_t n, int8_t* dst,
+                               float* scales, void* stream);
+/* fp32 -> bf16 bits, round to nearest even (compiler.cpp:34-43). */
+int sfg_hip_to_bf16_v1(const float* src, uint16_t* dst, int64_t count, void* stream);
+/* RoPE table [seq][head_dim/2][2] = (cos, sin) of float(pos) * powf(theta, -(2i)/D),
+ * computed on the HOST with the reference's float expressions
+ * (decoder_compiler.cpp:101-106).  Plain host memory. */
+int sfg_hip_rope_table_host_v1(float* table, int64_t seq, int64_t head_dim, float theta);
+
+/* ---------------- per-op kernels ---------------- */
+
+/* rms_norm (decoder_compiler.cpp:41-62): y = x * (1/sqrtf(float(sum x^2 / H) + eps)) * w,
+ * sum in double.  x fp32 [rows][width]; y fp32 or bf16. */
+int sfg_hip_rmsnorm_v1(const float* x, const float* w, void* y, int y_dtype, int64_t rows,
+                       int64_t width, float eps, void* stream);
+
+/* C[M][N] = A[M][K] * B^T with B stored [N][K] (or [2N][K] for GLU epilogues).
+ * a_dtype: SFG_F32 (only with b_dtype SFG_F32) or SFG_BF16.  b_dtype: SFG_F32,
+ * SFG_BF16 or SFG_I8 (then b_scales[N or 2N] per output channel).
+ * c_dtype: SFG_F32 or SFG_BF16.  Replaces execute(LoopIR) (runtime.cpp:581-626)
+ * for the four projections and quantized_invoke (next_milestones.cpp:50-69).
+ * workspace: sfg_hip_gemm_workspace_v1 bytes (split-K partials + tile counters),
+ * which must be zero-filled once before first use (the kernels keep the
+ * counters zero between calls). */
+typedef struct {
+    const void* a; int32_t a_dtype; int64_t lda;
+    const void* b; int32_t b_dtype; int64_t ldb; const float* b_scales;
+    void* c; int32_t c_dtype; int64_t ldc;
+    const float* residual; int64_t ldr;
+    int64_t m, n, k;
+    int32_t epilogue;
+} sfg_gemm_args;
+size_t sfg_hip_gemm_workspace_v1(int64_t m, int64_t n, int64_t k);
+int sfg_hip_gemm_v1(const sfg_gemm_args* args, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
+/* split_qkv + apply_rope (decoder_compiler.cpp:96-148).  qkv fp32
+ * [B*S][H + 2 Hkv D]; rope_table [S][D/2][2] device copy of
+ * sfg_hip_rope_table_host_v1.  q [B][Hq][S][D], k/v [B][Hkv][S][D] in out_dtype
+ * (k and v may be NULL: a decode step discards them, decoder_compiler.cpp:238-243). */
+int sfg_hip_qkv_split_rope_v1(const float* qkv, const float* rope_table, int64_t batch,
+                              int64_t seq, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                              void* q, void* k, void* v, int out_dtype, void* stream);
+
+/* IO-aware causal/non-causal GQA prefill, online softmax
+ * (attention_compiler.cpp:286-377).  q [B][Hq][Sq][D], k/v [B][Hkv][Skv][D] in dtype
+ * (SFG_F32 or SFG_BF16); out is written merged [B*Sq][Hq*D] in out_dtype
+ * (merge_attention, decoder_compiler.cpp:150-174).  scale <= 0: 1/sqrt(D). */
+int sfg_hip_attn_prefill_v1(const void* q, const void* k, const void* v, void* out,
+                            int dtype, int out_dtype, int64_t batch, int64_t q_heads,
+                            int64_t kv_heads, int64_t seq_q, int64_t seq_kv, int64_t head_dim,
+                            int causal, float scale, void* stream);
+
+/* Paged Split-KV decode (attention_compiler.cpp:244-285 split/merge,
+ * next_milestones.cpp:137-184 page walk).  q fp32 [B][Hq][D] (one new token per
+ * sequence), pools bf16 [num_pages][Hkv][page_tokens][D], page_table
+ * [B][pages_per_seq], seq_lens[B] (each <= pages_per_seq*page_tokens).  out
+ * merged [B][Hq*D] in out_dtype.  kv_splits <= 0 picks a split count.  Page ids
+ * are validated on the host against num_pages only when validate_pages != 0
+ * (this reads the table back and synchronises the stream). */
+size_t sfg_hip_attn_decode_workspace_v1(int64_t batch, int64_t q_heads, int64_t head_dim,
+                                        int64_t max_context, int64_t page_tokens,
+                                        int32_t kv_splits);
+int sfg_hip_attn_decode_paged_v1(const float* q, const uint16_t* k_pool,
+                                 const uint16_t* v_pool, const int32_t* page_table,
+                                 const int32_t* seq_lens, void* out, int out_dtype,
+                                 int64_t batch, int64_t q_heads, int64_t kv_heads,
+                                 int64_t head_dim, int64_t page_tokens, int64_t pages_per_seq,
+                                 int64_t num_pages, int64_t max_context, int32_t kv_splits,
+                                 float scale, int validate_pages, void* workspace,
+                                 size_t workspace_bytes, void* stream);
+
+/* MoE routing: Router -> Softmax -> TopK -> Histogram -> PrefixSum -> Dispatch
+ * (route_topk, moe_compiler.cpp:412-455; dispatch_tokens, 496-528).
+ * x fp32 [T][H], router fp32 [H][E], bias fp32 [E] or NULL.  Logits are
+ * sequential fp32 FMA chains over H (bit-identical to the oracle); top-k by
+ * logit, ties to the lower expert index.  Outputs (device, int32 / fp32):
+ * ids/weights [T][k]; counts [E]; offsets [E+1]; token_ids, route_slots,
+ * routing_weights [T*k] in expert-major, token-ascending order; and
+ * position [T][k] = index of each (token, slot) in that order. */
+size_t sfg_hip_moe_route_workspace_v1(int64_t tokens, int64_t experts, int64_t top_k);
+int sfg_hip_moe_route_v1(const float* x, const float* router, const float* bias,
+                         int64_t tokens, int64_t hidden, int64_t experts, int64_t top_k,
+                         int32_t* ids, float* weights, int32_t* counts, int32_t* offsets,
+                         int32_t* token_ids, int32_t* route_slots, float* routing_weights,
+                         int32_t* position, void* workspace, size_t workspace_bytes,
+                         void* stream);
+/* Same pipeline from a given routing trace (decoder_compiler.cpp:281-284). */
+int sfg_hip_moe_dispatch_trace_v1(const int32_t* ids, const float* weights, int64_t tokens,
+                                  int64_t experts, int64_t top_k, int32_t* counts,
+                                  int32_t* offsets, int32_t* token_ids, int32_t* route_slots,
+                                  float* routing_weights, int32_t* position, void* stream);
+
+/* Variable-M grouped expert GEMMs (compute_task, moe_compiler.cpp:121-155):
+ * stage 1: act[r] = (x[tok(r)] W1[e]) * silu(x[tok(r)] W3[e]) for dispatched rows r
+ *          of expert e = segment(r); w13 [E][2I][H] (rows [0,I) W1^T, [I,2I) W3^T),
+ *          x bf16 [T][H], act bf16 [T*k][I];
+ * stage 2: y[r] = act[r] W2[e], w2 [E][H][I], y fp32 [T*k][H].
+ * w dtype SFG_BF16 or SFG_I8 (+ scales [E][2I] / [E][H]). */
+size_t sfg_hip_moe_expert_workspace_v1(int64_t tokens, int64_t hidden, int64_t inter,
+                                       int64_t experts, int64_t top_k);
+int sfg_hip_moe_experts_v1(const uint16_t* x, const int32_t* offsets, const int32_t* token_ids,
+                           const void* w13, const float* s13, const void* w2, const float* s2,
+                           int w_dtype, uint16_t* act, float* y, int64_t tokens,
+                           int64_t hidden, int64_t inter, int64_t experts, int64_t top_k,
+                           void* workspace, size_t workspace_bytes, void* stream);
+/* Weighted combine (moe_compiler.cpp:219-226) fused with the FFN residual
+ * (decoder_compiler.cpp:277): out[t] = residual[t] + sum_s w[t][s] * y[position[t][s]]. */
+int sfg_hip_moe_combine_v1(const float* y, const int32_t* position, const float* weights,
+                           const float* residual, float* out, int64_t tokens, int64_t hidden,
+                           int64_t top_k, void* stream);
+
+/* ---------------- whole layer: execute_once (decoder_compiler.cpp:218-304) ---------------- */
+
+typedef struct {
+    int32_t abi;  /* SFG_HIP_ABI_VERSION */
+    int32_t batch, sequence, hidden, intermediate, query_heads, kv_heads, head_dim;
+    float rms_epsilon, rope_theta;
+    int32_t causal;
+    int32_t ffn;        /* 0 dense SwiGLU, 1 MoE */
+    int32_t experts, top_k;
+    int32_t context;    /* 0: prefill; > 0: decode step over this many cached tokens */
+    int32_t page_tokens, pages_per_seq, num_pages;
+    int32_t act_dtype;  /* SFG_F32 (all-fp32 path) or SFG_BF16 */
+    int32_t weight_dtype; /* SFG_F32, SFG_BF16 or SFG_I8 */
+    int32_t kv_splits;  /* decode; <= 0: automatic */
+    int32_t use_routing_trace;
+} sfg_layer_desc;
+
+typedef struct {
+    const float* rms1; const float* rms2;        /* [H] */
+    const void* w_qkv; const float* s_qkv;       /* [H + 2 Hkv D][H] */
+    const void* w_o; const float* s_o;           /* [H][H] */
+    const void* w_gate_up; const float* s_gate_up; /* dense: [2I][H] */
+    const void* w_down; const float* s_down;     /* dense: [H][I] */
+    const float* router; const float* router_bias; /* MoE: [H][E], [E] or NULL */
+    const void* w13; const float* s13;           /* MoE: [E][2I][H] */
+    const void* w2; const float* s2;             /* MoE: [E][H][I] */
+    const uint16_t* k_pool; const uint16_t* v_pool; /* decode: paged bf16 pools */
+    const int32_t* page_table;                   /* decode: [B][pages_per_seq] */
+    const float* rope_table;                     /* [S][D/2][2] */
+} sfg_layer_weights;
+
+/* Stage marks recorded into caller-created events when io->stage_events != NULL. */
+enum sfg_stage_mark {
+    SFG_MARK_START = 0, SFG_MARK_NORM1, SFG_MARK_QKV, SFG_MARK_ROPE, SFG_MARK_ATTN_MAIN,
+    SFG_MARK_ATTN, SFG_MARK_OPROJ, SFG_MARK_NORM2, SFG_MARK_ROUTE, SFG_MARK_FFN_UP,
+    SFG_MARK_FFN_DOWN, SFG_MARK_END, SFG_NUM_MARKS
+};
+
+typedef struct {
+    const float* x;                  /* [rows][H] fp32 */
+    float* out;                      /* [rows][H] fp32 */
+    const int32_t* trace_ids;        /* optional routing trace [rows][k] */
+    const float* trace_weights;
+    void** stage_events;             /* NULL or SFG_NUM_MARKS hipEvent_t */
+} sfg_layer_io;
+
+size_t sfg_hip_decoder_layer_workspace_v1(const sfg_layer_desc* desc);
+int sfg_hip_decoder_layer_v1(const sfg_layer_desc* desc, const sfg_layer_weights* weights,
+                             const sfg_layer_io* io, void* workspace, size_t workspace_bytes,
+                             void* stream);
+
+/* ---------------- event helpers (for stage timing from any host language) ---------------- */
+int sfg_hip_events_create_v1(int count, void** events);
+int sfg_hip_events_destroy_v1(int count, void** events);
+int sfg_hip_event_elapsed_v1(void* start, void* end, float* milliseconds);
+int sfg_hip_stream_synchronize_v1(void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,661 @@
+// sfg_api.hip -- the C ABI (include/sfg_hip.h) and the decoder-layer
+// orchestration: the GPU counterpart of execute_once
+// (decoder_compiler.cpp:218-304).
+//
+// Every entry point validates its arguments on the host before launching, so
+// shape and guard violations come back as SFG_ERR_* codes (the reference's
+// std::invalid_argument cases) instead of faults; HIP failures come back as
+// SFG_ERR_DEVICE with the runtime's message.
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+#include <vector>
+
+#include "sfg_kernels.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int check_launch(const char* what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(SFG_ERR_DEVICE, "%s: %s", what, hipGetErrorString(e));
+    return SFG_OK;
+}
+
+hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+size_t align256(size_t v) { return (v + 255) / 256 * 256; }
+
+float default_scale(int64_t head_dim, float scale) {
+    return scale > 0.0f ? scale : 1.0f / sqrtf(static_cast<float>(head_dim));
+}
+
+// Bump allocator over the caller's workspace.
+struct Carve {
+    char* base;
+    size_t used = 0;
+    explicit Carve(void* b) : base(static_cast<char*>(b)) {}
+    void* take(size_t bytes) {
+        void* p = base ? base + used : nullptr;
+        used += align256(bytes);
+        return p;
+    }
+};
+
+}  // namespace
+
+extern "C" {
+
+int sfg_hip_abi_version(void) { return SFG_HIP_ABI_VERSION; }
+
+const char* sfg_hip_metadata_v1(void) {
+    return "abi=1;arch=gfx950;wavefront=64;dtypes=f32,bf16,i8;weight_layout=NK;"
+           "kv_layout=page,kv_head,page_token,head_dim;page_tokens=16;head_dim=128(bf16 paths);"
+           "accumulate=f32;bf16_rounding=rne";
+}
+
+const char* sfg_hip_last_error(void) { return g_last_error.c_str(); }
+
+int sfg_hip_device_info_v1(int device, int* cu_count, int* xcd_count, int64_t* hbm_bytes) {
+    hipDeviceProp_t prop;
+    const hipError_t e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess) return fail(SFG_ERR_DEVICE, "hipGetDeviceProperties: %s", hipGetErrorString(e));
+    if (cu_count) *cu_count = prop.multiProcessorCount;
+    if (xcd_count) *xcd_count = 8;
+    if (hbm_bytes) *hbm_bytes = static_cast<int64_t>(prop.totalGlobalMem);
+    return SFG_OK;
+}
+
+int sfg_hip_pack_weight_v1(const float* src, int64_t k, int64_t n, int64_t ld_src, void* dst,
+                           int dst_dtype, void* stream) {
+    if (!src || !dst || k <= 0 || n <= 0 || ld_src < n)
+        return fail(SFG_ERR_SHAPE, "pack_weight: invalid arguments k=%lld n=%lld ld=%lld",
+                    (long long)k, (long long)n, (long long)ld_src);
+    if (dst_dtype != SFG_F32 && dst_dtype != SFG_BF16)
+        return fail(SFG_ERR_UNSUPPORTED, "pack_weight: dtype %d", dst_dtype);
+    sfg::launch_pack_weight(src, k, n, ld_src, dst, dst_dtype, as_stream(stream));
+    return check_launch("pack_weight");
+}
+
+int sfg_hip_quantize_weight_v1(const float* src, int64_t k, int64_t n, int8_t* dst,
+                               float* scales, void* stream) {
+    if (!src || !dst || !scales || k <= 0 || n <= 0)
+        return fail(SFG_ERR_SHAPE, "quantize_weight: invalid arguments");
+    sfg::launch_quantize_weight(src, k, n, dst, scales, as_stream(stream));
+    return check_launch("quantize_weight");
+}
+
+int sfg_hip_to_bf16_v1(const float* src, uint16_t* dst, int64_t count, void* stream) {
+    if (count < 0 || (count > 0 && (!src || !dst))) return fail(SFG_ERR_SHAPE, "to_bf16: invalid");
+    if (count == 0) return SFG_OK;
+    sfg::launch_to_bf16(src, dst, count, as_stream(stream));
+    return check_launch("to_bf16");
+}
+
+int sfg_hip_rope_table_host_v1(float* table, int64_t seq, int64_t head_dim, float theta) {
+    if (!table || seq <= 0 || head_dim <= 0 || (head_dim & 1))
+        return fail(SFG_ERR_SHAPE, "rope_table: invalid arguments");
+    // The reference's expressions (decoder_compiler.cpp:101-106), evaluated
+    // with the host libm: f = powf(theta, -float(2i)/float(D)); a = float(pos) * f.
+    for (int64_t s = 0; s < seq; ++s)
+        for (int64_t i = 0; i < head_dim / 2; ++i) {
+            const float freq = powf(theta, -static_cast<float>(2 * i) / static_cast<float>(head_dim));
+            const float angle = static_cast<float>(s) * freq;
+            table[(s * (head_dim / 2) + i) * 2] = cosf(angle);
+            table[(s * (head_dim / 2) + i) * 2 + 1] = sinf(angle);
+        }
+    return SFG_OK;
+}
+
+int sfg_hip_rmsnorm_v1(const float* x, const float* w, void* y, int y_dtype, int64_t rows,
+                       int64_t width, float eps, void* stream) {
+    if (!x || !w || !y || rows <= 0 || width <= 0 || !(eps > 0.0f))
+        return fail(SFG_ERR_SHAPE, "rmsnorm: invalid arguments");
+    if (y_dtype != SFG_F32 && y_dtype != SFG_BF16)
+        return fail(SFG_ERR_UNSUPPORTED, "rmsnorm: dtype %d", y_dtype);
+    sfg::launch_rmsnorm(x, w, y, y_dtype, rows, width, eps, as_stream(stream));
+    return check_launch("rmsnorm");
+}
+
+size_t sfg_hip_gemm_workspace_v1(int64_t m, int64_t n, int64_t k) {
+    return sfg::gemm_workspace_bytes(m, 2 * n, k);
+}
+
+int sfg_hip_gemm_v1(const sfg_gemm_args* a, void* workspace, size_t workspace_bytes, void* stream) {
+    if (!a || !a->a || !a->b || !a->c || a->m <= 0 || a->n <= 0 || a->k <= 0)
+        return fail(SFG_ERR_SHAPE, "gemm: invalid arguments");
+    if (a->lda < a->k || a->ldb < a->k)
+        return fail(SFG_ERR_SHAPE, "gemm: leading dimension smaller than k");
+    const bool glu = a->epilogue == SFG_EPI_SWIGLU || a->epilogue == SFG_EPI_GLU_SILU_UP;
+    if (a->ldc < a->n) return fail(SFG_ERR_SHAPE, "gemm: ldc < n");
+    if (a->epilogue == SFG_EPI_RESIDUAL && (!a->residual || a->ldr < a->n))
+        return fail(SFG_ERR_SHAPE, "gemm: residual epilogue needs residual [m][n]");
+    if (a->epilogue < SFG_EPI_NONE || a->epilogue > SFG_EPI_GLU_SILU_UP)
+        return fail(SFG_ERR_SHAPE, "gemm: unknown epilogue %d", a->epilogue);
+    (void)glu;
+    sfg::GemmProblem p{};
+    p.a = a->a; p.a_dtype = a->a_dtype; p.lda = a->lda; p.a_rows = nullptr;
+    p.b = a->b; p.b_dtype = a->b_dtype; p.ldb = a->ldb; p.b_scales = a->b_scales;
+    p.c = a->c; p.c_dtype = a->c_dtype; p.ldc = a->ldc;
+    p.residual = a->residual; p.ldr = a->ldr;
+    p.m = a->m; p.n = a->n; p.k = a->k; p.epilogue = a->epilogue;
+    p.offsets = nullptr; p.groups = 1;
+    const int rc = sfg::launch_gemm(p, workspace, workspace_bytes, as_stream(stream));
+    if (rc != SFG_OK)
+        return fail(rc, "gemm: unsupported or invalid combination (a=%d b=%d m=%lld n=%lld k=%lld epi=%d)",
+                    a->a_dtype, a->b_dtype, (long long)a->m, (long long)a->n, (long long)a->k,
+                    a->epilogue);
+    return check_launch("gemm");
+}
+
+int sfg_hip_qkv_split_rope_v1(const float* qkv, const float* rope_table, int64_t batch,
+                              int64_t seq, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                              void* q, void* k, void* v, int out_dtype, void* stream) {
+    if (!qkv || !rope_table || !q || batch <= 0 || seq <= 0 || q_heads <= 0 || kv_heads <= 0 ||
+        head_dim <= 0 || (head_dim & 1) || q_heads % kv_heads)
+        return fail(SFG_ERR_SHAPE, "qkv_split_rope: invalid arguments");
+    if (out_dtype != SFG_F32 && out_dtype != SFG_BF16)
+        return fail(SFG_ERR_UNSUPPORTED, "qkv_split_rope: dtype %d", out_dtype);
+    sfg::launch_split_rope(qkv, rope_table, batch, seq, q_heads, kv_heads, head_dim, q, k, v,
+                           out_dtype, as_stream(stream));
+    return check_launch("qkv_split_rope");
+}
+
+int sfg_hip_attn_prefill_v1(const void* q, const void* k, const void* v, void* out, int dtype,
+                            int out_dtype, int64_t batch, int64_t q_heads, int64_t kv_heads,
+                            int64_t seq_q, int64_t seq_kv, int64_t head_dim, int causal,
+                            float scale, void* stream) {
+    // validate_config (attention_compiler.cpp:23-29)
+    if (!q || !k || !v || !out || batch <= 0 || q_heads <= 0 || kv_heads <= 0 || seq_q <= 0 ||
+        seq_kv <= 0 || head_dim <= 0 || q_heads % kv_heads || (causal && seq_q > seq_kv))
+        return fail(SFG_ERR_INVALID_CONFIG, "invalid attention configuration");
+    const float s = default_scale(head_dim, scale);
+    if (dtype == SFG_F32) {
+        if (head_dim > 128) return fail(SFG_ERR_UNSUPPORTED, "attn_prefill f32: head_dim > 128");
+        sfg::launch_attn_prefill_f32(static_cast<const float*>(q), static_cast<const float*>(k),
+                                     static_cast<const float*>(v), out, out_dtype, batch, q_heads,
+                                     kv_heads, seq_q, seq_kv, head_dim, causal, s,
+                                     as_stream(stream));
+    } else if (dtype == SFG_BF16) {
+        const int rc = sfg::launch_attn_prefill_bf16(
+            static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+            static_cast<const uint16_t*>(v), out, out_dtype, batch, q_heads, kv_heads, seq_q,
+            seq_kv, head_dim, causal, s, as_stream(stream));
+        if (rc != SFG_OK) return fail(rc, "attn_prefill bf16: head_dim %lld not lowered", (long long)head_dim);
+    } else {
+        return fail(SFG_ERR_UNSUPPORTED, "attn_prefill: dtype %d", dtype);
+    }
+    return check_launch("attn_prefill");
+}
+
+size_t sfg_hip_attn_decode_workspace_v1(int64_t batch, int64_t q_heads, int64_t head_dim,
+                                        int64_t max_context, int64_t page_tokens,
+                                        int32_t kv_splits) {
+    // kv_heads only bounds the automatic split choice from below; using q_heads
+    // here gives an upper bound on the split count chosen for any kv_heads.
+    const int splits = sfg::decode_split_count(batch, 1, max_context, page_tokens, kv_splits);
+    return sfg::decode_workspace_bytes(batch, q_heads, head_dim, splits);
+}
+
+int sfg_hip_attn_decode_paged_v1(const float* q, const uint16_t* k_pool, const uint16_t* v_pool,
+                                 const int32_t* page_table, const int32_t* seq_lens, void* out,
+                                 int out_dtype, int64_t batch, int64_t q_heads, int64_t kv_heads,
+                                 int64_t head_dim, int64_t page_tokens, int64_t pages_per_seq,
+                                 int64_t num_pages, int64_t max_context, int32_t kv_splits,
+                                 float scale, int validate_pages, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+    if (!q || !k_pool || !v_pool || !page_table || !out || batch <= 0 || q_heads <= 0 ||
+        kv_heads <= 0 || q_heads % kv_heads || head_dim <= 0 || page_tokens <= 0 ||
+        pages_per_seq <= 0 || num_pages <= 0 || max_context <= 0)
+        return fail(SFG_ERR_INVALID_CONFIG, "attn_decode_paged: invalid configuration");
+    if (max_context > pages_per_seq * page_tokens)
+        return fail(SFG_ERR_GUARD, "paged KV length violates compiled guard (%lld > %lld)",
+                    (long long)max_context, (long long)(pages_per_seq * page_tokens));
+    if (validate_pages) {
+        std::vector<int32_t> table(static_cast<size_t>(batch * pages_per_seq));
+        hipError_t e = hipMemcpyAsync(table.data(), page_table, table.size() * sizeof(int32_t),
+                                      hipMemcpyDeviceToHost, as_stream(stream));
+        if (e == hipSuccess) e = hipStreamSynchronize(as_stream(stream));
+        if (e != hipSuccess) return fail(SFG_ERR_DEVICE, "page table readback: %s", hipGetErrorString(e));
+        const int64_t used = (max_context + page_tokens - 1) / page_tokens;
+        for (int64_t b = 0; b < batch; ++b)
+            for (int64_t p = 0; p < used; ++p) {
+                const int32_t id = table[static_cast<size_t>(b * pages_per_seq + p)];
+                if (id < 0 || id >= num_pages)
+                    return fail(SFG_ERR_GUARD, "invalid physical KV page %d (sequence %lld, page %lld)",
+                                id, (long long)b, (long long)p);
+            }
+    }
+    const int splits = sfg::decode_split_count(batch, kv_heads, max_context, page_tokens, kv_splits);
+    const size_t need = sfg::decode_workspace_bytes(batch, q_heads, head_dim, splits);
+    if (!workspace || workspace_bytes < need)
+        return fail(SFG_ERR_WORKSPACE, "attn_decode_paged: workspace %zu < %zu", workspace_bytes, need);
+    const int rc = sfg::launch_attn_decode_paged(
+        q, k_pool, v_pool, page_table, seq_lens, max_context, out, out_dtype, batch, q_heads,
+        kv_heads, head_dim, page_tokens, pages_per_seq, num_pages, splits,
+        default_scale(head_dim, scale), workspace, as_stream(stream), nullptr);
+    if (rc != SFG_OK)
+        return fail(rc, "attn_decode_paged: head_dim %lld / page_tokens %lld / group %lld not lowered",
+                    (long long)head_dim, (long long)page_tokens, (long long)(q_heads / kv_heads));
+    return check_launch("attn_decode_paged");
+}
+
+size_t sfg_hip_moe_route_workspace_v1(int64_t tokens, int64_t experts, int64_t top_k) {
+    return sfg::moe_route_workspace_bytes(tokens, experts, top_k);
+}
+
+int sfg_hip_moe_route_v1(const float* x, const float* router, const float* bias, int64_t tokens,
+                         int64_t hidden, int64_t experts, int64_t top_k, int32_t* ids,
+                         float* weights, int32_t* counts, int32_t* offsets, int32_t* token_ids,
+                         int32_t* route_slots, float* routing_weights, int32_t* position,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+    (void)workspace; (void)workspace_bytes;
+    // validate_config (moe_compiler.cpp:41-45)
+    if (!x || !router || !ids || !weights || !counts || !offsets || !token_ids || !route_slots ||
+        !routing_weights || !position || tokens <= 0 || hidden <= 0 || experts <= 0 ||
+        top_k <= 0 || top_k > experts)
+        return fail(SFG_ERR_INVALID_CONFIG, "invalid MoE configuration");
+    int rc = sfg::launch_moe_router(x, router, bias, tokens, hidden, experts, top_k, ids, weights,
+                                    as_stream(stream));
+    if (rc != SFG_OK) return fail(rc, "moe_route: experts %lld / top_k %lld not lowered",
+                                  (long long)experts, (long long)top_k);
+    rc = sfg::launch_moe_dispatch(ids, weights, tokens, experts, top_k, counts, offsets, token_ids,
+                                  route_slots, routing_weights, position, as_stream(stream));
+    if (rc != SFG_OK) return fail(rc, "moe_dispatch: not lowered");
+    return check_launch("moe_route");
+}
+
+int sfg_hip_moe_dispatch_trace_v1(const int32_t* ids, const float* weights, int64_t tokens,
+                                  int64_t experts, int64_t top_k, int32_t* counts,
+                                  int32_t* offsets, int32_t* token_ids, int32_t* route_slots,
+                                  float* routing_weights, int32_t* position, void* stream) {
+    if (!ids || !weights || !counts || !offsets || !token_ids || !route_slots ||
+        !routing_weights || !position || tokens <= 0 || experts <= 0 || top_k <= 0 ||
+        top_k > experts)
+        return fail(SFG_ERR_INVALID_CONFIG, "routing trace does not match MoE configuration");
+    const int rc = sfg::launch_moe_dispatch(ids, weights, tokens, experts, top_k, counts, offsets,
+                                            token_ids, route_slots, routing_weights, position,
+                                            as_stream(stream));
+    if (rc != SFG_OK) return fail(rc, "moe_dispatch: not lowered");
+    return check_launch("moe_dispatch_trace");
+}
+
+size_t sfg_hip_moe_expert_workspace_v1(int64_t tokens, int64_t hidden, int64_t inter,
+                                       int64_t experts, int64_t top_k) {
+    (void)tokens; (void)hidden; (void)inter; (void)experts; (void)top_k;
+    return 0;
+}
+
+static int moe_experts(const uint16_t* x, const int32_t* offsets, const int32_t* token_ids,
+                       const void* w13, const float* s13, const void* w2, const float* s2,
+                       int w_dtype, uint16_t* act, float* y, int64_t tokens, int64_t hidden,
+                       int64_t inter, int64_t experts, int64_t top_k, hipStream_t stream) {
+    sfg::GemmProblem p{};
+    p.a = x; p.a_dtype = SFG_BF16; p.lda = hidden; p.a_rows = token_ids;
+    p.b = w13; p.b_dtype = w_dtype; p.ldb = hidden; p.b_scales = s13;
+    p.b_group_stride = 2 * inter * hidden; p.s_group_stride = 2 * inter;
+    p.c = act; p.c_dtype = SFG_BF16; p.ldc = inter;
+    p.m = tokens * top_k; p.n = inter; p.k = hidden; p.epilogue = SFG_EPI_GLU_SILU_UP;
+    p.offsets = offsets; p.groups = static_cast<int>(experts);
+    int rc = sfg::launch_gemm(p, nullptr, 0, stream);
+    if (rc != SFG_OK) return fail(rc, "moe experts W1/W3: shape not lowered (H=%lld I=%lld)",
+                                  (long long)hidden, (long long)inter);
+    sfg::GemmProblem q{};
+    q.a = act; q.a_dtype = SFG_BF16; q.lda = inter; q.a_rows = nullptr;
+    q.b = w2; q.b_dtype = w_dtype; q.ldb = inter; q.b_scales = s2;
+    q.b_group_stride = hidden * inter; q.s_group_stride = hidden;
+    q.c = y; q.c_dtype = SFG_F32; q.ldc = hidden;
+    q.m = tokens * top_k; q.n = hidden; q.k = inter; q.epilogue = SFG_EPI_NONE;
+    q.offsets = offsets; q.groups = static_cast<int>(experts);
+    rc = sfg::launch_gemm(q, nullptr, 0, stream);
+    if (rc != SFG_OK) return fail(rc, "moe experts W2: shape not lowered");
+    return check_launch("moe_experts");
+}
+
+int sfg_hip_moe_experts_v1(const uint16_t* x, const int32_t* offsets, const int32_t* token_ids,
+                           const void* w13, const float* s13, const void* w2, const float* s2,
+                           int w_dtype, uint16_t* act, float* y, int64_t tokens, int64_t hidden,
+                           int64_t inter, int64_t experts, int64_t top_k, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+    (void)workspace; (void)workspace_bytes;
+    if (!x || !offsets || !token_ids || !w13 || !w2 || !act || !y || tokens <= 0 || hidden <= 0 ||
+        inter <= 0 || experts <= 0 || top_k <= 0 || top_k > experts)
+        return fail(SFG_ERR_INVALID_CONFIG, "invalid MoE configuration");
+    if (w_dtype == SFG_I8 && (!s13 || !s2)) return fail(SFG_ERR_SHAPE, "int8 experts need scales");
+    if (w_dtype != SFG_BF16 && w_dtype != SFG_I8) return fail(SFG_ERR_UNSUPPORTED, "expert dtype %d", w_dtype);
+    return moe_experts(x, offsets, token_ids, w13, s13, w2, s2, w_dtype, act, y, tokens, hidden,
+                       inter, experts, top_k, as_stream(stream));
+}
+
+int sfg_hip_moe_combine_v1(const float* y, const int32_t* position, const float* weights,
+                           const float* residual, float* out, int64_t tokens, int64_t hidden,
+                           int64_t top_k, void* stream) {
+    if (!y || !position || !weights || !residual || !out || tokens <= 0 || hidden <= 0 ||
+        top_k <= 0 || (hidden & 3))
+        return fail(SFG_ERR_SHAPE, "moe_combine: invalid arguments");
+    sfg::launch_moe_combine(y, position, weights, residual, out, tokens, hidden, top_k,
+                            as_stream(stream));
+    return check_launch("moe_combine");
+}
+
+// ---------------------------------------------------------------------------
+// Whole layer.
+// ---------------------------------------------------------------------------
+
+}  // extern "C"
+
+namespace {
+
+struct LayerBuffers {
+    void* xn = nullptr;       // [rows][H] act dtype
+    float* xn2_f32 = nullptr; // MoE router input [rows][H]
+    float* qkv = nullptr;     // [rows][qkvw]
+    void* q = nullptr;        // prefill: [B][Hq][S][D] act; decode: fp32 [B][Hq][D]
+    void* k = nullptr;
+    void* v = nullptr;
+    void* attn = nullptr;     // merged [rows][H] act dtype
+    float* r1 = nullptr;      // [rows][H]
+    void* act = nullptr;      // dense [rows][I] / MoE [rows*k][I]
+    float* y = nullptr;       // MoE [rows*k][H]
+    int32_t* ids = nullptr; float* wts = nullptr; int32_t* counts = nullptr;
+    int32_t* offsets = nullptr; int32_t* token_ids = nullptr; int32_t* slots = nullptr;
+    float* rweights = nullptr; int32_t* position = nullptr;
+    void* attn_ws = nullptr;
+    void* gemm_ws = nullptr; size_t gemm_ws_bytes = 0;
+    size_t total = 0;
+};
+
+int validate_desc(const sfg_layer_desc* d) {
+    if (!d) return fail(SFG_ERR_INVALID_CONFIG, "null layer descriptor");
+    if (d->abi != SFG_HIP_ABI_VERSION)
+        return fail(SFG_ERR_ABI, "layer descriptor ABI %d, library ABI %d", d->abi, SFG_HIP_ABI_VERSION);
+    // validate (decoder_compiler.cpp:26-39)
+    if (d->batch <= 0 || d->sequence <= 0 || d->hidden <= 0 || d->intermediate <= 0 ||
+        d->query_heads <= 0 || d->kv_heads <= 0 || d->head_dim <= 0 ||
+        d->hidden != d->query_heads * d->head_dim || d->query_heads % d->kv_heads != 0 ||
+        !(d->rms_epsilon > 0.0f))
+        return fail(SFG_ERR_INVALID_CONFIG, "invalid decoder configuration");
+    if (d->ffn == 1 && (d->experts <= 0 || d->top_k <= 0 || d->top_k > d->experts))
+        return fail(SFG_ERR_INVALID_CONFIG, "invalid decoder MoE configuration");
+    if (d->context < 0) return fail(SFG_ERR_INVALID_CONFIG, "invalid decoder context sequence");
+    if (d->act_dtype != SFG_F32 && d->act_dtype != SFG_BF16)
+        return fail(SFG_ERR_UNSUPPORTED, "activation dtype %d", d->act_dtype);
+    if (d->act_dtype == SFG_F32 && d->weight_dtype != SFG_F32)
+        return fail(SFG_ERR_UNSUPPORTED, "fp32 activations need fp32 weights");
+    if (d->act_dtype == SFG_BF16 && d->weight_dtype != SFG_BF16 && d->weight_dtype != SFG_I8)
+        return fail(SFG_ERR_UNSUPPORTED, "bf16 activations need bf16 or int8 weights");
+    if (d->context > 0) {
+        if (d->act_dtype != SFG_BF16)
+            return fail(SFG_ERR_UNSUPPORTED, "decode runs on a bf16 paged KV cache");
+        if (d->page_tokens <= 0 || d->pages_per_seq <= 0 || d->num_pages <= 0)
+            return fail(SFG_ERR_INVALID_CONFIG, "invalid paged KV configuration");
+        if (d->context > d->pages_per_seq * d->page_tokens)
+            return fail(SFG_ERR_GUARD, "KV cache length violates compiled guard");
+    } else if (d->causal && d->sequence <= 0) {
+        return fail(SFG_ERR_INVALID_CONFIG, "invalid attention configuration");
+    }
+    if (d->ffn == 1 && d->act_dtype != SFG_BF16)
+        return fail(SFG_ERR_UNSUPPORTED, "MoE layers run with bf16 activations");
+    return SFG_OK;
+}
+
+LayerBuffers plan_buffers(const sfg_layer_desc* d, void* ws) {
+    LayerBuffers b;
+    Carve c(ws);
+    const int64_t rows = static_cast<int64_t>(d->batch) * d->sequence;
+    const int64_t H = d->hidden, I = d->intermediate, D = d->head_dim;
+    const int64_t kvd = static_cast<int64_t>(d->kv_heads) * D;
+    const int64_t qkvw = H + 2 * kvd;
+    const size_t ae = d->act_dtype == SFG_F32 ? 4 : 2;
+    const bool moe = d->ffn == 1;
+    b.xn = c.take(rows * H * ae);
+    if (moe) b.xn2_f32 = static_cast<float*>(c.take(rows * H * 4));
+    b.qkv = static_cast<float*>(c.take(rows * qkvw * 4));
+    if (d->context > 0) {
+        b.q = c.take(rows * H * 4);
+    } else {
+        b.q = c.take(rows * H * ae);
+        b.k = c.take(rows * kvd * ae);
+        b.v = c.take(rows * kvd * ae);
+    }
+    b.attn = c.take(rows * H * ae);
+    b.r1 = static_cast<float*>(c.take(rows * H * 4));
+    if (moe) {
+        const int64_t assign = rows * d->top_k;
+        b.act = c.take(assign * I * 2);
+        b.y = static_cast<float*>(c.take(assign * H * 4));
+        b.ids = static_cast<int32_t*>(c.take(assign * 4));
+        b.wts = static_cast<float*>(c.take(assign * 4));
+        b.counts = static_cast<int32_t*>(c.take(static_cast<size_t>(d->experts) * 4));
+        b.offsets = static_cast<int32_t*>(c.take(static_cast<size_t>(d->experts + 1) * 4));
+        b.token_ids = static_cast<int32_t*>(c.take(assign * 4));
+        b.slots = static_cast<int32_t*>(c.take(assign * 4));
+        b.rweights = static_cast<float*>(c.take(assign * 4));
+        b.position = static_cast<int32_t*>(c.take(assign * 4));
+    } else {
+        b.act = c.take(rows * I * ae);
+    }
+    if (d->context > 0) {
+        const int splits = sfg::decode_split_count(d->batch, d->kv_heads, d->context,
+                                                   d->page_tokens, d->kv_splits);
+        b.attn_ws = c.take(sfg::decode_workspace_bytes(d->batch, d->query_heads, D, splits));
+    }
+    // Split-K scratch sized for the widest projection.
+    size_t g = 0;
+    const int64_t ns[4] = {qkvw, H, 2 * I, H};
+    const int64_t ks[4] = {H, H, H, I};
+    for (int i = 0; i < 4; ++i) {
+        const size_t s = sfg::gemm_workspace_bytes(rows, ns[i], ks[i]);
+        if (s > g) g = s;
+    }
+    b.gemm_ws_bytes = g;
+    b.gemm_ws = c.take(g);
+    b.total = c.used;
+    return b;
+}
+
+struct Marks {
+    void** ev;
+    hipStream_t s;
+    void mark(int id) const {
+        if (ev && ev[id]) (void)hipEventRecord(static_cast<hipEvent_t>(ev[id]), s);
+    }
+};
+
+}  // namespace
+
+extern "C" {
+
+size_t sfg_hip_decoder_layer_workspace_v1(const sfg_layer_desc* desc) {
+    if (validate_desc(desc) != SFG_OK) return 0;
+    return plan_buffers(desc, nullptr).total;
+}
+
+int sfg_hip_decoder_layer_v1(const sfg_layer_desc* d, const sfg_layer_weights* w,
+                             const sfg_layer_io* io, void* workspace, size_t workspace_bytes,
+                             void* stream_ptr) {
+    int rc = validate_desc(d);
+    if (rc != SFG_OK) return rc;
+    if (!w || !io || !io->x || !io->out) return fail(SFG_ERR_SHAPE, "decoder layer: null weights or io");
+    const hipStream_t s = as_stream(stream_ptr);
+    const LayerBuffers need = plan_buffers(d, nullptr);
+    if (!workspace || workspace_bytes < need.total)
+        return fail(SFG_ERR_WORKSPACE, "decoder layer: workspace %zu < %zu", workspace_bytes, need.total);
+    const LayerBuffers b = plan_buffers(d, workspace);
+    const bool moe = d->ffn == 1;
+    const bool decode = d->context > 0;
+    const int64_t rows = static_cast<int64_t>(d->batch) * d->sequence;
+    const int64_t H = d->hidden, I = d->intermediate, D = d->head_dim;
+    const int64_t kvd = static_cast<int64_t>(d->kv_heads) * D;
+    const int64_t qkvw = H + 2 * kvd;
+    const int act = d->act_dtype;
+    const int wdt = d->weight_dtype;
+    if (!w->rms1 || !w->rms2 || !w->w_qkv || !w->w_o || !w->rope_table)
+        return fail(SFG_ERR_SHAPE, "decoder layer: missing attention weights");
+    if (wdt == SFG_I8 && (!w->s_qkv || !w->s_o)) return fail(SFG_ERR_SHAPE, "int8 weights need scales");
+    if (moe) {
+        if (!w->router || !w->w13 || !w->w2) return fail(SFG_ERR_SHAPE, "MoE layer: missing expert weights");
+        if (wdt == SFG_I8 && (!w->s13 || !w->s2)) return fail(SFG_ERR_SHAPE, "int8 experts need scales");
+        if (d->use_routing_trace && (!io->trace_ids || !io->trace_weights))
+            return fail(SFG_ERR_SHAPE, "routing trace requested but not supplied");
+    } else {
+        if (!w->w_gate_up || !w->w_down) return fail(SFG_ERR_SHAPE, "dense layer: missing FFN weights");
+        if (wdt == SFG_I8 && (!w->s_gate_up || !w->s_down)) return fail(SFG_ERR_SHAPE, "int8 weights need scales");
+    }
+    if (decode && (!w->k_pool || !w->v_pool || !w->page_table))
+        return fail(SFG_ERR_SHAPE, "decode step needs the paged KV pools and page table");
+
+    const Marks mk{io->stage_events, s};
+    auto gemm = [&](const void* a, int64_t lda, const void* bw, const float* bs, void* c, int c_dtype,
+                    const float* res, int64_t m, int64_t n, int64_t k, int epi) -> int {
+        sfg::GemmProblem p{};
+        p.a = a; p.a_dtype = act; p.lda = lda;
+        p.b = bw; p.b_dtype = wdt; p.ldb = k; p.b_scales = bs;
+        p.c = c; p.c_dtype = c_dtype; p.ldc = n;
+        p.residual = res; p.ldr = n;
+        p.m = m; p.n = n; p.k = k; p.epilogue = epi; p.groups = 1;
+        const int r = sfg::launch_gemm(p, b.gemm_ws, b.gemm_ws_bytes, s);
+        if (r != SFG_OK)
+            return fail(r, "decoder layer GEMM %lldx%lldx%lld not lowered for dtype %d/%d",
+                        (long long)m, (long long)n, (long long)k, act, wdt);
+        return SFG_OK;
+    };
+
+    mk.mark(SFG_MARK_START);
+    // 1. RMSNorm
+    sfg::launch_rmsnorm(io->x, w->rms1, b.xn, act, rows, H, d->rms_epsilon, s);
+    mk.mark(SFG_MARK_NORM1);
+    // 2. fused QKV projection -> fp32
+    if ((rc = gemm(b.xn, H, w->w_qkv, w->s_qkv, b.qkv, SFG_F32, nullptr, rows, qkvw, H, SFG_EPI_NONE)))
+        return rc;
+    mk.mark(SFG_MARK_QKV);
+    // 3. split + RoPE (decode keeps only Q: the step's K/V are discarded,
+    //    decoder_compiler.cpp:238-243)
+    const float scale = default_scale(D, 0.0f);
+    if (decode) {
+        sfg::launch_split_rope(b.qkv, w->rope_table, d->batch, d->sequence, d->query_heads,
+                               d->kv_heads, D, b.q, nullptr, nullptr, SFG_F32, s);
+    } else {
+        sfg::launch_split_rope(b.qkv, w->rope_table, d->batch, d->sequence, d->query_heads,
+                               d->kv_heads, D, b.q, b.k, b.v, act, s);
+    }
+    mk.mark(SFG_MARK_ROPE);
+    // 4. attention -> merged [rows][H]
+    if (decode) {
+        if (d->sequence != 1) return fail(SFG_ERR_UNSUPPORTED, "decode lowers one new token per sequence");
+        const int splits = sfg::decode_split_count(d->batch, d->kv_heads, d->context, d->page_tokens,
+                                                   d->kv_splits);
+        rc = sfg::launch_attn_decode_paged(
+            static_cast<const float*>(b.q), w->k_pool, w->v_pool, w->page_table, nullptr, d->context,
+            b.attn, act, d->batch, d->query_heads, d->kv_heads, D, d->page_tokens, d->pages_per_seq,
+            d->num_pages, splits, scale, b.attn_ws, s,
+            io->stage_events ? static_cast<hipEvent_t>(io->stage_events[SFG_MARK_ATTN_MAIN]) : nullptr);
+        if (rc != SFG_OK) return fail(rc, "decode attention not lowered (head_dim %lld)", (long long)D);
+    } else {
+        if (act == SFG_F32) {
+            if (D > 128) return fail(SFG_ERR_UNSUPPORTED, "fp32 attention head_dim > 128");
+            sfg::launch_attn_prefill_f32(static_cast<const float*>(b.q), static_cast<const float*>(b.k),
+                                         static_cast<const float*>(b.v), b.attn, act, d->batch,
+                                         d->query_heads, d->kv_heads, d->sequence, d->sequence, D,
+                                         d->causal, scale, s);
+        } else {
+            rc = sfg::launch_attn_prefill_bf16(static_cast<const uint16_t*>(b.q),
+                                               static_cast<const uint16_t*>(b.k),
+                                               static_cast<const uint16_t*>(b.v), b.attn, act,
+                                               d->batch, d->query_heads, d->kv_heads, d->sequence,
+                                               d->sequence, D, d->causal, scale, s);
+            if (rc != SFG_OK) return fail(rc, "bf16 prefill attention not lowered (head_dim %lld)", (long long)D);
+        }
+        mk.mark(SFG_MARK_ATTN_MAIN);
+    }
+    mk.mark(SFG_MARK_ATTN);
+    // 5. O-projection + residual: r1 = attn Wo + x
+    if ((rc = gemm(b.attn, H, w->w_o, w->s_o, b.r1, SFG_F32, io->x, rows, H, H, SFG_EPI_RESIDUAL)))
+        return rc;
+    mk.mark(SFG_MARK_OPROJ);
+    // 6. RMSNorm
+    sfg::launch_rmsnorm(b.r1, w->rms2, b.xn, act, rows, H, d->rms_epsilon, s);
+    if (moe) sfg::launch_rmsnorm(b.r1, w->rms2, b.xn2_f32, SFG_F32, rows, H, d->rms_epsilon, s);
+    mk.mark(SFG_MARK_NORM2);
+    if (!moe) {
+        mk.mark(SFG_MARK_ROUTE);
+        // 7. gate_up + SwiGLU -> act ; down + residual -> out
+        if ((rc = gemm(b.xn, H, w->w_gate_up, w->s_gate_up, b.act, act, nullptr, rows, I, H, SFG_EPI_SWIGLU)))
+            return rc;
+        mk.mark(SFG_MARK_FFN_UP);
+        if ((rc = gemm(b.act, I, w->w_down, w->s_down, io->out, SFG_F32, b.r1, rows, H, I, SFG_EPI_RESIDUAL)))
+            return rc;
+        mk.mark(SFG_MARK_FFN_DOWN);
+    } else {
+        const int64_t E = d->experts, K = d->top_k;
+        if (d->use_routing_trace) {
+            rc = sfg::launch_moe_dispatch(io->trace_ids, io->trace_weights, rows, E, K, b.counts,
+                                          b.offsets, b.token_ids, b.slots, b.rweights, b.position, s);
+        } else {
+            rc = sfg::launch_moe_router(b.xn2_f32, w->router, w->router_bias, rows, H, E, K, b.ids,
+                                        b.wts, s);
+            if (rc != SFG_OK) return fail(rc, "MoE router not lowered (E=%lld k=%lld)", (long long)E, (long long)K);
+            rc = sfg::launch_moe_dispatch(b.ids, b.wts, rows, E, K, b.counts, b.offsets, b.token_ids,
+                                          b.slots, b.rweights, b.position, s);
+        }
+        if (rc != SFG_OK) return fail(rc, "MoE dispatch not lowered");
+        mk.mark(SFG_MARK_ROUTE);
+        const float* route_w = d->use_routing_trace ? io->trace_weights : b.wts;
+        rc = moe_experts(static_cast<const uint16_t*>(b.xn), b.offsets, b.token_ids, w->w13, w->s13,
+                         w->w2, w->s2, wdt, static_cast<uint16_t*>(b.act), b.y, rows, H, I, E, K, s);
+        if (rc != SFG_OK) return rc;
+        mk.mark(SFG_MARK_FFN_UP);
+        sfg::launch_moe_combine(b.y, b.position, route_w, b.r1, io->out, rows, H, K, s);
+        mk.mark(SFG_MARK_FFN_DOWN);
+    }
+    mk.mark(SFG_MARK_END);
+    return check_launch("decoder_layer");
+}
+
+int sfg_hip_events_create_v1(int count, void** events) {
+    if (count <= 0 || !events) return fail(SFG_ERR_SHAPE, "events_create: invalid");
+    for (int i = 0; i < count; ++i) {
+        hipEvent_t e;
+        const hipError_t r = hipEventCreate(&e);
+        if (r != hipSuccess) return fail(SFG_ERR_DEVICE, "hipEventCreate: %s", hipGetErrorString(r));
+        events[i] = e;
+    }
+    return SFG_OK;
+}
+
+int sfg_hip_events_destroy_v1(int count, void** events) {
+    if (count < 0 || (count > 0 && !events)) return fail(SFG_ERR_SHAPE, "events_destroy: invalid");
+    for (int i = 0; i < count; ++i)
+        if (events[i]) (void)hipEventDestroy(static_cast<hipEvent_t>(events[i]));
+    return SFG_OK;
+}
+
+int sfg_hip_event_elapsed_v1(void* start, void* end, float* ms) {
+    if (!start || !end || !ms) return fail(SFG_ERR_SHAPE, "event_elapsed: invalid");
+    const hipError_t r = hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(end));
+    if (r != hipSuccess) return fail(SFG_ERR_DEVICE, "hipEventElapsedTime: %s", hipGetErrorString(r));
+    return SFG_OK;
+}
+
+int sfg_hip_stream_synchronize_v1(void* stream) {
+    const hipError_t r = hipStreamSynchronize(as_stream(stream));
+    if (r != hipSuccess) return fail(SFG_ERR_DEVICE, "hipStreamSynchronize: %s", hipGetErrorString(r));
+    return SFG_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,87 @@
+// sfg_device.hpp -- device-side helpers shared by the gfx950 kernels.
+//
+// bf16 values live in memory as uint16_t bit patterns.  Conversion from fp32 is
+// round-to-nearest-even by adding 0x7FFF + lsb, the rule of the reference's
+// convert_to_bf16 (src/compiler.cpp:34-43), so host-rounded inputs and
+// device-rounded intermediates agree bit for bit on finite values.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sfg {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef uint16_t bf16_t;
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t v) {
+    return __uint_as_float(static_cast<uint32_t>(v) << 16);
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    const uint32_t bits = __float_as_uint(f);
+    return static_cast<uint16_t>((bits + 0x7FFFu + ((bits >> 16) & 1u)) >> 16);
+}
+
+// Two fp32 values -> packed bf16 pair (low half = a).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+    return static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
+}
+
+// 8 bf16 held in a uint4 -> MFMA operand.
+__device__ __forceinline__ bf16x8 as_bf16x8(const uint4& v) {
+    return __builtin_bit_cast(bf16x8, v);
+}
+
+// 8 int8 (two dwords) -> 8 bf16.  |q| <= 127 has at most 7 significant bits,
+// so the fp32 value's low 16 bits are zero and truncation is exact.
+__device__ __forceinline__ uint4 i8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
+    uint4 r;
+    const int8_t* p0 = reinterpret_cast<const int8_t*>(&lo);
+    const int8_t* p1 = reinterpret_cast<const int8_t*>(&hi);
+    r.x = (__float_as_uint(static_cast<float>(p0[0])) >> 16) |
+          (__float_as_uint(static_cast<float>(p0[1])) & 0xFFFF0000u);
+    r.y = (__float_as_uint(static_cast<float>(p0[2])) >> 16) |
+          (__float_as_uint(static_cast<float>(p0[3])) & 0xFFFF0000u);
+    r.z = (__float_as_uint(static_cast<float>(p1[0])) >> 16) |
+          (__float_as_uint(static_cast<float>(p1[1])) & 0xFFFF0000u);
+    r.w = (__float_as_uint(static_cast<float>(p1[2])) >> 16) |
+          (__float_as_uint(static_cast<float>(p1[3])) & 0xFFFF0000u);
+    return r;
+}
+
+// 8 fp32 -> 8 bf16 packed in a uint4.
+__device__ __forceinline__ uint4 f32x8_to_bf16x8(const float* v) {
+    uint4 r;
+    r.x = pack_bf16x2(v[0], v[1]);
+    r.y = pack_bf16x2(v[2], v[3]);
+    r.z = pack_bf16x2(v[4], v[5]);
+    r.w = pack_bf16x2(v[6], v[7]);
+    return r;
+}
+
+__device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+    return v;
+}
+
+// v_exp_f32: 2^x.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+}  // namespace sfg

@@ -1,0 +1,257 @@
+// sfg_elementwise.hip -- HBM-bound row kernels: RMSNorm, split+RoPE, weight
+// packing / quantisation, fp32->bf16.
+//
+// All of these move each byte once; launches are sized to put >= 2 workgroups
+// per CU on the 256-CU part and every global access is 16-byte vectorised where
+// the row width allows.
+#include "sfg_kernels.hpp"
+
+namespace sfg {
+
+// ---------------------------------------------------------------------------
+// RMSNorm (decoder_compiler.cpp:41-62).  One workgroup per row; 256 threads
+// stream the row with float4 loads, sum squares in double (the reference's
+// accumulator type), reduce across the wave with shuffles and across waves in
+// LDS, then scale.  inverse = 1/sqrtf(float(sum/width) + eps), both correctly
+// rounded (hipcc's default for sqrtf and fp32 division).
+// ---------------------------------------------------------------------------
+template <typename OutT>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x,
+                                                      const float* __restrict__ w,
+                                                      OutT* __restrict__ y, int width, float eps) {
+    const int row = blockIdx.x;
+    const float* xr = x + static_cast<int64_t>(row) * width;
+    OutT* yr = y + static_cast<int64_t>(row) * width;
+    __shared__ double partial[4];
+    __shared__ float inv_shared;
+    double sum = 0.0;
+    const bool vec = (width & 3) == 0;
+    if (vec) {
+        for (int c = threadIdx.x * 4; c < width; c += 256 * 4) {
+            const float4 v = *reinterpret_cast<const float4*>(xr + c);
+            sum += static_cast<double>(v.x) * v.x;
+            sum += static_cast<double>(v.y) * v.y;
+            sum += static_cast<double>(v.z) * v.z;
+            sum += static_cast<double>(v.w) * v.w;
+        }
+    } else {
+        for (int c = threadIdx.x; c < width; c += 256) sum += static_cast<double>(xr[c]) * xr[c];
+    }
+    sum = wave_sum(sum);
+    if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = sum;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const double total = partial[0] + partial[1] + partial[2] + partial[3];
+        inv_shared = 1.0f / sqrtf(static_cast<float>(total / static_cast<double>(width)) + eps);
+    }
+    __syncthreads();
+    const float inv = inv_shared;
+    if (vec) {
+        for (int c = threadIdx.x * 4; c < width; c += 256 * 4) {
+            const float4 v = *reinterpret_cast<const float4*>(xr + c);
+            const float4 g = *reinterpret_cast<const float4*>(w + c);
+            const float o0 = v.x * inv * g.x, o1 = v.y * inv * g.y;
+            const float o2 = v.z * inv * g.z, o3 = v.w * inv * g.w;
+            if constexpr (sizeof(OutT) == 4) {
+                *reinterpret_cast<float4*>(yr + c) = make_float4(o0, o1, o2, o3);
+            } else {
+                uint2 packed;
+                packed.x = pack_bf16x2(o0, o1);
+                packed.y = pack_bf16x2(o2, o3);
+                *reinterpret_cast<uint2*>(yr + c) = packed;
+            }
+        }
+    } else {
+        for (int c = threadIdx.x; c < width; c += 256) {
+            const float o = xr[c] * inv * w[c];
+            if constexpr (sizeof(OutT) == 4) yr[c] = o;
+            else yr[c] = f32_to_bf16(o);
+        }
+    }
+}
+
+void launch_rmsnorm(const float* x, const float* w, void* y, int y_dtype, int64_t rows,
+                    int64_t width, float eps, hipStream_t stream) {
+    if (y_dtype == SFG_F32)
+        rmsnorm_kernel<float><<<dim3(rows), dim3(256), 0, stream>>>(x, w, static_cast<float*>(y),
+                                                                     static_cast<int>(width), eps);
+    else
+        rmsnorm_kernel<uint16_t><<<dim3(rows), dim3(256), 0, stream>>>(
+            x, w, static_cast<uint16_t*>(y), static_cast<int>(width), eps);
+}
+
+// ---------------------------------------------------------------------------
+// split_qkv + apply_rope (decoder_compiler.cpp:96-148).  One thread per
+// (row, head-slot, pair): Q heads, then K heads, then V heads of one row.  The
+// rotation uses the host-built table (cos, sin per position and pair), whose
+// float expressions are the reference's, so no device libm enters the angle.
+// ---------------------------------------------------------------------------
+template <typename OutT>
+__global__ __launch_bounds__(256) void split_rope_kernel(
+    const float* __restrict__ qkv, const float2* __restrict__ table, int batch, int seq,
+    int q_heads, int kv_heads, int head_dim, OutT* __restrict__ q, OutT* __restrict__ k,
+    OutT* __restrict__ v) {
+    const int half = head_dim >> 1;
+    const int heads_total = q_heads + 2 * kv_heads;
+    const int64_t total = static_cast<int64_t>(batch) * seq * heads_total * half;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= total) return;
+    const int pair = static_cast<int>(idx % half);
+    const int64_t rest = idx / half;
+    const int slot = static_cast<int>(rest % heads_total);
+    const int64_t row = rest / heads_total;
+    const int b = static_cast<int>(row / seq);
+    const int s = static_cast<int>(row % seq);
+    const int width = heads_total * head_dim;
+    const float2 ev = *reinterpret_cast<const float2*>(qkv + row * width + slot * head_dim +
+                                                       2 * pair);
+    float o0 = ev.x, o1 = ev.y;
+    OutT* dst;
+    if (slot < q_heads) {
+        dst = q + ((static_cast<int64_t>(b) * q_heads + slot) * seq + s) * head_dim;
+    } else if (slot < q_heads + kv_heads) {
+        if (k == nullptr) return;
+        dst = k + ((static_cast<int64_t>(b) * kv_heads + (slot - q_heads)) * seq + s) * head_dim;
+    } else {
+        if (v == nullptr) return;
+        dst = v + ((static_cast<int64_t>(b) * kv_heads + (slot - q_heads - kv_heads)) * seq + s) *
+                      head_dim;
+    }
+    if (slot < q_heads + kv_heads) {
+        const float2 cs = table[static_cast<int64_t>(s) * half + pair];
+        o0 = ev.x * cs.x - ev.y * cs.y;
+        o1 = ev.x * cs.y + ev.y * cs.x;
+    }
+    if constexpr (sizeof(OutT) == 4) {
+        *reinterpret_cast<float2*>(dst + 2 * pair) = make_float2(o0, o1);
+    } else {
+        *reinterpret_cast<uint32_t*>(dst + 2 * pair) = pack_bf16x2(o0, o1);
+    }
+}
+
+void launch_split_rope(const float* qkv, const float* table, int64_t batch, int64_t seq,
+                       int64_t q_heads, int64_t kv_heads, int64_t head_dim, void* q, void* k,
+                       void* v, int out_dtype, hipStream_t stream) {
+    const int64_t total = batch * seq * (q_heads + 2 * kv_heads) * (head_dim / 2);
+    const dim3 grid(static_cast<unsigned>((total + 255) / 256));
+    const float2* t = reinterpret_cast<const float2*>(table);
+    if (out_dtype == SFG_F32)
+        split_rope_kernel<float><<<grid, 256, 0, stream>>>(
+            qkv, t, batch, seq, q_heads, kv_heads, head_dim, static_cast<float*>(q),
+            static_cast<float*>(k), static_cast<float*>(v));
+    else
+        split_rope_kernel<uint16_t><<<grid, 256, 0, stream>>>(
+            qkv, t, batch, seq, q_heads, kv_heads, head_dim, static_cast<uint16_t*>(q),
+            static_cast<uint16_t*>(k), static_cast<uint16_t*>(v));
+}
+
+// ---------------------------------------------------------------------------
+// Weight packing: fp32 [K][N] -> [N][K] (fp32 or bf16) through a 64x64 LDS tile
+// so both the read and the write are coalesced.
+// ---------------------------------------------------------------------------
+template <typename OutT>
+__global__ __launch_bounds__(256) void transpose_pack_kernel(const float* __restrict__ src,
+                                                             int64_t k, int64_t n, int64_t ld,
+                                                             OutT* __restrict__ dst) {
+    __shared__ float tile[64][65];
+    const int64_t k0 = static_cast<int64_t>(blockIdx.y) * 64;
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 64;
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    for (int r = ty; r < 64; r += 4) {
+        const int64_t kk = k0 + r, nn = n0 + tx;
+        tile[r][tx] = (kk < k && nn < n) ? src[kk * ld + nn] : 0.0f;
+    }
+    __syncthreads();
+    for (int r = ty; r < 64; r += 4) {
+        const int64_t nn = n0 + r, kk = k0 + tx;
+        if (nn < n && kk < k) {
+            const float val = tile[tx][r];
+            if constexpr (sizeof(OutT) == 4) dst[nn * k + kk] = val;
+            else dst[nn * k + kk] = f32_to_bf16(val);
+        }
+    }
+}
+
+void launch_pack_weight(const float* src, int64_t k, int64_t n, int64_t ld, void* dst,
+                        int dtype, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>((n + 63) / 64), static_cast<unsigned>((k + 63) / 64));
+    if (dtype == SFG_F32)
+        transpose_pack_kernel<float><<<grid, 256, 0, stream>>>(src, k, n, ld,
+                                                              static_cast<float*>(dst));
+    else
+        transpose_pack_kernel<uint16_t><<<grid, 256, 0, stream>>>(src, k, n, ld,
+                                                                 static_cast<uint16_t*>(dst));
+}
+
+// quantize_matmul_weights (next_milestones.cpp:611-637) applied to the
+// transposed weight (transpose_decoder_weight, 233-244).  Pass 1: one thread per
+// output channel n walks its column of src [K][N] (coalesced across n) for the
+// absmax.  Pass 2: the transposing tile kernel quantises.
+__global__ __launch_bounds__(256) void column_absmax_kernel(const float* __restrict__ src,
+                                                            int64_t k, int64_t n,
+                                                            float* __restrict__ scales) {
+    const int64_t col = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (col >= n) return;
+    float maximum = 0.0f;
+    for (int64_t r = 0; r < k; ++r) maximum = fmaxf(maximum, fabsf(src[r * n + col]));
+    float scale = maximum > 0.0f ? maximum / 127.0f : 1.0f;
+    if (scale == 0.0f) scale = 1.0f;
+    scales[col] = scale;
+}
+
+__global__ __launch_bounds__(256) void quantize_pack_kernel(const float* __restrict__ src,
+                                                            int64_t k, int64_t n,
+                                                            const float* __restrict__ scales,
+                                                            int8_t* __restrict__ dst) {
+    __shared__ float tile[64][65];
+    const int64_t k0 = static_cast<int64_t>(blockIdx.y) * 64;
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 64;
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    for (int r = ty; r < 64; r += 4) {
+        const int64_t kk = k0 + r, nn = n0 + tx;
+        tile[r][tx] = (kk < k && nn < n) ? src[kk * n + nn] : 0.0f;
+    }
+    __syncthreads();
+    for (int r = ty; r < 64; r += 4) {
+        const int64_t nn = n0 + r, kk = k0 + tx;
+        if (nn < n && kk < k) {
+            float q = roundf(tile[tx][r] / scales[nn]);
+            q = fminf(fmaxf(q, -127.0f), 127.0f);
+            dst[nn * k + kk] = static_cast<int8_t>(q);
+        }
+    }
+}
+
+void launch_quantize_weight(const float* src, int64_t k, int64_t n, int8_t* dst, float* scales,
+                            hipStream_t stream) {
+    column_absmax_kernel<<<dim3(static_cast<unsigned>((n + 255) / 256)), 256, 0, stream>>>(
+        src, k, n, scales);
+    const dim3 grid(static_cast<unsigned>((n + 63) / 64), static_cast<unsigned>((k + 63) / 64));
+    quantize_pack_kernel<<<grid, 256, 0, stream>>>(src, k, n, scales, dst);
+}
+
+__global__ __launch_bounds__(256) void to_bf16_kernel(const float* __restrict__ src,
+                                                      uint16_t* __restrict__ dst, int64_t count) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < count) dst[i] = f32_to_bf16(src[i]);
+}
+
+void launch_to_bf16(const float* src, uint16_t* dst, int64_t count, hipStream_t stream) {
+    to_bf16_kernel<<<dim3(static_cast<unsigned>((count + 255) / 256)), 256, 0, stream>>>(
+        src, dst, count);
+}
+
+// Zero-fill (used instead of hipMemsetAsync so the layer stays capturable).
+__global__ __launch_bounds__(256) void fill_zero_kernel(uint32_t* __restrict__ dst, int64_t words) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < words) dst[i] = 0u;
+}
+
+void launch_fill_zero(void* dst, size_t bytes, hipStream_t stream) {
+    const int64_t words = static_cast<int64_t>(bytes / 4);
+    if (words == 0) return;
+    fill_zero_kernel<<<dim3(static_cast<unsigned>((words + 255) / 256)), 256, 0, stream>>>(
+        static_cast<uint32_t*>(dst), words);
+}
+
+}  // namespace sfg

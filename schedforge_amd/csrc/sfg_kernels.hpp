@@ -1,0 +1,83 @@
+// sfg_kernels.hpp -- launchers shared between the kernel translation units and
+// the C-ABI layer (sfg_api.hip).  Launchers assume arguments were validated by
+// the ABI layer; they never allocate.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/sfg_hip.h"
+#include "sfg_device.hpp"
+
+namespace sfg {
+
+// elementwise
+void launch_rmsnorm(const float* x, const float* w, void* y, int y_dtype, int64_t rows,
+                    int64_t width, float eps, hipStream_t stream);
+void launch_split_rope(const float* qkv, const float* table, int64_t batch, int64_t seq,
+                       int64_t q_heads, int64_t kv_heads, int64_t head_dim, void* q, void* k,
+                       void* v, int out_dtype, hipStream_t stream);
+void launch_pack_weight(const float* src, int64_t k, int64_t n, int64_t ld, void* dst,
+                        int dtype, hipStream_t stream);
+void launch_quantize_weight(const float* src, int64_t k, int64_t n, int8_t* dst, float* scales,
+                            hipStream_t stream);
+void launch_to_bf16(const float* src, uint16_t* dst, int64_t count, hipStream_t stream);
+void launch_fill_zero(void* dst, size_t bytes, hipStream_t stream);
+
+// GEMM family.  A grouped problem: `groups` independent products sharing N, K;
+// group g covers rows [row_begin(g), row_end(g)) of the (virtual) row space,
+// given by `offsets` (device, groups+1 entries) or a single dense group.  A's
+// row r is read from a_rows[r] when a_rows != nullptr (dispatch gather).
+struct GemmProblem {
+    const void* a; int a_dtype; int64_t lda;
+    const int32_t* a_rows;      // optional gather (row indices into A)
+    const void* b; int b_dtype; int64_t ldb; const float* b_scales;
+    int64_t b_group_stride;     // elements between groups' B matrices
+    int64_t s_group_stride;     // scales between groups
+    void* c; int c_dtype; int64_t ldc;
+    const float* residual; int64_t ldr;
+    int64_t m, n, k;            // m: total rows (dense) or upper bound (grouped)
+    int epilogue;
+    const int32_t* offsets;     // grouped: device [groups+1]; nullptr = dense
+    int groups;
+};
+
+size_t gemm_workspace_bytes(int64_t m, int64_t n, int64_t k);
+// Returns SFG_OK or an error code (unsupported combination).
+int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes,
+                hipStream_t stream);
+
+// attention
+void launch_attn_prefill_f32(const float* q, const float* k, const float* v, void* out,
+                             int out_dtype, int64_t batch, int64_t q_heads, int64_t kv_heads,
+                             int64_t seq_q, int64_t seq_kv, int64_t head_dim, int causal,
+                             float scale, hipStream_t stream);
+int launch_attn_prefill_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v, void* out,
+                             int out_dtype, int64_t batch, int64_t q_heads, int64_t kv_heads,
+                             int64_t seq_q, int64_t seq_kv, int64_t head_dim, int causal,
+                             float scale, hipStream_t stream);
+int decode_split_count(int64_t batch, int64_t kv_heads, int64_t max_context,
+                       int64_t page_tokens, int32_t requested);
+size_t decode_workspace_bytes(int64_t batch, int64_t q_heads, int64_t head_dim, int splits);
+int launch_attn_decode_paged(const float* q, const uint16_t* k_pool, const uint16_t* v_pool,
+                             const int32_t* page_table, const int32_t* seq_lens, int64_t max_context,
+                             void* out, int out_dtype, int64_t batch, int64_t q_heads,
+                             int64_t kv_heads, int64_t head_dim, int64_t page_tokens,
+                             int64_t pages_per_seq, int64_t num_pages, int splits, float scale,
+                             void* workspace, hipStream_t stream, hipEvent_t mid_event);
+
+// MoE
+size_t moe_route_workspace_bytes(int64_t tokens, int64_t experts, int64_t top_k);
+int launch_moe_router(const float* x, const float* router, const float* bias, int64_t tokens,
+                      int64_t hidden, int64_t experts, int64_t top_k, int32_t* ids,
+                      float* weights, hipStream_t stream);
+int launch_moe_dispatch(const int32_t* ids, const float* weights, int64_t tokens,
+                        int64_t experts, int64_t top_k, int32_t* counts, int32_t* offsets,
+                        int32_t* token_ids, int32_t* route_slots, float* routing_weights,
+                        int32_t* position, hipStream_t stream);
+void launch_moe_combine(const float* y, const int32_t* position, const float* weights,
+                        const float* residual, float* out, int64_t tokens, int64_t hidden,
+                        int64_t top_k, hipStream_t stream);
+
+}  // namespace sfg

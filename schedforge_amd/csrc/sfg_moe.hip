@@ -1,0 +1,201 @@
+// sfg_moe.hip -- MoE routing pipeline for gfx950:
+//   Router -> Softmax -> TopK   (route_topk, moe_compiler.cpp:412-455)
+//   Histogram -> PrefixSum -> Segmented Dispatch (dispatch_tokens, 496-528)
+//   weighted combine (219-226) fused with the FFN residual (decoder_compiler.cpp:277).
+// The grouped expert GEMMs run on the GEMM family (sfg_gemm.hip) with the
+// dispatch offsets as device-side group bounds and token_ids as the A gather.
+//
+// Integer outputs (ids, counts, offsets, token_ids, route_slots, positions)
+// are exact: logits are sequential fp32 FMA chains in feature order (the order
+// the reference's scalar loop accumulates), selection compares logits with ties
+// to the lower expert index, and the dispatch rank of an assignment is the
+// number of earlier (token, slot) assignments routed to the same expert.
+#include "sfg_kernels.hpp"
+
+namespace sfg {
+
+// One thread per (token, expert) chain; the block then runs softmax + top-k for
+// its tokens with one thread per token.  E <= 256, top_k <= 8.
+__global__ __launch_bounds__(256) void moe_router_kernel(
+    const float* __restrict__ x, const float* __restrict__ router, const float* __restrict__ bias,
+    int tokens, int hidden, int experts, int top_k, int32_t* __restrict__ ids,
+    float* __restrict__ weights) {
+    __shared__ float logits[256];
+    const int per_block = 256 / experts;
+    const int t_local = threadIdx.x / experts;
+    const int e = threadIdx.x % experts;
+    const int t = blockIdx.x * per_block + t_local;
+    if (t_local < per_block && t < tokens) {
+        const float* xr = x + static_cast<int64_t>(t) * hidden;
+        float acc = 0.f;
+        for (int f = 0; f < hidden; ++f) acc = __builtin_fmaf(xr[f], router[static_cast<int64_t>(f) * experts + e], acc);
+        if (bias) acc = acc + bias[e];
+        logits[t_local * experts + e] = acc;
+    }
+    __syncthreads();
+    if (threadIdx.x >= per_block) return;
+    const int tok = blockIdx.x * per_block + threadIdx.x;
+    if (tok >= tokens) return;
+    const float* lg = logits + threadIdx.x * experts;
+    float maximum = -INFINITY;
+    for (int j = 0; j < experts; ++j) maximum = fmaxf(maximum, lg[j]);
+    float denom = 0.f;
+    for (int j = 0; j < experts; ++j) denom += expf(lg[j] - maximum);
+    uint32_t taken[8] = {0, 0, 0, 0, 0, 0, 0, 0};  // bitmask over <= 256 experts
+    int sel[8];
+    float selected = 0.f;
+    for (int s = 0; s < top_k; ++s) {
+        int best = -1;
+        for (int j = 0; j < experts; ++j) {
+            if (taken[j >> 5] & (1u << (j & 31))) continue;
+            if (best < 0 || lg[j] > lg[best]) best = j;
+        }
+        taken[best >> 5] |= 1u << (best & 31);
+        sel[s] = best;
+        selected += expf(lg[best] - maximum) / denom;
+    }
+    for (int s = 0; s < top_k; ++s) {
+        const int j = sel[s];
+        ids[static_cast<int64_t>(tok) * top_k + s] = j;
+        weights[static_cast<int64_t>(tok) * top_k + s] = (expf(lg[j] - maximum) / denom) / selected;
+    }
+}
+
+int launch_moe_router(const float* x, const float* router, const float* bias, int64_t tokens,
+                      int64_t hidden, int64_t experts, int64_t top_k, int32_t* ids,
+                      float* weights, hipStream_t stream) {
+    if (experts <= 0 || experts > 256 || top_k <= 0 || top_k > 8 || top_k > experts)
+        return SFG_ERR_UNSUPPORTED;
+    const int per_block = static_cast<int>(256 / experts);
+    const dim3 grid(static_cast<unsigned>((tokens + per_block - 1) / per_block));
+    moe_router_kernel<<<grid, 256, 0, stream>>>(x, router, bias, static_cast<int>(tokens),
+                                                static_cast<int>(hidden), static_cast<int>(experts),
+                                                static_cast<int>(top_k), ids, weights);
+    return SFG_OK;
+}
+
+// Single workgroup of 1024 threads: histogram (LDS atomics), exclusive prefix
+// over experts, then a stable scatter: assignments are visited in chunks of
+// 1024 in (token, slot) order; inside a wave the rank among equal experts is a
+// popcount of the matching-lanes ballot below the lane, across waves an
+// exclusive scan of per-wave counts, across chunks a running cursor.
+__global__ __launch_bounds__(1024) void moe_dispatch_kernel(
+    const int32_t* __restrict__ ids, const float* __restrict__ weights, int total, int experts,
+    int top_k, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+    int32_t* __restrict__ token_ids, int32_t* __restrict__ route_slots,
+    float* __restrict__ routing_weights, int32_t* __restrict__ position) {
+    __shared__ int s_count[256];
+    __shared__ int s_cursor[256];
+    __shared__ int s_wave[16][256];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    for (int e = tid; e < experts; e += 1024) s_count[e] = 0;
+    __syncthreads();
+    for (int a = tid; a < total; a += 1024) {
+        const int e = ids[a];
+        if (e >= 0 && e < experts) atomicAdd(&s_count[e], 1);
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int run = 0;
+        for (int e = 0; e < experts; ++e) {
+            offsets[e] = run;
+            s_cursor[e] = run;
+            counts[e] = s_count[e];
+            run += s_count[e];
+        }
+        offsets[experts] = run;
+    }
+    __syncthreads();
+    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    for (int base = 0; base < total; base += 1024) {
+        const int a = base + tid;
+        const bool active = a < total;
+        const int e = active ? ids[a] : -1;
+        for (int j = tid; j < 16 * experts; j += 1024) s_wave[j / experts][j % experts] = 0;
+        __syncthreads();
+        // Per-wave ranks: peel off one expert value per iteration.
+        int rank = 0;
+        uint64_t pending = __ballot(active && e >= 0 && e < experts);
+        while (pending) {
+            const int leader = __ffsll(static_cast<unsigned long long>(pending)) - 1;
+            const int le = __shfl(e, leader, 64);
+            const uint64_t match = __ballot(active && e == le);
+            if (active && e == le) rank = __popcll(match & below);
+            if (lane == 0) s_wave[wave][le] = __popcll(match);
+            pending &= ~match;
+        }
+        __syncthreads();
+        // Exclusive scan across the 16 waves, per expert; advance cursors.
+        for (int x = tid; x < experts; x += 1024) {
+            int run = s_cursor[x];
+            for (int w = 0; w < 16; ++w) {
+                const int c = s_wave[w][x];
+                s_wave[w][x] = run;
+                run += c;
+            }
+            s_cursor[x] = run;
+        }
+        __syncthreads();
+        if (active && e >= 0 && e < experts) {
+            const int dst = s_wave[wave][e] + rank;
+            token_ids[dst] = a / top_k;
+            route_slots[dst] = a % top_k;
+            routing_weights[dst] = weights[a];
+            position[a] = dst;
+        }
+        __syncthreads();
+    }
+}
+
+int launch_moe_dispatch(const int32_t* ids, const float* weights, int64_t tokens,
+                        int64_t experts, int64_t top_k, int32_t* counts, int32_t* offsets,
+                        int32_t* token_ids, int32_t* route_slots, float* routing_weights,
+                        int32_t* position, hipStream_t stream) {
+    if (experts <= 0 || experts > 256) return SFG_ERR_UNSUPPORTED;
+    const int64_t total = tokens * top_k;
+    if (total > (1ll << 30)) return SFG_ERR_UNSUPPORTED;
+    moe_dispatch_kernel<<<1, 1024, 0, stream>>>(ids, weights, static_cast<int>(total),
+                                                 static_cast<int>(experts), static_cast<int>(top_k),
+                                                 counts, offsets, token_ids, route_slots,
+                                                 routing_weights, position);
+    return SFG_OK;
+}
+
+size_t moe_route_workspace_bytes(int64_t tokens, int64_t experts, int64_t top_k) {
+    (void)tokens; (void)experts; (void)top_k;
+    return 0;
+}
+
+// out[t][f] = residual[t][f] + sum_s w[t][s] * y[position[t][s]][f], slots in
+// order (the token-major order of reference_moe, moe_compiler.cpp:651-679).
+__global__ __launch_bounds__(256) void moe_combine_kernel(
+    const float* __restrict__ y, const int32_t* __restrict__ position,
+    const float* __restrict__ weights, const float* __restrict__ residual,
+    float* __restrict__ out, int hidden, int top_k) {
+    const int t = blockIdx.x;
+    for (int f = threadIdx.x * 4; f < hidden; f += 256 * 4) {
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int s = 0; s < top_k; ++s) {
+            const float w = weights[static_cast<int64_t>(t) * top_k + s];
+            const int64_t pos = position[static_cast<int64_t>(t) * top_k + s];
+            const float4 v = *reinterpret_cast<const float4*>(y + pos * hidden + f);
+            acc.x = fmaf(w, v.x, acc.x);
+            acc.y = fmaf(w, v.y, acc.y);
+            acc.z = fmaf(w, v.z, acc.z);
+            acc.w = fmaf(w, v.w, acc.w);
+        }
+        const float4 r = *reinterpret_cast<const float4*>(residual + static_cast<int64_t>(t) * hidden + f);
+        *reinterpret_cast<float4*>(out + static_cast<int64_t>(t) * hidden + f) =
+            make_float4(r.x + acc.x, r.y + acc.y, r.z + acc.z, r.w + acc.w);
+    }
+}
+
+void launch_moe_combine(const float* y, const int32_t* position, const float* weights,
+                        const float* residual, float* out, int64_t tokens, int64_t hidden,
+                        int64_t top_k, hipStream_t stream) {
+    moe_combine_kernel<<<dim3(static_cast<unsigned>(tokens)), 256, 0, stream>>>(
+        y, position, weights, residual, out, static_cast<int>(hidden), static_cast<int>(top_k));
+}
+
+}  // namespace sfg

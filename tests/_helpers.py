@@ -1,0 +1,62 @@
+"""Shared test helpers: device buffers, oracle-data -> DecoderData, reduced configs."""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from schedforge_amd import CONFIGS
+
+# Reduced versions of the five configs: same structure (dtype, GQA ratio,
+# head_dim 128, paging, MoE top-2 of 8) at sizes the CPU oracle finishes in
+# seconds.
+SMALL = {
+    "c1": CONFIGS["c1"],
+    "c2": CONFIGS["c2"].replace(batch=4, hidden=1024, intermediate=2816, query_heads=8,
+                                kv_heads=2, context_sequence=1000),
+    "c3": CONFIGS["c3"].replace(batch=2, sequence=256, hidden=1024, intermediate=512,
+                                query_heads=8, kv_heads=2),
+    "c4": CONFIGS["c4"].replace(sequence=512, hidden=1024, intermediate=2048, query_heads=8,
+                                kv_heads=2),
+    "c5": CONFIGS["c5"].replace(batch=16, hidden=1024, intermediate=2048, query_heads=8,
+                                kv_heads=2, context_sequence=1024),
+}
+
+TOL = {"f32": 1e-4, "bf16": 2e-2, "w8": 1e-2}
+
+
+def decoder_data(d):
+    from schedforge_amd.layer import DecoderData
+    return DecoderData(**{k: getattr(d, k) for k in DecoderData.__dataclass_fields__
+                          if hasattr(d, k)})
+
+
+def stream():
+    import torch
+    return torch.cuda.current_stream().cuda_stream
+
+
+def dev(a, dtype=None):
+    import torch
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if dtype is not None:
+        t = t.to(dtype)
+    return t.cuda()
+
+
+def bf16_dev(a):
+    """fp32 numpy -> device int16 tensor holding bf16 bits (RNE)."""
+    import oracle
+    import torch
+    bits = oracle.to_bf16_bits(a).view(np.int16)
+    return torch.from_numpy(bits).cuda()
+
+
+def host(t):
+    return t.detach().cpu().numpy()
+
+
+def bf16_host(t):
+    """device int16 bf16 bits -> fp32 numpy."""
+    bits = host(t).view(np.uint16).astype(np.uint32) << 16
+    return bits.view(np.float32)
