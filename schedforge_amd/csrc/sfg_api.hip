@@ -306,7 +306,7 @@ static int moe_experts(const uint16_t* x, const int32_t* offsets, const int32_t*
                        int w_dtype, uint16_t* act, float* y, int64_t tokens, int64_t hidden,
                        int64_t inter, int64_t experts, int64_t top_k, hipStream_t stream) {
     sfg::GemmProblem p{};
-    p.a = x; p.a_dtype = SFG_BF16; p.lda = hidden; p.a_rows = token_ids;
+    p.a = x; p.a_dtype = SFG_BF16; p.lda = hidden; p.a_rows = token_ids; p.a_rows_limit = tokens;
     p.b = w13; p.b_dtype = w_dtype; p.ldb = hidden; p.b_scales = s13;
     p.b_group_stride = 2 * inter * hidden; p.s_group_stride = 2 * inter;
     p.c = act; p.c_dtype = SFG_BF16; p.ldc = inter;

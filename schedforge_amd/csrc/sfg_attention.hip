@@ -305,7 +305,7 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(
     const int wave = threadIdx.x >> 6;
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int q_heads = kv_heads * G;
-    const int len = seq_lens ? seq_lens[b] : uniform_len;
+    const int len = min(seq_lens ? seq_lens[b] : uniform_len, pages_per_seq * kPageTok);
     const int pages = (len + kPageTok - 1) / kPageTok;
     // Pages of this split, then of this wave (contiguous ranges).
     const int sp_begin = static_cast<int>(static_cast<int64_t>(pages) * split / splits);

@@ -44,7 +44,7 @@ __device__ __forceinline__ void store_out(void* c, int c_dtype, int64_t idx, flo
 // Skinny (decode) GEMM.
 // ===========================================================================
 struct SkinnyArgs {
-    const uint16_t* a; int64_t lda; const int32_t* a_rows;
+    const uint16_t* a; int64_t lda; const int32_t* a_rows; int64_t a_rows_limit;
     const void* b; int64_t ldb; const float* scales;
     int64_t b_group_stride, s_group_stride;
     void* c; int c_dtype; int64_t ldc;
@@ -68,8 +68,10 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(SkinnyArgs p) {
     const int ks = blockIdx.y;
     int64_t rb = 0, re = p.m;
     if (p.offsets) {
-        rb = p.offsets[g];
-        re = p.offsets[g + 1];
+        // Device-side bounds are data: clamp them so a corrupt table cannot
+        // send the kernel outside [0, m).
+        rb = min(max(static_cast<int64_t>(p.offsets[g]), int64_t(0)), p.m);
+        re = min(max(static_cast<int64_t>(p.offsets[g + 1]), rb), p.m);
     }
     if (re <= rb) return;
 
@@ -118,7 +120,8 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(SkinnyArgs p) {
         for (int i = 0; i < MT; ++i) {
             const int64_t r = pass + i * 16 + lr;
             avalid[i] = r < re;
-            const int64_t src = avalid[i] ? (p.a_rows ? p.a_rows[r] : r) : 0;
+            int64_t src = avalid[i] ? (p.a_rows ? p.a_rows[r] : r) : 0;
+            if (src < 0 || src >= p.a_rows_limit) { avalid[i] = false; src = 0; }
             arow[i] = p.a + src * p.lda + lg * 32;
         }
 
@@ -272,7 +275,7 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(SkinnyArgs p) {
 // 16-byte fragment reads of 32 consecutive rows spread over the banks.
 // ===========================================================================
 struct TiledArgs {
-    const uint16_t* a; int64_t lda; const int32_t* a_rows;
+    const uint16_t* a; int64_t lda; const int32_t* a_rows; int64_t a_rows_limit;
     const void* b; int64_t ldb; const float* scales;
     int64_t b_group_stride, s_group_stride;
     void* c; int c_dtype; int64_t ldc;
@@ -303,15 +306,19 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(TiledArgs p) {
     if (p.offsets) {
         int64_t t = blockIdx.y;
         g = -1;
+        auto bound = [&](int e) {
+            return min(max(static_cast<int64_t>(p.offsets[e]), int64_t(0)), p.m);
+        };
         for (int e = 0; e < p.groups; ++e) {
-            const int64_t rows = p.offsets[e + 1] - p.offsets[e];
+            const int64_t lo = bound(e);
+            const int64_t rows = max(bound(e + 1) - lo, int64_t(0));
             const int64_t tiles = (rows + kTM - 1) / kTM;
             if (t < tiles) { g = e; break; }
             t -= tiles;
         }
         if (g < 0) return;
-        rb = p.offsets[g];
-        re = p.offsets[g + 1];
+        rb = bound(g);
+        re = max(bound(g + 1), rb);
         mtile = t;
     }
     const int64_t row0 = rb + mtile * kTM;
@@ -335,7 +342,8 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(TiledArgs p) {
         ld_col[h] = (idx & 3) * 8;         // 0,8,16,24
         const int64_t r = row0 + ld_row[h];
         a_ok[h] = r < re;
-        const int64_t src = a_ok[h] ? (p.a_rows ? p.a_rows[r] : r) : 0;
+        int64_t src = a_ok[h] ? (p.a_rows ? p.a_rows[r] : r) : 0;
+        if (src < 0 || src >= p.a_rows_limit) { a_ok[h] = false; src = 0; }
         a_src[h] = src * p.lda + ld_col[h];
         int64_t brow;
         if (kGlu) {
@@ -526,12 +534,13 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(F32Args p) {
 namespace {
 
 constexpr int kTargetWorkgroups = 768;  // ~3 per CU on 256 CUs
+constexpr size_t kCounterBytes = 65536;   // split-K tile counters (16384 column tiles)
 constexpr int kMaxSplit = 16;
 
 int skinny_split(int64_t col_tiles, int64_t k) {
     const int64_t chunks = k / kSkinnyChunk;
     int ks = 1;
-    while (ks < kMaxSplit && col_tiles * ks < kTargetWorkgroups && chunks >= (ks * 2) * 4 * 2) ks *= 2;
+    while (ks < kMaxSplit && col_tiles * ks < kTargetWorkgroups && chunks >= (ks * 2) * 4) ks *= 2;
     return ks;
 }
 
@@ -574,11 +583,17 @@ constexpr int64_t kSkinnyGroupedMaxTotal = 512;
 
 size_t gemm_workspace_bytes(int64_t m, int64_t n, int64_t k) {
     (void)m;
-    const int64_t col_tiles = (n + 15) / 16;
-    const int ks = skinny_split(col_tiles, k);
-    const size_t partial = static_cast<size_t>(col_tiles) * ks * 4 * 2 * 64 * sizeof(floatx4);
-    const size_t counters = static_cast<size_t>(col_tiles) * sizeof(uint32_t);
-    return ((partial + 255) / 256) * 256 + ((counters + 255) / 256) * 256;
+    // Fixed tile-counter region first (shared by every GEMM that uses this
+    // workspace, so no GEMM's partials can land on another's counters), then
+    // split-K partials: upper bound over both column-tile widths.
+    size_t best = 0;
+    for (int64_t width : {int64_t(16), int64_t(32)}) {
+        const int64_t col_tiles = (n + width - 1) / width;
+        const int ks = skinny_split(col_tiles, k);
+        const size_t partial = static_cast<size_t>(col_tiles) * ks * 4 * 2 * 64 * sizeof(floatx4);
+        if (partial > best) best = partial;
+    }
+    return kCounterBytes + ((best + 255) / 256) * 256;
 }
 
 int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes, hipStream_t stream) {
@@ -608,6 +623,7 @@ int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes, h
         const int64_t col_tiles = glu ? p.n / 16 : p.n / 32;
         SkinnyArgs a{};
         a.a = static_cast<const uint16_t*>(p.a); a.lda = p.lda; a.a_rows = p.a_rows;
+    a.a_rows_limit = p.a_rows ? p.a_rows_limit : p.m;
         a.b = p.b; a.ldb = p.ldb; a.scales = p.b_scales;
         a.b_group_stride = p.b_group_stride; a.s_group_stride = p.s_group_stride;
         a.c = p.c; a.c_dtype = p.c_dtype; a.ldc = p.ldc;
@@ -623,11 +639,12 @@ int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes, h
         }
         if (a.ks > 1) {
             const size_t partial_bytes = static_cast<size_t>(col_tiles) * a.ks * mt * 2 * 64 * sizeof(floatx4);
-            const size_t need = ((partial_bytes + 255) / 256) * 256 + static_cast<size_t>(col_tiles) * 4;
-            if (workspace == nullptr || workspace_bytes < need) return SFG_ERR_WORKSPACE;
-            a.partials = static_cast<float*>(workspace);
-            a.counters = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) +
-                                                     ((partial_bytes + 255) / 256) * 256);
+            const size_t need = kCounterBytes + partial_bytes;
+            if (workspace == nullptr || workspace_bytes < need ||
+                static_cast<size_t>(col_tiles) * sizeof(uint32_t) > kCounterBytes)
+                return SFG_ERR_WORKSPACE;
+            a.counters = static_cast<uint32_t*>(workspace);
+            a.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
         }
         const dim3 grid(static_cast<unsigned>(col_tiles), static_cast<unsigned>(a.ks),
                         static_cast<unsigned>(groups));
@@ -638,6 +655,7 @@ int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes, h
     if (p.n % (glu ? 64 : 128) != 0 || p.k % kTK != 0) return SFG_ERR_UNSUPPORTED;
     TiledArgs a{};
     a.a = static_cast<const uint16_t*>(p.a); a.lda = p.lda; a.a_rows = p.a_rows;
+    a.a_rows_limit = p.a_rows ? p.a_rows_limit : p.m;
     a.b = p.b; a.ldb = p.ldb; a.scales = p.b_scales;
     a.b_group_stride = p.b_group_stride; a.s_group_stride = p.s_group_stride;
     a.c = p.c; a.c_dtype = p.c_dtype; a.ldc = p.ldc;

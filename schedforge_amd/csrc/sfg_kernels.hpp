@@ -32,6 +32,7 @@ void launch_fill_zero(void* dst, size_t bytes, hipStream_t stream);
 struct GemmProblem {
     const void* a; int a_dtype; int64_t lda;
     const int32_t* a_rows;      // optional gather (row indices into A)
+    int64_t a_rows_limit;       // rows of A addressable through a_rows
     const void* b; int b_dtype; int64_t ldb; const float* b_scales;
     int64_t b_group_stride;     // elements between groups' B matrices
     int64_t s_group_stride;     // scales between groups

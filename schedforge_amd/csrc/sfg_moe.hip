@@ -172,13 +172,14 @@ size_t moe_route_workspace_bytes(int64_t tokens, int64_t experts, int64_t top_k)
 __global__ __launch_bounds__(256) void moe_combine_kernel(
     const float* __restrict__ y, const int32_t* __restrict__ position,
     const float* __restrict__ weights, const float* __restrict__ residual,
-    float* __restrict__ out, int hidden, int top_k) {
+    float* __restrict__ out, int hidden, int top_k, int64_t total) {
     const int t = blockIdx.x;
     for (int f = threadIdx.x * 4; f < hidden; f += 256 * 4) {
         float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
         for (int s = 0; s < top_k; ++s) {
             const float w = weights[static_cast<int64_t>(t) * top_k + s];
             const int64_t pos = position[static_cast<int64_t>(t) * top_k + s];
+            if (pos < 0 || pos >= total) continue;  // corrupt index: contributes nothing
             const float4 v = *reinterpret_cast<const float4*>(y + pos * hidden + f);
             acc.x = fmaf(w, v.x, acc.x);
             acc.y = fmaf(w, v.y, acc.y);
@@ -195,7 +196,8 @@ void launch_moe_combine(const float* y, const int32_t* position, const float* we
                         const float* residual, float* out, int64_t tokens, int64_t hidden,
                         int64_t top_k, hipStream_t stream) {
     moe_combine_kernel<<<dim3(static_cast<unsigned>(tokens)), 256, 0, stream>>>(
-        y, position, weights, residual, out, static_cast<int>(hidden), static_cast<int>(top_k));
+        y, position, weights, residual, out, static_cast<int>(hidden), static_cast<int>(top_k),
+        tokens * top_k);
 }
 
 }  // namespace sfg

@@ -31,6 +31,14 @@ def decoder_data(d):
                           if hasattr(d, k)})
 
 
+# Device tensors handed to the C ABI as raw pointers must outlive the
+# asynchronous kernels that read them: a temporary's block goes back to
+# torch's caching allocator at once and the next allocation can reuse it.
+# Every tensor made here stays referenced until the test ends (see the
+# autouse fixture in conftest.py, which synchronises first).
+KEEP_ALIVE: list = []
+
+
 def stream():
     import torch
     return torch.cuda.current_stream().cuda_stream
@@ -41,7 +49,9 @@ def dev(a, dtype=None):
     t = torch.from_numpy(np.ascontiguousarray(a))
     if dtype is not None:
         t = t.to(dtype)
-    return t.cuda()
+    t = t.cuda()
+    KEEP_ALIVE.append(t)
+    return t
 
 
 def bf16_dev(a):
@@ -49,7 +59,9 @@ def bf16_dev(a):
     import oracle
     import torch
     bits = oracle.to_bf16_bits(a).view(np.int16)
-    return torch.from_numpy(bits).cuda()
+    t = torch.from_numpy(bits).cuda()
+    KEEP_ALIVE.append(t)
+    return t
 
 
 def host(t):

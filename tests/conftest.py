@@ -5,8 +5,9 @@ from pathlib import Path
 import pytest
 
 ROOT = Path(__file__).resolve().parents[1]
-if str(ROOT) not in sys.path:
-    sys.path.insert(0, str(ROOT))
+for p in (ROOT, ROOT / "tests"):
+    if str(p) not in sys.path:
+        sys.path.insert(0, str(p))
 
 
 def pytest_configure(config):
@@ -28,3 +29,13 @@ def pytest_collection_modifyitems(config, items):
     for item in items:
         if "gpu" in item.keywords:
             item.add_marker(skip)
+
+
+@pytest.fixture(autouse=True)
+def _device_buffers_outlive_kernels():
+    yield
+    from _helpers import KEEP_ALIVE
+    if KEEP_ALIVE:
+        import torch
+        torch.cuda.synchronize()
+        KEEP_ALIVE.clear()
