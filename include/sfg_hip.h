@@ -24,8 +24,11 @@
  *                 sfg_hip_pack_weight_v1 produces the transposed packed form.
  *                 int8 weights are [N][K] with per-channel fp32 scales, exactly
  *                 the reference's QuantizedMatMulWeights (next_milestones.h:52-56).
- *   paged KV      [page][Hkv][page_tokens][D] bf16, one page table row per
- *                 sequence [B][pages_per_seq] int32.
+ *   paged KV      K pool [page][Hkv][page_tokens][D] bf16, V pool
+ *                 [page][Hkv][D][page_tokens] bf16 (token-minor inside a page:
+ *                 the decode kernel reads V^T operands as 8-byte runs); each
+ *                 (page, kv_head) is one contiguous 4 KB run at D=128, 16-token
+ *                 pages.  One page-table row per sequence [B][pages_per_seq].
  */
 #ifndef SFG_HIP_H
 #define SFG_HIP_H
@@ -97,9 +100,8 @@ int sfg_hip_rmsnorm_v1(const float* x, const float* w, void* y, int y_dtype, int
  * SFG_BF16 or SFG_I8 (then b_scales[N or 2N] per output channel).
  * c_dtype: SFG_F32 or SFG_BF16.  Replaces execute(LoopIR) (runtime.cpp:581-626)
  * for the four projections and quantized_invoke (next_milestones.cpp:50-69).
- * workspace: sfg_hip_gemm_workspace_v1 bytes (split-K partials + tile counters),
- * which must be zero-filled once before first use (the kernels keep the
- * counters zero between calls). */
+ * workspace: sfg_hip_gemm_workspace_v1 bytes (currently 0: every kernel reduces
+ * inside its workgroup; the argument is kept for split-K variants). */
 typedef struct {
     const void* a; int32_t a_dtype; int64_t lda;
     const void* b; int32_t b_dtype; int64_t ldb; const float* b_scales;
@@ -131,7 +133,8 @@ int sfg_hip_attn_prefill_v1(const void* q, const void* k, const void* v, void* o
 
 /* Paged Split-KV decode (attention_compiler.cpp:244-285 split/merge,
  * next_milestones.cpp:137-184 page walk).  q fp32 [B][Hq][D] (one new token per
- * sequence), pools bf16 [num_pages][Hkv][page_tokens][D], page_table
+ * sequence), pools bf16: K [num_pages][Hkv][page_tokens][D], V
+ * [num_pages][Hkv][D][page_tokens]; page_table
  * [B][pages_per_seq], seq_lens[B] (each <= pages_per_seq*page_tokens).  out
  * merged [B][Hq*D] in out_dtype.  kv_splits <= 0 picks a split count.  Page ids
  * are validated on the host against num_pages only when validate_pages != 0

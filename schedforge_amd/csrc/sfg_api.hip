@@ -246,7 +246,8 @@ int sfg_hip_attn_decode_paged_v1(const float* q, const uint16_t* k_pool, const u
     if (!workspace || workspace_bytes < need)
         return fail(SFG_ERR_WORKSPACE, "attn_decode_paged: workspace %zu < %zu", workspace_bytes, need);
     const int rc = sfg::launch_attn_decode_paged(
-        q, k_pool, v_pool, page_table, seq_lens, max_context, out, out_dtype, batch, q_heads,
+        q, q_heads * head_dim, nullptr, 0, k_pool, v_pool, page_table, seq_lens, max_context, out,
+        out_dtype, batch, q_heads,
         kv_heads, head_dim, page_tokens, pages_per_seq, num_pages, splits,
         default_scale(head_dim, scale), workspace, as_stream(stream), nullptr);
     if (rc != SFG_OK)
@@ -426,9 +427,7 @@ LayerBuffers plan_buffers(const sfg_layer_desc* d, void* ws) {
     b.xn = c.take(rows * H * ae);
     if (moe) b.xn2_f32 = static_cast<float*>(c.take(rows * H * 4));
     b.qkv = static_cast<float*>(c.take(rows * qkvw * 4));
-    if (d->context > 0) {
-        b.q = c.take(rows * H * 4);
-    } else {
+    if (d->context == 0) {
         b.q = c.take(rows * H * ae);
         b.k = c.take(rows * kvd * ae);
         b.v = c.take(rows * kvd * ae);
@@ -547,10 +546,7 @@ int sfg_hip_decoder_layer_v1(const sfg_layer_desc* d, const sfg_layer_weights* w
     // 3. split + RoPE (decode keeps only Q: the step's K/V are discarded,
     //    decoder_compiler.cpp:238-243)
     const float scale = default_scale(D, 0.0f);
-    if (decode) {
-        sfg::launch_split_rope(b.qkv, w->rope_table, d->batch, d->sequence, d->query_heads,
-                               d->kv_heads, D, b.q, nullptr, nullptr, SFG_F32, s);
-    } else {
+    if (!decode) {
         sfg::launch_split_rope(b.qkv, w->rope_table, d->batch, d->sequence, d->query_heads,
                                d->kv_heads, D, b.q, b.k, b.v, act, s);
     }
@@ -560,8 +556,11 @@ int sfg_hip_decoder_layer_v1(const sfg_layer_desc* d, const sfg_layer_weights* w
         if (d->sequence != 1) return fail(SFG_ERR_UNSUPPORTED, "decode lowers one new token per sequence");
         const int splits = sfg::decode_split_count(d->batch, d->kv_heads, d->context, d->page_tokens,
                                                    d->kv_splits);
+        // RoPE of the new token's query (position 0 within the step, as the
+        // reference rotates it, decoder_compiler.cpp:96-104) is applied while
+        // the kernel loads Q straight from the QKV rows.
         rc = sfg::launch_attn_decode_paged(
-            static_cast<const float*>(b.q), w->k_pool, w->v_pool, w->page_table, nullptr, d->context,
+            b.qkv, qkvw, w->rope_table, 0, w->k_pool, w->v_pool, w->page_table, nullptr, d->context,
             b.attn, act, d->batch, d->query_heads, d->kv_heads, D, d->page_tokens, d->pages_per_seq,
             d->num_pages, splits, scale, b.attn_ws, s,
             io->stage_events ? static_cast<hipEvent_t>(io->stage_events[SFG_MARK_ATTN_MAIN]) : nullptr);

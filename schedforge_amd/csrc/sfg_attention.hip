@@ -15,8 +15,8 @@
 //    decode (attention_compiler.cpp:244-285 split, 132-145 merge_online;
 //    next_milestones.cpp:137-184 page walk).  A workgroup owns (sequence,
 //    kv_head, split) and serves the whole GQA group, so each K/V byte is read
-//    once; lanes split a 16-token page as 4 tokens x 16 chunks of 8 dims, pages
-//    are double-buffered in registers, waves merge in LDS, splits merge in a
+//    once; scores and the value product run on MFMA (see below), pages are
+//    double-buffered in registers, waves merge in LDS, splits merge in a
 //    second small kernel.
 #include "sfg_kernels.hpp"
 
@@ -289,186 +289,172 @@ int launch_attn_prefill_bf16(const uint16_t* q, const uint16_t* k, const uint16_
 }
 
 // ===========================================================================
-// Paged Split-KV decode, head_dim 128, 16-token pages.
+// Paged Split-KV decode on MFMA, head_dim 128, 16-token pages.
+//
+// Pool layouts (one 4 KB run per (page, kv_head)):
+//   K [page][Hkv][16 tokens][128 dims]   V [page][Hkv][128 dims][16 tokens]
+// V is token-minor inside a page so that the MFMA operand V^T (dims x tokens)
+// is read as 8-byte runs.  Per page a wave does
+//   S^T[16 tok][16 q] = K[16 tok][128] Q^T[128][16 q]   4 x mfma_16x16x32_bf16
+//   O^T[128 d][16 q] += V^T[128 d][16 tok] P^T[16 tok][16 q]  8 x mfma_16x16x16_bf16
+// where the GQA group's G query heads occupy the first G columns.  In the
+// S^T accumulator lane l holds query (l & 15) and tokens 4 (l >> 4) + r, which
+// is exactly the P^T operand layout, and the O^T accumulator holds the same
+// query per lane: the online softmax needs only a 4-lane max per page and a
+// per-lane rescale.
 // ===========================================================================
 constexpr int kDecD = 128;
 constexpr int kPageTok = 16;
 
+typedef short short4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ short4v as_short4(const uint2& v) { return __builtin_bit_cast(short4v, v); }
+
 template <int G>
 __global__ __launch_bounds__(256) void attn_decode_split_kernel(
-    const float* __restrict__ q, const uint16_t* __restrict__ k_pool,
-    const uint16_t* __restrict__ v_pool, const int32_t* __restrict__ page_table,
-    const int32_t* __restrict__ seq_lens, int uniform_len, int kv_heads, int pages_per_seq,
-    int num_pages, int splits, float scale_log2, float* __restrict__ part_ml,
-    float* __restrict__ part_acc) {
+    const float* __restrict__ q, int64_t q_row_stride, const float* __restrict__ rope,
+    int rope_pos, const uint16_t* __restrict__ k_pool, const uint16_t* __restrict__ v_pool,
+    const int32_t* __restrict__ page_table, const int32_t* __restrict__ seq_lens, int uniform_len,
+    int kv_heads, int pages_per_seq, int num_pages, int splits, float scale_log2,
+    float* __restrict__ part_ml, float* __restrict__ part_acc) {
+    static_assert(G >= 1 && G <= 16, "GQA group must fit the 16 MFMA columns");
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int q_heads = kv_heads * G;
+    const int lr = lane & 15, lg = lane >> 4;
     const int len = min(seq_lens ? seq_lens[b] : uniform_len, pages_per_seq * kPageTok);
     const int pages = (len + kPageTok - 1) / kPageTok;
-    // Pages of this split, then of this wave (contiguous ranges).
     const int sp_begin = static_cast<int>(static_cast<int64_t>(pages) * split / splits);
     const int sp_end = static_cast<int>(static_cast<int64_t>(pages) * (split + 1) / splits);
     const int n_sp = sp_end - sp_begin;
     const int w_begin = sp_begin + n_sp * wave / 4;
     const int w_end = sp_begin + n_sp * (wave + 1) / 4;
 
-    const int dc = (lane & 15) * 8;  // 8 dims per lane
-    const int ts = lane >> 4;        // token slot 0..3 within each group of 4 tokens
+    // Q^T operand: lane supplies query head lr (zero beyond the group), dims
+    // 32 s + 8 lg + [0, 8), rotated by the host table at rope_pos when given.
+    bf16x8 qf[4];
+    {
+        const bool has = lr < G;
+        const float* qr = q + static_cast<int64_t>(b) * q_row_stride +
+                          static_cast<int64_t>(kvh * G + (has ? lr : 0)) * kDecD;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int d0 = 32 * s + 8 * lg;
+            float v[8];
+            const float4 a = *reinterpret_cast<const float4*>(qr + d0);
+            const float4 c = *reinterpret_cast<const float4*>(qr + d0 + 4);
+            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+            v[4] = c.x; v[5] = c.y; v[6] = c.z; v[7] = c.w;
+            if (rope) {
+                const float2* t = reinterpret_cast<const float2*>(rope) +
+                                  static_cast<int64_t>(rope_pos) * (kDecD / 2) + d0 / 2;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float2 cs = t[e];
+                    const float ev = v[2 * e], od = v[2 * e + 1];
+                    v[2 * e] = ev * cs.x - od * cs.y;
+                    v[2 * e + 1] = ev * cs.y + od * cs.x;
+                }
+            }
+            if (!has) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = 0.f;
+            }
+            qf[s] = as_bf16x8(f32x8_to_bf16x8(v));
+        }
+    }
 
-    float qv[G][8];
+    floatx4 acc[8];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const float* qr = q + (static_cast<int64_t>(b) * q_heads + kvh * G + g) * kDecD + dc;
-        const float4 a = *reinterpret_cast<const float4*>(qr);
-        const float4 c = *reinterpret_cast<const float4*>(qr + 4);
-        qv[g][0] = a.x * scale_log2; qv[g][1] = a.y * scale_log2;
-        qv[g][2] = a.z * scale_log2; qv[g][3] = a.w * scale_log2;
-        qv[g][4] = c.x * scale_log2; qv[g][5] = c.y * scale_log2;
-        qv[g][6] = c.z * scale_log2; qv[g][7] = c.w * scale_log2;
-    }
-    float m_run[G], l_run[G], acc[G][8];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        m_run[g] = -INFINITY;
-        l_run[g] = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
-    }
+    for (int i = 0; i < 8; ++i) acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.f;
 
     const int32_t* ptab = page_table + static_cast<int64_t>(b) * pages_per_seq;
-    const int64_t head_stride = static_cast<int64_t>(kPageTok) * kDecD;       // one (page, kv_head)
+    const int64_t head_stride = static_cast<int64_t>(kPageTok) * kDecD;
     const int64_t page_stride = head_stride * kv_heads;
-    auto page_ptr = [&](int p, const uint16_t* pool) -> const uint16_t* {
-        const int phys = ptab[p];
-        return pool + static_cast<int64_t>(phys) * page_stride + kvh * head_stride +
-               static_cast<int64_t>(ts) * kDecD + dc;
-    };
-    auto page_ok = [&](int p) -> bool {
-        const int phys = ptab[p];
-        return phys >= 0 && phys < num_pages;
-    };
+    // per-lane offsets inside a (page, kv_head) block
+    const int k_off = lr * kDecD + 8 * lg;  // + 32 s
+    const int v_off = lr * kPageTok + 4 * lg;  // + 16 dt * 16
 
-    uint4 kbuf[4], vbuf[4];
-    auto load_page = [&](int p) {
-        if (page_ok(p)) {
-            const uint16_t* kp = page_ptr(p, k_pool);
-            const uint16_t* vp = page_ptr(p, v_pool);
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                kbuf[u] = *reinterpret_cast<const uint4*>(kp + u * 4 * kDecD);
-                vbuf[u] = *reinterpret_cast<const uint4*>(vp + u * 4 * kDecD);
-            }
-        } else {
-#pragma unroll
-            for (int u = 0; u < 4; ++u) { kbuf[u] = make_uint4(0, 0, 0, 0); vbuf[u] = kbuf[u]; }
-        }
-    };
-    if (w_begin < w_end) load_page(w_begin);
+    uint4 kb[4];
+    uint2 vb[8];
+    bool okb = false;
+    // Load page p (guarded: an id outside the pool reads nothing).
+#define SFG_LOAD_PAGE(p)                                                                   \
+    {                                                                                      \
+        const int phys = ptab[(p)];                                                        \
+        okb = phys >= 0 && phys < num_pages;                                               \
+        const int64_t base = okb ? static_cast<int64_t>(phys) * page_stride + kvh * head_stride : 0; \
+        const uint16_t* kp = k_pool + base + k_off;                                        \
+        const uint16_t* vp = v_pool + base + v_off;                                        \
+        _Pragma("unroll") for (int s = 0; s < 4; ++s)                                      \
+            kb[s] = okb ? *reinterpret_cast<const uint4*>(kp + 32 * s) : make_uint4(0, 0, 0, 0); \
+        _Pragma("unroll") for (int dt = 0; dt < 8; ++dt)                                   \
+            vb[dt] = okb ? *reinterpret_cast<const uint2*>(vp + dt * 16 * kPageTok) : make_uint2(0, 0); \
+    }
+    if (w_begin < w_end) SFG_LOAD_PAGE(w_begin);
     for (int p = w_begin; p < w_end; ++p) {
-        uint4 kc[4], vc[4];
+        uint4 kc[4];
+        uint2 vc[8];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) { kc[u] = kbuf[u]; vc[u] = vbuf[u]; }
-        const bool ok = page_ok(p);
-        if (p + 1 < w_end) load_page(p + 1);
-        // scores s[u][g] for token 16 p + 4 u + ts
-        float s[4][G];
+        for (int s = 0; s < 4; ++s) kc[s] = kb[s];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            float kf[8];
-            const uint32_t* kw = reinterpret_cast<const uint32_t*>(&kc[u]);
+        for (int dt = 0; dt < 8; ++dt) vc[dt] = vb[dt];
+        const bool ok = okb;
+        if (p + 1 < w_end) SFG_LOAD_PAGE(p + 1);
+        floatx4 st = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                kf[2 * e] = __uint_as_float(kw[e] << 16);
-                kf[2 * e + 1] = __uint_as_float(kw[e] & 0xFFFF0000u);
-            }
+        for (int s = 0; s < 4; ++s)
+            st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kc[s]), qf[s], st, 0, 0, 0);
+        // st[r]: token 16 p + 4 lg + r, query lr
+        float sv[4];
+        float mx = -INFINITY;
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                float d = 0.f;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) d = fmaf(qv[g][e], kf[e], d);
-                s[u][g] = d;
-            }
+        for (int r = 0; r < 4; ++r) {
+            const int tok = p * kPageTok + 4 * lg + r;
+            sv[r] = (ok && tok < len) ? st[r] * scale_log2 : -INFINITY;
+            mx = fmaxf(mx, sv[r]);
         }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m_run, mx);
+        if (m_new != -INFINITY) {
+            const float alpha = (m_run == -INFINITY) ? 0.f : fast_exp2(m_run - m_new);
+            float pv[4];
 #pragma unroll
-        for (int off = 1; off < 16; off <<= 1)
+            for (int r = 0; r < 4; ++r) pv[r] = (sv[r] == -INFINITY) ? 0.f : fast_exp2(sv[r] - m_new);
+            l_run = l_run * alpha + (pv[0] + pv[1] + pv[2] + pv[3]);
+            uint2 pk;
+            pk.x = pack_bf16x2(pv[0], pv[1]);
+            pk.y = pack_bf16x2(pv[2], pv[3]);
+            const short4v pb = as_short4(pk);
 #pragma unroll
-            for (int u = 0; u < 4; ++u)
-#pragma unroll
-                for (int g = 0; g < G; ++g) s[u][g] += __shfl_xor(s[u][g], off, 64);
-        float mx[G];
-#pragma unroll
-        for (int g = 0; g < G; ++g) mx[g] = -INFINITY;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int tok = p * kPageTok + 4 * u + ts;
-            const bool valid = ok && tok < len;
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                if (!valid) s[u][g] = -INFINITY;
-                mx[g] = fmaxf(mx[g], s[u][g]);
+            for (int dt = 0; dt < 8; ++dt) {
+                acc[dt] *= alpha;
+                acc[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(as_short4(vc[dt]), pb, acc[dt], 0, 0, 0);
             }
-        }
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            mx[g] = fmaxf(mx[g], __shfl_xor(mx[g], 16, 64));
-            mx[g] = fmaxf(mx[g], __shfl_xor(mx[g], 32, 64));
-        }
-        float vf[4][8];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const uint32_t* vw = reinterpret_cast<const uint32_t*>(&vc[u]);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                vf[u][2 * e] = __uint_as_float(vw[e] << 16);
-                vf[u][2 * e + 1] = __uint_as_float(vw[e] & 0xFFFF0000u);
-            }
-        }
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const float m_new = fmaxf(m_run[g], mx[g]);
-            if (m_new == -INFINITY) continue;  // nothing valid yet (uniform across the wave)
-            const float alpha = (m_run[g] == -INFINITY) ? 0.f : fast_exp2(m_run[g] - m_new);
-            l_run[g] *= alpha;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[g][e] *= alpha;
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const float pu = (s[u][g] == -INFINITY) ? 0.f : fast_exp2(s[u][g] - m_new);
-                l_run[g] += pu;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(pu, vf[u][e], acc[g][e]);
-            }
-            m_run[g] = m_new;
+            m_run = m_new;
         }
     }
-    // Combine the 4 token slots of the wave (lanes l, l^16, l^32, l^48).
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        l_run[g] += __shfl_xor(l_run[g], 16, 64);
-        l_run[g] += __shfl_xor(l_run[g], 32, 64);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            acc[g][e] += __shfl_xor(acc[g][e], 16, 64);
-            acc[g][e] += __shfl_xor(acc[g][e], 32, 64);
-        }
-    }
-    // Merge the 4 waves in LDS.
+#undef SFG_LOAD_PAGE
+    l_run += __shfl_xor(l_run, 16, 64);
+    l_run += __shfl_xor(l_run, 32, 64);
+
+    // Merge the 4 waves in LDS.  acc[dt][r] = O^T[d = 16 dt + 4 lg + r][query lr].
     __shared__ float s_m[4][G], s_l[4][G];
     __shared__ float s_acc[4][G][kDecD];
-    if (lane < 16) {
+    if (lr < G) {
 #pragma unroll
-        for (int g = 0; g < G; ++g)
+        for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) s_acc[wave][g][dc + e] = acc[g][e];
-    }
-    if (lane == 0) {
-#pragma unroll
-        for (int g = 0; g < G; ++g) { s_m[wave][g] = m_run[g]; s_l[wave][g] = l_run[g]; }
+            for (int r = 0; r < 4; ++r) s_acc[wave][lr][16 * dt + 4 * lg + r] = acc[dt][r];
+        if (lg == 0) {
+            s_m[wave][lr] = m_run;
+            s_l[wave][lr] = l_run;
+        }
     }
     __syncthreads();
-    // thread -> (g, d): G * 128 outputs over 256 threads
     for (int o = threadIdx.x; o < G * kDecD; o += 256) {
         const int g = o / kDecD, d = o % kDecD;
         float mm = -INFINITY;
@@ -517,9 +503,9 @@ int decode_split_count(int64_t batch, int64_t kv_heads, int64_t max_context, int
                        int32_t requested) {
     const int64_t pages = (max_context + page_tokens - 1) / page_tokens;
     if (requested > 0) return static_cast<int>(requested < pages ? requested : (pages > 0 ? pages : 1));
-    // Aim for >= 1024 workgroups with >= 8 pages per workgroup (2 per wave).
+    // Aim for >= 1024 workgroups while keeping >= 32 pages (8 per wave) each.
     int s = 1;
-    while (batch * kv_heads * s < 1024 && pages / (s * 2) >= 8) s *= 2;
+    while (batch * kv_heads * s < 1024 && pages / (s * 2) >= 32) s *= 2;
     return s;
 }
 
@@ -530,7 +516,8 @@ size_t decode_workspace_bytes(int64_t batch, int64_t q_heads, int64_t head_dim, 
     return ml + acc;
 }
 
-int launch_attn_decode_paged(const float* q, const uint16_t* k_pool, const uint16_t* v_pool,
+int launch_attn_decode_paged(const float* q, int64_t q_row_stride, const float* rope, int rope_pos,
+                             const uint16_t* k_pool, const uint16_t* v_pool,
                              const int32_t* page_table, const int32_t* seq_lens, int64_t max_context,
                              void* out, int out_dtype, int64_t batch, int64_t q_heads,
                              int64_t kv_heads, int64_t head_dim, int64_t page_tokens,
@@ -548,13 +535,16 @@ int launch_attn_decode_paged(const float* q, const uint16_t* k_pool, const uint1
     const int len = static_cast<int>(max_context);
     const int pps = static_cast<int>(pages_per_seq);
     const int np = static_cast<int>(num_pages);
+#define SFG_DECODE(G) attn_decode_split_kernel<G><<<grid, 256, 0, stream>>>(q, q_row_stride, rope, rope_pos, k_pool, v_pool, page_table, seq_lens, len, static_cast<int>(kv_heads), pps, np, splits, scale_log2, part_ml, part_acc)
     switch (group) {
-        case 1: attn_decode_split_kernel<1><<<grid, 256, 0, stream>>>(q, k_pool, v_pool, page_table, seq_lens, len, kv_heads, pps, np, splits, scale_log2, part_ml, part_acc); break;
-        case 2: attn_decode_split_kernel<2><<<grid, 256, 0, stream>>>(q, k_pool, v_pool, page_table, seq_lens, len, kv_heads, pps, np, splits, scale_log2, part_ml, part_acc); break;
-        case 4: attn_decode_split_kernel<4><<<grid, 256, 0, stream>>>(q, k_pool, v_pool, page_table, seq_lens, len, kv_heads, pps, np, splits, scale_log2, part_ml, part_acc); break;
-        case 8: attn_decode_split_kernel<8><<<grid, 256, 0, stream>>>(q, k_pool, v_pool, page_table, seq_lens, len, kv_heads, pps, np, splits, scale_log2, part_ml, part_acc); break;
+        case 1: SFG_DECODE(1); break;
+        case 2: SFG_DECODE(2); break;
+        case 4: SFG_DECODE(4); break;
+        case 8: SFG_DECODE(8); break;
+        case 16: SFG_DECODE(16); break;
         default: return SFG_ERR_UNSUPPORTED;
     }
+#undef SFG_DECODE
     if (mid_event) (void)hipEventRecord(mid_event, stream);
     const dim3 cgrid(static_cast<unsigned>(batch * q_heads));
     if (out_dtype == SFG_F32)

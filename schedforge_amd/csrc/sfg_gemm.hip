@@ -6,12 +6,11 @@
 // weight-only int8 quantized_invoke (next_milestones.cpp:50-69).
 //
 // Three kernels, picked by shape:
-//  * gemm_skinny_kernel   M <= 128 rows per group (decode): weight-streaming,
-//    HBM bound.  v_mfma_f32_16x16x32_bf16 with the activation rows as the A
-//    operand; bf16 or int8 weights (int8 -> bf16 is exact), 64 B contiguous per
-//    lane per 128-k chunk, split-K over the 4 waves of a workgroup (LDS reduce)
-//    and, for dense problems, over workgroups with a deterministic last-arriver
-//    fixup (fixed summation order, counters self-reset).
+//  * gemm_skinny_kernel   M <= 64 rows (decode; grouped experts loop over
+//    64-row passes): weight-streaming, HBM bound.  v_mfma_f32_16x16x32_bf16
+//    with the activation rows as the A operand; bf16 or int8 weights (int8 ->
+//    bf16 is exact), 64 B contiguous per lane per 128-k chunk, split-K over up
+//    to 16 waves of one workgroup with a fixed-order LDS reduction.
 //  * gemm_mfma_kernel     large M (prefill, grouped experts): 128x128x32 tiles,
 //    v_mfma_f32_32x32x16_bf16, A/B staged through padded LDS with register
 //    prefetch of the next k-slab, optional A-row gather for dispatched tokens
@@ -42,6 +41,14 @@ __device__ __forceinline__ void store_out(void* c, int c_dtype, int64_t idx, flo
 
 // ===========================================================================
 // Skinny (decode) GEMM.
+//
+// A workgroup owns NBT 16-row tiles of B (16 or 32 output columns; for GLU
+// epilogues one gate tile and the matching up tile) and ALL of K: its WAVES
+// waves split K into contiguous chunk ranges and reduce through LDS in a fixed
+// order, so no workgroup ever waits for or publishes to another (no device-
+// scope fences, which on gfx950 write back and invalidate the L2).  Each lane
+// streams 64 B (bf16) / 32 B (int8) of one weight row per 128-k chunk with the
+// next chunk prefetched into registers.
 // ===========================================================================
 struct SkinnyArgs {
     const uint16_t* a; int64_t lda; const int32_t* a_rows; int64_t a_rows_limit;
@@ -51,21 +58,18 @@ struct SkinnyArgs {
     const float* residual; int64_t ldr;
     int64_t m, n, k;
     const int32_t* offsets;
-    int ks;             // workgroups along K (dense only)
-    float* partials;    // [col_tiles][ks][MT][2][64][4]
-    uint32_t* counters; // [col_tiles]
 };
 
 constexpr int kSkinnyChunk = 128;  // k per lane-chunk: 4 MFMA steps of 32
 
-template <int BDT, int MT, int EPI>
-__global__ __launch_bounds__(256) void gemm_skinny_kernel(SkinnyArgs p) {
+template <int BDT, int MT, int NBT, int EPI, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void gemm_skinny_kernel(SkinnyArgs p) {
     constexpr bool kGlu = EpiTraits<EPI>::glu;
+    static_assert(!kGlu || NBT == 2, "GLU epilogues pair one gate and one up tile");
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int g = blockIdx.z;
     const int tile = blockIdx.x;
-    const int ks = blockIdx.y;
     int64_t rb = 0, re = p.m;
     if (p.offsets) {
         // Device-side bounds are data: clamp them so a corrupt table cannot
@@ -75,45 +79,40 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(SkinnyArgs p) {
     }
     if (re <= rb) return;
 
-    // B rows of the two 16-wide column tiles handled by this workgroup.
-    int64_t brow[2];
+    int64_t brow[NBT];
     int64_t out_col;
     if (kGlu) {
         out_col = static_cast<int64_t>(tile) * 16;
         brow[0] = out_col;           // gate (or W1)
-        brow[1] = p.n + out_col;     // up   (or W3)
+        brow[NBT - 1] = p.n + out_col;  // up (or W3)
     } else {
-        out_col = static_cast<int64_t>(tile) * 32;
-        brow[0] = out_col;
-        brow[1] = out_col + 16;
+        out_col = static_cast<int64_t>(tile) * (16 * NBT);
+#pragma unroll
+        for (int j = 0; j < NBT; ++j) brow[j] = out_col + 16 * j;
     }
-    const int lr = lane & 15;   // row within a 16-tile (A) / column (B)
-    const int lg = lane >> 4;   // k-group: 32 contiguous k per chunk
+    const int lr = lane & 15;   // A row / B column within a 16-tile
+    const int lg = lane >> 4;   // 32 contiguous k per lane per chunk
     const char* bbase = static_cast<const char*>(p.b);
     const int64_t belem = (BDT == SFG_I8) ? 1 : 2;
     const int64_t bgroup = static_cast<int64_t>(g) * p.b_group_stride;
-    const char* bptr0 = bbase + (bgroup + (brow[0] + lr) * p.ldb + lg * 32) * belem;
-    const char* bptr1 = bbase + (bgroup + (brow[1] + lr) * p.ldb + lg * 32) * belem;
+    const char* bptr[NBT];
+#pragma unroll
+    for (int j = 0; j < NBT; ++j) bptr[j] = bbase + (bgroup + (brow[j] + lr) * p.ldb + lg * 32) * belem;
     const float* scales = p.scales ? p.scales + static_cast<int64_t>(g) * p.s_group_stride : nullptr;
 
-    // K chunks owned by this wave.
     const int chunks = static_cast<int>(p.k / kSkinnyChunk);
-    const int parts = p.ks * 4;
-    const int part = ks * 4 + wave;
-    const int c_begin = static_cast<int>(static_cast<int64_t>(chunks) * part / parts);
-    const int c_end = static_cast<int>(static_cast<int64_t>(chunks) * (part + 1) / parts);
+    const int c_begin = chunks * wave / WAVES;
+    const int c_end = chunks * (wave + 1) / WAVES;
 
-    __shared__ floatx4 red[3][MT][2][64];
-    __shared__ int s_last;
+    __shared__ floatx4 red[WAVES - 1][MT][NBT][64];
 
     for (int64_t pass = rb; pass < re; pass += MT * 16) {
-        floatx4 acc[MT][2];
+        floatx4 acc[MT][NBT];
 #pragma unroll
         for (int i = 0; i < MT; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+            for (int j = 0; j < NBT; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-        // Row pointers of this lane's A rows (one per row tile).
         const uint16_t* arow[MT];
         bool avalid[MT];
 #pragma unroll
@@ -125,33 +124,44 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(SkinnyArgs p) {
             arow[i] = p.a + src * p.lda + lg * 32;
         }
 
-        // Weight fragments: 64 B (bf16) / 32 B (int8) per lane per chunk and tile.
-        uint4 bq[2][4];
-        auto load_b = [&](int chunk, uint4 (&dst)[2][4]) {
+        uint4 bq[NBT][4];
+        auto load_b = [&](int chunk, uint4 (&dst)[NBT][4]) {
             const int64_t koff = static_cast<int64_t>(chunk) * kSkinnyChunk * belem;
-            if (BDT == SFG_I8) {
-                const uint4* p0 = reinterpret_cast<const uint4*>(bptr0 + koff);
-                const uint4* p1 = reinterpret_cast<const uint4*>(bptr1 + koff);
-                dst[0][0] = p0[0]; dst[0][1] = p0[1];
-                dst[1][0] = p1[0]; dst[1][1] = p1[1];
-            } else {
-                const uint4* p0 = reinterpret_cast<const uint4*>(bptr0 + koff);
-                const uint4* p1 = reinterpret_cast<const uint4*>(bptr1 + koff);
 #pragma unroll
-                for (int s = 0; s < 4; ++s) { dst[0][s] = p0[s]; dst[1][s] = p1[s]; }
+            for (int j = 0; j < NBT; ++j) {
+                const uint4* pj = reinterpret_cast<const uint4*>(bptr[j] + koff);
+                if (BDT == SFG_I8) {
+                    dst[j][0] = pj[0]; dst[j][1] = pj[1];
+                } else {
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) dst[j][s] = pj[s];
+                }
             }
         };
         if (c_begin < c_end) load_b(c_begin, bq);
         for (int chunk = c_begin; chunk < c_end; ++chunk) {
-            uint4 cur[2][4];
+            uint4 cur[NBT][4];
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < NBT; ++j)
 #pragma unroll
                 for (int s = 0; s < 4; ++s) cur[j][s] = bq[j][s];
             if (chunk + 1 < c_end) load_b(chunk + 1, bq);
-            bf16x8 bf[2][4];
+            uint4 af[MT][4];
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
+            for (int i = 0; i < MT; ++i) {
+                if (avalid[i]) {
+                    const uint4* ap = reinterpret_cast<const uint4*>(
+                        arow[i] + static_cast<int64_t>(chunk) * kSkinnyChunk);
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) af[i][s] = ap[s];
+                } else {
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) af[i][s] = make_uint4(0, 0, 0, 0);
+                }
+            }
+            bf16x8 bf[NBT][4];
+#pragma unroll
+            for (int j = 0; j < NBT; ++j) {
                 if (BDT == SFG_I8) {
                     bf[j][0] = as_bf16x8(i8x8_to_bf16x8(cur[j][0].x, cur[j][0].y));
                     bf[j][1] = as_bf16x8(i8x8_to_bf16x8(cur[j][0].z, cur[j][0].w));
@@ -163,79 +173,30 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(SkinnyArgs p) {
                 }
             }
 #pragma unroll
-            for (int i = 0; i < MT; ++i) {
-                uint4 af[4];
-                if (avalid[i]) {
-                    const uint4* ap = reinterpret_cast<const uint4*>(
-                        arow[i] + static_cast<int64_t>(chunk) * kSkinnyChunk);
-#pragma unroll
-                    for (int s = 0; s < 4; ++s) af[s] = ap[s];
-                } else {
-#pragma unroll
-                    for (int s = 0; s < 4; ++s) af[s] = make_uint4(0, 0, 0, 0);
-                }
+            for (int i = 0; i < MT; ++i)
 #pragma unroll
                 for (int s = 0; s < 4; ++s) {
-                    const bf16x8 a = as_bf16x8(af[s]);
-                    acc[i][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bf[0][s], acc[i][0], 0, 0, 0);
-                    acc[i][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bf[1][s], acc[i][1], 0, 0, 0);
+                    const bf16x8 a = as_bf16x8(af[i][s]);
+#pragma unroll
+                    for (int j = 0; j < NBT; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bf[j][s], acc[i][j], 0, 0, 0);
                 }
-            }
         }
 
-        // Reduce the 4 waves' partial sums in a fixed order (wave 0 + 1 + 2 + 3).
+        // Reduce the waves' partial sums in a fixed order (0 + 1 + ... ).
         if (wave > 0) {
 #pragma unroll
             for (int i = 0; i < MT; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j) red[wave - 1][i][j][lane] = acc[i][j];
+                for (int j = 0; j < NBT; ++j) red[wave - 1][i][j][lane] = acc[i][j];
         }
         __syncthreads();
         if (wave == 0) {
-#pragma unroll
-            for (int w = 0; w < 3; ++w)
-#pragma unroll
-                for (int i = 0; i < MT; ++i)
-#pragma unroll
-                    for (int j = 0; j < 2; ++j) acc[i][j] += red[w][i][j][lane];
-        }
-
-        if (p.ks > 1) {
-            // Cross-workgroup split-K: publish, count, last arriver sums in ks order.
-            floatx4* part_base = reinterpret_cast<floatx4*>(p.partials) +
-                                 (static_cast<int64_t>(tile) * p.ks) * MT * 2 * 64;
-            if (wave == 0) {
+            for (int w = 0; w < WAVES - 1; ++w)
 #pragma unroll
                 for (int i = 0; i < MT; ++i)
 #pragma unroll
-                    for (int j = 0; j < 2; ++j)
-                        part_base[((static_cast<int64_t>(ks) * MT + i) * 2 + j) * 64 + lane] = acc[i][j];
-            }
-            __threadfence();
-            __syncthreads();
-            if (threadIdx.x == 0) {
-                const uint32_t prev = atomicAdd(&p.counters[tile], 1u);
-                s_last = (prev == static_cast<uint32_t>(p.ks - 1)) ? 1 : 0;
-            }
-            __syncthreads();
-            if (!s_last) return;
-            __threadfence();
-            if (wave == 0) {
-#pragma unroll
-                for (int i = 0; i < MT; ++i)
-#pragma unroll
-                    for (int j = 0; j < 2; ++j) {
-                        floatx4 sum = floatx4{0.f, 0.f, 0.f, 0.f};
-                        for (int s = 0; s < p.ks; ++s)
-                            sum += __builtin_nontemporal_load(
-                                &part_base[((static_cast<int64_t>(s) * MT + i) * 2 + j) * 64 + lane]);
-                        acc[i][j] = sum;
-                    }
-            }
-            if (threadIdx.x == 0) p.counters[tile] = 0u;
-        }
-
-        if (wave == 0) {
+                    for (int j = 0; j < NBT; ++j) acc[i][j] += red[w][i][j][lane];
             // D layout: lane holds column (lane & 15), rows 4*(lane >> 4) + r.
 #pragma unroll
             for (int i = 0; i < MT; ++i) {
@@ -245,7 +206,7 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(SkinnyArgs p) {
                     if (row >= re) continue;
                     if (kGlu) {
                         const int64_t col = out_col + lr;
-                        float gv = acc[i][0][r], uv = acc[i][1][r];
+                        float gv = acc[i][0][r], uv = acc[i][NBT - 1][r];
                         if (scales) {
                             gv *= scales[col];
                             uv *= scales[p.n + col];
@@ -253,7 +214,7 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(SkinnyArgs p) {
                         store_out(p.c, p.c_dtype, row * p.ldc + col, glu_combine(EPI, gv, uv));
                     } else {
 #pragma unroll
-                        for (int j = 0; j < 2; ++j) {
+                        for (int j = 0; j < NBT; ++j) {
                             const int64_t col = out_col + j * 16 + lr;
                             float v = acc[i][j][r];
                             if (scales) v *= scales[col];
@@ -533,32 +494,47 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(F32Args p) {
 // ===========================================================================
 namespace {
 
-constexpr int kTargetWorkgroups = 768;  // ~3 per CU on 256 CUs
-constexpr size_t kCounterBytes = 65536;   // split-K tile counters (16384 column tiles)
-constexpr int kMaxSplit = 16;
+constexpr int kMaxWaves = 16;
 
-int skinny_split(int64_t col_tiles, int64_t k) {
+// Waves per workgroup: enough that each wave owns >= 2 chunks of 128 k when
+// K allows, capped so the LDS reduction buffer stays under 64 KB.
+int skinny_waves(int64_t k, int mt, int nbt) {
     const int64_t chunks = k / kSkinnyChunk;
-    int ks = 1;
-    while (ks < kMaxSplit && col_tiles * ks < kTargetWorkgroups && chunks >= (ks * 2) * 4) ks *= 2;
-    return ks;
+    int w = 4;
+    while (w < kMaxWaves && chunks >= 2 * (w * 2)) w *= 2;
+    while (w > 4 && (w - 1) * mt * nbt * 1024 > 64 * 1024) w /= 2;
+    return w;
+}
+
+template <int BDT, int MT, int NBT, int EPI>
+void launch_skinny_w(const SkinnyArgs& a, dim3 grid, int waves, hipStream_t s) {
+    if (waves == 4) gemm_skinny_kernel<BDT, MT, NBT, EPI, 4><<<grid, 256, 0, s>>>(a);
+    else if (waves == 8) gemm_skinny_kernel<BDT, MT, NBT, EPI, 8><<<grid, 512, 0, s>>>(a);
+    else gemm_skinny_kernel<BDT, MT, NBT, EPI, 16><<<grid, 1024, 0, s>>>(a);
 }
 
 template <int BDT, int MT>
-void launch_skinny_mt(const SkinnyArgs& a, dim3 grid, int epi, hipStream_t s) {
+void launch_skinny_e(const SkinnyArgs& a, dim3 grid, int nbt, int waves, int epi, hipStream_t s) {
     switch (epi) {
-        case SFG_EPI_NONE: gemm_skinny_kernel<BDT, MT, SFG_EPI_NONE><<<grid, 256, 0, s>>>(a); break;
-        case SFG_EPI_RESIDUAL: gemm_skinny_kernel<BDT, MT, SFG_EPI_RESIDUAL><<<grid, 256, 0, s>>>(a); break;
-        case SFG_EPI_SWIGLU: gemm_skinny_kernel<BDT, MT, SFG_EPI_SWIGLU><<<grid, 256, 0, s>>>(a); break;
-        default: gemm_skinny_kernel<BDT, MT, SFG_EPI_GLU_SILU_UP><<<grid, 256, 0, s>>>(a); break;
+        case SFG_EPI_NONE:
+            if (nbt == 1) launch_skinny_w<BDT, MT, 1, SFG_EPI_NONE>(a, grid, waves, s);
+            else launch_skinny_w<BDT, MT, 2, SFG_EPI_NONE>(a, grid, waves, s);
+            break;
+        case SFG_EPI_RESIDUAL:
+            if (nbt == 1) launch_skinny_w<BDT, MT, 1, SFG_EPI_RESIDUAL>(a, grid, waves, s);
+            else launch_skinny_w<BDT, MT, 2, SFG_EPI_RESIDUAL>(a, grid, waves, s);
+            break;
+        case SFG_EPI_SWIGLU: launch_skinny_w<BDT, MT, 2, SFG_EPI_SWIGLU>(a, grid, waves, s); break;
+        default: launch_skinny_w<BDT, MT, 2, SFG_EPI_GLU_SILU_UP>(a, grid, waves, s); break;
     }
 }
 
 template <int BDT>
-void launch_skinny_b(const SkinnyArgs& a, dim3 grid, int mt, int epi, hipStream_t s) {
-    if (mt == 1) launch_skinny_mt<BDT, 1>(a, grid, epi, s);
-    else if (mt == 2) launch_skinny_mt<BDT, 2>(a, grid, epi, s);
-    else launch_skinny_mt<BDT, 4>(a, grid, epi, s);
+void launch_skinny_b(const SkinnyArgs& a, dim3 grid, int mt, int nbt, int waves, int epi,
+                     hipStream_t s) {
+    if (mt == 1) launch_skinny_e<BDT, 1>(a, grid, nbt, waves, epi, s);
+    else if (mt == 2) launch_skinny_e<BDT, 2>(a, grid, nbt, waves, epi, s);
+    else launch_skinny_e<BDT, 4>(a, grid, nbt, waves, epi, s);
 }
 
 template <int BDT>
@@ -582,18 +558,8 @@ constexpr int64_t kSkinnyGroupedMaxTotal = 512;
 }  // namespace
 
 size_t gemm_workspace_bytes(int64_t m, int64_t n, int64_t k) {
-    (void)m;
-    // Fixed tile-counter region first (shared by every GEMM that uses this
-    // workspace, so no GEMM's partials can land on another's counters), then
-    // split-K partials: upper bound over both column-tile widths.
-    size_t best = 0;
-    for (int64_t width : {int64_t(16), int64_t(32)}) {
-        const int64_t col_tiles = (n + width - 1) / width;
-        const int ks = skinny_split(col_tiles, k);
-        const size_t partial = static_cast<size_t>(col_tiles) * ks * 4 * 2 * 64 * sizeof(floatx4);
-        if (partial > best) best = partial;
-    }
-    return kCounterBytes + ((best + 255) / 256) * 256;
+    (void)m; (void)n; (void)k;
+    return 0;  // every GEMM reduces inside its workgroup
 }
 
 int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes, hipStream_t stream) {
@@ -619,37 +585,23 @@ int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes, h
     const int groups = p.offsets ? p.groups : 1;
     const bool skinny = p.offsets ? (p.m <= kSkinnyGroupedMaxTotal) : (p.m <= kSkinnyMaxRows);
     if (skinny) {
-        if (p.n % (glu ? 16 : 32) != 0) return SFG_ERR_UNSUPPORTED;
-        const int64_t col_tiles = glu ? p.n / 16 : p.n / 32;
+        const int64_t rows_hint = p.offsets ? kSkinnyMaxRows : p.m;
+        const int mt = rows_hint <= 16 ? 1 : (rows_hint <= 32 ? 2 : 4);
+        const int nbt = glu ? 2 : (rows_hint <= 16 ? 1 : 2);
+        const int64_t tile_cols = glu ? 16 : 16 * nbt;
+        if (p.n % tile_cols != 0) return SFG_ERR_UNSUPPORTED;
+        const int waves = skinny_waves(p.k, mt, nbt);
         SkinnyArgs a{};
         a.a = static_cast<const uint16_t*>(p.a); a.lda = p.lda; a.a_rows = p.a_rows;
-    a.a_rows_limit = p.a_rows ? p.a_rows_limit : p.m;
+        a.a_rows_limit = p.a_rows ? p.a_rows_limit : p.m;
         a.b = p.b; a.ldb = p.ldb; a.scales = p.b_scales;
         a.b_group_stride = p.b_group_stride; a.s_group_stride = p.s_group_stride;
         a.c = p.c; a.c_dtype = p.c_dtype; a.ldc = p.ldc;
         a.residual = p.residual; a.ldr = p.ldr;
         a.m = p.m; a.n = p.n; a.k = p.k; a.offsets = p.offsets;
-        int mt;
-        if (p.offsets) {
-            a.ks = 1;
-            mt = 4;  // rows per pass 64; groups with more rows loop over passes
-        } else {
-            a.ks = skinny_split(col_tiles, p.k);
-            mt = p.m <= 16 ? 1 : (p.m <= 32 ? 2 : 4);
-        }
-        if (a.ks > 1) {
-            const size_t partial_bytes = static_cast<size_t>(col_tiles) * a.ks * mt * 2 * 64 * sizeof(floatx4);
-            const size_t need = kCounterBytes + partial_bytes;
-            if (workspace == nullptr || workspace_bytes < need ||
-                static_cast<size_t>(col_tiles) * sizeof(uint32_t) > kCounterBytes)
-                return SFG_ERR_WORKSPACE;
-            a.counters = static_cast<uint32_t*>(workspace);
-            a.partials = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
-        }
-        const dim3 grid(static_cast<unsigned>(col_tiles), static_cast<unsigned>(a.ks),
-                        static_cast<unsigned>(groups));
-        if (p.b_dtype == SFG_I8) launch_skinny_b<SFG_I8>(a, grid, mt, p.epilogue, stream);
-        else launch_skinny_b<SFG_BF16>(a, grid, mt, p.epilogue, stream);
+        const dim3 grid(static_cast<unsigned>(p.n / tile_cols), 1u, static_cast<unsigned>(groups));
+        if (p.b_dtype == SFG_I8) launch_skinny_b<SFG_I8>(a, grid, mt, nbt, waves, p.epilogue, stream);
+        else launch_skinny_b<SFG_BF16>(a, grid, mt, nbt, waves, p.epilogue, stream);
         return SFG_OK;
     }
     if (p.n % (glu ? 64 : 128) != 0 || p.k % kTK != 0) return SFG_ERR_UNSUPPORTED;

@@ -61,7 +61,8 @@ int launch_attn_prefill_bf16(const uint16_t* q, const uint16_t* k, const uint16_
 int decode_split_count(int64_t batch, int64_t kv_heads, int64_t max_context,
                        int64_t page_tokens, int32_t requested);
 size_t decode_workspace_bytes(int64_t batch, int64_t q_heads, int64_t head_dim, int splits);
-int launch_attn_decode_paged(const float* q, const uint16_t* k_pool, const uint16_t* v_pool,
+int launch_attn_decode_paged(const float* q, int64_t q_row_stride, const float* rope, int rope_pos,
+                             const uint16_t* k_pool, const uint16_t* v_pool,
                              const int32_t* page_table, const int32_t* seq_lens, int64_t max_context,
                              void* out, int out_dtype, int64_t batch, int64_t q_heads,
                              int64_t kv_heads, int64_t head_dim, int64_t page_tokens,

@@ -15,20 +15,54 @@
 namespace sfg {
 
 // One thread per (token, expert) chain; the block then runs softmax + top-k for
-// its tokens with one thread per token.  E <= 256, top_k <= 8.
+// its tokens with one thread per token.  E <= 256, top_k <= 8.  The chain runs
+// over features in order (bit-identical to a sequential fp32 FMA loop); its
+// operands for the next 32 features are fetched into registers while the
+// current 32 FMAs issue, so the chain never waits on a load.
+constexpr int kRouteStep = 32;
+constexpr int kRouteTokens = 32;     // tokens per workgroup
+
 __global__ __launch_bounds__(256) void moe_router_kernel(
     const float* __restrict__ x, const float* __restrict__ router, const float* __restrict__ bias,
     int tokens, int hidden, int experts, int top_k, int32_t* __restrict__ ids,
     float* __restrict__ weights) {
     __shared__ float logits[256];
-    const int per_block = 256 / experts;
+    const int per_block = min(kRouteTokens, 256 / experts);
     const int t_local = threadIdx.x / experts;
     const int e = threadIdx.x % experts;
     const int t = blockIdx.x * per_block + t_local;
-    if (t_local < per_block && t < tokens) {
+    const bool active = t_local < per_block && t < tokens;
+    if (active) {
         const float* xr = x + static_cast<int64_t>(t) * hidden;
+        const float* wc = router + e;
         float acc = 0.f;
-        for (int f = 0; f < hidden; ++f) acc = __builtin_fmaf(xr[f], router[static_cast<int64_t>(f) * experts + e], acc);
+        const int full = hidden / kRouteStep * kRouteStep;
+        float xa[kRouteStep], wa[kRouteStep], xb[kRouteStep], wb[kRouteStep];
+        auto fetch = [&](int f0, float (&xs)[kRouteStep], float (&ws)[kRouteStep]) {
+#pragma unroll
+            for (int j = 0; j < kRouteStep; j += 4) {
+                const float4 v = *reinterpret_cast<const float4*>(xr + f0 + j);
+                xs[j] = v.x; xs[j + 1] = v.y; xs[j + 2] = v.z; xs[j + 3] = v.w;
+            }
+#pragma unroll
+            for (int j = 0; j < kRouteStep; ++j) ws[j] = wc[static_cast<int64_t>(f0 + j) * experts];
+        };
+        const bool vec = (hidden & 3) == 0;
+        int f0 = 0;
+        if (vec && full > 0) {
+            fetch(0, xa, wa);
+            for (; f0 < full; f0 += 2 * kRouteStep) {
+                if (f0 + kRouteStep < full) fetch(f0 + kRouteStep, xb, wb);
+#pragma unroll
+                for (int j = 0; j < kRouteStep; ++j) acc = __builtin_fmaf(xa[j], wa[j], acc);
+                if (f0 + kRouteStep >= full) { f0 += kRouteStep; break; }
+                if (f0 + 2 * kRouteStep < full) fetch(f0 + 2 * kRouteStep, xa, wa);
+#pragma unroll
+                for (int j = 0; j < kRouteStep; ++j) acc = __builtin_fmaf(xb[j], wb[j], acc);
+            }
+            if (f0 > full) f0 = full;
+        }
+        for (; f0 < hidden; ++f0) acc = __builtin_fmaf(xr[f0], wc[static_cast<int64_t>(f0) * experts], acc);
         if (bias) acc = acc + bias[e];
         logits[t_local * experts + e] = acc;
     }
@@ -66,7 +100,7 @@ int launch_moe_router(const float* x, const float* router, const float* bias, in
                       float* weights, hipStream_t stream) {
     if (experts <= 0 || experts > 256 || top_k <= 0 || top_k > 8 || top_k > experts)
         return SFG_ERR_UNSUPPORTED;
-    const int per_block = static_cast<int>(256 / experts);
+    const int per_block = static_cast<int>(256 / experts < kRouteTokens ? 256 / experts : kRouteTokens);
     const dim3 grid(static_cast<unsigned>((tokens + per_block - 1) / per_block));
     moe_router_kernel<<<grid, 256, 0, stream>>>(x, router, bias, static_cast<int>(tokens),
                                                 static_cast<int>(hidden), static_cast<int>(experts),

@@ -9,8 +9,8 @@ device layouts (constant specialisation, decoder_compiler.cpp:535-552):
   w_qkv [H + 2 kvD][H], w_o [H][H], w_gate_up [2I][H], w_down [H][I],
   w13 [E][2I][H] (W1^T rows then W3^T rows), w2 [E][H][I];
   bf16 (round to nearest even) or int8 + per-channel scales.
-Decode steps read K/V from a paged bf16 pool [page][Hkv][16][D] addressed by a
-per-sequence page table.
+Decode steps read K/V from paged bf16 pools -- K [page][Hkv][16][D], V
+[page][Hkv][D][16] -- addressed by a per-sequence page table.
 """
 from __future__ import annotations
 
@@ -221,7 +221,10 @@ def compile_decoder(config: DecoderConfig, data: DecoderData, device="cuda",
             padded[:, :, :cfg.context_sequence] = flat
             del flat
             blocks = padded.reshape(cfg.batch, cfg.kv_heads, pages_per_seq, pt, D) \
-                           .permute(0, 2, 1, 3, 4).reshape(num_pages, cfg.kv_heads, pt, D)
+                           .permute(0, 2, 1, 3, 4)
+            if name == "v_pool":  # V is token-minor inside a page: [page][Hkv][D][16]
+                blocks = blocks.transpose(-1, -2)
+            blocks = blocks.reshape(num_pages, cfg.kv_heads, *blocks.shape[-2:])
             del padded
             pool32 = torch.empty_like(blocks)
             idx = t["page_table"].reshape(-1).long()
@@ -279,10 +282,18 @@ def compile_decoder(config: DecoderConfig, data: DecoderData, device="cuda",
 class StageEvents:
     """SFG_NUM_MARKS HIP events created through the ABI, for per-stage timing."""
 
-    def __init__(self, lib):
+    def __init__(self, lib, marks=None):
+        """marks: iterable of mark ids to record (None: all).  Unrecorded marks
+        stay NULL and the layer skips them."""
         self.lib = lib
         self.arr = (ctypes.c_void_p * _abi.NUM_MARKS)()
         check(lib.sfg_hip_events_create_v1(_abi.NUM_MARKS, self.arr))
+        if marks is not None:
+            keep = set(marks)
+            for i in range(_abi.NUM_MARKS):
+                if i not in keep:
+                    lib.sfg_hip_events_destroy_v1(1, ctypes.byref(ctypes.c_void_p(self.arr[i])))
+                    self.arr[i] = None
 
     def elapsed(self, a: int, b: int) -> float:
         ms = ctypes.c_float()

@@ -285,12 +285,13 @@ def _decode_case(lib, B, Hq, Hkv, ctx, seq_lens=None, splits=0, seed=91):
     q = oracle.normal(seed, 0, (B, Hq, 1, D))
     kp = oracle.paged_scatter(kc, table, num_pages, PT)
     vp = oracle.paged_scatter(vc, table, num_pages, PT)
+    vp_t = np.ascontiguousarray(vp.transpose(0, 1, 3, 2))  # V pool is token-minor per page
     out = torch.empty((B, Hq * D), dtype=torch.float32, device="cuda")
     wsb = lib.sfg_hip_attn_decode_workspace_v1(B, Hq, D, ctx, PT, splits)
     ws = torch.zeros(wsb, dtype=torch.uint8, device="cuda")
     sl = dev(np.asarray(seq_lens, np.int32)) if seq_lens is not None else None
     _abi.check(lib.sfg_hip_attn_decode_paged_v1(
-        dev(q).data_ptr(), bf16_dev(kp).data_ptr(), bf16_dev(vp).data_ptr(), dev(table).data_ptr(),
+        dev(q).data_ptr(), bf16_dev(kp).data_ptr(), bf16_dev(vp_t).data_ptr(), dev(table).data_ptr(),
         sl.data_ptr() if sl is not None else None, out.data_ptr(), F32, B, Hq, Hkv, D, PT, pps,
         num_pages, ctx, splits, ctypes.c_float(0.0), 1, ws.data_ptr(), ws.numel(), stream()))
     _sync()
@@ -315,8 +316,10 @@ def test_decode_ragged_lengths_and_split_invariance(lib):
     lens = [1000, 1, 513, 640]
     a = _decode_case(lib, 4, 8, 2, 1000, seq_lens=lens, splits=1)
     b = _decode_case(lib, 4, 8, 2, 1000, seq_lens=lens, splits=8)
-    # merge_online is exact up to rounding: any split count gives the same result
-    assert np.max(np.abs(a - b)) < 1e-5
+    # merge_online is exact up to rounding: any split count gives the same
+    # result; P enters the value MFMA as bf16 after a split-dependent max
+    # shift, so the two agree to bf16 rounding.
+    assert oracle.rel_error(a, b) < 1e-2
 
 
 def test_decode_rejects_bad_page_ids(lib):
