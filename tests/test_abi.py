@@ -1,0 +1,123 @@
+"""C-ABI checks that need no GPU: the library loads, exports every entry point
+include/sfg_hip.h declares, and rejects invalid arguments on the host with the
+reference's error classes (codes < 16 -> ValueError, the reference's
+std::invalid_argument; validate() at decoder_compiler.cpp:26-39)."""
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from schedforge_amd import _abi
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "sfg_hip.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(sfg_hip_\w+)\s*\(", text, re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _abi.load()
+
+
+def test_every_declared_symbol_is_exported_and_bound(lib):
+    names = declared_functions()
+    assert len(names) >= 25
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_abi.LIB_PATH)], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (sfg_hip_\w+)", out))
+    missing = [n for n in names if n not in exported]
+    assert not missing, missing
+    # and the Python binding covers exactly the declared surface
+    assert sorted(_abi.EXPORTED) == names
+
+
+def test_identity(lib):
+    assert lib.sfg_hip_abi_version() == _abi.ABI_VERSION
+    meta = lib.sfg_hip_metadata_v1().decode()
+    assert "abi=1" in meta and "arch=gfx950" in meta
+
+
+def _desc(**kw):
+    d = _abi.LayerDesc()
+    d.abi = _abi.ABI_VERSION
+    base = dict(batch=2, sequence=1, hidden=256, intermediate=512, query_heads=2, kv_heads=1,
+                head_dim=128, rms_epsilon=1e-5, rope_theta=1e4, causal=1, ffn=0, experts=4, top_k=2,
+                context=64, page_tokens=16, pages_per_seq=4, num_pages=8, act_dtype=_abi.BF16,
+                weight_dtype=_abi.BF16, kv_splits=0, use_routing_trace=0)
+    base.update(kw)
+    for k, v in base.items():
+        setattr(d, k, v)
+    return d
+
+
+def _call_layer(lib, d):
+    io = _abi.LayerIO()
+    w = _abi.LayerWeights()
+    return lib.sfg_hip_decoder_layer_v1(ctypes.byref(d), ctypes.byref(w), ctypes.byref(io), None, 0, None)
+
+
+def test_workspace_query_and_validation(lib):
+    assert lib.sfg_hip_decoder_layer_workspace_v1(ctypes.byref(_desc())) > 0
+    for bad in (dict(hidden=250), dict(kv_heads=3, query_heads=2), dict(rms_epsilon=0.0),
+                dict(ffn=1, top_k=5), dict(context=-1)):
+        d = _desc(**bad)
+        assert lib.sfg_hip_decoder_layer_workspace_v1(ctypes.byref(d)) == 0
+        assert _call_layer(lib, d) == _abi.ERR_INVALID_CONFIG, bad
+
+
+def test_abi_mismatch_and_guards(lib):
+    d = _desc()
+    d.abi = 99
+    assert _call_layer(lib, d) == _abi.ERR_ABI
+    # context beyond the plan's page capacity: compiled guard
+    assert _call_layer(lib, _desc(context=65)) == _abi.ERR_GUARD
+    # fp32 activations with int8 weights are not lowered
+    assert _call_layer(lib, _desc(act_dtype=_abi.F32, weight_dtype=_abi.I8, context=0)) == _abi.ERR_UNSUPPORTED
+    # missing weights / io
+    assert _call_layer(lib, _desc()) == _abi.ERR_SHAPE
+    with pytest.raises(ValueError, match="null weights or io"):
+        _abi.check(_call_layer(lib, _desc()))
+
+
+def test_op_entry_points_validate_on_host(lib):
+    args = _abi.GemmArgs()
+    assert lib.sfg_hip_gemm_v1(ctypes.byref(args), None, 0, None) == _abi.ERR_SHAPE
+    assert lib.sfg_hip_rmsnorm_v1(None, None, None, _abi.F32, 0, 0, ctypes.c_float(1e-5), None) == _abi.ERR_SHAPE
+    # causal attention with Sq > Skv (attention_compiler.cpp:23-29)
+    rc = lib.sfg_hip_attn_prefill_v1(1, 1, 1, 1, _abi.BF16, _abi.BF16, 1, 2, 1, 8, 4, 128, 1,
+                                     ctypes.c_float(0.0), None)
+    assert rc == _abi.ERR_INVALID_CONFIG
+    # paged decode: context beyond the page table (guard) and bad GQA ratio (config)
+    rc = lib.sfg_hip_attn_decode_paged_v1(1, 1, 1, 1, None, 1, _abi.F32, 1, 4, 1, 128, 16, 2, 2, 33,
+                                          0, ctypes.c_float(0.0), 0, None, 0, None)
+    assert rc == _abi.ERR_GUARD
+    rc = lib.sfg_hip_attn_decode_paged_v1(1, 1, 1, 1, None, 1, _abi.F32, 1, 4, 3, 128, 16, 2, 2, 32,
+                                          0, ctypes.c_float(0.0), 0, None, 0, None)
+    assert rc == _abi.ERR_INVALID_CONFIG
+    # MoE: top_k > experts (moe_compiler.cpp:41-45)
+    rc = lib.sfg_hip_moe_route_v1(1, 1, None, 4, 8, 2, 3, 1, 1, 1, 1, 1, 1, 1, 1, None, 0, None)
+    assert rc == _abi.ERR_INVALID_CONFIG
+    msg = lib.sfg_hip_last_error().decode()
+    assert "MoE" in msg
+
+
+def test_rope_table_matches_reference_expressions(lib):
+    seq, d, theta = 5, 16, 10000.0
+    t = np.empty((seq, d // 2, 2), np.float32)
+    assert lib.sfg_hip_rope_table_host_v1(t.ctypes.data, seq, d, ctypes.c_float(theta)) == 0
+    i = np.arange(0, d, 2, dtype=np.float32)
+    f = np.power(np.float32(theta), -i / np.float32(d)).astype(np.float32)
+    ang = (np.arange(seq, dtype=np.float32)[:, None] * f[None, :]).astype(np.float32)
+    np.testing.assert_allclose(t[..., 0], np.cos(ang.astype(np.float64)), atol=2e-7)
+    np.testing.assert_allclose(t[..., 1], np.sin(ang.astype(np.float64)), atol=2e-7)
+    np.testing.assert_array_equal(t[0, :, 0], 1.0)
+    np.testing.assert_array_equal(t[0, :, 1], 0.0)

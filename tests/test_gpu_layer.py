@@ -77,3 +77,13 @@ def test_layer_reduced_moe_device_routing(name):
     bad = np.nonzero(rows_err >= TOL[cfg.dtype])[0]
     print(f"{name}-small (device routing): max rel {rows_err.max():.3e}, rows over tol {len(bad)}")
     assert len(bad) <= max(1, cfg.rows // 200), bad
+
+
+def test_layer_reduced_w8_dense():
+    """Weight-only int8 dense decode layer (execute_quantized_decoder_layer,
+    next_milestones.cpp:339-385, 676-697) against the oracle's int8 path."""
+    cfg = SMALL["c2"].replace(dtype="w8")
+    res, ref, _ = _run(cfg, CONFIG_SEEDS["c2"] + 5)
+    err = oracle.rel_error(res.output, ref)
+    print(f"c2-small w8 dense: rel_err {err:.3e}")
+    assert err < TOL["w8"], err

@@ -1,0 +1,306 @@
+"""Pins of the CPU oracle (oracle/sfg_oracle.c) -- CPU only.
+
+Each oracle function is checked against something that does not share its code:
+golden vectors written by tests/golden/make_golden.py in float64 NumPy from the
+reference's definitions, closed forms, brute force, the reference's own
+known-answer tests, and an independent float64 formulation of the whole layer.
+
+  function                 pinned by
+  sfgo_rms_norm            golden; closed form x=c -> c w / sqrt(c^2+eps)
+  sfgo_matmul              integer operands (exact) vs NumPy int64
+  sfgo_rope / split_qkv    golden; position-0 identity; pair norms; known angle
+  sfgo_attention           golden (causal + full); equal keys -> prefix mean;
+                           one-hot V -> probability row
+  sfgo_route_topk          golden ids/weights; ties -> lower index; invariants
+                           (test_schedforge.cpp:630-640)
+  sfgo_dispatch            golden offsets/tokens/slots (stable argsort)
+  sfgo_moe_reference       golden (silu on W3, renormalised weights)
+  sfgo_quantize_nk         golden incl. zero column; constant-weight matmul
+                           (test_schedforge.cpp:411-417); half-away rounding
+  sfgo_quantized_matmul    integer-exact closed form
+  sfgo_to/from_bf16        golden bits incl. ties; test_schedforge.cpp:252-254
+  sfgo_paged_gather        iota round trip (test_schedforge.cpp:369-379)
+  sfgo_decoder_layer       float64 NumPy layer (dense prefill, dense decode, MoE,
+                           int8 dense)
+  generators               determinism, moments, permutation property
+"""
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle
+from schedforge_amd import CONFIGS
+
+GOLDEN = np.load(Path(__file__).resolve().parent / "golden" / "golden_v1.npz")
+
+
+def rel(a, b):
+    return oracle.rel_error(a, b)
+
+
+# ------------------------------------------------------------------ golden vectors
+def test_golden_rmsnorm():
+    y = oracle.rms_norm(GOLDEN["rms_x"], GOLDEN["rms_w"], 1e-5)
+    assert rel(y, GOLDEN["rms_y"]) < 1e-6
+
+
+@pytest.mark.parametrize("causal,key", [(True, "att_causal"), (False, "att_full")])
+def test_golden_attention(causal, key):
+    out = oracle.attention(GOLDEN["att_q"], GOLDEN["att_k"], GOLDEN["att_v"], causal)
+    assert rel(out, GOLDEN[key]) < 1e-6
+
+
+def test_golden_route_dispatch_moe():
+    ids, w, counts = oracle.route_topk(GOLDEN["route_x"], GOLDEN["route_w"], GOLDEN["route_b"], 2)
+    np.testing.assert_array_equal(ids, GOLDEN["route_ids"])
+    np.testing.assert_allclose(w, GOLDEN["route_wts"], rtol=1e-6)
+    np.testing.assert_array_equal(counts, np.bincount(GOLDEN["route_ids"].reshape(-1), minlength=6))
+    c2, off, tok, slots, rw = oracle.dispatch(ids, w, 6)
+    np.testing.assert_array_equal(off, GOLDEN["disp_offsets"])
+    np.testing.assert_array_equal(tok, GOLDEN["disp_tokens"])
+    np.testing.assert_array_equal(slots, GOLDEN["disp_slots"])
+    out = oracle.moe_reference(GOLDEN["route_x"], GOLDEN["moe_w1"], GOLDEN["moe_w3"],
+                               GOLDEN["moe_w2"], ids, w)
+    assert rel(out, GOLDEN["moe_out"]) < 1e-5
+
+
+def test_golden_quantize():
+    q, s = oracle.quantize_kn(GOLDEN["q_w"])
+    np.testing.assert_array_equal(q, GOLDEN["q_q"])
+    np.testing.assert_array_equal(s, GOLDEN["q_s"])
+    assert s[4] == 1.0 and not q[4].any()
+
+
+def test_golden_rope():
+    t = GOLDEN["rope_in"]
+    b, h, s, d = t.shape
+    qkv = np.zeros((b * s, h * d + 2 * d), np.float32)
+    for hh in range(h):
+        qkv[:, hh * d:(hh + 1) * d] = t[0, hh]
+    q, k, v = oracle.split_qkv_rope(qkv, b, s, h * d, h, 1, d, 10000.0)
+    assert rel(q, GOLDEN["rope_out"]) < 1e-6
+
+
+def test_golden_bf16_bits():
+    np.testing.assert_array_equal(oracle.to_bf16_bits(GOLDEN["bf16_in"]), GOLDEN["bf16_bits"])
+
+
+# ------------------------------------------------------------------ closed forms
+def test_rmsnorm_constant_row():
+    c, eps = 0.375, 1e-6
+    w = np.linspace(0.25, 2.0, 300).astype(np.float32)
+    y = oracle.rms_norm(np.full((2, 300), c, np.float32), w, eps)
+    np.testing.assert_allclose(y, np.broadcast_to(c * w / np.sqrt(c * c + eps), (2, 300)), rtol=2e-7)
+
+
+def test_matmul_integer_operands_exact():
+    rng = np.random.default_rng(3)
+    a = rng.integers(-7, 8, size=(33, 70))
+    b = rng.integers(-7, 8, size=(70, 45))
+    np.testing.assert_array_equal(oracle.matmul(a.astype(np.float32), b.astype(np.float32)),
+                                  (a @ b).astype(np.float32))
+
+
+def test_rope_identity_at_zero_and_rotation():
+    d, s = 8, 3
+    rng = np.random.default_rng(5)
+    qkv = rng.standard_normal((s, 2 * d + 2 * d)).astype(np.float32)
+    q, k, _ = oracle.split_qkv_rope(qkv, 1, s, 2 * d, 2, 1, d, 10000.0)
+    np.testing.assert_array_equal(q[0, 0, 0], qkv[0, :d])       # position 0: identity
+    # pair norms preserved
+    src = qkv[:, :d].reshape(s, d // 2, 2)
+    dst = q[0, 0].reshape(s, d // 2, 2)
+    np.testing.assert_allclose(np.hypot(*dst.transpose(2, 0, 1)), np.hypot(*src.transpose(2, 0, 1)),
+                               rtol=1e-6)
+    # pair 0 at position 1 rotates by exactly 1 radian (frequency 1)
+    e, o = qkv[1, 0], qkv[1, 1]
+    np.testing.assert_allclose(dst[1, 0], [e * np.cos(1.0) - o * np.sin(1.0),
+                                           e * np.sin(1.0) + o * np.cos(1.0)], rtol=1e-6)
+
+
+def test_attention_equal_keys_prefix_mean_and_one_hot():
+    rng = np.random.default_rng(7)
+    s, d = 9, 8
+    q = rng.standard_normal((1, 1, s, d)).astype(np.float32)
+    k = np.broadcast_to(rng.standard_normal(d).astype(np.float32), (1, 1, s, d)).copy()
+    v = rng.standard_normal((1, 1, s, d)).astype(np.float32)
+    out = oracle.attention(q, k, v, True)[0, 0]
+    np.testing.assert_allclose(out, np.cumsum(v[0, 0], 0) / np.arange(1, s + 1)[:, None], rtol=1e-5)
+    # one-hot values: output row j equals the softmax probability of key j
+    k2 = rng.standard_normal((1, 1, s, d)).astype(np.float32)
+    eye = np.eye(s, dtype=np.float32)[None, None]
+    p = oracle.attention(q, k2, eye, False)[0, 0]
+    sc = q[0, 0].astype(np.float64) @ k2[0, 0].T.astype(np.float64) / np.sqrt(d)
+    ref = np.exp(sc - sc.max(1, keepdims=True))
+    np.testing.assert_allclose(p, ref / ref.sum(1, keepdims=True), rtol=1e-5)
+
+
+def test_route_ties_and_invariants():
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((64, 16)).astype(np.float32)
+    r = (rng.standard_normal((16, 5)) * 0.3).astype(np.float32)
+    r[:, 3] = r[:, 1]  # experts 1 and 3 always tie: 1 must win
+    ids, w, counts = oracle.route_topk(x, r, None, 2)
+    assert counts.sum() == 64 * 2                              # test_schedforge.cpp:630-633
+    np.testing.assert_allclose(w.sum(1), 1.0, atol=1e-6)        # :634-640
+    assert not np.any(ids == 3) or np.all(np.any(ids == 1, 1)[np.any(ids == 3, 1)])
+    assert np.all(ids[:, 0] != ids[:, 1])
+
+
+def test_quantized_constant_matmul():
+    """test_schedforge.cpp:411-417: input 0.25, weights 0.2 (7x9, k=5)."""
+    w = np.full((5, 9), 0.2, np.float32)
+    q, s = oracle.quantize_kn(w)
+    assert np.all(q == 127)
+    np.testing.assert_allclose(s, np.float32(0.2) / np.float32(127.0))
+    y = oracle.quantized_matmul(np.full((7, 5), 0.25, np.float32), q, s)
+    assert np.max(np.abs(y - 0.25)) < 0.01
+
+
+def test_quantize_rounds_half_away_from_zero():
+    # column max 127 -> scale 1: values x.5 must round away from zero
+    w = np.array([[127.0], [2.5], [-2.5], [0.5], [-0.5], [1.49]], np.float32)
+    q, s = oracle.quantize_kn(w)
+    assert s[0] == 1.0
+    np.testing.assert_array_equal(q[0], [127, 3, -3, 1, -1, 1])
+
+
+def test_quantized_matmul_integer_exact():
+    rng = np.random.default_rng(11)
+    q = rng.integers(-127, 128, size=(12, 40)).astype(np.int8)
+    s = np.ones(12, np.float32)
+    x = rng.integers(-3, 4, size=(5, 40)).astype(np.float32)
+    np.testing.assert_array_equal(oracle.quantized_matmul(x, q, s), x @ q.T.astype(np.float32))
+
+
+def test_bf16_reference_values():
+    vals = np.array([-1.25, 0.0, 0.75, 3.5], np.float32)   # test_schedforge.cpp:252-254
+    np.testing.assert_array_equal(oracle.round_bf16(vals), vals)
+
+
+def test_paged_gather_iota_round_trip():
+    """test_schedforge.cpp:369-379 with per-sequence tables: scatter then gather
+    reproduces iota keys in logical order."""
+    b, h, ctx, d, pt = 2, 2, 7, 4, 4
+    keys = np.arange(b * h * ctx * d, dtype=np.float32).reshape(b, h, ctx, d)
+    table = np.array([[3, 0], [1, 4]], np.int32)
+    pool = oracle.paged_scatter(keys, table, 6, pt)
+    np.testing.assert_array_equal(oracle.paged_gather(pool, table, b, h, ctx, pt, d), keys)
+    # page 3, kv head 1, token 2 of sequence 0 holds logical token 2
+    np.testing.assert_array_equal(pool[3, 1, 2], keys[0, 1, 2])
+
+
+# ------------------------------------------------------------------ whole layer
+def _np_layer(cfg, d, quant=None):
+    """Independent float64 formulation of reference_decoder_layer."""
+    x = d.input.astype(np.float64)
+    B, S, H, Hq, Hkv, D = cfg.batch, cfg.sequence, cfg.hidden, cfg.query_heads, cfg.kv_heads, cfg.head_dim
+
+    def rms(v, w):
+        return v / np.sqrt((v ** 2).mean(1, keepdims=True) + cfg.rms_epsilon) * w
+
+    def W(name, i=None):
+        if quant is None:
+            return getattr(d, name).astype(np.float64)
+        q, s = quant.dense[i]
+        return (q.astype(np.float64) * s[:, None].astype(np.float64)).T
+
+    n1 = rms(x, d.rms1_weight)
+    qkv = np.concatenate([n1 @ W("query_weight", 0), n1 @ W("key_weight", 1), n1 @ W("value_weight", 2)], 1)
+    q = qkv[:, :H].reshape(B, S, Hq, D).transpose(0, 2, 1, 3)
+    k = qkv[:, H:H + Hkv * D].reshape(B, S, Hkv, D).transpose(0, 2, 1, 3)
+    v = qkv[:, H + Hkv * D:].reshape(B, S, Hkv, D).transpose(0, 2, 1, 3)
+    pos = np.arange(S)[:, None].astype(np.float32)
+    fr = np.float32(cfg.rope_theta) ** (-np.arange(0, D, 2, dtype=np.float32) / np.float32(D))
+    ang = (pos * fr).astype(np.float64)
+
+    def rope(t):
+        e, o = t[..., 0::2].copy(), t[..., 1::2].copy()
+        t = t.copy()
+        t[..., 0::2] = e * np.cos(ang) - o * np.sin(ang)
+        t[..., 1::2] = e * np.sin(ang) + o * np.cos(ang)
+        return t
+
+    q, k = rope(q), rope(k)
+    if cfg.context_sequence > 0:
+        k, v = d.cached_key.astype(np.float64), d.cached_value.astype(np.float64)
+    skv = k.shape[2]
+    g = Hq // Hkv
+    k, v = np.repeat(k, g, 1), np.repeat(v, g, 1)
+    s = q @ k.transpose(0, 1, 3, 2) / np.sqrt(D)
+    if cfg.causal:
+        for i in range(S):
+            s[:, :, i, skv - S + i + 1:] = -np.inf
+    p = np.exp(s - s.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    o = (p @ v).transpose(0, 2, 1, 3).reshape(B * S, H)
+    r1 = o @ W("output_weight", 3) + x
+    n2 = rms(r1, d.rms2_weight)
+    if cfg.ffn == "moe":
+        ids, w, _ = oracle.route_topk(n2.astype(np.float32), d.router_weight, d.router_bias, cfg.top_k)
+        f = np.zeros_like(r1)
+        for t in range(B * S):
+            for sl in range(cfg.top_k):
+                e = ids[t, sl]
+                gg = n2[t] @ d.w1[e]
+                uu = n2[t] @ d.w3[e]
+                f[t] += w[t, sl] * ((gg * uu / (1 + np.exp(-uu))) @ d.w2[e])
+        return r1 + f
+    gate, up = n2 @ W("gate_weight", 4), n2 @ W("up_weight", 5)
+    return r1 + (gate / (1 + np.exp(-gate)) * up) @ W("down_weight", 6)
+
+
+@pytest.mark.parametrize("name,overrides", [
+    ("c1", {}),
+    ("c2", {"batch": 2, "hidden": 256, "intermediate": 512, "query_heads": 2, "kv_heads": 1,
+            "context_sequence": 100}),
+    ("c3", {"batch": 1, "sequence": 24, "hidden": 128, "intermediate": 96, "query_heads": 2,
+            "kv_heads": 1, "head_dim": 64}),
+])
+def test_layer_matches_float64_formulation(name, overrides):
+    cfg = CONFIGS[name].replace(**overrides)
+    d = oracle.make_layer_data(cfg, 4242)
+    out = oracle.decoder_layer(cfg, d)
+    assert rel(out, _np_layer(cfg, d)) < 2e-6
+
+
+def test_int8_dense_layer_matches_dequantized_float64():
+    cfg = CONFIGS["c2"].replace(batch=2, hidden=256, intermediate=512, query_heads=2, kv_heads=1,
+                                context_sequence=64, dtype="w8")
+    d = oracle.make_layer_data(cfg, 4343)
+    q = oracle.quantize_layer(cfg, d)
+    out = oracle.decoder_layer(cfg, d, quant=q)
+    assert rel(out, _np_layer(cfg, d, quant=q)) < 2e-6
+
+
+def test_routing_trace_replaces_router():
+    cfg = CONFIGS["c3"].replace(batch=1, sequence=16, hidden=128, intermediate=64, query_heads=2,
+                                kv_heads=1, head_dim=64)
+    d = oracle.make_layer_data(cfg, 77)
+    out, taps = oracle.decoder_layer(cfg, d, taps=True)
+    out2 = oracle.decoder_layer(cfg, d, trace=(taps["ids"], taps["weights"]))
+    np.testing.assert_array_equal(out, out2)
+
+
+# ------------------------------------------------------------------ generators
+def test_generator_determinism_and_moments():
+    a = oracle.normal(1000, "wq", (4096,), 0.02)
+    b = oracle.normal(1000, "wq", (4096,), 0.02)
+    c = oracle.normal(1000, "wk", (4096,), 0.02)
+    np.testing.assert_array_equal(a, b)
+    assert not np.array_equal(a, c)
+    big = oracle.normal(7, 0, (200000,))
+    assert abs(big.mean()) < 0.01 and abs(big.std() - 1.0) < 0.01
+    perm = oracle.page_permutation(5, 1000)
+    np.testing.assert_array_equal(np.sort(perm), np.arange(1000))
+    assert not np.array_equal(perm, np.arange(1000))
+
+
+def test_oracle_rejects_invalid_config():
+    cfg = CONFIGS["c1"].replace(hidden=250)  # hidden != Hq * D
+    d = oracle.make_layer_data(CONFIGS["c1"], 1)
+    with pytest.raises(ValueError):
+        oracle.decoder_layer(cfg, d)
