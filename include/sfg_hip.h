@@ -24,6 +24,13 @@
  *                 sfg_hip_pack_weight_v1 produces the transposed packed form.
  *                 int8 weights are [N][K] with per-channel fp32 scales, exactly
  *                 the reference's QuantizedMatMulWeights (next_milestones.h:52-56).
+ *   tiled weights SFG_LAYOUT_TILED (decode plans): the [N][K] matrix cut into
+ *                 16-row x 128-k tiles stored [N/16][K/128] contiguously, each
+ *                 tile in MFMA-fragment order -- bf16: 4 x [64 lanes][8 values]
+ *                 with lane l = 16 g + r holding row r, k = 32 s + 8 g + [0,8)
+ *                 for fragment s; int8: 2 x [64 lanes][16 values] with k =
+ *                 32 g + 16 t + [0,16) -- so every load a wave issues reads 1 KB
+ *                 contiguous.  Same bytes as [N][K].
  *   paged KV      K pool [page][Hkv][page_tokens][D] bf16, V pool
  *                 [page][Hkv][D][page_tokens] bf16 (token-minor inside a page:
  *                 the decode kernel reads V^T operands as 8-byte runs); each
@@ -55,6 +62,8 @@ enum sfg_status {
 
 enum sfg_dtype { SFG_F32 = 0, SFG_BF16 = 1, SFG_I8 = 2 };
 
+enum sfg_layout { SFG_LAYOUT_NK = 0, SFG_LAYOUT_TILED = 1 };
+
 enum sfg_epilogue {
     SFG_EPI_NONE = 0,      /* C = A B                                             */
     SFG_EPI_RESIDUAL = 1,  /* C = A B + R  (R fp32 [M][N]); decoder_compiler.cpp:256,277 */
@@ -74,13 +83,17 @@ int sfg_hip_device_info_v1(int device, int* cu_count, int* xcd_count, int64_t* h
  * specialisation, decoder_compiler.cpp:535-552; quantize_matmul_weights,
  * next_milestones.cpp:611-637) ---------------- */
 
-/* src fp32 [K][N] (ld_src >= N) -> dst [N][K] in dtype (SFG_F32 or SFG_BF16). */
+/* src fp32 [K][N] (ld_src >= N) -> dst [N][K] in dtype (SFG_F32 or SFG_BF16),
+ * layout SFG_LAYOUT_NK or SFG_LAYOUT_TILED (bf16, N % 16 == 0, K % 128 == 0). */
 int sfg_hip_pack_weight_v1(const float* src, int64_t k, int64_t n, int64_t ld_src, void* dst,
-                           int dst_dtype, void* stream);
-/* src fp32 [K][N] -> int8 [N][K] + scales[N]: s = max|w|/127 (1 if zero),
- * q = clamp(round-half-away(w/s), -127, 127). */
+                           int dst_dtype, int layout, void* stream);
+/* src fp32 [K][N] -> int8 [N][K] (layout NK or TILED) + scales[N]:
+ * s = max|w|/127 (1 if zero), q = clamp(round-half-away(w/s), -127, 127). */
 int sfg_hip_quantize_weight_v1(const float* src, int64_t k, int64_t n, int8_t* dst,
-                               float* scales, void* stream);
+                               float* scales, int layout, void* stream);
+/* Weight layout the GEMM family reads fastest for a product with `rows`
+ * activation rows (grouped: total dispatched rows) and reduction length k. */
+int sfg_hip_preferred_weight_layout_v1(int64_t rows, int64_t k, int grouped);
 /* fp32 -> bf16 bits, round to nearest even (compiler.cpp:34-43). */
 int sfg_hip_to_bf16_v1(const float* src, uint16_t* dst, int64_t count, void* stream);
 /* RoPE table [seq][head_dim/2][2] = (cos, sin) of float(pos) * powf(theta, -(2i)/D),
@@ -109,6 +122,7 @@ typedef struct {
     const float* residual; int64_t ldr;
     int64_t m, n, k;
     int32_t epilogue;
+    int32_t b_layout;   /* SFG_LAYOUT_NK or SFG_LAYOUT_TILED */
 } sfg_gemm_args;
 size_t sfg_hip_gemm_workspace_v1(int64_t m, int64_t n, int64_t k);
 int sfg_hip_gemm_v1(const sfg_gemm_args* args, void* workspace, size_t workspace_bytes,
@@ -182,7 +196,7 @@ size_t sfg_hip_moe_expert_workspace_v1(int64_t tokens, int64_t hidden, int64_t i
                                        int64_t experts, int64_t top_k);
 int sfg_hip_moe_experts_v1(const uint16_t* x, const int32_t* offsets, const int32_t* token_ids,
                            const void* w13, const float* s13, const void* w2, const float* s2,
-                           int w_dtype, uint16_t* act, float* y, int64_t tokens,
+                           int w_dtype, int w_layout, uint16_t* act, float* y, int64_t tokens,
                            int64_t hidden, int64_t inter, int64_t experts, int64_t top_k,
                            void* workspace, size_t workspace_bytes, void* stream);
 /* Weighted combine (moe_compiler.cpp:219-226) fused with the FFN residual
@@ -206,6 +220,7 @@ typedef struct {
     int32_t weight_dtype; /* SFG_F32, SFG_BF16 or SFG_I8 */
     int32_t kv_splits;  /* decode; <= 0: automatic */
     int32_t use_routing_trace;
+    int32_t weight_layout; /* layout of every projection / expert weight */
 } sfg_layer_desc;
 
 typedef struct {

@@ -17,6 +17,7 @@ ABI_VERSION = 1
 
 F32, BF16, I8 = 0, 1, 2
 EPI_NONE, EPI_RESIDUAL, EPI_SWIGLU, EPI_GLU_SILU_UP = 0, 1, 2, 3
+LAYOUT_NK, LAYOUT_TILED = 0, 1
 
 (MARK_START, MARK_NORM1, MARK_QKV, MARK_ROPE, MARK_ATTN_MAIN, MARK_ATTN, MARK_OPROJ,
  MARK_NORM2, MARK_ROUTE, MARK_FFN_UP, MARK_FFN_DOWN, MARK_END, NUM_MARKS) = range(13)
@@ -47,7 +48,7 @@ class GemmArgs(ctypes.Structure):
         ("c", c_vp), ("c_dtype", c_i32), ("ldc", c_i64),
         ("residual", c_vp), ("ldr", c_i64),
         ("m", c_i64), ("n", c_i64), ("k", c_i64),
-        ("epilogue", c_i32),
+        ("epilogue", c_i32), ("b_layout", c_i32),
     ]
 
 
@@ -60,7 +61,7 @@ class LayerDesc(ctypes.Structure):
         ("causal", c_i32), ("ffn", c_i32), ("experts", c_i32), ("top_k", c_i32),
         ("context", c_i32), ("page_tokens", c_i32), ("pages_per_seq", c_i32),
         ("num_pages", c_i32), ("act_dtype", c_i32), ("weight_dtype", c_i32),
-        ("kv_splits", c_i32), ("use_routing_trace", c_i32),
+        ("kv_splits", c_i32), ("use_routing_trace", c_i32), ("weight_layout", c_i32),
     ]
 
 
@@ -94,8 +95,10 @@ _SIGNATURES = {
     "sfg_hip_last_error": (ctypes.c_char_p, []),
     "sfg_hip_device_info_v1": (c_i32, [ctypes.c_int, ctypes.POINTER(ctypes.c_int),
                                        ctypes.POINTER(ctypes.c_int), ctypes.POINTER(c_i64)]),
-    "sfg_hip_pack_weight_v1": (c_i32, [c_vp, c_i64, c_i64, c_i64, c_vp, ctypes.c_int, c_vp]),
-    "sfg_hip_quantize_weight_v1": (c_i32, [c_vp, c_i64, c_i64, c_vp, c_vp, c_vp]),
+    "sfg_hip_pack_weight_v1": (c_i32, [c_vp, c_i64, c_i64, c_i64, c_vp, ctypes.c_int, ctypes.c_int,
+                                       c_vp]),
+    "sfg_hip_quantize_weight_v1": (c_i32, [c_vp, c_i64, c_i64, c_vp, c_vp, ctypes.c_int, c_vp]),
+    "sfg_hip_preferred_weight_layout_v1": (c_i32, [c_i64, c_i64, ctypes.c_int]),
     "sfg_hip_to_bf16_v1": (c_i32, [c_vp, c_vp, c_i64, c_vp]),
     "sfg_hip_rope_table_host_v1": (c_i32, [c_vp, c_i64, c_i64, c_f32]),
     "sfg_hip_rmsnorm_v1": (c_i32, [c_vp, c_vp, c_vp, ctypes.c_int, c_i64, c_i64, c_f32, c_vp]),
@@ -118,7 +121,7 @@ _SIGNATURES = {
                                               c_vp, c_vp, c_vp, c_vp]),
     "sfg_hip_moe_expert_workspace_v1": (c_sz, [c_i64, c_i64, c_i64, c_i64, c_i64]),
     "sfg_hip_moe_experts_v1": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, ctypes.c_int,
-                                       c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp,
+                                       ctypes.c_int, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_vp,
                                        c_sz, c_vp]),
     "sfg_hip_moe_combine_v1": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp]),
     "sfg_hip_decoder_layer_workspace_v1": (c_sz, [ctypes.POINTER(LayerDesc)]),

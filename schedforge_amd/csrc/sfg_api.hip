@@ -81,23 +81,42 @@ int sfg_hip_device_info_v1(int device, int* cu_count, int* xcd_count, int64_t* h
     return SFG_OK;
 }
 
+static int check_layout(int layout, int64_t k, int64_t n, const char* what) {
+    if (layout != SFG_LAYOUT_NK && layout != SFG_LAYOUT_TILED)
+        return fail(SFG_ERR_SHAPE, "%s: unknown layout %d", what, layout);
+    if (layout == SFG_LAYOUT_TILED && (n % 16 != 0 || k % 128 != 0))
+        return fail(SFG_ERR_SHAPE, "%s: tiled layout needs N %% 16 == 0 and K %% 128 == 0 (N=%lld K=%lld)",
+                    what, (long long)n, (long long)k);
+    return SFG_OK;
+}
+
 int sfg_hip_pack_weight_v1(const float* src, int64_t k, int64_t n, int64_t ld_src, void* dst,
-                           int dst_dtype, void* stream) {
+                           int dst_dtype, int layout, void* stream) {
     if (!src || !dst || k <= 0 || n <= 0 || ld_src < n)
         return fail(SFG_ERR_SHAPE, "pack_weight: invalid arguments k=%lld n=%lld ld=%lld",
                     (long long)k, (long long)n, (long long)ld_src);
     if (dst_dtype != SFG_F32 && dst_dtype != SFG_BF16)
         return fail(SFG_ERR_UNSUPPORTED, "pack_weight: dtype %d", dst_dtype);
-    sfg::launch_pack_weight(src, k, n, ld_src, dst, dst_dtype, as_stream(stream));
+    int rc = check_layout(layout, k, n, "pack_weight");
+    if (rc) return rc;
+    if (layout == SFG_LAYOUT_TILED && dst_dtype != SFG_BF16)
+        return fail(SFG_ERR_UNSUPPORTED, "pack_weight: tiled layout is bf16 / int8 only");
+    sfg::launch_pack_weight(src, k, n, ld_src, dst, dst_dtype, layout, as_stream(stream));
     return check_launch("pack_weight");
 }
 
 int sfg_hip_quantize_weight_v1(const float* src, int64_t k, int64_t n, int8_t* dst,
-                               float* scales, void* stream) {
+                               float* scales, int layout, void* stream) {
     if (!src || !dst || !scales || k <= 0 || n <= 0)
         return fail(SFG_ERR_SHAPE, "quantize_weight: invalid arguments");
-    sfg::launch_quantize_weight(src, k, n, dst, scales, as_stream(stream));
+    int rc = check_layout(layout, k, n, "quantize_weight");
+    if (rc) return rc;
+    sfg::launch_quantize_weight(src, k, n, dst, scales, layout, as_stream(stream));
     return check_launch("quantize_weight");
+}
+
+int sfg_hip_preferred_weight_layout_v1(int64_t rows, int64_t k, int grouped) {
+    return sfg::gemm_preferred_layout(rows, k, grouped != 0);
 }
 
 int sfg_hip_to_bf16_v1(const float* src, uint16_t* dst, int64_t count, void* stream) {
@@ -154,7 +173,10 @@ int sfg_hip_gemm_v1(const sfg_gemm_args* a, void* workspace, size_t workspace_by
     p.c = a->c; p.c_dtype = a->c_dtype; p.ldc = a->ldc;
     p.residual = a->residual; p.ldr = a->ldr;
     p.m = a->m; p.n = a->n; p.k = a->k; p.epilogue = a->epilogue;
+    p.b_layout = a->b_layout;
     p.offsets = nullptr; p.groups = 1;
+    if (a->b_layout != SFG_LAYOUT_NK && a->b_layout != SFG_LAYOUT_TILED)
+        return fail(SFG_ERR_SHAPE, "gemm: unknown weight layout %d", a->b_layout);
     const int rc = sfg::launch_gemm(p, workspace, workspace_bytes, as_stream(stream));
     if (rc != SFG_OK)
         return fail(rc, "gemm: unsupported or invalid combination (a=%d b=%d m=%lld n=%lld k=%lld epi=%d)",
@@ -304,7 +326,7 @@ size_t sfg_hip_moe_expert_workspace_v1(int64_t tokens, int64_t hidden, int64_t i
 
 static int moe_experts(const uint16_t* x, const int32_t* offsets, const int32_t* token_ids,
                        const void* w13, const float* s13, const void* w2, const float* s2,
-                       int w_dtype, uint16_t* act, float* y, int64_t tokens, int64_t hidden,
+                       int w_dtype, int w_layout, uint16_t* act, float* y, int64_t tokens, int64_t hidden,
                        int64_t inter, int64_t experts, int64_t top_k, hipStream_t stream) {
     sfg::GemmProblem p{};
     p.a = x; p.a_dtype = SFG_BF16; p.lda = hidden; p.a_rows = token_ids; p.a_rows_limit = tokens;
@@ -312,6 +334,7 @@ static int moe_experts(const uint16_t* x, const int32_t* offsets, const int32_t*
     p.b_group_stride = 2 * inter * hidden; p.s_group_stride = 2 * inter;
     p.c = act; p.c_dtype = SFG_BF16; p.ldc = inter;
     p.m = tokens * top_k; p.n = inter; p.k = hidden; p.epilogue = SFG_EPI_GLU_SILU_UP;
+    p.b_layout = w_layout;
     p.offsets = offsets; p.groups = static_cast<int>(experts);
     int rc = sfg::launch_gemm(p, nullptr, 0, stream);
     if (rc != SFG_OK) return fail(rc, "moe experts W1/W3: shape not lowered (H=%lld I=%lld)",
@@ -322,6 +345,7 @@ static int moe_experts(const uint16_t* x, const int32_t* offsets, const int32_t*
     q.b_group_stride = hidden * inter; q.s_group_stride = hidden;
     q.c = y; q.c_dtype = SFG_F32; q.ldc = hidden;
     q.m = tokens * top_k; q.n = hidden; q.k = inter; q.epilogue = SFG_EPI_NONE;
+    q.b_layout = w_layout;
     q.offsets = offsets; q.groups = static_cast<int>(experts);
     rc = sfg::launch_gemm(q, nullptr, 0, stream);
     if (rc != SFG_OK) return fail(rc, "moe experts W2: shape not lowered");
@@ -330,7 +354,7 @@ static int moe_experts(const uint16_t* x, const int32_t* offsets, const int32_t*
 
 int sfg_hip_moe_experts_v1(const uint16_t* x, const int32_t* offsets, const int32_t* token_ids,
                            const void* w13, const float* s13, const void* w2, const float* s2,
-                           int w_dtype, uint16_t* act, float* y, int64_t tokens, int64_t hidden,
+                           int w_dtype, int w_layout, uint16_t* act, float* y, int64_t tokens, int64_t hidden,
                            int64_t inter, int64_t experts, int64_t top_k, void* workspace,
                            size_t workspace_bytes, void* stream) {
     (void)workspace; (void)workspace_bytes;
@@ -339,8 +363,10 @@ int sfg_hip_moe_experts_v1(const uint16_t* x, const int32_t* offsets, const int3
         return fail(SFG_ERR_INVALID_CONFIG, "invalid MoE configuration");
     if (w_dtype == SFG_I8 && (!s13 || !s2)) return fail(SFG_ERR_SHAPE, "int8 experts need scales");
     if (w_dtype != SFG_BF16 && w_dtype != SFG_I8) return fail(SFG_ERR_UNSUPPORTED, "expert dtype %d", w_dtype);
-    return moe_experts(x, offsets, token_ids, w13, s13, w2, s2, w_dtype, act, y, tokens, hidden,
-                       inter, experts, top_k, as_stream(stream));
+    if (w_layout != SFG_LAYOUT_NK && w_layout != SFG_LAYOUT_TILED)
+        return fail(SFG_ERR_SHAPE, "moe experts: unknown weight layout %d", w_layout);
+    return moe_experts(x, offsets, token_ids, w13, s13, w2, s2, w_dtype, w_layout, act, y, tokens,
+                       hidden, inter, experts, top_k, as_stream(stream));
 }
 
 int sfg_hip_moe_combine_v1(const float* y, const int32_t* position, const float* weights,
@@ -412,6 +438,10 @@ int validate_desc(const sfg_layer_desc* d) {
     }
     if (d->ffn == 1 && d->act_dtype != SFG_BF16)
         return fail(SFG_ERR_UNSUPPORTED, "MoE layers run with bf16 activations");
+    if (d->weight_layout != SFG_LAYOUT_NK && d->weight_layout != SFG_LAYOUT_TILED)
+        return fail(SFG_ERR_SHAPE, "unknown weight layout %d", d->weight_layout);
+    if (d->weight_layout == SFG_LAYOUT_TILED && d->act_dtype != SFG_BF16)
+        return fail(SFG_ERR_UNSUPPORTED, "tiled weights are bf16 / int8");
     return SFG_OK;
 }
 
@@ -528,6 +558,7 @@ int sfg_hip_decoder_layer_v1(const sfg_layer_desc* d, const sfg_layer_weights* w
         p.c = c; p.c_dtype = c_dtype; p.ldc = n;
         p.residual = res; p.ldr = n;
         p.m = m; p.n = n; p.k = k; p.epilogue = epi; p.groups = 1;
+        p.b_layout = d->weight_layout;
         const int r = sfg::launch_gemm(p, b.gemm_ws, b.gemm_ws_bytes, s);
         if (r != SFG_OK)
             return fail(r, "decoder layer GEMM %lldx%lldx%lld not lowered for dtype %d/%d",
@@ -616,7 +647,8 @@ int sfg_hip_decoder_layer_v1(const sfg_layer_desc* d, const sfg_layer_weights* w
         mk.mark(SFG_MARK_ROUTE);
         const float* route_w = d->use_routing_trace ? io->trace_weights : b.wts;
         rc = moe_experts(static_cast<const uint16_t*>(b.xn), b.offsets, b.token_ids, w->w13, w->s13,
-                         w->w2, w->s2, wdt, static_cast<uint16_t*>(b.act), b.y, rows, H, I, E, K, s);
+                         w->w2, w->s2, wdt, d->weight_layout, static_cast<uint16_t*>(b.act), b.y, rows,
+                         H, I, E, K, s);
         if (rc != SFG_OK) return rc;
         mk.mark(SFG_MARK_FFN_UP);
         sfg::launch_moe_combine(b.y, b.position, route_w, b.r1, io->out, rows, H, K, s);

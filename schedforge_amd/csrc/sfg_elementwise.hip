@@ -172,8 +172,63 @@ __global__ __launch_bounds__(256) void transpose_pack_kernel(const float* __rest
     }
 }
 
+// Fragment-tiled packing (SFG_LAYOUT_TILED): one thread per 16-byte lane
+// fragment.  bf16 tile = 16 rows x 128 k = 4 fragments x 64 lanes x 8 values;
+// lane l = 16 g + r holds row r and k = 32 s + 8 g + [0, 8) of fragment s.
+__global__ __launch_bounds__(256) void pack_tiled_bf16_kernel(const float* __restrict__ src,
+                                                              int64_t k, int64_t n, int64_t ld,
+                                                              uint16_t* __restrict__ dst) {
+    const int64_t chunks = k / 128;
+    const int64_t total = (n / 16) * chunks * 4 * 64;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= total) return;
+    const int lane = static_cast<int>(idx & 63);
+    const int s = static_cast<int>((idx >> 6) & 3);
+    const int64_t tc = idx >> 8;
+    const int64_t kc = tc % chunks, nt = tc / chunks;
+    const int64_t col = nt * 16 + (lane & 15);
+    const int64_t k0 = kc * 128 + 32 * s + 8 * (lane >> 4);
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = src[(k0 + j) * ld + col];
+    *reinterpret_cast<uint4*>(dst + idx * 8) = f32x8_to_bf16x8(v);
+}
+
+// int8 tile = 16 rows x 128 k = 2 fragments x 64 lanes x 16 values; lane
+// l = 16 g + r holds row r and k = 32 g + 16 t + [0, 16) of fragment t.
+__global__ __launch_bounds__(256) void quantize_tiled_kernel(const float* __restrict__ src,
+                                                             int64_t k, int64_t n,
+                                                             const float* __restrict__ scales,
+                                                             int8_t* __restrict__ dst) {
+    const int64_t chunks = k / 128;
+    const int64_t total = (n / 16) * chunks * 2 * 64;
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= total) return;
+    const int lane = static_cast<int>(idx & 63);
+    const int t = static_cast<int>((idx >> 6) & 1);
+    const int64_t tc = idx >> 7;
+    const int64_t kc = tc % chunks, nt = tc / chunks;
+    const int64_t col = nt * 16 + (lane & 15);
+    const int64_t k0 = kc * 128 + 32 * (lane >> 4) + 16 * t;
+    const float sc = scales[col];
+    int8_t q[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        float r = roundf(src[(k0 + j) * n + col] / sc);
+        r = fminf(fmaxf(r, -127.0f), 127.0f);
+        q[j] = static_cast<int8_t>(r);
+    }
+    *reinterpret_cast<uint4*>(dst + idx * 16) = *reinterpret_cast<const uint4*>(q);
+}
+
 void launch_pack_weight(const float* src, int64_t k, int64_t n, int64_t ld, void* dst,
-                        int dtype, hipStream_t stream) {
+                        int dtype, int layout, hipStream_t stream) {
+    if (layout == SFG_LAYOUT_TILED) {
+        const int64_t total = (n / 16) * (k / 128) * 256;
+        pack_tiled_bf16_kernel<<<dim3(static_cast<unsigned>((total + 255) / 256)), 256, 0, stream>>>(
+            src, k, n, ld, static_cast<uint16_t*>(dst));
+        return;
+    }
     const dim3 grid(static_cast<unsigned>((n + 63) / 64), static_cast<unsigned>((k + 63) / 64));
     if (dtype == SFG_F32)
         transpose_pack_kernel<float><<<grid, 256, 0, stream>>>(src, k, n, ld,
@@ -223,9 +278,15 @@ __global__ __launch_bounds__(256) void quantize_pack_kernel(const float* __restr
 }
 
 void launch_quantize_weight(const float* src, int64_t k, int64_t n, int8_t* dst, float* scales,
-                            hipStream_t stream) {
+                            int layout, hipStream_t stream) {
     column_absmax_kernel<<<dim3(static_cast<unsigned>((n + 255) / 256)), 256, 0, stream>>>(
         src, k, n, scales);
+    if (layout == SFG_LAYOUT_TILED) {
+        const int64_t total = (n / 16) * (k / 128) * 128;
+        quantize_tiled_kernel<<<dim3(static_cast<unsigned>((total + 255) / 256)), 256, 0, stream>>>(
+            src, k, n, scales, dst);
+        return;
+    }
     const dim3 grid(static_cast<unsigned>((n + 63) / 64), static_cast<unsigned>((k + 63) / 64));
     quantize_pack_kernel<<<grid, 256, 0, stream>>>(src, k, n, scales, dst);
 }

@@ -10,7 +10,7 @@
 //    64-row passes): weight-streaming, HBM bound.  v_mfma_f32_16x16x32_bf16
 //    with the activation rows as the A operand; bf16 or int8 weights (int8 ->
 //    bf16 is exact), 64 B contiguous per lane per 128-k chunk, split-K over up
-//    to 16 waves of one workgroup with a fixed-order LDS reduction.
+//    to 8 waves of one workgroup with a fixed-order LDS reduction.
 //  * gemm_mfma_kernel     large M (prefill, grouped experts): 128x128x32 tiles,
 //    v_mfma_f32_32x32x16_bf16, A/B staged through padded LDS with register
 //    prefetch of the next k-slab, optional A-row gather for dispatched tokens
@@ -45,10 +45,12 @@ __device__ __forceinline__ void store_out(void* c, int c_dtype, int64_t idx, flo
 // A workgroup owns NBT 16-row tiles of B (16 or 32 output columns; for GLU
 // epilogues one gate tile and the matching up tile) and ALL of K: its WAVES
 // waves split K into contiguous chunk ranges and reduce through LDS in a fixed
-// order, so no workgroup ever waits for or publishes to another (no device-
-// scope fences, which on gfx950 write back and invalidate the L2).  Each lane
-// streams 64 B (bf16) / 32 B (int8) of one weight row per 128-k chunk with the
-// next chunk prefetched into registers.
+// order, so no workgroup waits for or publishes to another (no device-scope
+// fences: on gfx950 they write back and invalidate the L2).  Each lane reads
+// 64 B (bf16) / 32 B (int8) of one weight row per 128-k chunk.  A wave issues
+// the loads of CB chunks (weights and activations) back to back before the
+// first MFMA: loads retire in order, so interleaving prefetches with waits
+// would expose the full memory latency on every chunk.
 // ===========================================================================
 struct SkinnyArgs {
     const uint16_t* a; int64_t lda; const int32_t* a_rows; int64_t a_rows_limit;
@@ -61,10 +63,16 @@ struct SkinnyArgs {
 };
 
 constexpr int kSkinnyChunk = 128;  // k per lane-chunk: 4 MFMA steps of 32
+// Chunks whose loads a wave keeps in flight at once: what fits the register
+// file at 8 waves per workgroup without spilling.
+template <int MT>
+constexpr int kSkinnyBatch = MT == 1 ? 4 : (MT == 2 ? 2 : 1);
 
-template <int BDT, int MT, int NBT, int EPI, int WAVES>
+template <int BDT, int MT, int NBT, int EPI, int WAVES, bool TILED>
 __global__ __launch_bounds__(WAVES * 64) void gemm_skinny_kernel(SkinnyArgs p) {
     constexpr bool kGlu = EpiTraits<EPI>::glu;
+    constexpr int CB = kSkinnyBatch<MT>;           // chunks in flight per wave
+    constexpr int BQ = (BDT == SFG_I8) ? 2 : 4;    // uint4 per lane per chunk and tile
     static_assert(!kGlu || NBT == 2, "GLU epilogues pair one gate and one up tile");
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -83,7 +91,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny_kernel(SkinnyArgs p) {
     int64_t out_col;
     if (kGlu) {
         out_col = static_cast<int64_t>(tile) * 16;
-        brow[0] = out_col;           // gate (or W1)
+        brow[0] = out_col;              // gate (or W1)
         brow[NBT - 1] = p.n + out_col;  // up (or W3)
     } else {
         out_col = static_cast<int64_t>(tile) * (16 * NBT);
@@ -91,13 +99,26 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny_kernel(SkinnyArgs p) {
         for (int j = 0; j < NBT; ++j) brow[j] = out_col + 16 * j;
     }
     const int lr = lane & 15;   // A row / B column within a 16-tile
-    const int lg = lane >> 4;   // 32 contiguous k per lane per chunk
+    const int lg = lane >> 4;   // k-group of the MFMA operand
+    // MFMA k order is free as long as A and B agree.  bf16: step s of a chunk
+    // reads k = 32 s + 8 lg + [0, 8), so the four lanes of a row read 64
+    // contiguous bytes per instruction.  int8: a lane's 32 k are contiguous
+    // (32 lg + 8 s + [0, 8)) and arrive as two 16-byte loads.
+    constexpr int kLaneK = (BDT == SFG_I8) ? 32 : 8;
+    constexpr int kStepK = (BDT == SFG_I8) ? 8 : 32;
     const char* bbase = static_cast<const char*>(p.b);
     const int64_t belem = (BDT == SFG_I8) ? 1 : 2;
     const int64_t bgroup = static_cast<int64_t>(g) * p.b_group_stride;
     const char* bptr[NBT];
+    const int64_t chunk_count = p.k / kSkinnyChunk;
+    constexpr int64_t kTileBytes = 16 * kSkinnyChunk * ((BDT == SFG_I8) ? 1 : 2);
 #pragma unroll
-    for (int j = 0; j < NBT; ++j) bptr[j] = bbase + (bgroup + (brow[j] + lr) * p.ldb + lg * 32) * belem;
+    for (int j = 0; j < NBT; ++j) {
+        if (TILED)  // fragment-tiled: tile (brow / 16, chunk) is kTileBytes contiguous
+            bptr[j] = bbase + bgroup * belem + (brow[j] / 16) * chunk_count * kTileBytes + lane * 16;
+        else
+            bptr[j] = bbase + (bgroup + (brow[j] + lr) * p.ldb + lg * kLaneK) * belem;
+    }
     const float* scales = p.scales ? p.scales + static_cast<int64_t>(g) * p.s_group_stride : nullptr;
 
     const int chunks = static_cast<int>(p.k / kSkinnyChunk);
@@ -121,66 +142,67 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny_kernel(SkinnyArgs p) {
             avalid[i] = r < re;
             int64_t src = avalid[i] ? (p.a_rows ? p.a_rows[r] : r) : 0;
             if (src < 0 || src >= p.a_rows_limit) { avalid[i] = false; src = 0; }
-            arow[i] = p.a + src * p.lda + lg * 32;
+            arow[i] = p.a + src * p.lda + lg * kLaneK;
         }
 
-        uint4 bq[NBT][4];
-        auto load_b = [&](int chunk, uint4 (&dst)[NBT][4]) {
-            const int64_t koff = static_cast<int64_t>(chunk) * kSkinnyChunk * belem;
+        for (int c0 = c_begin; c0 < c_end; c0 += CB) {
+            uint4 bq[CB][NBT][BQ];
+            uint4 aq[CB][MT][4];
 #pragma unroll
-            for (int j = 0; j < NBT; ++j) {
-                const uint4* pj = reinterpret_cast<const uint4*>(bptr[j] + koff);
-                if (BDT == SFG_I8) {
-                    dst[j][0] = pj[0]; dst[j][1] = pj[1];
-                } else {
+            for (int c = 0; c < CB; ++c) {
+                if (c0 + c >= c_end) break;
+                const int64_t kofs = static_cast<int64_t>(c0 + c) * kSkinnyChunk;
 #pragma unroll
-                    for (int s = 0; s < 4; ++s) dst[j][s] = pj[s];
+                for (int j = 0; j < NBT; ++j) {
+                    if (TILED) {
+                        // fragment s of this lane: 1 KB-contiguous wave loads
+                        const char* pj = bptr[j] + static_cast<int64_t>(c0 + c) * kTileBytes;
+#pragma unroll
+                        for (int s = 0; s < BQ; ++s)
+                            bq[c][j][s] = *reinterpret_cast<const uint4*>(pj + 1024 * s);
+                    } else {
+                        const char* pj = bptr[j] + kofs * belem;
+#pragma unroll
+                        for (int s = 0; s < BQ; ++s)
+                            bq[c][j][s] = *reinterpret_cast<const uint4*>(
+                                pj + (BDT == SFG_I8 ? 16 * s : 2 * kStepK * s));
+                    }
                 }
-            }
-        };
-        if (c_begin < c_end) load_b(c_begin, bq);
-        for (int chunk = c_begin; chunk < c_end; ++chunk) {
-            uint4 cur[NBT][4];
 #pragma unroll
-            for (int j = 0; j < NBT; ++j)
+                for (int i = 0; i < MT; ++i) {
+                    const uint16_t* ap = arow[i] + kofs;
 #pragma unroll
-                for (int s = 0; s < 4; ++s) cur[j][s] = bq[j][s];
-            if (chunk + 1 < c_end) load_b(chunk + 1, bq);
-            uint4 af[MT][4];
-#pragma unroll
-            for (int i = 0; i < MT; ++i) {
-                if (avalid[i]) {
-                    const uint4* ap = reinterpret_cast<const uint4*>(
-                        arow[i] + static_cast<int64_t>(chunk) * kSkinnyChunk);
-#pragma unroll
-                    for (int s = 0; s < 4; ++s) af[i][s] = ap[s];
-                } else {
-#pragma unroll
-                    for (int s = 0; s < 4; ++s) af[i][s] = make_uint4(0, 0, 0, 0);
-                }
-            }
-            bf16x8 bf[NBT][4];
-#pragma unroll
-            for (int j = 0; j < NBT; ++j) {
-                if (BDT == SFG_I8) {
-                    bf[j][0] = as_bf16x8(i8x8_to_bf16x8(cur[j][0].x, cur[j][0].y));
-                    bf[j][1] = as_bf16x8(i8x8_to_bf16x8(cur[j][0].z, cur[j][0].w));
-                    bf[j][2] = as_bf16x8(i8x8_to_bf16x8(cur[j][1].x, cur[j][1].y));
-                    bf[j][3] = as_bf16x8(i8x8_to_bf16x8(cur[j][1].z, cur[j][1].w));
-                } else {
-#pragma unroll
-                    for (int s = 0; s < 4; ++s) bf[j][s] = as_bf16x8(cur[j][s]);
+                    for (int s = 0; s < 4; ++s)
+                        aq[c][i][s] = avalid[i] ? *reinterpret_cast<const uint4*>(ap + kStepK * s)
+                                                : make_uint4(0, 0, 0, 0);
                 }
             }
 #pragma unroll
-            for (int i = 0; i < MT; ++i)
+            for (int c = 0; c < CB; ++c) {
+                if (c0 + c >= c_end) break;
+                bf16x8 bf[NBT][4];
 #pragma unroll
-                for (int s = 0; s < 4; ++s) {
-                    const bf16x8 a = as_bf16x8(af[i][s]);
+                for (int j = 0; j < NBT; ++j) {
+                    if (BDT == SFG_I8) {
+                        bf[j][0] = as_bf16x8(i8x8_to_bf16x8(bq[c][j][0].x, bq[c][j][0].y));
+                        bf[j][1] = as_bf16x8(i8x8_to_bf16x8(bq[c][j][0].z, bq[c][j][0].w));
+                        bf[j][2] = as_bf16x8(i8x8_to_bf16x8(bq[c][j][1].x, bq[c][j][1].y));
+                        bf[j][3] = as_bf16x8(i8x8_to_bf16x8(bq[c][j][1].z, bq[c][j][1].w));
+                    } else {
 #pragma unroll
-                    for (int j = 0; j < NBT; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bf[j][s], acc[i][j], 0, 0, 0);
+                        for (int s = 0; s < 4; ++s) bf[j][s] = as_bf16x8(bq[c][j][s]);
+                    }
                 }
+#pragma unroll
+                for (int i = 0; i < MT; ++i)
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) {
+                        const bf16x8 a = as_bf16x8(aq[c][i][s]);
+#pragma unroll
+                        for (int j = 0; j < NBT; ++j)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bf[j][s], acc[i][j], 0, 0, 0);
+                    }
+            }
         }
 
         // Reduce the waves' partial sums in a fixed order (0 + 1 + ... ).
@@ -409,6 +431,190 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(TiledArgs p) {
 }
 
 // ===========================================================================
+// Large-M MFMA GEMM, second generation: 256x128 output tile per workgroup (for
+// GLU epilogues 256 rows x 64 outputs, i.e. 64 gate + 64 up B rows), BK = 64.
+// Four waves each own 64 rows x 128 B-columns = 2 x 4 tiles of
+// v_mfma_f32_32x32x16_bf16 (128 fp32 accumulators per lane).  The k-slabs are
+// double-buffered in LDS (rows padded to 144 B), the next slab is fetched into
+// registers while the current one feeds the MFMAs, and there is one barrier
+// per slab.  Dense problems map workgroups XCD-aware: consecutive workgroup
+// ids are spread over the 8 XCDs by the dispatcher, so each XCD is handed a
+// contiguous run of tiles in grouped (8 M-tiles) order, which shares A and B
+// tiles inside one L2.
+// ===========================================================================
+constexpr int kGM = 256, kGN = 128, kGK = 64;
+constexpr int kGRow = kGK + 8;  // padded LDS row, bf16 elements
+
+template <int BDT, int EPI>
+__global__ __launch_bounds__(256) void gemm_mfma256_kernel(TiledArgs p, int tiles_m, int tiles_n) {
+    constexpr bool kGlu = EpiTraits<EPI>::glu;
+    __shared__ __attribute__((aligned(16))) uint16_t sA[2][kGM * kGRow];
+    __shared__ __attribute__((aligned(16))) uint16_t sB[2][kGN * kGRow];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+
+    int g = 0;
+    int64_t rb = 0, re = p.m;
+    int64_t tm, tn;
+    if (p.offsets) {
+        tn = blockIdx.x;
+        int64_t t = blockIdx.y;
+        auto bound = [&](int e) {
+            return min(max(static_cast<int64_t>(p.offsets[e]), int64_t(0)), p.m);
+        };
+        g = -1;
+        for (int e = 0; e < p.groups; ++e) {
+            const int64_t rows = max(bound(e + 1) - bound(e), int64_t(0));
+            const int64_t tiles = (rows + kGM - 1) / kGM;
+            if (t < tiles) { g = e; break; }
+            t -= tiles;
+        }
+        if (g < 0) return;
+        rb = bound(g);
+        re = max(bound(g + 1), rb);
+        tm = t;
+    } else {
+        const int64_t total = static_cast<int64_t>(tiles_m) * tiles_n;
+        const int64_t i = blockIdx.x;
+        const int64_t full = total - total % 8;
+        int64_t L = i;
+        if (i < full) L = (i % 8) * (full / 8) + i / 8;
+        constexpr int64_t kGroupM = 8;
+        const int64_t group = L / (kGroupM * tiles_n);
+        const int64_t first_m = group * kGroupM;
+        const int64_t gsize = min(static_cast<int64_t>(tiles_m) - first_m, kGroupM);
+        const int64_t in_group = L % (kGroupM * tiles_n);
+        tm = first_m + in_group % gsize;
+        tn = in_group / gsize;
+    }
+    const int64_t row0 = rb + tm * kGM;
+    if (row0 >= re) return;
+    const int64_t ncol0 = tn * (kGlu ? kGN / 2 : kGN);
+    const int64_t bgroup = static_cast<int64_t>(g) * p.b_group_stride;
+    const float* scales = p.scales ? p.scales + static_cast<int64_t>(g) * p.s_group_stride : nullptr;
+
+    // Global -> register staging: A 256 x 64 = 8 chunks of 16 B per thread,
+    // B 128 x 64 = 4 chunks.  Chunk (row, kc): row = (tid >> 3) + 32 i, kc = 8 (tid & 7).
+    const int kc = (tid & 7) * 8;
+    const uint16_t* a_src[8];
+    bool a_ok[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int64_t r = row0 + (tid >> 3) + 32 * i;
+        a_ok[i] = r < re;
+        int64_t src = a_ok[i] ? (p.a_rows ? p.a_rows[r] : r) : 0;
+        if (src < 0 || src >= p.a_rows_limit) { a_ok[i] = false; src = 0; }
+        a_src[i] = p.a + src * p.lda + kc;
+    }
+    const char* bbytes = static_cast<const char*>(p.b);
+    int64_t b_src[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int local = (tid >> 3) + 32 * i;
+        int64_t brow;
+        if (kGlu) brow = local < 64 ? ncol0 + local : p.n + ncol0 + local - 64;
+        else brow = ncol0 + local;
+        b_src[i] = bgroup + brow * p.ldb + kc;  // elements
+    }
+    uint4 ra[8], rbv[4];
+    auto fetch = [&](int64_t k0) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            ra[i] = a_ok[i] ? *reinterpret_cast<const uint4*>(a_src[i] + k0) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (BDT == SFG_I8) {
+                const uint2 q = *reinterpret_cast<const uint2*>(bbytes + b_src[i] + k0);
+                rbv[i] = i8x8_to_bf16x8(q.x, q.y);
+            } else {
+                rbv[i] = *reinterpret_cast<const uint4*>(bbytes + (b_src[i] + k0) * 2);
+            }
+        }
+    };
+    auto stash = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            *reinterpret_cast<uint4*>(&sA[buf][((tid >> 3) + 32 * i) * kGRow + kc]) = ra[i];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            *reinterpret_cast<uint4*>(&sB[buf][((tid >> 3) + 32 * i) * kGRow + kc]) = rbv[i];
+    };
+
+    floatx16 acc[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    const int64_t slabs = p.k / kGK;
+    fetch(0);
+    stash(0);
+    __syncthreads();
+    const int l32 = lane & 31, lh = (lane >> 5) * 8;
+    for (int64_t kt = 0; kt < slabs; ++kt) {
+        const int cur = static_cast<int>(kt & 1);
+        if (kt + 1 < slabs) fetch((kt + 1) * kGK);
+        const uint16_t* A = sA[cur];
+        const uint16_t* B = sB[cur];
+#pragma unroll
+        for (int kk = 0; kk < kGK / 16; ++kk) {
+            bf16x8 af[2], bf[4];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                af[i] = as_bf16x8(*reinterpret_cast<const uint4*>(
+                    &A[(wave * 64 + i * 32 + l32) * kGRow + kk * 16 + lh]));
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                bf[j] = as_bf16x8(*reinterpret_cast<const uint4*>(
+                    &B[(j * 32 + l32) * kGRow + kk * 16 + lh]));
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+        if (kt + 1 < slabs) stash(cur ^ 1);
+        __syncthreads();
+    }
+
+    // Epilogue: 32x32 D layout, lane holds column (lane & 31) and rows
+    // 8 (r / 4) + 4 (lane >> 5) + (r % 4).
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int64_t row = row0 + wave * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            if (row >= re) continue;
+            if (kGlu) {
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int64_t col = ncol0 + j * 32 + l32;
+                    float gv = acc[i][j][r], uv = acc[i][j + 2][r];
+                    if (scales) {
+                        gv *= scales[col];
+                        uv *= scales[p.n + col];
+                    }
+                    store_out(p.c, p.c_dtype, row * p.ldc + col, glu_combine(EPI, gv, uv));
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int64_t col = ncol0 + j * 32 + l32;
+                    float v = acc[i][j][r];
+                    if (scales) v *= scales[col];
+                    if (EPI == SFG_EPI_RESIDUAL) v += p.residual[row * p.ldr + col];
+                    store_out(p.c, p.c_dtype, row * p.ldc + col, v);
+                }
+            }
+        }
+    }
+}
+
+// ===========================================================================
 // fp32 GEMM (VALU): 64x64 tile, BK 16, 256 threads x (4 rows x 4 cols).
 // For GLU epilogues the tile covers 32 outputs: thread columns {2t, 2t+1}
 // of the gate block and the same two of the up block.
@@ -494,47 +700,64 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(F32Args p) {
 // ===========================================================================
 namespace {
 
-constexpr int kMaxWaves = 16;
+constexpr int kMaxWaves = 8;
 
-// Waves per workgroup: enough that each wave owns >= 2 chunks of 128 k when
-// K allows, capped so the LDS reduction buffer stays under 64 KB.
+// Waves per workgroup: enough that each wave owns at most one batch of chunks
+// (4 at MT = 1, 2 otherwise) when K allows, capped so the LDS reduction
+// buffer stays under 64 KB.
 int skinny_waves(int64_t k, int mt, int nbt) {
     const int64_t chunks = k / kSkinnyChunk;
+    const int64_t per_wave = mt == 1 ? kSkinnyBatch<1> : (mt == 2 ? kSkinnyBatch<2> : kSkinnyBatch<4>);
     int w = 4;
-    while (w < kMaxWaves && chunks >= 2 * (w * 2)) w *= 2;
+    while (w < kMaxWaves && chunks > per_wave * w) w *= 2;
     while (w > 4 && (w - 1) * mt * nbt * 1024 > 64 * 1024) w /= 2;
     return w;
 }
 
 template <int BDT, int MT, int NBT, int EPI>
-void launch_skinny_w(const SkinnyArgs& a, dim3 grid, int waves, hipStream_t s) {
-    if (waves == 4) gemm_skinny_kernel<BDT, MT, NBT, EPI, 4><<<grid, 256, 0, s>>>(a);
-    else if (waves == 8) gemm_skinny_kernel<BDT, MT, NBT, EPI, 8><<<grid, 512, 0, s>>>(a);
-    else gemm_skinny_kernel<BDT, MT, NBT, EPI, 16><<<grid, 1024, 0, s>>>(a);
+void launch_skinny_w(const SkinnyArgs& a, dim3 grid, int waves, bool tiled, hipStream_t s) {
+    if (tiled) {
+        if (waves == 4) gemm_skinny_kernel<BDT, MT, NBT, EPI, 4, true><<<grid, 256, 0, s>>>(a);
+        else gemm_skinny_kernel<BDT, MT, NBT, EPI, 8, true><<<grid, 512, 0, s>>>(a);
+    } else {
+        if (waves == 4) gemm_skinny_kernel<BDT, MT, NBT, EPI, 4, false><<<grid, 256, 0, s>>>(a);
+        else gemm_skinny_kernel<BDT, MT, NBT, EPI, 8, false><<<grid, 512, 0, s>>>(a);
+    }
 }
 
 template <int BDT, int MT>
-void launch_skinny_e(const SkinnyArgs& a, dim3 grid, int nbt, int waves, int epi, hipStream_t s) {
+void launch_skinny_e(const SkinnyArgs& a, dim3 grid, int nbt, int waves, int epi, bool tiled,
+                     hipStream_t s) {
     switch (epi) {
         case SFG_EPI_NONE:
-            if (nbt == 1) launch_skinny_w<BDT, MT, 1, SFG_EPI_NONE>(a, grid, waves, s);
-            else launch_skinny_w<BDT, MT, 2, SFG_EPI_NONE>(a, grid, waves, s);
+            if (nbt == 1) launch_skinny_w<BDT, MT, 1, SFG_EPI_NONE>(a, grid, waves, tiled, s);
+            else launch_skinny_w<BDT, MT, 2, SFG_EPI_NONE>(a, grid, waves, tiled, s);
             break;
         case SFG_EPI_RESIDUAL:
-            if (nbt == 1) launch_skinny_w<BDT, MT, 1, SFG_EPI_RESIDUAL>(a, grid, waves, s);
-            else launch_skinny_w<BDT, MT, 2, SFG_EPI_RESIDUAL>(a, grid, waves, s);
+            if (nbt == 1) launch_skinny_w<BDT, MT, 1, SFG_EPI_RESIDUAL>(a, grid, waves, tiled, s);
+            else launch_skinny_w<BDT, MT, 2, SFG_EPI_RESIDUAL>(a, grid, waves, tiled, s);
             break;
-        case SFG_EPI_SWIGLU: launch_skinny_w<BDT, MT, 2, SFG_EPI_SWIGLU>(a, grid, waves, s); break;
-        default: launch_skinny_w<BDT, MT, 2, SFG_EPI_GLU_SILU_UP>(a, grid, waves, s); break;
+        case SFG_EPI_SWIGLU: launch_skinny_w<BDT, MT, 2, SFG_EPI_SWIGLU>(a, grid, waves, tiled, s); break;
+        default: launch_skinny_w<BDT, MT, 2, SFG_EPI_GLU_SILU_UP>(a, grid, waves, tiled, s); break;
     }
 }
 
 template <int BDT>
 void launch_skinny_b(const SkinnyArgs& a, dim3 grid, int mt, int nbt, int waves, int epi,
-                     hipStream_t s) {
-    if (mt == 1) launch_skinny_e<BDT, 1>(a, grid, nbt, waves, epi, s);
-    else if (mt == 2) launch_skinny_e<BDT, 2>(a, grid, nbt, waves, epi, s);
-    else launch_skinny_e<BDT, 4>(a, grid, nbt, waves, epi, s);
+                     bool tiled, hipStream_t s) {
+    if (mt == 1) launch_skinny_e<BDT, 1>(a, grid, nbt, waves, epi, tiled, s);
+    else if (mt == 2) launch_skinny_e<BDT, 2>(a, grid, nbt, waves, epi, tiled, s);
+    else launch_skinny_e<BDT, 4>(a, grid, nbt, waves, epi, tiled, s);
+}
+
+template <int BDT>
+void launch_big_b(const TiledArgs& a, dim3 grid, int tm, int tn, int epi, hipStream_t s) {
+    switch (epi) {
+        case SFG_EPI_NONE: gemm_mfma256_kernel<BDT, SFG_EPI_NONE><<<grid, 256, 0, s>>>(a, tm, tn); break;
+        case SFG_EPI_RESIDUAL: gemm_mfma256_kernel<BDT, SFG_EPI_RESIDUAL><<<grid, 256, 0, s>>>(a, tm, tn); break;
+        case SFG_EPI_SWIGLU: gemm_mfma256_kernel<BDT, SFG_EPI_SWIGLU><<<grid, 256, 0, s>>>(a, tm, tn); break;
+        default: gemm_mfma256_kernel<BDT, SFG_EPI_GLU_SILU_UP><<<grid, 256, 0, s>>>(a, tm, tn); break;
+    }
 }
 
 template <int BDT>
@@ -554,8 +777,16 @@ bool is_glu(int epi) { return epi == SFG_EPI_SWIGLU || epi == SFG_EPI_GLU_SILU_U
 // tiled kernel.
 constexpr int64_t kSkinnyMaxRows = 64;
 constexpr int64_t kSkinnyGroupedMaxTotal = 512;
+// Problems with at least this many rows use the 256x128 kernel.
+constexpr int64_t kBigMinRows = 1024;
 
 }  // namespace
+
+int gemm_preferred_layout(int64_t rows, int64_t k, bool grouped) {
+    const bool skinny = k % kSkinnyChunk == 0 &&
+                        (grouped ? rows <= kSkinnyGroupedMaxTotal : rows <= kSkinnyMaxRows);
+    return skinny ? SFG_LAYOUT_TILED : SFG_LAYOUT_NK;
+}
 
 size_t gemm_workspace_bytes(int64_t m, int64_t n, int64_t k) {
     (void)m; (void)n; (void)k;
@@ -565,7 +796,8 @@ size_t gemm_workspace_bytes(int64_t m, int64_t n, int64_t k) {
 int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes, hipStream_t stream) {
     const bool glu = is_glu(p.epilogue);
     if (p.a_dtype == SFG_F32) {
-        if (p.b_dtype != SFG_F32 || p.offsets || p.a_rows) return SFG_ERR_UNSUPPORTED;
+        if (p.b_dtype != SFG_F32 || p.offsets || p.a_rows || p.b_layout != SFG_LAYOUT_NK)
+            return SFG_ERR_UNSUPPORTED;
         F32Args a{static_cast<const float*>(p.a), p.lda, static_cast<const float*>(p.b), p.ldb,
                   p.c, p.c_dtype, p.ldc, p.residual, p.ldr, p.m, p.n, p.k};
         const dim3 grid(static_cast<unsigned>((p.n + (glu ? 31 : 63)) / (glu ? 32 : 64)),
@@ -580,12 +812,14 @@ int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes, h
     }
     if (p.a_dtype != SFG_BF16 || (p.b_dtype != SFG_BF16 && p.b_dtype != SFG_I8))
         return SFG_ERR_UNSUPPORTED;
-    if (p.k % kSkinnyChunk != 0) return SFG_ERR_UNSUPPORTED;
     if (p.b_dtype == SFG_I8 && p.b_scales == nullptr) return SFG_ERR_SHAPE;
     const int groups = p.offsets ? p.groups : 1;
-    const bool skinny = p.offsets ? (p.m <= kSkinnyGroupedMaxTotal) : (p.m <= kSkinnyMaxRows);
+    // The skinny kernel streams K in 128-element chunks; other K go tiled.
+    const bool skinny = p.k % kSkinnyChunk == 0 &&
+                        (p.offsets ? (p.m <= kSkinnyGroupedMaxTotal) : (p.m <= kSkinnyMaxRows));
     if (skinny) {
-        const int64_t rows_hint = p.offsets ? kSkinnyMaxRows : p.m;
+        // grouped problems: 32 rows per pass covers the typical decode expert
+        const int64_t rows_hint = p.offsets ? 32 : p.m;
         const int mt = rows_hint <= 16 ? 1 : (rows_hint <= 32 ? 2 : 4);
         const int nbt = glu ? 2 : (rows_hint <= 16 ? 1 : 2);
         const int64_t tile_cols = glu ? 16 : 16 * nbt;
@@ -600,11 +834,14 @@ int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes, h
         a.residual = p.residual; a.ldr = p.ldr;
         a.m = p.m; a.n = p.n; a.k = p.k; a.offsets = p.offsets;
         const dim3 grid(static_cast<unsigned>(p.n / tile_cols), 1u, static_cast<unsigned>(groups));
-        if (p.b_dtype == SFG_I8) launch_skinny_b<SFG_I8>(a, grid, mt, nbt, waves, p.epilogue, stream);
-        else launch_skinny_b<SFG_BF16>(a, grid, mt, nbt, waves, p.epilogue, stream);
+        const bool tiled = p.b_layout == SFG_LAYOUT_TILED;
+        if (p.b_dtype == SFG_I8) launch_skinny_b<SFG_I8>(a, grid, mt, nbt, waves, p.epilogue, tiled, stream);
+        else launch_skinny_b<SFG_BF16>(a, grid, mt, nbt, waves, p.epilogue, tiled, stream);
         return SFG_OK;
     }
+    if (p.b_layout == SFG_LAYOUT_TILED) return SFG_ERR_UNSUPPORTED;  // tiled weights feed the skinny kernel only
     if (p.n % (glu ? 64 : 128) != 0 || p.k % kTK != 0) return SFG_ERR_UNSUPPORTED;
+    const bool big = p.k % kGK == 0 && p.m >= kBigMinRows;
     TiledArgs a{};
     a.a = static_cast<const uint16_t*>(p.a); a.lda = p.lda; a.a_rows = p.a_rows;
     a.a_rows_limit = p.a_rows ? p.a_rows_limit : p.m;
@@ -613,6 +850,20 @@ int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes, h
     a.c = p.c; a.c_dtype = p.c_dtype; a.ldc = p.ldc;
     a.residual = p.residual; a.ldr = p.ldr;
     a.m = p.m; a.n = p.n; a.k = p.k; a.offsets = p.offsets; a.groups = groups;
+    if (big) {
+        const int64_t tn = glu ? p.n / 64 : p.n / 128;
+        if (p.offsets) {
+            const dim3 grid(static_cast<unsigned>(tn), static_cast<unsigned>((p.m + kGM - 1) / kGM + groups));
+            if (p.b_dtype == SFG_I8) launch_big_b<SFG_I8>(a, grid, 0, static_cast<int>(tn), p.epilogue, stream);
+            else launch_big_b<SFG_BF16>(a, grid, 0, static_cast<int>(tn), p.epilogue, stream);
+        } else {
+            const int64_t tm = (p.m + kGM - 1) / kGM;
+            const dim3 grid(static_cast<unsigned>(tm * tn));
+            if (p.b_dtype == SFG_I8) launch_big_b<SFG_I8>(a, grid, static_cast<int>(tm), static_cast<int>(tn), p.epilogue, stream);
+            else launch_big_b<SFG_BF16>(a, grid, static_cast<int>(tm), static_cast<int>(tn), p.epilogue, stream);
+        }
+        return SFG_OK;
+    }
     const int64_t row_tiles = p.offsets ? (p.m + kTM - 1) / kTM + groups : (p.m + kTM - 1) / kTM;
     const dim3 grid(static_cast<unsigned>(glu ? p.n / 64 : p.n / 128), static_cast<unsigned>(row_tiles));
     if (p.b_dtype == SFG_I8) launch_tiled_b<SFG_I8>(a, grid, p.epilogue, stream);

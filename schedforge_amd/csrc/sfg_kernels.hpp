@@ -19,9 +19,9 @@ void launch_split_rope(const float* qkv, const float* table, int64_t batch, int6
                        int64_t q_heads, int64_t kv_heads, int64_t head_dim, void* q, void* k,
                        void* v, int out_dtype, hipStream_t stream);
 void launch_pack_weight(const float* src, int64_t k, int64_t n, int64_t ld, void* dst,
-                        int dtype, hipStream_t stream);
+                        int dtype, int layout, hipStream_t stream);
 void launch_quantize_weight(const float* src, int64_t k, int64_t n, int8_t* dst, float* scales,
-                            hipStream_t stream);
+                            int layout, hipStream_t stream);
 void launch_to_bf16(const float* src, uint16_t* dst, int64_t count, hipStream_t stream);
 void launch_fill_zero(void* dst, size_t bytes, hipStream_t stream);
 
@@ -40,11 +40,14 @@ struct GemmProblem {
     const float* residual; int64_t ldr;
     int64_t m, n, k;            // m: total rows (dense) or upper bound (grouped)
     int epilogue;
+    int b_layout;               // SFG_LAYOUT_NK or SFG_LAYOUT_TILED
     const int32_t* offsets;     // grouped: device [groups+1]; nullptr = dense
     int groups;
 };
 
 size_t gemm_workspace_bytes(int64_t m, int64_t n, int64_t k);
+// The layout launch_gemm reads fastest for these rows (see sfg_layout).
+int gemm_preferred_layout(int64_t rows, int64_t k, bool grouped);
 // Returns SFG_OK or an error code (unsupported combination).
 int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes,
                 hipStream_t stream);

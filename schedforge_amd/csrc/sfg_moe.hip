@@ -16,53 +16,60 @@ namespace sfg {
 
 // One thread per (token, expert) chain; the block then runs softmax + top-k for
 // its tokens with one thread per token.  E <= 256, top_k <= 8.  The chain runs
-// over features in order (bit-identical to a sequential fp32 FMA loop); its
-// operands for the next 32 features are fetched into registers while the
-// current 32 FMAs issue, so the chain never waits on a load.
-constexpr int kRouteStep = 32;
-constexpr int kRouteTokens = 32;     // tokens per workgroup
+// over features in order (bit-identical to a sequential fp32 FMA loop).  Its
+// operands are staged through LDS in 512-feature chunks, double-buffered: the
+// whole workgroup loads chunk c + 1 (many loads in flight) while each thread
+// runs its chain over chunk c from LDS.
+constexpr int kRouteChunk = 512;
+constexpr int kRouteTokens = 4;        // tokens per workgroup
+constexpr int kRouteMaxExperts = 16;   // LDS sized for E <= 16 (larger E: direct path)
 
 __global__ __launch_bounds__(256) void moe_router_kernel(
     const float* __restrict__ x, const float* __restrict__ router, const float* __restrict__ bias,
     int tokens, int hidden, int experts, int top_k, int32_t* __restrict__ ids,
     float* __restrict__ weights) {
     __shared__ float logits[256];
-    const int per_block = min(kRouteTokens, 256 / experts);
+    __shared__ __attribute__((aligned(16))) float sx[2][kRouteTokens][kRouteChunk];
+    __shared__ __attribute__((aligned(16))) float sw[2][kRouteChunk * kRouteMaxExperts];
+    const bool staged = experts <= kRouteMaxExperts;
+    const int per_block = staged ? kRouteTokens : min(kRouteTokens, 256 / experts);
     const int t_local = threadIdx.x / experts;
     const int e = threadIdx.x % experts;
-    const int t = blockIdx.x * per_block + t_local;
+    const int t0 = blockIdx.x * per_block;
+    const int t = t0 + t_local;
     const bool active = t_local < per_block && t < tokens;
-    if (active) {
-        const float* xr = x + static_cast<int64_t>(t) * hidden;
-        const float* wc = router + e;
-        float acc = 0.f;
-        const int full = hidden / kRouteStep * kRouteStep;
-        float xa[kRouteStep], wa[kRouteStep], xb[kRouteStep], wb[kRouteStep];
-        auto fetch = [&](int f0, float (&xs)[kRouteStep], float (&ws)[kRouteStep]) {
-#pragma unroll
-            for (int j = 0; j < kRouteStep; j += 4) {
-                const float4 v = *reinterpret_cast<const float4*>(xr + f0 + j);
-                xs[j] = v.x; xs[j + 1] = v.y; xs[j + 2] = v.z; xs[j + 3] = v.w;
+    float acc = 0.f;
+    if (staged) {
+        auto stage = [&](int buf, int f0) {
+            const int fc = min(kRouteChunk, hidden - f0);
+            for (int i = threadIdx.x; i < per_block * fc; i += 256) {
+                const int tt = i / fc, ff = i % fc;
+                sx[buf][tt][ff] = (t0 + tt < tokens) ? x[static_cast<int64_t>(t0 + tt) * hidden + f0 + ff] : 0.f;
             }
-#pragma unroll
-            for (int j = 0; j < kRouteStep; ++j) ws[j] = wc[static_cast<int64_t>(f0 + j) * experts];
+            for (int i = threadIdx.x; i < fc * experts; i += 256)
+                sw[buf][i] = router[static_cast<int64_t>(f0) * experts + i];
         };
-        const bool vec = (hidden & 3) == 0;
-        int f0 = 0;
-        if (vec && full > 0) {
-            fetch(0, xa, wa);
-            for (; f0 < full; f0 += 2 * kRouteStep) {
-                if (f0 + kRouteStep < full) fetch(f0 + kRouteStep, xb, wb);
-#pragma unroll
-                for (int j = 0; j < kRouteStep; ++j) acc = __builtin_fmaf(xa[j], wa[j], acc);
-                if (f0 + kRouteStep >= full) { f0 += kRouteStep; break; }
-                if (f0 + 2 * kRouteStep < full) fetch(f0 + 2 * kRouteStep, xa, wa);
-#pragma unroll
-                for (int j = 0; j < kRouteStep; ++j) acc = __builtin_fmaf(xb[j], wb[j], acc);
+        stage(0, 0);
+        __syncthreads();
+        int buf = 0;
+        for (int f0 = 0; f0 < hidden; f0 += kRouteChunk) {
+            if (f0 + kRouteChunk < hidden) stage(buf ^ 1, f0 + kRouteChunk);
+            const int fc = min(kRouteChunk, hidden - f0);
+            if (active) {
+                const float* xr = sx[buf][t_local];
+                const float* wr = sw[buf] + e;
+#pragma unroll 16
+                for (int f = 0; f < fc; ++f) acc = __builtin_fmaf(xr[f], wr[f * experts], acc);
             }
-            if (f0 > full) f0 = full;
+            __syncthreads();
+            buf ^= 1;
         }
-        for (; f0 < hidden; ++f0) acc = __builtin_fmaf(xr[f0], wc[static_cast<int64_t>(f0) * experts], acc);
+    } else if (active) {
+        const float* xr = x + static_cast<int64_t>(t) * hidden;
+        for (int f = 0; f < hidden; ++f)
+            acc = __builtin_fmaf(xr[f], router[static_cast<int64_t>(f) * experts + e], acc);
+    }
+    if (active) {
         if (bias) acc = acc + bias[e];
         logits[t_local * experts + e] = acc;
     }
@@ -100,7 +107,8 @@ int launch_moe_router(const float* x, const float* router, const float* bias, in
                       float* weights, hipStream_t stream) {
     if (experts <= 0 || experts > 256 || top_k <= 0 || top_k > 8 || top_k > experts)
         return SFG_ERR_UNSUPPORTED;
-    const int per_block = static_cast<int>(256 / experts < kRouteTokens ? 256 / experts : kRouteTokens);
+    const int per_block = experts <= kRouteMaxExperts
+        ? kRouteTokens : static_cast<int>(256 / experts < kRouteTokens ? 256 / experts : kRouteTokens);
     const dim3 grid(static_cast<unsigned>((tokens + per_block - 1) / per_block));
     moe_router_kernel<<<grid, 256, 0, stream>>>(x, router, bias, static_cast<int>(tokens),
                                                 static_cast<int>(hidden), static_cast<int>(experts),

@@ -105,7 +105,8 @@ class DecoderExecutablePlan:
         self.lib = _abi.load()
 
     # ---- helpers -------------------------------------------------------
-    def _pack(self, name_rows: list, k: int, wdt: int, stream: int, key: str) -> None:
+    def _pack(self, name_rows: list, k: int, wdt: int, stream: int, key: str,
+              layout: int = _abi.LAYOUT_NK) -> None:
         """Pack a list of (fp32 [k][n] weight) blocks into one [sum n][k] matrix."""
         n_total = sum(int(w.shape[1]) for w in name_rows)
         if wdt == I8:
@@ -123,10 +124,12 @@ class DecoderExecutablePlan:
             if wdt == I8:
                 check(self.lib.sfg_hip_quantize_weight_v1(wd.data_ptr(), k, n,
                                                           dst.data_ptr() + row * k * esz,
-                                                          scales.data_ptr() + row * 4, stream))
+                                                          scales.data_ptr() + row * 4, layout,
+                                                          stream))
             else:
                 check(self.lib.sfg_hip_pack_weight_v1(wd.data_ptr(), k, n, n,
-                                                      dst.data_ptr() + row * k * esz, wdt, stream))
+                                                      dst.data_ptr() + row * k * esz, wdt, layout,
+                                                      stream))
             torch.cuda.current_stream(self.device).synchronize()
             del wd
             row += n
@@ -135,7 +138,7 @@ class DecoderExecutablePlan:
             self.t["s_" + key] = scales
 
     def _pack_experts(self, ws: list, k_dim: int, rows_per_expert: int, wdt: int, stream: int,
-                      key: str, experts: int) -> None:
+                      key: str, experts: int, layout: int = _abi.LAYOUT_NK) -> None:
         if wdt == I8:
             dst = torch.empty((experts, rows_per_expert, k_dim), dtype=torch.int8, device=self.device)
             scales = torch.empty((experts, rows_per_expert), dtype=torch.float32, device=self.device)
@@ -152,11 +155,11 @@ class DecoderExecutablePlan:
                 if wdt == I8:
                     check(self.lib.sfg_hip_quantize_weight_v1(
                         wd.data_ptr(), k_dim, n, dst.data_ptr() + base * k_dim * esz,
-                        scales.data_ptr() + base * 4, stream))
+                        scales.data_ptr() + base * 4, layout, stream))
                 else:
                     check(self.lib.sfg_hip_pack_weight_v1(
                         wd.data_ptr(), k_dim, n, n, dst.data_ptr() + base * k_dim * esz, wdt,
-                        stream))
+                        layout, stream))
                 torch.cuda.current_stream(self.device).synchronize()
                 del wd
                 row += n
@@ -182,17 +185,30 @@ def compile_decoder(config: DecoderConfig, data: DecoderData, device="cuda",
     t = plan.t
     t["rms1"] = _dev(data.rms1_weight, plan.device)
     t["rms2"] = _dev(data.rms2_weight, plan.device)
-    plan._pack([data.query_weight, data.key_weight, data.value_weight], H, wdt, stream, "w_qkv")
-    plan._pack([data.output_weight], H, wdt, stream, "w_o")
+    # One weight layout for the whole plan: fragment-tiled when every product
+    # runs on the decode (skinny) kernel, [N][K] otherwise.
+    layout = _abi.LAYOUT_NK
+    if wdt != F32:
+        ks = [H, I]
+        tiled = all(lib.sfg_hip_preferred_weight_layout_v1(cfg.rows, k, 0) == _abi.LAYOUT_TILED
+                    for k in ks)
+        if cfg.moe:
+            tiled = tiled and all(lib.sfg_hip_preferred_weight_layout_v1(
+                cfg.rows * cfg.top_k, k, 1) == _abi.LAYOUT_TILED for k in ks)
+        layout = _abi.LAYOUT_TILED if tiled else _abi.LAYOUT_NK
+    plan.layout = layout
+    plan._pack([data.query_weight, data.key_weight, data.value_weight], H, wdt, stream, "w_qkv",
+               layout)
+    plan._pack([data.output_weight], H, wdt, stream, "w_o", layout)
     if cfg.moe:
         t["router"] = _dev(data.router_weight, plan.device)
         if data.router_bias is not None:
             t["router_bias"] = _dev(data.router_bias, plan.device)
-        plan._pack_experts([data.w1, data.w3], H, 2 * I, wdt, stream, "w13", cfg.experts)
-        plan._pack_experts([data.w2], I, H, wdt, stream, "w2", cfg.experts)
+        plan._pack_experts([data.w1, data.w3], H, 2 * I, wdt, stream, "w13", cfg.experts, layout)
+        plan._pack_experts([data.w2], I, H, wdt, stream, "w2", cfg.experts, layout)
     else:
-        plan._pack([data.gate_weight, data.up_weight], H, wdt, stream, "w_gate_up")
-        plan._pack([data.down_weight], I, wdt, stream, "w_down")
+        plan._pack([data.gate_weight, data.up_weight], H, wdt, stream, "w_gate_up", layout)
+        plan._pack([data.down_weight], I, wdt, stream, "w_down", layout)
 
     # RoPE table [S][D/2][2], host-computed with the reference's expressions.
     table = np.empty((cfg.sequence, D // 2, 2), dtype=np.float32)
@@ -254,6 +270,7 @@ def compile_decoder(config: DecoderConfig, data: DecoderData, device="cuda",
     d.act_dtype, d.weight_dtype = act, wdt
     d.kv_splits = kv_splits
     d.use_routing_trace = int(data.routing_trace is not None)
+    d.weight_layout = layout
 
     w = plan.weights
     w.rms1, w.rms2 = _ptr(t["rms1"]), _ptr(t["rms2"])

@@ -72,3 +72,26 @@ def bf16_host(t):
     """device int16 bf16 bits -> fp32 numpy."""
     bits = host(t).view(np.uint16).astype(np.uint32) << 16
     return bits.view(np.float32)
+
+
+def tile_nk(w_nk, kind):
+    """NumPy restatement of SFG_LAYOUT_TILED for an [N][K] matrix.
+    bf16: [N/16][K/128][4 s][64 lanes][8], lane l holds row l % 16,
+          k = 32 s + 8 (l // 16) + j;
+    int8: [N/16][K/128][2 t][64 lanes][16], k = 32 (l // 16) + 16 t + j."""
+    n, k = w_nk.shape
+    lanes = np.arange(64)
+    r, g = lanes % 16, lanes // 16
+    if kind == "bf16":
+        s = np.arange(4)[:, None, None]
+        j = np.arange(8)[None, None, :]
+        kk = 32 * s + 8 * g[None, :, None] + j                      # [4][64][8]
+        rows = np.broadcast_to(r[None, :, None], kk.shape)
+    else:
+        t = np.arange(2)[:, None, None]
+        j = np.arange(16)[None, None, :]
+        kk = 32 * g[None, :, None] + 16 * t + j                     # [2][64][16]
+        rows = np.broadcast_to(r[None, :, None], kk.shape)
+    nt = np.arange(n // 16)[:, None, None, None, None] * 16
+    kc = np.arange(k // 128)[None, :, None, None, None] * 128
+    return np.ascontiguousarray(w_nk[nt + rows[None, None], kc + kk[None, None]])

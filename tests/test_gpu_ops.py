@@ -16,7 +16,7 @@ import oracle
 from schedforge_amd import _abi
 from schedforge_amd._abi import BF16, EPI_GLU_SILU_UP, EPI_NONE, EPI_RESIDUAL, EPI_SWIGLU, F32, I8
 
-from _helpers import bf16_dev, bf16_host, dev, host, stream
+from _helpers import bf16_dev, bf16_host, dev, host, stream, tile_nk
 
 pytestmark = pytest.mark.gpu
 
@@ -73,7 +73,7 @@ def test_rmsnorm_bf16_output_is_rne_of_f32(lib):
 
 # ------------------------------------------------------------------ GEMM
 def _gemm(lib, a_dev, a_dtype, b_dev, b_dtype, m, n, k, epi, c_dtype=F32, scales=None,
-          residual=None):
+          residual=None, layout=0):
     glu = epi in (EPI_SWIGLU, EPI_GLU_SILU_UP)
     c = torch.empty((m, n), dtype=torch.float32 if c_dtype == F32 else torch.int16, device="cuda")
     args = _abi.GemmArgs()
@@ -84,6 +84,7 @@ def _gemm(lib, a_dev, a_dtype, b_dev, b_dtype, m, n, k, epi, c_dtype=F32, scales
     args.residual = residual.data_ptr() if residual is not None else None
     args.ldr = n
     args.m, args.n, args.k, args.epilogue = m, n, k, epi
+    args.b_layout = layout
     wsb = lib.sfg_hip_gemm_workspace_v1(m, n, k)
     ws = torch.zeros(max(wsb, 256), dtype=torch.uint8, device="cuda")
     _abi.check(lib.sfg_hip_gemm_v1(ctypes.byref(args), ws.data_ptr(), ws.numel(), stream()))
@@ -103,7 +104,8 @@ def _ref_epilogue(acc, epi, n, residual=None):
 
 
 @pytest.mark.parametrize("m,n,k", [(16, 3072, 2048), (64, 1024, 512), (5, 256, 384),
-                                   (256, 512, 256), (512, 1024, 512), (300, 256, 128)])
+                                   (256, 512, 256), (512, 1024, 512), (300, 256, 128),
+                                   (1024, 512, 256), (1300, 256, 192), (2048, 1024, 1024)])
 def test_gemm_bf16_integer_operands_exact(lib, m, n, k):
     """Small-integer operands: every product and partial sum is exact in fp32,
     so any lane-layout or indexing mistake shows as a nonzero difference."""
@@ -114,7 +116,8 @@ def test_gemm_bf16_integer_operands_exact(lib, m, n, k):
     np.testing.assert_array_equal(host(c), a @ b.T)
 
 
-@pytest.mark.parametrize("m,n,k", [(16, 2048, 2048), (64, 512, 1024), (200, 512, 256)])
+@pytest.mark.parametrize("m,n,k", [(16, 2048, 2048), (64, 512, 1024), (200, 512, 256),
+                                   (1100, 256, 128)])
 def test_gemm_int8_integer_operands_exact(lib, m, n, k):
     rng = np.random.default_rng(m + n + k)
     a = rng.integers(-4, 5, size=(m, k)).astype(np.float32)
@@ -124,7 +127,7 @@ def test_gemm_int8_integer_operands_exact(lib, m, n, k):
     np.testing.assert_array_equal(host(c), a @ q.astype(np.float32).T)
 
 
-@pytest.mark.parametrize("m", [16, 64, 512])
+@pytest.mark.parametrize("m", [16, 64, 512, 1280])
 @pytest.mark.parametrize("epi", [EPI_NONE, EPI_RESIDUAL, EPI_SWIGLU, EPI_GLU_SILU_UP])
 def test_gemm_bf16_epilogues_match_oracle(lib, m, epi):
     n, k = 1024, 1024
@@ -178,10 +181,10 @@ def test_pack_and_quantize_match_oracle(lib):
     w[:, 3] = 0.0  # zero column -> scale 1
     wd = dev(w)
     dst = torch.empty((n, k), dtype=torch.int16, device="cuda")
-    _abi.check(lib.sfg_hip_pack_weight_v1(wd.data_ptr(), k, n, n, dst.data_ptr(), BF16, stream()))
+    _abi.check(lib.sfg_hip_pack_weight_v1(wd.data_ptr(), k, n, n, dst.data_ptr(), BF16, 0, stream()))
     q = torch.empty((n, k), dtype=torch.int8, device="cuda")
     s = torch.empty((n,), dtype=torch.float32, device="cuda")
-    _abi.check(lib.sfg_hip_quantize_weight_v1(wd.data_ptr(), k, n, q.data_ptr(), s.data_ptr(), stream()))
+    _abi.check(lib.sfg_hip_quantize_weight_v1(wd.data_ptr(), k, n, q.data_ptr(), s.data_ptr(), 0, stream()))
     _sync()
     np.testing.assert_array_equal(host(dst).view(np.uint16), oracle.to_bf16_bits(w.T))
     qr, sr = oracle.quantize_kn(w)
@@ -405,7 +408,7 @@ def test_moe_route_ties_go_to_lower_expert(lib):
 
 # ------------------------------------------------------------------ MoE experts + combine
 @pytest.mark.parametrize("wdt", ["bf16", "w8"])
-@pytest.mark.parametrize("T", [256, 16, 700])
+@pytest.mark.parametrize("T", [256, 16, 700, 1500])
 def test_moe_experts_and_combine_match_oracle(lib, wdt, T):
     H, I, E, k = 512, 256, 8, 2
     x = oracle.round_bf16(oracle.normal(111, 0, (T, H)))
@@ -438,7 +441,7 @@ def test_moe_experts_and_combine_match_oracle(lib, wdt, T):
                                           dev(tok).data_ptr(), w13d.data_ptr(),
                                           s13d.data_ptr() if s13d is not None else None,
                                           w2d.data_ptr(), s2d.data_ptr() if s2d is not None else None,
-                                          dt, act.data_ptr(), y.data_ptr(), T, H, I, E, k, None, 0,
+                                          dt, 0, act.data_ptr(), y.data_ptr(), T, H, I, E, k, None, 0,
                                           stream()))
     resid = oracle.normal(111, 5, (T, H))
     out = torch.empty((T, H), dtype=torch.float32, device="cuda")
@@ -460,3 +463,57 @@ def test_moe_experts_and_combine_match_oracle(lib, wdt, T):
     assert oracle.rel_error(host(out), ref) < tol
     # FFN part alone (residual removed) within the same tolerance
     assert oracle.rel_error(host(out) - resid, ffn) < tol
+
+
+# ------------------------------------------------------------------ fragment-tiled weights
+def test_pack_tiled_matches_numpy_order(lib):
+    k, n = 256, 48
+    w = oracle.normal(52, 2, (k, n), 0.02)
+    wd = dev(w)
+    dst = torch.empty((n * k,), dtype=torch.int16, device="cuda")
+    _abi.check(lib.sfg_hip_pack_weight_v1(wd.data_ptr(), k, n, n, dst.data_ptr(), BF16, 1, stream()))
+    q = torch.empty((n * k,), dtype=torch.int8, device="cuda")
+    s = torch.empty((n,), dtype=torch.float32, device="cuda")
+    _abi.check(lib.sfg_hip_quantize_weight_v1(wd.data_ptr(), k, n, q.data_ptr(), s.data_ptr(), 1, stream()))
+    _sync()
+    bits = oracle.to_bf16_bits(np.ascontiguousarray(w.T))
+    np.testing.assert_array_equal(host(dst).view(np.uint16).reshape(-1), tile_nk(bits, "bf16").reshape(-1))
+    qr, sr = oracle.quantize_kn(w)
+    np.testing.assert_array_equal(host(q), tile_nk(qr, "int8").reshape(-1))
+    np.testing.assert_array_equal(host(s), sr)
+
+
+@pytest.mark.parametrize("m,n,k", [(16, 3072, 2048), (64, 512, 1024), (7, 256, 384)])
+def test_gemm_tiled_integer_operands_exact(lib, m, n, k):
+    rng = np.random.default_rng(m * 3 + n)
+    a = rng.integers(-3, 4, size=(m, k)).astype(np.float32)
+    b = rng.integers(-3, 4, size=(n, k)).astype(np.float32)
+    bt = tile_nk(oracle.to_bf16_bits(b), "bf16").view(np.int16)
+    c = _gemm(lib, bf16_dev(a), BF16, dev(bt), BF16, m, n, k, EPI_NONE, layout=1)
+    np.testing.assert_array_equal(host(c), a @ b.T)
+    q = rng.integers(-127, 128, size=(n, k)).astype(np.int8)
+    c8 = _gemm(lib, bf16_dev(a), BF16, dev(tile_nk(q, "int8")), I8, m, n, k, EPI_NONE,
+               scales=dev(np.ones(n, np.float32)), layout=1)
+    np.testing.assert_array_equal(host(c8), a @ q.astype(np.float32).T)
+
+
+@pytest.mark.parametrize("epi", [EPI_RESIDUAL, EPI_SWIGLU, EPI_GLU_SILU_UP])
+def test_gemm_tiled_epilogues_match_nk(lib, epi):
+    m, n, k = 16, 512, 1024
+    glu = epi in (EPI_SWIGLU, EPI_GLU_SILU_UP)
+    a = oracle.round_bf16(oracle.normal(23, 0, (m, k)))
+    b = oracle.normal(23, 2, (2 * n if glu else n, k), 0.02)
+    res = oracle.normal(23, 5, (m, n))
+    rd = dev(res) if epi == EPI_RESIDUAL else None
+    nk = _gemm(lib, bf16_dev(a), BF16, bf16_dev(b), BF16, m, n, k, epi, residual=rd)
+    tl = _gemm(lib, bf16_dev(a), BF16, dev(tile_nk(oracle.to_bf16_bits(b), "bf16").view(np.int16)),
+               BF16, m, n, k, epi, residual=rd, layout=1)
+    # same products, same per-wave k ranges: identical up to summation order inside a wave
+    assert oracle.rel_error(host(tl), host(nk)) < 1e-5
+
+
+def test_gemm_tiled_rejects_prefill_shapes(lib):
+    a = torch.zeros((2048, 256), dtype=torch.int16, device="cuda")
+    b = torch.zeros((256 * 256,), dtype=torch.int16, device="cuda")
+    with pytest.raises(ValueError):
+        _gemm(lib, a, BF16, b, BF16, 2048, 256, 256, EPI_NONE, layout=1)
