@@ -16,13 +16,16 @@ namespace sfg {
 
 // One thread per (token, expert) chain; the block then runs softmax + top-k for
 // its tokens with one thread per token.  E <= 256, top_k <= 8.  The chain runs
-// over features in order (bit-identical to a sequential fp32 FMA loop).  Its
-// operands are staged through LDS in 512-feature chunks, double-buffered: the
-// whole workgroup loads chunk c + 1 (many loads in flight) while each thread
-// runs its chain over chunk c from LDS.
+// over features in order (bit-identical to a sequential fp32 FMA loop).
+// Operands are staged through LDS in 512-feature chunks (x as [token][f], the
+// router transposed to [e][f]) and fed to the chain from registers 16 features
+// at a time, the next 16 already in flight; the next chunk's global loads are
+// held in registers while the current chunk's chain runs.
 constexpr int kRouteChunk = 512;
 constexpr int kRouteTokens = 4;        // tokens per workgroup
-constexpr int kRouteMaxExperts = 16;   // LDS sized for E <= 16 (larger E: direct path)
+constexpr int kRouteMaxExperts = 8;    // staged path; larger E uses the direct chain
+constexpr int kRouteBlock = 16;        // chain operands per register block
+constexpr int kRouteLoads = (kRouteTokens * kRouteChunk + kRouteChunk * kRouteMaxExperts) / 256 / 4;
 
 __global__ __launch_bounds__(256) void moe_router_kernel(
     const float* __restrict__ x, const float* __restrict__ router, const float* __restrict__ bias,
@@ -30,8 +33,8 @@ __global__ __launch_bounds__(256) void moe_router_kernel(
     float* __restrict__ weights) {
     __shared__ float logits[256];
     __shared__ __attribute__((aligned(16))) float sx[2][kRouteTokens][kRouteChunk];
-    __shared__ __attribute__((aligned(16))) float sw[2][kRouteChunk * kRouteMaxExperts];
-    const bool staged = experts <= kRouteMaxExperts;
+    __shared__ __attribute__((aligned(16))) float sw[2][kRouteMaxExperts][kRouteChunk];
+    const bool staged = experts <= kRouteMaxExperts && (hidden % kRouteChunk) == 0;
     const int per_block = staged ? kRouteTokens : min(kRouteTokens, 256 / experts);
     const int t_local = threadIdx.x / experts;
     const int e = threadIdx.x % experts;
@@ -40,27 +43,78 @@ __global__ __launch_bounds__(256) void moe_router_kernel(
     const bool active = t_local < per_block && t < tokens;
     float acc = 0.f;
     if (staged) {
-        auto stage = [&](int buf, int f0) {
-            const int fc = min(kRouteChunk, hidden - f0);
-            for (int i = threadIdx.x; i < per_block * fc; i += 256) {
-                const int tt = i / fc, ff = i % fc;
-                sx[buf][tt][ff] = (t0 + tt < tokens) ? x[static_cast<int64_t>(t0 + tt) * hidden + f0 + ff] : 0.f;
+        // Each thread moves kRouteLoads float4 per chunk: x rows first, then the
+        // router slice [f][e] (contiguous in memory) scattered to sw[e][f].
+        const int x_vecs = kRouteTokens * kRouteChunk / 4;
+        const int w_vecs = kRouteChunk * experts / 4;
+        float4 reg[kRouteLoads];
+        auto fetch = [&](int f0) {
+#pragma unroll
+            for (int i = 0; i < kRouteLoads; ++i) {
+                const int v = threadIdx.x + 256 * i;
+                float4 val = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (v < x_vecs) {
+                    const int tt = v / (kRouteChunk / 4), f4 = v % (kRouteChunk / 4);
+                    if (t0 + tt < tokens)
+                        val = *reinterpret_cast<const float4*>(x + static_cast<int64_t>(t0 + tt) * hidden + f0 + 4 * f4);
+                } else if (v - x_vecs < w_vecs) {
+                    val = *reinterpret_cast<const float4*>(router + static_cast<int64_t>(f0) * experts + 4 * (v - x_vecs));
+                }
+                reg[i] = val;
             }
-            for (int i = threadIdx.x; i < fc * experts; i += 256)
-                sw[buf][i] = router[static_cast<int64_t>(f0) * experts + i];
         };
-        stage(0, 0);
+        auto stash = [&](int buf) {
+#pragma unroll
+            for (int i = 0; i < kRouteLoads; ++i) {
+                const int v = threadIdx.x + 256 * i;
+                if (v < x_vecs) {
+                    const int tt = v / (kRouteChunk / 4), f4 = v % (kRouteChunk / 4);
+                    *reinterpret_cast<float4*>(&sx[buf][tt][4 * f4]) = reg[i];
+                } else if (v - x_vecs < w_vecs) {
+                    const int flat = 4 * (v - x_vecs);  // = f * experts + e
+                    const float vals[4] = {reg[i].x, reg[i].y, reg[i].z, reg[i].w};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) sw[buf][(flat + j) % experts][(flat + j) / experts] = vals[j];
+                }
+            }
+        };
+        fetch(0);
+        stash(0);
         __syncthreads();
         int buf = 0;
         for (int f0 = 0; f0 < hidden; f0 += kRouteChunk) {
-            if (f0 + kRouteChunk < hidden) stage(buf ^ 1, f0 + kRouteChunk);
-            const int fc = min(kRouteChunk, hidden - f0);
+            const bool more = f0 + kRouteChunk < hidden;
+            if (more) fetch(f0 + kRouteChunk);
             if (active) {
                 const float* xr = sx[buf][t_local];
-                const float* wr = sw[buf] + e;
-#pragma unroll 16
-                for (int f = 0; f < fc; ++f) acc = __builtin_fmaf(xr[f], wr[f * experts], acc);
+                const float* wr = sw[buf][e];
+                float xa[kRouteBlock], wa[kRouteBlock], xb[kRouteBlock], wb[kRouteBlock];
+#pragma unroll
+                for (int j = 0; j < kRouteBlock; j += 4) {
+                    *reinterpret_cast<float4*>(&xa[j]) = *reinterpret_cast<const float4*>(xr + j);
+                    *reinterpret_cast<float4*>(&wa[j]) = *reinterpret_cast<const float4*>(wr + j);
+                }
+                for (int f = 0; f < kRouteChunk; f += 2 * kRouteBlock) {
+#pragma unroll
+                    for (int j = 0; j < kRouteBlock; j += 4) {
+                        *reinterpret_cast<float4*>(&xb[j]) = *reinterpret_cast<const float4*>(xr + f + kRouteBlock + j);
+                        *reinterpret_cast<float4*>(&wb[j]) = *reinterpret_cast<const float4*>(wr + f + kRouteBlock + j);
+                    }
+#pragma unroll
+                    for (int j = 0; j < kRouteBlock; ++j) acc = __builtin_fmaf(xa[j], wa[j], acc);
+                    if (f + 2 * kRouteBlock < kRouteChunk) {
+#pragma unroll
+                        for (int j = 0; j < kRouteBlock; j += 4) {
+                            *reinterpret_cast<float4*>(&xa[j]) = *reinterpret_cast<const float4*>(xr + f + 2 * kRouteBlock + j);
+                            *reinterpret_cast<float4*>(&wa[j]) = *reinterpret_cast<const float4*>(wr + f + 2 * kRouteBlock + j);
+                        }
+                    }
+#pragma unroll
+                    for (int j = 0; j < kRouteBlock; ++j) acc = __builtin_fmaf(xb[j], wb[j], acc);
+                }
             }
+            __syncthreads();
+            if (more) stash(buf ^ 1);
             __syncthreads();
             buf ^= 1;
         }
