@@ -1,4 +1,4 @@
-"""Build libsfg_hip.so (gfx950) in-tree with hipcc.
+"""Build libsfg_hip.so (gfx950) and the C++20 host runtime in-tree.
 
 Every translation unit under csrc/ is compiled to an object in parallel, then
 linked into schedforge_amd/lib/libsfg_hip.so.  Flags:
@@ -6,6 +6,9 @@ linked into schedforge_amd/lib/libsfg_hip.so.  Flags:
   -Xclang -target-feature -Xclang -packed-fp32-ops
                                  no packed-fp32 VALU ops in device code
   -O3 -std=c++20 -fPIC
+The host runtime under runtime/ is plain C++20 (g++, the reference's own
+toolchain) against the HIP runtime API: schedforge_amd/lib/libsfg_decoder.so
+and the driver schedforge_amd/bin/sfg-decoder.
 """
 from __future__ import annotations
 
@@ -21,6 +24,15 @@ CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIBDIR = PKG / "lib"
 LIB = LIBDIR / "libsfg_hip.so"
+RUNTIME = PKG / "runtime"
+BINDIR = PKG / "bin"
+RUNTIME_LIB = LIBDIR / "libsfg_decoder.so"
+DECODER_CLI = BINDIR / "sfg-decoder"
+ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+CXX = os.environ.get("CXX", "g++")
+HOST_FLAGS = ["-std=c++20", "-O2", "-Wall", "-Wextra", "-fPIC", "-D__HIP_PLATFORM_AMD__",
+              f"-I{PKG.parent / 'include'}", f"-I{ROCM / 'include'}"]
+HIP_LINK = [f"-L{ROCM / 'lib'}", "-lamdhip64", f"-Wl,-rpath,{ROCM / 'lib'}", "-ldl", "-pthread"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -50,6 +62,37 @@ def _compile(src: Path) -> Path:
     return obj
 
 
+def _run(cmd: list, what: str) -> None:
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"{what} failed:\n{proc.stderr}")
+    if proc.stderr.strip():
+        sys.stderr.write(proc.stderr)
+
+
+def build_runtime() -> Path:
+    """libsfg_decoder.so + sfg-decoder from runtime/*.cpp."""
+    BUILD.mkdir(exist_ok=True)
+    BINDIR.mkdir(exist_ok=True)
+    lib_obj = BUILD / "sfg_decoder.o"
+    cli_obj = BUILD / "sfg_decoder_cli.o"
+    with cf.ThreadPoolExecutor(max_workers=2) as pool:
+        jobs = [pool.submit(_run, [CXX, *HOST_FLAGS, "-c", str(RUNTIME / "sfg_decoder.cpp"), "-o",
+                                   str(lib_obj)], "g++ sfg_decoder.cpp"),
+                pool.submit(_run, [CXX, *HOST_FLAGS, "-c", str(RUNTIME / "sfg_decoder_cli.cpp"), "-o",
+                                   str(cli_obj)], "g++ sfg_decoder_cli.cpp")]
+        for j in jobs:
+            j.result()
+    tmp = RUNTIME_LIB.with_suffix(".so.tmp")
+    _run([CXX, "-shared", "-o", str(tmp), str(lib_obj), *HIP_LINK], "link libsfg_decoder.so")
+    os.replace(tmp, RUNTIME_LIB)
+    tmp_cli = DECODER_CLI.with_suffix(".tmp")
+    _run([CXX, "-o", str(tmp_cli), str(cli_obj), f"-L{LIBDIR}", "-lsfg_decoder",
+          "-Wl,-rpath,$ORIGIN/../lib", *HIP_LINK], "link sfg-decoder")
+    os.replace(tmp_cli, DECODER_CLI)
+    return DECODER_CLI
+
+
 def build(verbose: bool = False) -> Path:
     if shutil.which(HIPCC) is None and not Path(HIPCC).exists():
         raise RuntimeError(f"hipcc not found at {HIPCC}")
@@ -65,8 +108,9 @@ def build(verbose: bool = False) -> Path:
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stderr}")
     os.replace(tmp, LIB)
+    build_runtime()
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB}, {RUNTIME_LIB} and {DECODER_CLI}")
     return LIB
 
 

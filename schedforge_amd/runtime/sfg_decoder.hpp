@@ -1,0 +1,223 @@
+// C++20 host runtime for the gfx950 decoder-layer backend.
+//
+// The reference's operator boundary for this path is the public C++ API of
+// include/schedforge/decoder_compiler.h:
+//   DecoderCompiler::compile(graph, config, data, options)   (205-214)
+//   execute_decoder_layer(plan, data, warmup, repetitions)    (220-223)
+// This header restates that API with the same type and field names for a plan
+// whose target is an MI355X.  Everything below the plan is libsfg_hip.so's C ABI
+// (include/sfg_hip.h), loaded with dlopen + dlsym and validated against its
+// metadata string before the first call, as the reference's AOT loader does
+// (src/aot_runtime.cpp:152-196, 259).
+//
+// Differences from the reference, all additive:
+//   - DecoderConfig::precision selects fp32, bf16 or int8-weight plans (the
+//     reference runs those as separate entry points).
+//   - DecoderData carries an optional router bias and a paged-KV page table.
+//   - The StableHLO graph argument of compile() is absent: the GPU target
+//     executes the fixed decoder-layer structure the reference's fusion pass
+//     checks for (decoder_compiler.cpp:531-533).
+//   - execute_decoder_layer's max_error compares with a caller-supplied
+//     expected output (the reference calls its scalar CPU layer there,
+//     decoder_compiler.cpp:690); without one it is NaN.
+// Errors follow the reference's convention: configuration, shape and guard
+// violations throw std::invalid_argument; device and resource failures throw
+// std::runtime_error.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <filesystem>
+#include <memory>
+#include <mutex>
+#include <optional>
+#include <string>
+#include <vector>
+
+#include "sfg_hip.h"
+
+namespace schedforge::hip {
+
+enum class DecoderFFNKind { Dense, MoE };
+// Arithmetic of a plan: all-fp32; bf16 weights and activations; int8
+// per-output-channel weights with bf16 activations.
+enum class DecoderPrecision { F32, BF16, W8 };
+
+// decoder_compiler.h:17-32 (+ precision and page_tokens).
+struct DecoderConfig {
+    int batch = 1;
+    int sequence = 16;
+    int hidden = 64;
+    int intermediate = 128;
+    int query_heads = 4;
+    int kv_heads = 2;
+    int head_dim = 16;
+    float rms_epsilon = 1.0e-5F;
+    float rope_theta = 10000.0F;
+    bool causal = true;
+    DecoderFFNKind ffn = DecoderFFNKind::Dense;
+    int experts = 4;
+    int top_k = 2;
+    int context_sequence = 0;
+    DecoderPrecision precision = DecoderPrecision::F32;
+    int page_tokens = 16;
+
+    int rows() const { return batch * sequence; }
+    int kv_width() const { return kv_heads * head_dim; }
+    bool decode() const { return context_sequence > 0; }
+    int pages_per_sequence() const { return (context_sequence + page_tokens - 1) / page_tokens; }
+};
+
+// Throws std::invalid_argument as validate() does (decoder_compiler.cpp:26-39).
+void validate(const DecoderConfig& config);
+
+// moe_compiler.h:51-59.
+struct RoutingTrace {
+    int tokens = 0;
+    int experts = 0;
+    int top_k = 0;
+    std::vector<int> expert_ids;        // [tokens][top_k]
+    std::vector<float> expert_weights;  // [tokens][top_k]
+    std::vector<int> counts;            // [experts]
+};
+
+// moe_compiler.h:79-85.
+struct MoeData {
+    std::vector<float> input;
+    std::vector<float> router_weight;  // [H][E]
+    std::vector<float> w1;             // [E][H][I]
+    std::vector<float> w3;             // [E][H][I]
+    std::vector<float> w2;             // [E][I][H]
+};
+
+// decoder_compiler.h:34-49: host fp32 tensors in the reference's layouts
+// ([K][N] weights, [B][Hkv][ctx][D] cached K/V).
+struct DecoderData {
+    std::vector<float> input;  // [B*S][H]
+    std::vector<float> rms1_weight;
+    std::vector<float> query_weight;
+    std::vector<float> key_weight;
+    std::vector<float> value_weight;
+    std::vector<float> output_weight;
+    std::vector<float> rms2_weight;
+    std::vector<float> gate_weight;
+    std::vector<float> up_weight;
+    std::vector<float> down_weight;
+    MoeData moe;
+    std::vector<float> cached_key;
+    std::vector<float> cached_value;
+    std::optional<RoutingTrace> routing_trace;
+    std::vector<float> router_bias;              // [E], empty: none
+    std::optional<std::vector<int32_t>> page_table;  // [B][pages_per_seq]; default identity
+};
+
+// decoder_compiler.h:133-139, reduced to what a GPU plan uses.
+struct DecoderCompileOptions {
+    int device = 0;
+    int kv_splits = 0;             // decode split-KV count; <= 0 chooses per shape
+    std::filesystem::path library; // libsfg_hip.so; empty: beside this library
+};
+
+// decoder_compiler.h:67-74.
+struct DecoderConstant {
+    std::string name;
+    std::vector<int> logical_shape;
+    std::vector<int> packed_shape;
+    std::string layout;
+    std::size_t bytes = 0;
+    std::string dump() const;
+};
+
+// decoder_compiler.h:76-80.
+struct DecoderMemoryPlan {
+    std::size_t naive_bytes = 0;      // every intermediate materialised separately
+    std::size_t workspace_bytes = 0;  // the layer's planned workspace
+    std::size_t constant_bytes = 0;   // packed weights, KV pools, tables
+    std::string dump() const;
+};
+
+// decoder_compiler.h:119-130.
+struct DecoderBenchmarkResult {
+    double milliseconds = 0.0;
+    double attention_milliseconds = 0.0;
+    double projection_milliseconds = 0.0;
+    double norm_rope_milliseconds = 0.0;
+    double ffn_milliseconds = 0.0;
+    double residual_milliseconds = 0.0;
+    double dispatch_overhead_milliseconds = 0.0;
+    double tokens_per_second = 0.0;
+    double max_error = 0.0;
+    std::vector<float> output;
+};
+
+class SfgHipLibrary;
+struct DeviceBuffer;
+
+// decoder_compiler.h:97-117: an immutable, device-resident plan.  Owns the
+// packed weights, the paged KV pools, the RoPE table and the workspace.
+class DecoderExecutablePlan {
+public:
+    DecoderConfig config;
+    std::vector<DecoderConstant> constants;
+    DecoderMemoryPlan memory;
+    std::string hardware;
+    std::string library_metadata;
+    int weight_layout = SFG_LAYOUT_NK;
+    int kv_splits = 0;
+    double compile_milliseconds = 0.0;
+
+    DecoderExecutablePlan();
+    ~DecoderExecutablePlan();
+    DecoderExecutablePlan(DecoderExecutablePlan&&) noexcept;
+    DecoderExecutablePlan& operator=(DecoderExecutablePlan&&) noexcept;
+    DecoderExecutablePlan(const DecoderExecutablePlan&) = delete;
+    DecoderExecutablePlan& operator=(const DecoderExecutablePlan&) = delete;
+
+    std::string dump() const;
+    void save(const std::filesystem::path& path) const;
+
+    struct Device;
+    std::unique_ptr<Device> device;  // buffers, descriptor, stream
+};
+
+class DecoderCompiler {
+public:
+    DecoderExecutablePlan compile(const DecoderConfig& config, const DecoderData& data,
+                                  DecoderCompileOptions options = {}) const;
+};
+
+// The reference's decoder_compiler.cpp:675-692: warmup, timed repetitions,
+// median by time, tokens/s = rows * 1000 / ms, per-stage times from device
+// events.  `expected` (optional) fills max_error as max |output - expected|
+// (runtime.cpp:628-635).
+DecoderBenchmarkResult execute_decoder_layer(const DecoderExecutablePlan& plan,
+                                             const DecoderData& data, int warmup = 1,
+                                             int repetitions = 5,
+                                             const std::vector<float>* expected = nullptr);
+
+// Seeded synthetic inputs: a counter-based generator (SplitMix64 keyed by
+// seed and tensor id, Box-Muller in double) with activations N(0,1), weights
+// N(0,0.02), norm gains 1, cached K/V N(0,1), router bias N(0,router_bias_std)
+// when positive, and a seeded Fisher-Yates page permutation.  bf16 plans round
+// inputs, weights and the KV cache to bf16; int8 plans round inputs and the
+// KV cache.  Tensor ids: x 0, rms1 1, Wq 2, Wk 3, Wv 4, Wo 5, rms2 6, Wg 7,
+// Wu 8, Wd 9, router 10, router bias 11, W1 12, W3 13, W2 14, K 15, V 16,
+// page permutation 17.
+DecoderData make_decoder_data(const DecoderConfig& config, std::uint64_t seed,
+                              float router_bias_std = 0.0F);
+
+// The five benchmark configurations by name ("c1" ... "c5"), with their
+// seeds (1000 c) and router bias std.
+struct NamedDecoderConfig {
+    DecoderConfig config;
+    std::uint64_t seed = 0;
+    float router_bias_std = 0.0F;
+};
+NamedDecoderConfig named_decoder_config(const std::string& name);
+
+std::string decoder_ffn_name(DecoderFFNKind kind);
+std::string decoder_precision_name(DecoderPrecision precision);
+double max_abs_error(const std::vector<float>& a, const std::vector<float>& b);
+float round_to_bf16(float value);
+
+}  // namespace schedforge::hip
