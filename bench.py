@@ -31,10 +31,20 @@ from pathlib import Path
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
-# Kernel traffic per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
-# (KiB per dispatch), scaled by the copy-kernel calibration factor; see the
-# profiles/ summaries.  None until measured for a workload.
-MEASURED_TRAFFIC = {}
+# HBM traffic per launch of the roofline kernel, from two rocprofv3 --pmc runs
+# of this script (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch) with
+# --copy-calibration 1024.  The calibration kernel reads 1 GiB and writes 1 GiB;
+# the counters read 524311.8 KiB and 1048576.0 KiB for it, so FETCH_SIZE is
+# scaled by 1048576 / 524311.8 and WRITE_SIZE by 1.  Summaries:
+# profiles/pmc_traffic_c2.md, profiles/pmc_traffic_c5.md.
+PMC_FETCH_SCALE = 1048576.0 / 524311.8
+PMC_WRITE_SCALE = 1.0
+PMC_ATTENTION_KIB = {          # attn_decode_split_kernel: (FETCH_SIZE, WRITE_SIZE)
+    "c2": (66117.8, 1088.0),
+    "c5": (1049963.6, 2112.0),
+}
+MEASURED_TRAFFIC = {k: round((f * PMC_FETCH_SCALE + w * PMC_WRITE_SCALE) * 1024)
+                    for k, (f, w) in PMC_ATTENTION_KIB.items()}
 
 
 def parse():
@@ -46,6 +56,10 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="bound on the CPU-baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                   help="before warmup, stream MIB MiB through one elementwise kernel "
+                        "(reads MIB, writes MIB): the known-size reference for the "
+                        "FETCH_SIZE / WRITE_SIZE counter runs")
     return p.parse_args()
 
 
@@ -157,6 +171,16 @@ def main():
     torch.cuda.empty_cache()
     out = torch.empty((cfg.rows, cfg.hidden), dtype=torch.float32, device=device)
     stream = torch.cuda.current_stream()
+
+    if args.copy_calibration > 0:
+        n = args.copy_calibration * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=device)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        torch.mul(src, 1.0, out=dst)   # one launch: n*4 bytes read, n*4 written
+        torch.cuda.synchronize()
+        del src, dst
+        torch.cuda.empty_cache()
 
     for _ in range(args.warmup):
         run_layer(plan, x, out)
