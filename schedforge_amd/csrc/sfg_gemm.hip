@@ -19,6 +19,9 @@
 //    tiles on the VALU.
 #include "sfg_kernels.hpp"
 
+#include <cstdlib>
+#include <cstring>
+
 namespace sfg {
 
 namespace {
@@ -615,6 +618,233 @@ __global__ __launch_bounds__(256) void gemm_mfma256_kernel(TiledArgs p, int tile
 }
 
 // ===========================================================================
+// Large-M MFMA GEMM, third generation (bf16 operands): BM x BN output tile per
+// workgroup, BK = 64, four waves in a 2 x 2 grid, each owning a (BM/2) x (BN/2)
+// block of v_mfma_f32_32x32x16_bf16 tiles (accumulators in the AccVGPRs).
+// Operand slabs go from global memory straight into LDS
+// (global_load_lds_dwordx4): one wave instruction fills one contiguous 1 KB
+// block, i.e. 8 rows x 64 k of bf16.  Rows are 128 B; the 16-B chunk c of row
+// r sits in slot c ^ (r & 7) -- the loading lane picks the chunk it fetches so
+// that its fixed destination slot holds the swizzled one -- so the fragment
+// reads of 8 consecutive rows touch 8 different slots.  Two LDS stages: the
+// loads of slab k+1 are issued before the MFMAs of slab k and waited for at
+// the barrier that ends slab k.  Each stage lives in its own __shared__
+// array, so the compiler can tell the in-flight loads from the stage being
+// read and does not wait for them before the fragment reads.
+// For GLU epilogues the B tile interleaves 32-row blocks of gate and up rows
+// (block 2j: gate columns j*32.., block 2j+1: the same up columns), so every
+// lane holds matching gate and up accumulators.
+// ===========================================================================
+constexpr int kDK = 64;
+
+// 16 bytes per lane from global memory into LDS at lds_block + 16 * lane
+// (lds_block is wave-uniform).  A __device__ function, not a lambda: the
+// builtin exists on the device side only.
+__device__ __forceinline__ void lds_dma16(const uint16_t* src, uint16_t* lds_block) {
+    __builtin_amdgcn_global_load_lds(src, lds_block, 16, 0, 0);
+}
+
+__device__ __forceinline__ void wait_vmem_all() {
+    // s_waitcnt vmcnt(0), other counters untouched (gfx9 encoding: expcnt 7,
+    // lgkmcnt 15).  LDS DMA completes through vmcnt.
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+}
+
+template <int BM, int BN, int EPI>
+__global__ __launch_bounds__(256) void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
+    constexpr bool kGlu = EpiTraits<EPI>::glu;
+    constexpr int WM = BM / 64, WN = BN / 64;        // 32x32 tiles per wave
+    constexpr int kLoadsA = BM / 32, kLoadsB = BN / 32;  // 1 KB blocks per wave per stage
+    static_assert(!kGlu || WN % 2 == 0, "GLU tiles pair gate and up blocks");
+    __shared__ __attribute__((aligned(1024))) uint16_t sA0[BM * kDK];
+    __shared__ __attribute__((aligned(1024))) uint16_t sA1[BM * kDK];
+    __shared__ __attribute__((aligned(1024))) uint16_t sB0[BN * kDK];
+    __shared__ __attribute__((aligned(1024))) uint16_t sB1[BN * kDK];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    constexpr int kOutCols = kGlu ? BN / 2 : BN;
+
+    int g = 0;
+    int64_t rb = 0, re = p.m;
+    int64_t tm, tn;
+    if (p.offsets) {
+        tn = blockIdx.x;
+        int64_t t = blockIdx.y;
+        auto bound = [&](int e) {
+            return min(max(static_cast<int64_t>(p.offsets[e]), int64_t(0)), p.m);
+        };
+        g = -1;
+        for (int e = 0; e < p.groups; ++e) {
+            const int64_t rows = max(bound(e + 1) - bound(e), int64_t(0));
+            const int64_t tiles = (rows + BM - 1) / BM;
+            if (t < tiles) { g = e; break; }
+            t -= tiles;
+        }
+        if (g < 0) return;
+        rb = bound(g);
+        re = max(bound(g + 1), rb);
+        tm = t;
+    } else {
+        // XCD-aware order: the dispatcher deals consecutive workgroup ids to
+        // the 8 XCDs in turn, so hand each XCD a contiguous run of tiles and
+        // walk them in groups of 8 M-tiles (A and B tiles shared in one L2).
+        const int64_t total = static_cast<int64_t>(tiles_m) * tiles_n;
+        const int64_t i = blockIdx.x;
+        const int64_t full = total - total % 8;
+        int64_t L = i;
+        if (i < full) L = (i % 8) * (full / 8) + i / 8;
+        constexpr int64_t kGroupM = 8;
+        const int64_t group = L / (kGroupM * tiles_n);
+        const int64_t first_m = group * kGroupM;
+        const int64_t gsize = min(static_cast<int64_t>(tiles_m) - first_m, kGroupM);
+        const int64_t in_group = L % (kGroupM * tiles_n);
+        tm = first_m + in_group % gsize;
+        tn = in_group / gsize;
+    }
+    const int64_t row0 = rb + tm * BM;
+    if (row0 >= re) return;
+    const int64_t ncol0 = tn * kOutCols;
+    const int64_t bgroup = static_cast<int64_t>(g) * p.b_group_stride;
+    const float* scales = p.scales ? p.scales + static_cast<int64_t>(g) * p.s_group_stride : nullptr;
+
+    // Load assignment: wave instruction i fills block (i * 4 + wave); lane l
+    // covers row 8 * block + (l >> 3) and destination slot (l & 7), fetching
+    // the chunk (l & 7) ^ (l >> 3).  Rows past the tile's end read a valid
+    // row instead (their results are never stored).
+    const int lrow = lane >> 3;
+    const int chunk8 = ((lane & 7) ^ lrow) * 8;
+    const uint16_t* a_src[kLoadsA];
+#pragma unroll
+    for (int i = 0; i < kLoadsA; ++i) {
+        const int64_t r = row0 + (i * 4 + wave) * 8 + lrow;
+        int64_t src = r < re ? r : row0;
+        if (p.a_rows) src = p.a_rows[src];
+        if (src < 0 || src >= p.a_rows_limit) src = 0;
+        a_src[i] = p.a + src * p.lda + chunk8;
+    }
+    const uint16_t* bbase = static_cast<const uint16_t*>(p.b) + bgroup;
+    const uint16_t* b_src[kLoadsB];
+#pragma unroll
+    for (int i = 0; i < kLoadsB; ++i) {
+        const int local = (i * 4 + wave) * 8 + lrow;
+        int64_t brow;
+        if (kGlu) {
+            const int block = local >> 5;
+            const int64_t col = ncol0 + (block >> 1) * 32 + (local & 31);
+            brow = col < p.n ? ((block & 1) ? p.n + col : col) : 0;
+        } else {
+            const int64_t col = ncol0 + local;
+            brow = col < p.n ? col : 0;
+        }
+        b_src[i] = bbase + brow * p.ldb + chunk8;
+    }
+
+    auto issue = [&](uint16_t* da, uint16_t* db, int64_t k0) {
+#pragma unroll
+        for (int i = 0; i < kLoadsA; ++i)
+            lds_dma16(a_src[i] + k0, da + (i * 4 + wave) * 512);
+#pragma unroll
+        for (int i = 0; i < kLoadsB; ++i)
+            lds_dma16(b_src[i] + k0, db + (i * 4 + wave) * 512);
+    };
+
+    floatx16 acc[WM][WN];
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    const int l32 = lane & 31;
+    const int khalf = lane >> 5;
+    const int swz = lane & 7;  // == row & 7 for every fragment row this lane reads
+    // One slab: 4 k-steps of 16; the fragments of step kk+1 are read from LDS
+    // while the MFMAs of step kk run.
+    auto compute = [&](const uint16_t* A, const uint16_t* B) {
+        bf16x8 af[2][WM], bfr[2][WN];
+        auto load = [&](int kk, int buf) {
+            const int slot = ((kk * 2 + khalf) ^ swz) * 8;
+#pragma unroll
+            for (int i = 0; i < WM; ++i)
+                af[buf][i] = as_bf16x8(*reinterpret_cast<const uint4*>(
+                    &A[(wm * (BM / 2) + i * 32 + l32) * kDK + slot]));
+#pragma unroll
+            for (int j = 0; j < WN; ++j)
+                bfr[buf][j] = as_bf16x8(*reinterpret_cast<const uint4*>(
+                    &B[(wn * (BN / 2) + j * 32 + l32) * kDK + slot]));
+        };
+        load(0, 0);
+#pragma unroll
+        for (int kk = 0; kk < kDK / 16; ++kk) {
+            if (kk + 1 < kDK / 16) load(kk + 1, (kk + 1) & 1);
+#pragma unroll
+            for (int i = 0; i < WM; ++i)
+#pragma unroll
+                for (int j = 0; j < WN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[kk & 1][i], bfr[kk & 1][j],
+                                                                        acc[i][j], 0, 0, 0);
+        }
+    };
+
+    // Two-stage ring over slab pairs; an odd last slab runs after the loop.
+    const int64_t slabs = p.k / kDK;
+    issue(sA0, sB0, 0);
+    wait_vmem_all();
+    __syncthreads();
+    int64_t kt = 0;
+    for (; kt + 2 <= slabs; kt += 2) {
+        issue(sA1, sB1, (kt + 1) * kDK);
+        compute(sA0, sB0);
+        wait_vmem_all();
+        __syncthreads();
+        if (kt + 2 < slabs) issue(sA0, sB0, (kt + 2) * kDK);
+        compute(sA1, sB1);
+        wait_vmem_all();
+        __syncthreads();
+    }
+    if (kt < slabs) compute(sA0, sB0);
+
+    // Epilogue: 32x32 D layout, lane holds column (lane & 31) and rows
+    // 8 (r / 4) + 4 (lane >> 5) + (r % 4).
+#pragma unroll
+    for (int i = 0; i < WM; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int64_t row = row0 + wm * (BM / 2) + i * 32 + 8 * (r >> 2) + 4 * khalf + (r & 3);
+            if (row >= re) continue;
+            if (kGlu) {
+#pragma unroll
+                for (int j = 0; j < WN; j += 2) {
+                    const int block = wn * (BN / 64) + j;  // even: gate block
+                    const int64_t col = ncol0 + (block >> 1) * 32 + l32;
+                    if (col >= p.n) continue;
+                    float gv = acc[i][j][r], uv = acc[i][j + 1][r];
+                    if (scales) {
+                        gv *= scales[col];
+                        uv *= scales[p.n + col];
+                    }
+                    store_out(p.c, p.c_dtype, row * p.ldc + col, glu_combine(EPI, gv, uv));
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < WN; ++j) {
+                    const int64_t col = ncol0 + wn * (BN / 2) + j * 32 + l32;
+                    if (col >= p.n) continue;
+                    float v = acc[i][j][r];
+                    if (scales) v *= scales[col];
+                    if (EPI == SFG_EPI_RESIDUAL) v += p.residual[row * p.ldr + col];
+                    store_out(p.c, p.c_dtype, row * p.ldc + col, v);
+                }
+            }
+        }
+    }
+}
+
+// ===========================================================================
 // fp32 GEMM (VALU): 64x64 tile, BK 16, 256 threads x (4 rows x 4 cols).
 // For GLU epilogues the tile covers 32 outputs: thread columns {2t, 2t+1}
 // of the gate block and the same two of the up block.
@@ -760,6 +990,34 @@ void launch_big_b(const TiledArgs& a, dim3 grid, int tm, int tn, int epi, hipStr
     }
 }
 
+template <int BM, int BN>
+void launch_dma_b(const TiledArgs& a, dim3 grid, int tm, int tn, int epi, hipStream_t s) {
+    switch (epi) {
+        case SFG_EPI_NONE: gemm_dma_kernel<BM, BN, SFG_EPI_NONE><<<grid, 256, 0, s>>>(a, tm, tn); break;
+        case SFG_EPI_RESIDUAL: gemm_dma_kernel<BM, BN, SFG_EPI_RESIDUAL><<<grid, 256, 0, s>>>(a, tm, tn); break;
+        case SFG_EPI_SWIGLU: gemm_dma_kernel<BM, BN, SFG_EPI_SWIGLU><<<grid, 256, 0, s>>>(a, tm, tn); break;
+        default: gemm_dma_kernel<BM, BN, SFG_EPI_GLU_SILU_UP><<<grid, 256, 0, s>>>(a, tm, tn); break;
+    }
+}
+
+// Output tile of the direct-to-LDS kernel: the largest that still gives every
+// CU two workgroups; smaller problems take smaller tiles.
+struct DmaShape { int bm, bn; };
+DmaShape pick_dma_shape(int64_t m, int64_t n_out, bool glu, int groups) {
+    static const char* forced = std::getenv("SFG_GEMM_TILE");
+    if (forced && *forced) {
+        const int bm = std::atoi(forced), bn = std::atoi(std::strchr(forced, 'x') ? std::strchr(forced, 'x') + 1 : forced);
+        if ((bm == 128 || bm == 256) && (bn == 128 || bn == 256)) return {bm, bn};
+    }
+    const DmaShape shapes[] = {{256, 256}, {256, 128}, {128, 128}};
+    for (const DmaShape& sh : shapes) {
+        const int64_t cols = glu ? sh.bn / 2 : sh.bn;
+        const int64_t tiles = ((m + sh.bm - 1) / sh.bm + (groups > 1 ? groups : 0)) * ((n_out + cols - 1) / cols);
+        if (tiles >= 512) return sh;
+    }
+    return {128, 128};
+}
+
 template <int BDT>
 void launch_tiled_b(const TiledArgs& a, dim3 grid, int epi, hipStream_t s) {
     switch (epi) {
@@ -850,6 +1108,20 @@ int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes, h
     a.c = p.c; a.c_dtype = p.c_dtype; a.ldc = p.ldc;
     a.residual = p.residual; a.ldr = p.ldr;
     a.m = p.m; a.n = p.n; a.k = p.k; a.offsets = p.offsets; a.groups = groups;
+    if (big && p.b_dtype == SFG_BF16) {
+        const DmaShape sh = pick_dma_shape(p.m, p.n, glu, groups);
+        const int64_t cols = glu ? sh.bn / 2 : sh.bn;
+        const int64_t tn = (p.n + cols - 1) / cols;
+        const int64_t tm = (p.m + sh.bm - 1) / sh.bm;
+        const dim3 grid = p.offsets ? dim3(static_cast<unsigned>(tn), static_cast<unsigned>(tm + groups))
+                                    : dim3(static_cast<unsigned>(tm * tn));
+        const int itm = p.offsets ? 0 : static_cast<int>(tm);
+        if (sh.bm == 256 && sh.bn == 256) launch_dma_b<256, 256>(a, grid, itm, static_cast<int>(tn), p.epilogue, stream);
+        else if (sh.bm == 256) launch_dma_b<256, 128>(a, grid, itm, static_cast<int>(tn), p.epilogue, stream);
+        else if (sh.bn == 256) launch_dma_b<128, 256>(a, grid, itm, static_cast<int>(tn), p.epilogue, stream);
+        else launch_dma_b<128, 128>(a, grid, itm, static_cast<int>(tn), p.epilogue, stream);
+        return SFG_OK;
+    }
     if (big) {
         const int64_t tn = glu ? p.n / 64 : p.n / 128;
         if (p.offsets) {

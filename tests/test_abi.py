@@ -40,6 +40,15 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
     assert sorted(_abi.EXPORTED) == names
 
 
+def test_no_undefined_library_symbols():
+    """Every kernel's host launch stub is defined (a kernel whose host-side
+    instantiation fails leaves an undefined stub that only an eager load sees)."""
+    out = subprocess.run(["nm", "-D", "--undefined-only", str(_abi.LIB_PATH)], capture_output=True,
+                         text=True, check=True).stdout
+    undefined = [l for l in out.splitlines() if "sfg" in l]
+    assert not undefined, undefined[:5]
+
+
 def test_identity(lib):
     assert lib.sfg_hip_abi_version() == _abi.ABI_VERSION
     meta = lib.sfg_hip_metadata_v1().decode()
