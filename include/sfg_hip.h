@@ -145,6 +145,22 @@ int sfg_hip_attn_prefill_v1(const void* q, const void* k, const void* v, void* o
                             int64_t kv_heads, int64_t seq_q, int64_t seq_kv, int64_t head_dim,
                             int causal, float scale, void* stream);
 
+/* The same prefill (attention_compiler.cpp:286-377) over a transposed value
+ * tensor -- the layout the gfx950 flash kernel streams: q [B][Hq][Sq][128],
+ * k [B][Hkv][Skv][128], vt [B][Hkv][128][ld_vt] bf16 with
+ * ld_vt = sfg_hip_attn_vt_ld_v1(Skv) and keys in [Skv, ld_vt) zero.  head_dim
+ * must be 128.  sfg_hip_qkv_split_rope_vt_v1 is split_qkv + apply_rope
+ * (decoder_compiler.cpp:96-148) writing q, k and that vt from the fp32 QKV rows. */
+int64_t sfg_hip_attn_vt_ld_v1(int64_t seq_kv);
+int sfg_hip_qkv_split_rope_vt_v1(const float* qkv, const float* rope_table, int64_t batch,
+                                 int64_t seq, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                                 uint16_t* q, uint16_t* k, uint16_t* vt, int64_t ld_vt,
+                                 void* stream);
+int sfg_hip_attn_prefill_vt_v1(const uint16_t* q, const uint16_t* k, const uint16_t* vt,
+                               int64_t ld_vt, void* out, int out_dtype, int64_t batch,
+                               int64_t q_heads, int64_t kv_heads, int64_t seq_q, int64_t seq_kv,
+                               int64_t head_dim, int causal, float scale, void* stream);
+
 /* Paged Split-KV decode (attention_compiler.cpp:244-285 split/merge,
  * next_milestones.cpp:137-184 page walk).  q fp32 [B][Hq][D] (one new token per
  * sequence), pools bf16: K [num_pages][Hkv][page_tokens][D], V

@@ -109,6 +109,12 @@ _SIGNATURES = {
     "sfg_hip_attn_prefill_v1": (c_i32, [c_vp, c_vp, c_vp, c_vp, ctypes.c_int, ctypes.c_int,
                                         c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, ctypes.c_int,
                                         c_f32, c_vp]),
+    "sfg_hip_attn_vt_ld_v1": (c_i64, [c_i64]),
+    "sfg_hip_qkv_split_rope_vt_v1": (c_i32, [c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64,
+                                             c_vp, c_vp, c_vp, c_i64, c_vp]),
+    "sfg_hip_attn_prefill_vt_v1": (c_i32, [c_vp, c_vp, c_vp, c_i64, c_vp, ctypes.c_int, c_i64,
+                                           c_i64, c_i64, c_i64, c_i64, c_i64, ctypes.c_int, c_f32,
+                                           c_vp]),
     "sfg_hip_attn_decode_workspace_v1": (c_sz, [c_i64, c_i64, c_i64, c_i64, c_i64, c_i32]),
     "sfg_hip_attn_decode_paged_v1": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, ctypes.c_int,
                                              c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,

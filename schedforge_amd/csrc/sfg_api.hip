@@ -225,6 +225,45 @@ int sfg_hip_attn_prefill_v1(const void* q, const void* k, const void* v, void* o
     return check_launch("attn_prefill");
 }
 
+int64_t sfg_hip_attn_vt_ld_v1(int64_t seq_kv) { return seq_kv > 0 ? sfg::attn_vt_ld(seq_kv) : 0; }
+
+int sfg_hip_qkv_split_rope_vt_v1(const float* qkv, const float* rope_table, int64_t batch,
+                                 int64_t seq, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                                 uint16_t* q, uint16_t* k, uint16_t* vt, int64_t ld_vt,
+                                 void* stream) {
+    if (!qkv || !rope_table || !q || !k || !vt || batch <= 0 || seq <= 0 || q_heads <= 0 ||
+        kv_heads <= 0 || q_heads % kv_heads)
+        return fail(SFG_ERR_SHAPE, "qkv_split_rope_vt: invalid arguments");
+    if (head_dim != 128) return fail(SFG_ERR_UNSUPPORTED, "qkv_split_rope_vt: head_dim %lld", (long long)head_dim);
+    if (ld_vt != sfg::attn_vt_ld(seq))
+        return fail(SFG_ERR_SHAPE, "qkv_split_rope_vt: ld_vt %lld != %lld", (long long)ld_vt,
+                    (long long)sfg::attn_vt_ld(seq));
+    const hipStream_t s = as_stream(stream);
+    sfg::launch_split_rope(qkv, rope_table, batch, seq, q_heads, kv_heads, head_dim, q, k, nullptr,
+                           SFG_BF16, s);
+    sfg::launch_v_transpose(qkv, batch, seq, q_heads, kv_heads, ld_vt, vt, s);
+    return check_launch("qkv_split_rope_vt");
+}
+
+int sfg_hip_attn_prefill_vt_v1(const uint16_t* q, const uint16_t* k, const uint16_t* vt,
+                               int64_t ld_vt, void* out, int out_dtype, int64_t batch,
+                               int64_t q_heads, int64_t kv_heads, int64_t seq_q, int64_t seq_kv,
+                               int64_t head_dim, int causal, float scale, void* stream) {
+    if (!q || !k || !vt || !out || batch <= 0 || q_heads <= 0 || kv_heads <= 0 || seq_q <= 0 ||
+        seq_kv <= 0 || head_dim <= 0 || q_heads % kv_heads || (causal && seq_q > seq_kv))
+        return fail(SFG_ERR_INVALID_CONFIG, "invalid attention configuration");
+    if (out_dtype != SFG_F32 && out_dtype != SFG_BF16)
+        return fail(SFG_ERR_UNSUPPORTED, "attn_prefill_vt: out dtype %d", out_dtype);
+    if (ld_vt != sfg::attn_vt_ld(seq_kv))
+        return fail(SFG_ERR_SHAPE, "attn_prefill_vt: ld_vt %lld != %lld", (long long)ld_vt,
+                    (long long)sfg::attn_vt_ld(seq_kv));
+    const int rc = sfg::launch_attn_prefill_vt(q, k, vt, ld_vt, out, out_dtype, batch, q_heads,
+                                               kv_heads, seq_q, seq_kv, head_dim, causal,
+                                               default_scale(head_dim, scale), as_stream(stream));
+    if (rc != SFG_OK) return fail(rc, "attn_prefill_vt: head_dim %lld not lowered", (long long)head_dim);
+    return check_launch("attn_prefill_vt");
+}
+
 size_t sfg_hip_attn_decode_workspace_v1(int64_t batch, int64_t q_heads, int64_t head_dim,
                                         int64_t max_context, int64_t page_tokens,
                                         int32_t kv_splits) {
@@ -445,6 +484,11 @@ int validate_desc(const sfg_layer_desc* d) {
     return SFG_OK;
 }
 
+// The flash prefill over V^T serves bf16 activations at head_dim 128.
+bool use_vt(const sfg_layer_desc* d) {
+    return d->context == 0 && d->act_dtype == SFG_BF16 && d->head_dim == 128;
+}
+
 LayerBuffers plan_buffers(const sfg_layer_desc* d, void* ws) {
     LayerBuffers b;
     Carve c(ws);
@@ -460,7 +504,10 @@ LayerBuffers plan_buffers(const sfg_layer_desc* d, void* ws) {
     if (d->context == 0) {
         b.q = c.take(rows * H * ae);
         b.k = c.take(rows * kvd * ae);
-        b.v = c.take(rows * kvd * ae);
+        // bf16 head_dim-128 prefill keeps V transposed, keys padded to 64
+        b.v = use_vt(d) ? c.take(static_cast<int64_t>(d->batch) * kvd *
+                                 sfg::attn_vt_ld(d->sequence) * 2)
+                        : c.take(rows * kvd * ae);
     }
     b.attn = c.take(rows * H * ae);
     b.r1 = static_cast<float*>(c.take(rows * H * 4));
@@ -577,9 +624,14 @@ int sfg_hip_decoder_layer_v1(const sfg_layer_desc* d, const sfg_layer_weights* w
     // 3. split + RoPE (decode keeps only Q: the step's K/V are discarded,
     //    decoder_compiler.cpp:238-243)
     const float scale = default_scale(D, 0.0f);
+    const bool vt = use_vt(d);
+    const int64_t ld_vt = vt ? sfg::attn_vt_ld(d->sequence) : 0;
     if (!decode) {
         sfg::launch_split_rope(b.qkv, w->rope_table, d->batch, d->sequence, d->query_heads,
-                               d->kv_heads, D, b.q, b.k, b.v, act, s);
+                               d->kv_heads, D, b.q, b.k, vt ? nullptr : b.v, act, s);
+        if (vt)
+            sfg::launch_v_transpose(b.qkv, d->batch, d->sequence, d->query_heads, d->kv_heads, ld_vt,
+                                    static_cast<uint16_t*>(b.v), s);
     }
     mk.mark(SFG_MARK_ROPE);
     // 4. attention -> merged [rows][H]
@@ -603,6 +655,13 @@ int sfg_hip_decoder_layer_v1(const sfg_layer_desc* d, const sfg_layer_weights* w
                                          static_cast<const float*>(b.v), b.attn, act, d->batch,
                                          d->query_heads, d->kv_heads, d->sequence, d->sequence, D,
                                          d->causal, scale, s);
+        } else if (vt) {
+            rc = sfg::launch_attn_prefill_vt(static_cast<const uint16_t*>(b.q),
+                                             static_cast<const uint16_t*>(b.k),
+                                             static_cast<const uint16_t*>(b.v), ld_vt, b.attn, act,
+                                             d->batch, d->query_heads, d->kv_heads, d->sequence,
+                                             d->sequence, D, d->causal, scale, s);
+            if (rc != SFG_OK) return fail(rc, "bf16 prefill attention not lowered (head_dim %lld)", (long long)D);
         } else {
             rc = sfg::launch_attn_prefill_bf16(static_cast<const uint16_t*>(b.q),
                                                static_cast<const uint16_t*>(b.k),

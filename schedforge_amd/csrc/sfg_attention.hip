@@ -18,6 +18,8 @@
 //    once; scores and the value product run on MFMA (see below), pages are
 //    double-buffered in registers, waves merge in LDS, splits merge in a
 //    second small kernel.
+#include <cstdlib>
+
 #include "sfg_kernels.hpp"
 
 namespace sfg {
@@ -285,6 +287,275 @@ int launch_attn_prefill_bf16(const uint16_t* q, const uint16_t* k, const uint16_
         attn_prefill_bf16_kernel<uint16_t><<<grid, 256, 0, stream>>>(
             q, k, v, static_cast<uint16_t*>(out), q_heads, kv_heads, seq_q, seq_kv, causal,
             scale_log2);
+    return SFG_OK;
+}
+
+// ===========================================================================
+// bf16 flash prefill over a transposed value tensor, head_dim 128.
+//
+// Inputs: Q [B][Hq][Sq][128], K [B][Hkv][Skv][128], V^T [B][Hkv][128][ld_vt]
+// (keys in [Skv, ld_vt) are zero; ld_vt is a multiple of 64 >= Skv).
+// A workgroup of WAVES waves owns 32 * WAVES query rows of one (batch, head);
+// a wave owns 32 rows.  Per tile of 64 keys:
+//   S^T[64 keys][32 q] = K Q^T      2 x 8 mfma_f32_32x32x16_bf16 (Q in VGPRs)
+//   O^T[128 d][32 q] += V^T P^T     4 x 4 mfma_f32_32x32x16_bf16
+// K and V^T tiles go global -> LDS directly (global_load_lds_dwordx4), two
+// stages: the next tile is in flight while the current one is multiplied.
+// Key order: the K fragment of lane l is key row swap23(l & 31) of its 32-key
+// block (bits 2 and 3 of the index exchanged), so accumulator register r of
+// lane l holds key 16 (r / 8) + 8 (l / 32) + r % 8 -- eight consecutive keys
+// per MFMA k-step, which is the P^T operand layout and a single 16-byte V^T
+// fragment read.  LDS slots are XOR-swizzled by row so fragment reads of 16
+// consecutive lanes touch 16 distinct 16-byte slots.
+// Online softmax in the exp2 domain with a lazy rescale: a row keeps its
+// running max until a tile's max exceeds it by more than 8 (p <= 2^8), so the
+// O^T rescale runs only when some row of the wave moved that far.
+// Work order: consecutive workgroup ids go to the 8 XCDs in turn; each XCD
+// gets a contiguous run of (batch, kv_head) groups -- the Q heads sharing one
+// K/V stay in one L2 -- and within a group the longest causal blocks first.
+// ===========================================================================
+constexpr int kFa2BN = 64;
+
+struct Fa2Args {
+    const uint16_t* q;
+    const uint16_t* k;
+    const uint16_t* vt;
+    void* out;
+    int out_f32;
+    int q_heads, kv_heads, seq_q, seq_kv, ld_vt, causal, nqb;
+    float scale_log2;
+};
+
+__device__ __forceinline__ int swap23(int i) {
+    return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1);
+}
+
+template <int WAVES>
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void attn_prefill_fa2_kernel(Fa2Args p) {
+    constexpr int BM = WAVES * 32;
+    constexpr int kBlk = 16 / WAVES;  // 1 KB blocks of K (and of V^T) per wave per tile
+    __shared__ __attribute__((aligned(1024))) uint16_t sK0[kFa2BN * kFaD];
+    __shared__ __attribute__((aligned(1024))) uint16_t sK1[kFa2BN * kFaD];
+    __shared__ __attribute__((aligned(1024))) uint16_t sV0[kFaD * kFa2BN];
+    __shared__ __attribute__((aligned(1024))) uint16_t sV1[kFaD * kFa2BN];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int hl = lane >> 5;
+    const int l32 = lane & 31;
+
+    // --- work item -------------------------------------------------------
+    const int G = p.q_heads / p.kv_heads;
+    const int total = static_cast<int>(gridDim.x);
+    const int bid = static_cast<int>(blockIdx.x);
+    const int full = total - total % 8;
+    const int L = bid < full ? (bid % 8) * (full / 8) + bid / 8 : bid;
+    const int per_group = p.nqb * G;
+    const int grp = L / per_group;
+    const int rem = L - grp * per_group;
+    const int qblock = p.nqb - 1 - rem / G;
+    const int b = grp / p.kv_heads, kvh = grp - b * p.kv_heads;
+    const int h = kvh * G + rem % G;
+
+    const int offset = p.seq_kv - p.seq_q;
+    const int q0 = qblock * BM;
+    const int qw0 = q0 + wave * 32;
+    const int my_q = qw0 + l32;
+
+    // Q^T fragments: lane supplies query my_q, dims 16 s + 8 hl + [0, 8).
+    bf16x8 qf[8];
+    {
+        const int qrow = min(my_q, p.seq_q - 1);
+        const uint16_t* qr = p.q + ((static_cast<int64_t>(b) * p.q_heads + h) * p.seq_q + qrow) * kFaD;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) qf[s] = as_bf16x8(*reinterpret_cast<const uint4*>(qr + s * 16 + hl * 8));
+    }
+    const uint16_t* kb = p.k + (static_cast<int64_t>(b) * p.kv_heads + kvh) * p.seq_kv * kFaD;
+    const uint16_t* vtb = p.vt + (static_cast<int64_t>(b) * p.kv_heads + kvh) * kFaD * p.ld_vt;
+
+    const int block_last_q = min(q0 + BM, p.seq_q) - 1;
+    const int kv_limit = p.causal ? min(p.seq_kv, block_last_q + offset + 1) : p.seq_kv;
+    const int tiles = (kv_limit + kFa2BN - 1) / kFa2BN;
+    const int wave_last_key = p.causal ? (min(qw0 + 31, p.seq_q - 1) + offset) : (p.seq_kv - 1);
+    const int wave_first_limit = p.causal ? (qw0 + offset) : (p.seq_kv - 1);
+    const bool wave_live = qw0 < p.seq_q;
+
+    // --- loads: K block i = rows 4 i + (lane >> 4), slot lane & 15 holds
+    // chunk slot ^ swap23(row & 15); V^T block i = dims 8 i + (lane >> 3),
+    // slot lane & 7 holds chunk slot ^ (row & 7) ^ ((row >> 3) & 1).
+    int k_row[kBlk], k_chunk[kBlk];
+    int64_t v_off[kBlk];
+#pragma unroll
+    for (int n = 0; n < kBlk; ++n) {
+        const int blk = wave * kBlk + n;
+        const int row = 4 * blk + (lane >> 4);
+        k_row[n] = row;
+        k_chunk[n] = ((lane & 15) ^ swap23(row & 15)) * 8;
+        const int d = 8 * blk + (lane >> 3);
+        const int vch = (lane & 7) ^ (d & 7) ^ ((d >> 3) & 1);
+        v_off[n] = static_cast<int64_t>(d) * p.ld_vt + vch * 8;
+    }
+    auto issue = [&](uint16_t* dk, uint16_t* dv, int kv0) {
+#pragma unroll
+        for (int n = 0; n < kBlk; ++n) {
+            const int key = min(kv0 + k_row[n], p.seq_kv - 1);
+            lds_dma16(kb + static_cast<int64_t>(key) * kFaD + k_chunk[n], dk + (wave * kBlk + n) * 512);
+        }
+#pragma unroll
+        for (int n = 0; n < kBlk; ++n) lds_dma16(vtb + v_off[n] + kv0, dv + (wave * kBlk + n) * 512);
+    };
+
+    floatx16 acc_o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc_o[i][r] = 0.f;
+    float m_run = -INFINITY;  // running max, scaled (log2) units
+    float l_run = 0.f;        // this lane's partial row sum
+    const float c = p.scale_log2;
+    const int my_limit = p.causal ? (my_q + offset) : (p.seq_kv - 1);
+
+    // K fragment rows: key swap23(l32) of each 32-key block; slot chunk ^ (l32 & 15).
+    const int kfrag = swap23(l32) * kFaD;
+    const int kswz = l32 & 15;
+    const int vswz = (l32 & 7) ^ ((l32 >> 3) & 1);
+
+    auto compute = [&](const uint16_t* sK, const uint16_t* sV, int kv0) {
+        if (!wave_live || kv0 > wave_last_key) return;
+        floatx16 s[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s[j][r] = 0.f;
+#pragma unroll
+            for (int st = 0; st < 8; ++st) {
+                const bf16x8 kf = as_bf16x8(*reinterpret_cast<const uint4*>(
+                    &sK[j * 32 * kFaD + kfrag + (((2 * st + hl) ^ kswz) * 8)]));
+                s[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[st], s[j], 0, 0, 0);
+            }
+        }
+        // mask (only tiles crossing the diagonal or the end of the keys)
+        if (kv0 + kFa2BN - 1 > wave_first_limit || kv0 + kFa2BN > p.seq_kv) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = kv0 + 32 * j + 16 * (r >> 3) + 8 * hl + (r & 7);
+                    if (key > my_limit || key >= p.seq_kv) s[j][r] = -INFINITY;
+                }
+        }
+        float tmax = s[0][0];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, s[j][r]);
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64)) * c;
+        const bool upd = tmax > m_run + 8.0f;
+        if (__builtin_amdgcn_ballot_w64(upd)) {
+            const float m_new = upd ? tmax : m_run;
+            const float alpha = upd ? fast_exp2(m_run - m_new) : 1.0f;
+            l_run *= alpha;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc_o[i][r] *= alpha;
+            m_run = m_new;
+        }
+        const float nm = -m_run;
+        bf16x8 pf[2][2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                float pv[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    pv[e] = fast_exp2(fmaf(s[j][8 * t + e], c, nm));
+                    l_run += pv[e];
+                }
+                uint4 pk;
+                pk.x = cvt_pk_bf16(pv[0], pv[1]);
+                pk.y = cvt_pk_bf16(pv[2], pv[3]);
+                pk.z = cvt_pk_bf16(pv[4], pv[5]);
+                pk.w = cvt_pk_bf16(pv[6], pv[7]);
+                pf[j][t] = as_bf16x8(pk);
+            }
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const int slot = ((4 * j + 2 * t + hl) ^ vswz) * 8;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const bf16x8 vf = as_bf16x8(*reinterpret_cast<const uint4*>(
+                        &sV[(32 * i + l32) * kFa2BN + slot]));
+                    acc_o[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[j][t], acc_o[i], 0, 0, 0);
+                }
+            }
+    };
+
+    issue(sK0, sV0, 0);
+    wait_vmem_all();
+    __syncthreads();
+    for (int t = 0; t < tiles; t += 2) {
+        if (t + 1 < tiles) issue(sK1, sV1, (t + 1) * kFa2BN);
+        compute(sK0, sV0, t * kFa2BN);
+        wait_vmem_all();
+        __syncthreads();
+        if (t + 1 >= tiles) break;
+        if (t + 2 < tiles) issue(sK0, sV0, (t + 2) * kFa2BN);
+        compute(sK1, sV1, (t + 1) * kFa2BN);
+        wait_vmem_all();
+        __syncthreads();
+    }
+
+    if (my_q >= p.seq_q) return;
+    const float l_total = l_run + __shfl_xor(l_run, 32, 64);
+    const float inv = 1.0f / l_total;
+    // O^T layout: lane holds query my_q, dims 32 i + 8 (r / 4) + 4 hl + (r % 4).
+    const int64_t row = static_cast<int64_t>(b) * p.seq_q + my_q;
+    const int64_t obase = row * (static_cast<int64_t>(p.q_heads) * kFaD) + h * kFaD;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+            const int d = i * 32 + 8 * cc + 4 * hl;
+            const float o0 = acc_o[i][4 * cc + 0] * inv, o1 = acc_o[i][4 * cc + 1] * inv;
+            const float o2 = acc_o[i][4 * cc + 2] * inv, o3 = acc_o[i][4 * cc + 3] * inv;
+            if (p.out_f32) {
+                *reinterpret_cast<float4*>(static_cast<float*>(p.out) + obase + d) = make_float4(o0, o1, o2, o3);
+            } else {
+                uint2 pk;
+                pk.x = pack_bf16x2(o0, o1);
+                pk.y = pack_bf16x2(o2, o3);
+                *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.out) + obase + d) = pk;
+            }
+        }
+}
+
+int64_t attn_vt_ld(int64_t seq_kv) { return (seq_kv + kFa2BN - 1) / kFa2BN * kFa2BN; }
+
+int launch_attn_prefill_vt(const uint16_t* q, const uint16_t* k, const uint16_t* vt, int64_t ld_vt,
+                           void* out, int out_dtype, int64_t batch, int64_t q_heads,
+                           int64_t kv_heads, int64_t seq_q, int64_t seq_kv, int64_t head_dim,
+                           int causal, float scale, hipStream_t stream) {
+    if (head_dim != kFaD) return SFG_ERR_UNSUPPORTED;
+    if (ld_vt % kFa2BN != 0 || ld_vt < seq_kv) return SFG_ERR_SHAPE;
+    static const char* forced = std::getenv("SFG_FA_WAVES");
+    const int waves = (forced && std::atoi(forced) == 8) ? 8 : 4;
+    const int bm = waves * 32;
+    Fa2Args a{};
+    a.q = q; a.k = k; a.vt = vt; a.out = out; a.out_f32 = out_dtype == SFG_F32;
+    a.q_heads = static_cast<int>(q_heads); a.kv_heads = static_cast<int>(kv_heads);
+    a.seq_q = static_cast<int>(seq_q); a.seq_kv = static_cast<int>(seq_kv);
+    a.ld_vt = static_cast<int>(ld_vt); a.causal = causal;
+    a.nqb = static_cast<int>((seq_q + bm - 1) / bm);
+    a.scale_log2 = scale * kLog2e;
+    const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.nqb) * q_heads * batch));
+    if (waves == 8) attn_prefill_fa2_kernel<8><<<grid, 512, 0, stream>>>(a);
+    else attn_prefill_fa2_kernel<4><<<grid, 256, 0, stream>>>(a);
     return SFG_OK;
 }
 

@@ -84,4 +84,27 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// 16 bytes per lane from global memory into LDS at lds_block + 16 * lane
+// (global_load_lds_dwordx4; lds_block is wave-uniform).  A __device__
+// function, not a lambda: the builtin exists on the device side only.
+__device__ __forceinline__ void lds_dma16(const uint16_t* src, uint16_t* lds_block) {
+    __builtin_amdgcn_global_load_lds(src, lds_block, 16, 0, 0);
+}
+
+__device__ __forceinline__ void wait_vmem_all() {
+    // s_waitcnt vmcnt(0), other counters untouched (gfx9 encoding: expcnt 7,
+    // lgkmcnt 15).  LDS DMA completes through vmcnt.
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+}
+
+// Two fp32 -> packed bf16 pair with the hardware converter
+// (v_cvt_pk_bf16_f32, round to nearest even: the same bits as pack_bf16x2 for
+// finite values).
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
+    const f32x2v v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2v));
+}
+
 }  // namespace sfg

@@ -146,6 +146,59 @@ void launch_split_rope(const float* qkv, const float* table, int64_t batch, int6
 }
 
 // ---------------------------------------------------------------------------
+// The V part of split_qkv (decoder_compiler.cpp:116-148; V is not rotated)
+// written transposed for the flash prefill: V^T [B][Hkv][128][ld_vt] bf16 with
+// keys in [seq, ld_vt) zero.  One workgroup per (64-key block, kv_head, batch):
+// the fp32 [64 keys][128 dims] block is staged in LDS, then written as 16-byte
+// runs of 8 keys per dim row.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void v_transpose_kernel(const float* __restrict__ qkv,
+                                                         int64_t qkv_ld, int64_t v_col0, int seq,
+                                                         int kv_heads, int ld_vt,
+                                                         uint16_t* __restrict__ vt) {
+    __shared__ float tile[64][129];
+    const int s0 = blockIdx.x * 64;
+    const int hkv = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+        const int idx = tid + 256 * it;
+        const int key = idx >> 5, d4 = (idx & 31) * 4;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (s0 + key < seq)
+            v = *reinterpret_cast<const float4*>(qkv + (static_cast<int64_t>(b) * seq + s0 + key) * qkv_ld +
+                                                 v_col0 + hkv * 128 + d4);
+        tile[key][d4] = v.x;
+        tile[key][d4 + 1] = v.y;
+        tile[key][d4 + 2] = v.z;
+        tile[key][d4 + 3] = v.w;
+    }
+    __syncthreads();
+    uint16_t* dst = vt + (static_cast<int64_t>(b) * kv_heads + hkv) * 128 * ld_vt + s0;
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+        const int idx = tid + 256 * it;
+        const int d = idx >> 3, k8 = (idx & 7) * 8;
+        uint4 pk;
+        pk.x = pack_bf16x2(tile[k8 + 0][d], tile[k8 + 1][d]);
+        pk.y = pack_bf16x2(tile[k8 + 2][d], tile[k8 + 3][d]);
+        pk.z = pack_bf16x2(tile[k8 + 4][d], tile[k8 + 5][d]);
+        pk.w = pack_bf16x2(tile[k8 + 6][d], tile[k8 + 7][d]);
+        *reinterpret_cast<uint4*>(dst + static_cast<int64_t>(d) * ld_vt + k8) = pk;
+    }
+}
+
+void launch_v_transpose(const float* qkv, int64_t batch, int64_t seq, int64_t q_heads,
+                        int64_t kv_heads, int64_t ld_vt, uint16_t* vt, hipStream_t stream) {
+    const int64_t qkv_ld = (q_heads + 2 * kv_heads) * 128;
+    const int64_t v_col0 = (q_heads + kv_heads) * 128;
+    const dim3 grid(static_cast<unsigned>(ld_vt / 64), static_cast<unsigned>(kv_heads),
+                    static_cast<unsigned>(batch));
+    v_transpose_kernel<<<grid, 256, 0, stream>>>(qkv, qkv_ld, v_col0, static_cast<int>(seq),
+                                                 static_cast<int>(kv_heads), static_cast<int>(ld_vt), vt);
+}
+
+// ---------------------------------------------------------------------------
 // Weight packing: fp32 [K][N] -> [N][K] (fp32 or bf16) through a 64x64 LDS tile
 // so both the read and the write are coalesced.
 // ---------------------------------------------------------------------------

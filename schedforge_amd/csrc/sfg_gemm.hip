@@ -637,19 +637,6 @@ __global__ __launch_bounds__(256) void gemm_mfma256_kernel(TiledArgs p, int tile
 // ===========================================================================
 constexpr int kDK = 64;
 
-// 16 bytes per lane from global memory into LDS at lds_block + 16 * lane
-// (lds_block is wave-uniform).  A __device__ function, not a lambda: the
-// builtin exists on the device side only.
-__device__ __forceinline__ void lds_dma16(const uint16_t* src, uint16_t* lds_block) {
-    __builtin_amdgcn_global_load_lds(src, lds_block, 16, 0, 0);
-}
-
-__device__ __forceinline__ void wait_vmem_all() {
-    // s_waitcnt vmcnt(0), other counters untouched (gfx9 encoding: expcnt 7,
-    // lgkmcnt 15).  LDS DMA completes through vmcnt.
-    __builtin_amdgcn_s_waitcnt(0x0F70);
-}
-
 template <int BM, int BN, int EPI>
 __global__ __launch_bounds__(256) void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
     constexpr bool kGlu = EpiTraits<EPI>::glu;

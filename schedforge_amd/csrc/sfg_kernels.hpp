@@ -61,6 +61,15 @@ int launch_attn_prefill_bf16(const uint16_t* q, const uint16_t* k, const uint16_
                              int out_dtype, int64_t batch, int64_t q_heads, int64_t kv_heads,
                              int64_t seq_q, int64_t seq_kv, int64_t head_dim, int causal,
                              float scale, hipStream_t stream);
+// Flash prefill over V^T [B][Hkv][128][ld_vt] (keys >= seq_kv zero); ld_vt is
+// attn_vt_ld(seq_kv).  launch_v_transpose writes that V^T from fp32 QKV rows.
+int64_t attn_vt_ld(int64_t seq_kv);
+int launch_attn_prefill_vt(const uint16_t* q, const uint16_t* k, const uint16_t* vt, int64_t ld_vt,
+                           void* out, int out_dtype, int64_t batch, int64_t q_heads,
+                           int64_t kv_heads, int64_t seq_q, int64_t seq_kv, int64_t head_dim,
+                           int causal, float scale, hipStream_t stream);
+void launch_v_transpose(const float* qkv, int64_t batch, int64_t seq, int64_t q_heads,
+                        int64_t kv_heads, int64_t ld_vt, uint16_t* vt, hipStream_t stream);
 int decode_split_count(int64_t batch, int64_t kv_heads, int64_t max_context,
                        int64_t page_tokens, int32_t requested);
 size_t decode_workspace_bytes(int64_t batch, int64_t q_heads, int64_t head_dim, int splits);

@@ -20,7 +20,7 @@ HEADER = ROOT / "include" / "sfg_hip.h"
 
 def declared_functions():
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(sfg_hip_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|size_t|const char\*)\s+(sfg_hip_\w+)\s*\(", text, re.M)))
 
 
 @pytest.fixture(scope="module")
@@ -105,6 +105,19 @@ def test_op_entry_points_validate_on_host(lib):
     rc = lib.sfg_hip_attn_prefill_v1(1, 1, 1, 1, _abi.BF16, _abi.BF16, 1, 2, 1, 8, 4, 128, 1,
                                      ctypes.c_float(0.0), None)
     assert rc == _abi.ERR_INVALID_CONFIG
+    # flash prefill over V^T: keys padded to 64, head_dim 128 only
+    assert [lib.sfg_hip_attn_vt_ld_v1(s) for s in (1, 64, 65, 8192)] == [64, 64, 128, 8192]
+    rc = lib.sfg_hip_attn_prefill_vt_v1(1, 1, 1, 100, 1, _abi.F32, 1, 2, 1, 100, 100, 128, 1,
+                                        ctypes.c_float(0.0), None)
+    assert rc == _abi.ERR_SHAPE  # ld_vt must be 128 for 100 keys
+    rc = lib.sfg_hip_attn_prefill_vt_v1(1, 1, 1, 128, 1, _abi.F32, 1, 2, 1, 100, 100, 64, 1,
+                                        ctypes.c_float(0.0), None)
+    assert rc == _abi.ERR_UNSUPPORTED  # head_dim 64
+    rc = lib.sfg_hip_attn_prefill_vt_v1(1, 1, 1, 64, 1, _abi.F32, 1, 2, 1, 8, 4, 128, 1,
+                                        ctypes.c_float(0.0), None)
+    assert rc == _abi.ERR_INVALID_CONFIG
+    rc = lib.sfg_hip_qkv_split_rope_vt_v1(1, 1, 1, 8, 2, 1, 64, 1, 1, 1, 64, None)
+    assert rc == _abi.ERR_UNSUPPORTED
     # paged decode: context beyond the page table (guard) and bad GQA ratio (config)
     rc = lib.sfg_hip_attn_decode_paged_v1(1, 1, 1, 1, None, 1, _abi.F32, 1, 4, 1, 128, 16, 2, 2, 33,
                                           0, ctypes.c_float(0.0), 0, None, 0, None)

@@ -277,6 +277,104 @@ def test_attention_prefill_bf16_equal_keys_is_prefix_mean(lib):
         assert np.max(np.abs(got[:, h] - prefix)) < 2e-2
 
 
+# ------------------------------------------------------- flash prefill over V^T
+def _vt_host(v, ld):
+    """[B][Hkv][S][D] -> [B][Hkv][D][ld] with keys >= S zero."""
+    B, Hkv, S, D = v.shape
+    vt = np.zeros((B, Hkv, D, ld), np.float32)
+    vt[..., :S] = v.transpose(0, 1, 3, 2)
+    return vt
+
+
+def _prefill_vt(lib, q, k, v, causal, out_dtype=F32):
+    B, Hq, Sq, D = q.shape
+    Hkv, Skv = k.shape[1], k.shape[2]
+    ld = lib.sfg_hip_attn_vt_ld_v1(Skv)
+    assert ld % 64 == 0 and ld >= Skv
+    tdt = torch.float32 if out_dtype == F32 else torch.int16
+    out = torch.empty((B * Sq, Hq * D), dtype=tdt, device="cuda")
+    _abi.check(lib.sfg_hip_attn_prefill_vt_v1(bf16_dev(q).data_ptr(), bf16_dev(k).data_ptr(),
+                                              bf16_dev(_vt_host(v, ld)).data_ptr(), ld,
+                                              out.data_ptr(), out_dtype, B, Hq, Hkv, Sq, Skv, D,
+                                              int(causal), ctypes.c_float(0.0), stream()))
+    _sync()
+    return host(out) if out_dtype == F32 else bf16_host(out)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("shape", [(1, 4, 2, 256, 256), (2, 8, 2, 300, 300), (1, 2, 1, 64, 200),
+                                   (1, 2, 2, 1, 77), (1, 8, 1, 1000, 1000), (2, 4, 4, 130, 190),
+                                   (1, 16, 2, 520, 520)])
+def test_attention_prefill_vt_matches_oracle(lib, causal, shape):
+    B, Hq, Hkv, Sq, Skv = shape
+    D = 128
+    q = oracle.round_bf16(oracle.normal(83, 0, (B, Hq, Sq, D)))
+    k = oracle.round_bf16(oracle.normal(83, 1, (B, Hkv, Skv, D)))
+    v = oracle.round_bf16(oracle.normal(83, 2, (B, Hkv, Skv, D)))
+    got = _prefill_vt(lib, q, k, v, causal)
+    ref = oracle.attention(q, k, v, causal).transpose(0, 2, 1, 3).reshape(B * Sq, Hq * D)
+    assert np.isfinite(got).all()
+    assert oracle.rel_error(got, ref) < 2e-2
+
+
+def test_attention_prefill_vt_large_scores_stay_exact(lib):
+    """Scores spanning a wide range (scaled Q) exercise the lazy rescale: a
+    row's max moves by far more than the 2^8 slack several times."""
+    B, Hq, Hkv, S, D = 1, 2, 1, 384, 128
+    ramp = np.linspace(0.2, 6.0, S, dtype=np.float32)[None, None, :, None]
+    q = oracle.round_bf16(oracle.normal(84, 0, (B, Hq, S, D)) * 3.0)
+    k = oracle.round_bf16(oracle.normal(84, 1, (B, Hkv, S, D)) * ramp)
+    v = oracle.round_bf16(oracle.normal(84, 2, (B, Hkv, S, D)))
+    for causal in (True, False):
+        got = _prefill_vt(lib, q, k, v, causal)
+        ref = oracle.attention(q, k, v, causal).transpose(0, 2, 1, 3).reshape(B * S, Hq * D)
+        assert oracle.rel_error(got, ref) < 2e-2
+
+
+def test_attention_prefill_vt_equal_keys_is_prefix_mean(lib):
+    """Closed form: equal keys make causal softmax uniform over the prefix."""
+    B, Hq, Hkv, S, D = 1, 2, 1, 200, 128
+    q = oracle.round_bf16(oracle.normal(85, 0, (B, Hq, S, D)))
+    k = np.broadcast_to(oracle.round_bf16(oracle.normal(85, 1, (D,))), (B, Hkv, S, D)).copy()
+    v = oracle.round_bf16(oracle.normal(85, 2, (B, Hkv, S, D)))
+    got = _prefill_vt(lib, q, k, v, True, out_dtype=BF16).reshape(S, Hq, D)
+    prefix = np.cumsum(v[0, 0].astype(np.float64), axis=0) / np.arange(1, S + 1)[:, None]
+    for h in range(Hq):
+        assert np.max(np.abs(got[:, h] - prefix)) < 2e-2
+
+
+def test_split_rope_vt_matches_split_rope(lib):
+    """split_qkv + RoPE writing V^T: q and k bit-equal to the plain split, vt
+    the exact transpose of its v with zero key padding."""
+    B, S, Hq, Hkv, D = 2, 100, 4, 2, 128
+    H = Hq * D
+    qkv = oracle.normal(62, 0, (B * S, H + 2 * Hkv * D))
+    table = np.empty((S, D // 2, 2), np.float32)
+    _abi.check(lib.sfg_hip_rope_table_host_v1(table.ctypes.data, S, D, ctypes.c_float(1e4)))
+    qkv_d, table_d = dev(qkv), dev(table)
+    q, k, v = (torch.empty((B, h, S, D), dtype=torch.int16, device="cuda") for h in (Hq, Hkv, Hkv))
+    _abi.check(lib.sfg_hip_qkv_split_rope_v1(qkv_d.data_ptr(), table_d.data_ptr(), B, S, Hq, Hkv,
+                                             D, q.data_ptr(), k.data_ptr(), v.data_ptr(), BF16,
+                                             stream()))
+    ld = lib.sfg_hip_attn_vt_ld_v1(S)
+    q2 = torch.empty_like(q)
+    k2 = torch.empty_like(k)
+    vt = torch.full((B, Hkv, D, ld), 0x7FC0, dtype=torch.int16, device="cuda")  # NaN fill
+    _abi.check(lib.sfg_hip_qkv_split_rope_vt_v1(qkv_d.data_ptr(), table_d.data_ptr(), B, S, Hq,
+                                                Hkv, D, q2.data_ptr(), k2.data_ptr(), vt.data_ptr(),
+                                                ld, stream()))
+    _sync()
+    np.testing.assert_array_equal(host(q2), host(q))
+    np.testing.assert_array_equal(host(k2), host(k))
+    expect = np.zeros((B, Hkv, D, ld), np.int16)
+    expect[..., :S] = host(v).transpose(0, 1, 3, 2)
+    np.testing.assert_array_equal(host(vt), expect)
+    with pytest.raises(ValueError):
+        _abi.check(lib.sfg_hip_qkv_split_rope_vt_v1(qkv_d.data_ptr(), table_d.data_ptr(), B, S,
+                                                    Hq, Hkv, D, q2.data_ptr(), k2.data_ptr(),
+                                                    vt.data_ptr(), ld + 1, stream()))
+
+
 def _decode_case(lib, B, Hq, Hkv, ctx, seq_lens=None, splits=0, seed=91):
     D, PT = 128, 16
     pps = (ctx + PT - 1) // PT
