@@ -91,6 +91,22 @@ __device__ __forceinline__ void lds_dma16(const uint16_t* src, uint16_t* lds_blo
     __builtin_amdgcn_global_load_lds(src, lds_block, 16, 0, 0);
 }
 
+// The same 16-byte-per-lane LDS DMA through a buffer resource
+// (buffer_load_dwordx4 ... lds): byte offset voffset from the resource's base,
+// loads past its num_records bytes return zeros instead of faulting.  Unlike
+// the global form, the compiler does not count it as a pending FLAT access, so
+// fragment reads issued while it is in flight keep partial lgkmcnt waits.
+typedef __amdgpu_buffer_rsrc_t buf_rsrc;
+__device__ __forceinline__ buf_rsrc make_rsrc(const void* base, uint32_t bytes) {
+    // dword3 0x00020000: 32-bit data format, the raw-buffer setting of gfx9 parts
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0),
+                                             static_cast<int>(bytes), 0x00020000);
+}
+__device__ __forceinline__ void lds_dma16_buf(buf_rsrc r, uint32_t voffset, uint16_t* lds_block) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        r, (__attribute__((address_space(3))) void*)(lds_block), 16, voffset, 0, 0, 0);
+}
+
 __device__ __forceinline__ void wait_vmem_all() {
     // s_waitcnt vmcnt(0), other counters untouched (gfx9 encoding: expcnt 7,
     // lgkmcnt 15).  LDS DMA completes through vmcnt.

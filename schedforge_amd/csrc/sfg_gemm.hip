@@ -619,39 +619,87 @@ __global__ __launch_bounds__(256) void gemm_mfma256_kernel(TiledArgs p, int tile
 
 // ===========================================================================
 // Large-M MFMA GEMM, third generation (bf16 operands): BM x BN output tile per
-// workgroup, BK = 64, four waves in a 2 x 2 grid, each owning a (BM/2) x (BN/2)
-// block of v_mfma_f32_32x32x16_bf16 tiles (accumulators in the AccVGPRs).
-// Operand slabs go from global memory straight into LDS
-// (global_load_lds_dwordx4): one wave instruction fills one contiguous 1 KB
-// block, i.e. 8 rows x 64 k of bf16.  Rows are 128 B; the 16-B chunk c of row
-// r sits in slot c ^ (r & 7) -- the loading lane picks the chunk it fetches so
-// that its fixed destination slot holds the swizzled one -- so the fragment
-// reads of 8 consecutive rows touch 8 different slots.  Two LDS stages: the
-// loads of slab k+1 are issued before the MFMAs of slab k and waited for at
-// the barrier that ends slab k.  Each stage lives in its own __shared__
-// array, so the compiler can tell the in-flight loads from the stage being
-// read and does not wait for them before the fragment reads.
+// workgroup, four waves in a 2 x 2 grid, each owning a (BM/2) x (BN/2) block of
+// v_mfma_f32_32x32x16_bf16 tiles (accumulators in the AccVGPRs).
+// K advances in slabs of 32 through a ring of LDS stages (four, or three for
+// the two-workgroups-per-CU tiles): the operand slabs go from global memory
+// straight into LDS (global_load_lds_dwordx4, one wave instruction fills one
+// contiguous 1 KB block = 16 rows x 32 k of bf16), and the next slabs are in
+// flight while one is multiplied (one __shared__ array per stage: the A slab,
+// then the B slab).  Before slab k is
+// read each wave waits only for its own loads of slab k (vmcnt = the loads of
+// the slabs issued after it), then a barrier makes every wave's loads visible
+// and retires the stage the next issue overwrites.
+// Rows are 64 B = 4 chunks of 16 B; chunk c of row r sits in slot
+// c ^ ((r >> 2) & 3), so the fragment reads of 16 consecutive rows (one LDS
+// pass of 16 lanes over 64 banks) touch 16 distinct 16-byte bank groups.  The
+// loading lane picks the chunk it fetches so its fixed destination slot holds
+// the swizzled one.  Each stage lives in its own __shared__ array, so the
+// compiler can tell the in-flight loads from the stage being read.
 // For GLU epilogues the B tile interleaves 32-row blocks of gate and up rows
 // (block 2j: gate columns j*32.., block 2j+1: the same up columns), so every
 // lane holds matching gate and up accumulators.
 // ===========================================================================
-constexpr int kDK = 64;
+constexpr int kRK = 32;
 
-template <int BM, int BN, int EPI>
-__global__ __launch_bounds__(256) void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
+// s_waitcnt vmcnt(N), expcnt and lgkmcnt untouched (gfx9 encoding: vmcnt in
+// bits 3:0 and 15:14).
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+
+// s_waitcnt vmcnt(N) lgkmcnt(0): this wave's older loads and all its LDS
+// accesses are done.
+template <int N>
+__device__ __forceinline__ void wait_vmem_lds() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0070);
+}
+
+// Workgroup barrier without __syncthreads()'s release fence, which would wait
+// for every outstanding load (vmcnt(0)) including the LDS DMA of the slabs
+// still meant to be in flight.  The memory clobber keeps the compiler from
+// moving LDS accesses across it; each wave has already waited for its own
+// loads of the slab about to be read, and LDS is coherent inside the CU.
+__device__ __forceinline__ void barrier_no_fence() { asm volatile("s_barrier" ::: "memory"); }
+
+// Stages and workgroups per CU by tile: 256 x 256 holds 256 accumulator
+// registers per lane (one workgroup per CU, four stages = 128 KB of LDS);
+// smaller tiles leave room for two workgroups per CU, so one's barriers and
+// epilogue overlap the other's MFMAs (256 x 128: three stages = 72 KB each).
+// With eight waves (2 x 4) a 256 x 256 tile keeps 128 accumulator registers
+// per lane and two waves per SIMD, so one wave's LDS waits overlap the other's
+// MFMAs.
+template <int BM, int BN, int NW>
+struct DmaShapeTraits {
+    static constexpr bool big = BM * BN > 256 * 128;
+    static constexpr int stages = (big || BM * BN <= 128 * 128) ? 4 : 3;
+    static constexpr int occupancy = (big && NW == 4) ? 1 : 2;
+};
+
+template <int BM, int BN, int NW, int EPI>
+__global__ __launch_bounds__(NW * 64)
+__attribute__((amdgpu_waves_per_eu(DmaShapeTraits<BM, BN, NW>::occupancy,
+                                   DmaShapeTraits<BM, BN, NW>::occupancy)))
+void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
     constexpr bool kGlu = EpiTraits<EPI>::glu;
-    constexpr int WM = BM / 64, WN = BN / 64;        // 32x32 tiles per wave
-    constexpr int kLoadsA = BM / 32, kLoadsB = BN / 32;  // 1 KB blocks per wave per stage
+    constexpr int kStages = DmaShapeTraits<BM, BN, NW>::stages;
+    constexpr int kWavesM = 2, kWavesN = NW / 2;
+    constexpr int WM = BM / (32 * kWavesM), WN = BN / (32 * kWavesN);  // 32x32 tiles per wave
+    constexpr int kLoadsA = BM / 16 / NW, kLoadsB = BN / 16 / NW;      // 1 KB blocks per wave per slab
+    constexpr int kLoads = kLoadsA + kLoadsB;
     static_assert(!kGlu || WN % 2 == 0, "GLU tiles pair gate and up blocks");
-    __shared__ __attribute__((aligned(1024))) uint16_t sA0[BM * kDK];
-    __shared__ __attribute__((aligned(1024))) uint16_t sA1[BM * kDK];
-    __shared__ __attribute__((aligned(1024))) uint16_t sB0[BN * kDK];
-    __shared__ __attribute__((aligned(1024))) uint16_t sB1[BN * kDK];
+    __shared__ __attribute__((aligned(1024))) uint16_t sS0[(BM + BN) * kRK];
+    __shared__ __attribute__((aligned(1024))) uint16_t sS1[(BM + BN) * kRK];
+    __shared__ __attribute__((aligned(1024))) uint16_t sS2[(BM + BN) * kRK];
+    __shared__ __attribute__((aligned(1024))) uint16_t sS3[(BM + BN) * kRK];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / kWavesN, wn = wave % kWavesN;
     constexpr int kOutCols = kGlu ? BN / 2 : BN;
 
     int g = 0;
@@ -697,26 +745,30 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(TiledArgs p, int tiles_m,
     const int64_t bgroup = static_cast<int64_t>(g) * p.b_group_stride;
     const float* scales = p.scales ? p.scales + static_cast<int64_t>(g) * p.s_group_stride : nullptr;
 
-    // Load assignment: wave instruction i fills block (i * 4 + wave); lane l
-    // covers row 8 * block + (l >> 3) and destination slot (l & 7), fetching
-    // the chunk (l & 7) ^ (l >> 3).  Rows past the tile's end read a valid
-    // row instead (their results are never stored).
-    const int lrow = lane >> 3;
-    const int chunk8 = ((lane & 7) ^ lrow) * 8;
-    const uint16_t* a_src[kLoadsA];
+    // Load assignment: wave instruction i fills block (i * NW + wave); lane l
+    // covers row 16 * block + (l >> 2) and destination slot (l & 3), fetching
+    // the chunk (l & 3) ^ ((row >> 2) & 3).  Rows past the tile's end read a
+    // valid row instead (their results are never stored).
+    // The loads go through buffer resources over A and over this group's B
+    // (byte offsets; the host guarantees both fit 32 bits).
+    const int lrow = lane >> 2;
+    const int chunk8 = ((lane & 3) ^ ((lrow >> 2) & 3)) * 8;
+    const buf_rsrc ra = make_rsrc(p.a, static_cast<uint32_t>(p.a_rows_limit * p.lda * 2));
+    uint32_t a_off[kLoadsA];
 #pragma unroll
     for (int i = 0; i < kLoadsA; ++i) {
-        const int64_t r = row0 + (i * 4 + wave) * 8 + lrow;
+        const int64_t r = row0 + (i * NW + wave) * 16 + lrow;
         int64_t src = r < re ? r : row0;
         if (p.a_rows) src = p.a_rows[src];
         if (src < 0 || src >= p.a_rows_limit) src = 0;
-        a_src[i] = p.a + src * p.lda + chunk8;
+        a_off[i] = static_cast<uint32_t>((src * p.lda + chunk8) * 2);
     }
     const uint16_t* bbase = static_cast<const uint16_t*>(p.b) + bgroup;
-    const uint16_t* b_src[kLoadsB];
+    const buf_rsrc rb_ = make_rsrc(bbase, static_cast<uint32_t>((kGlu ? 2 : 1) * p.n * p.ldb * 2));
+    uint32_t b_off[kLoadsB];
 #pragma unroll
     for (int i = 0; i < kLoadsB; ++i) {
-        const int local = (i * 4 + wave) * 8 + lrow;
+        const int local = (i * NW + wave) * 16 + lrow;
         int64_t brow;
         if (kGlu) {
             const int block = local >> 5;
@@ -726,16 +778,16 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(TiledArgs p, int tiles_m,
             const int64_t col = ncol0 + local;
             brow = col < p.n ? col : 0;
         }
-        b_src[i] = bbase + brow * p.ldb + chunk8;
+        b_off[i] = static_cast<uint32_t>((brow * p.ldb + chunk8) * 2);
     }
 
-    auto issue = [&](uint16_t* da, uint16_t* db, int64_t k0) {
+    auto issue = [&](uint16_t* da, int64_t k0) {
+        uint16_t* db = da + BM * kRK;
+        const uint32_t kb = static_cast<uint32_t>(k0 * 2);
 #pragma unroll
-        for (int i = 0; i < kLoadsA; ++i)
-            lds_dma16(a_src[i] + k0, da + (i * 4 + wave) * 512);
+        for (int i = 0; i < kLoadsA; ++i) lds_dma16_buf(ra, a_off[i] + kb, da + (i * NW + wave) * 512);
 #pragma unroll
-        for (int i = 0; i < kLoadsB; ++i)
-            lds_dma16(b_src[i] + k0, db + (i * 4 + wave) * 512);
+        for (int i = 0; i < kLoadsB; ++i) lds_dma16_buf(rb_, b_off[i] + kb, db + (i * NW + wave) * 512);
     };
 
     floatx16 acc[WM][WN];
@@ -748,52 +800,81 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(TiledArgs p, int tiles_m,
 
     const int l32 = lane & 31;
     const int khalf = lane >> 5;
-    const int swz = lane & 7;  // == row & 7 for every fragment row this lane reads
-    // One slab: 4 k-steps of 16; the fragments of step kk+1 are read from LDS
-    // while the MFMAs of step kk run.
-    auto compute = [&](const uint16_t* A, const uint16_t* B) {
-        bf16x8 af[2][WM], bfr[2][WN];
-        auto load = [&](int kk, int buf) {
-            const int slot = ((kk * 2 + khalf) ^ swz) * 8;
+    const int swz = (l32 >> 2) & 3;  // == (row >> 2) & 3 for every fragment row this lane reads
+    // Fragments of one 16-k step: A tiles WM, B tiles WN.
+    auto load_frags = [&](const uint16_t* S, int kk, bf16x8* fa, bf16x8* fb) {
+        const uint16_t* A = S;
+        const uint16_t* B = S + BM * kRK;
+        const int slot = ((kk * 2 + khalf) ^ swz) * 8;
 #pragma unroll
-            for (int i = 0; i < WM; ++i)
-                af[buf][i] = as_bf16x8(*reinterpret_cast<const uint4*>(
-                    &A[(wm * (BM / 2) + i * 32 + l32) * kDK + slot]));
+        for (int i = 0; i < WM; ++i)
+            fa[i] = as_bf16x8(*reinterpret_cast<const uint4*>(&A[(wm * (BM / kWavesM) + i * 32 + l32) * kRK + slot]));
+#pragma unroll
+        for (int j = 0; j < WN; ++j)
+            fb[j] = as_bf16x8(*reinterpret_cast<const uint4*>(&B[(wn * (BN / kWavesN) + j * 32 + l32) * kRK + slot]));
+    };
+    auto mfmas = [&](const bf16x8* fa, const bf16x8* fb) {
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
 #pragma unroll
             for (int j = 0; j < WN; ++j)
-                bfr[buf][j] = as_bf16x8(*reinterpret_cast<const uint4*>(
-                    &B[(wn * (BN / 2) + j * 32 + l32) * kDK + slot]));
-        };
-        load(0, 0);
-#pragma unroll
-        for (int kk = 0; kk < kDK / 16; ++kk) {
-            if (kk + 1 < kDK / 16) load(kk + 1, (kk + 1) & 1);
-#pragma unroll
-            for (int i = 0; i < WM; ++i)
-#pragma unroll
-                for (int j = 0; j < WN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[kk & 1][i], bfr[kk & 1][j],
-                                                                        acc[i][j], 0, 0, 0);
-        }
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
     };
 
-    // Two-stage ring over slab pairs; an odd last slab runs after the loop.
-    const int64_t slabs = p.k / kDK;
-    issue(sA0, sB0, 0);
-    wait_vmem_all();
-    __syncthreads();
-    int64_t kt = 0;
-    for (; kt + 2 <= slabs; kt += 2) {
-        issue(sA1, sB1, (kt + 1) * kDK);
-        compute(sA0, sB0);
-        wait_vmem_all();
-        __syncthreads();
-        if (kt + 2 < slabs) issue(sA0, sB0, (kt + 2) * kDK);
-        compute(sA1, sB1);
-        wait_vmem_all();
-        __syncthreads();
+    // Ring of kStages stages, software-pipelined one half-slab ahead.  Slab kt
+    // (stage cur) runs as
+    //   read the k-step-1 fragments of slab kt     | MFMAs of k-step 0
+    //   issue slab kt + kStages - 1 into the stage slab kt - 1 used
+    //   wait for this wave's loads of slab kt + 1 and its fragment reads, barrier
+    //   read the k-step-0 fragments of slab kt + 1 | MFMAs of k-step 1
+    // so every LDS read overlaps WM x WN MFMAs, and the barrier that publishes
+    // slab kt + 1 also retires every read of stage cur before a later issue
+    // overwrites it.  The issue sits right before the wait: the compiler counts
+    // an LDS DMA as a pending FLAT access on lgkmcnt and, while one is pending,
+    // waits for lgkmcnt(0) before using any fragment; the wait's lgkmcnt(0)
+    // retires it, so the fragment reads after the barrier get partial waits.
+    // Every slab issues exactly one load group (past
+    // the end it re-fetches the last slab into a stage nobody reads again), so
+    // the wait is always "all but the kStages - 2 newest groups" and the
+    // compiler's LDS-DMA tracking sees one uniform pattern (with conditional
+    // issues it waits for every load before the fragment reads).  The loop is
+    // unrolled by kStages so every stage is a fixed __shared__ array.
+    const int64_t slabs = p.k / kRK;
+    bf16x8 f0a[WM], f0b[WN], f1a[WM], f1b[WN];
+    auto slab = [&](int64_t kt, const uint16_t* cur, uint16_t* prev, const uint16_t* next) {
+        load_frags(cur, 1, f1a, f1b);
+        __builtin_amdgcn_sched_barrier(0);
+        if (kt < slabs) mfmas(f0a, f0b);
+        __builtin_amdgcn_sched_barrier(0);
+        issue(prev, min(kt + kStages - 1, slabs - 1) * kRK);
+        wait_vmem_lds<(kStages - 2) * kLoads>();
+        barrier_no_fence();
+        load_frags(next, 0, f0a, f0b);
+        __builtin_amdgcn_sched_barrier(0);
+        if (kt < slabs) mfmas(f1a, f1b);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    issue(sS0, 0);
+    issue(sS1, min(int64_t(1), slabs - 1) * kRK);
+    if constexpr (kStages == 4) issue(sS2, min(int64_t(2), slabs - 1) * kRK);
+    wait_vmem_lds<(kStages - 2) * kLoads>();
+    barrier_no_fence();
+    load_frags(sS0, 0, f0a, f0b);
+    if constexpr (kStages == 4) {
+        for (int64_t kt = 0; kt < slabs; kt += 4) {
+            slab(kt, sS0, sS3, sS1);
+            slab(kt + 1, sS1, sS0, sS2);
+            slab(kt + 2, sS2, sS1, sS3);
+            slab(kt + 3, sS3, sS2, sS0);
+        }
+    } else {
+        for (int64_t kt = 0; kt < slabs; kt += 3) {
+            slab(kt, sS0, sS2, sS1);
+            slab(kt + 1, sS1, sS0, sS2);
+            slab(kt + 2, sS2, sS1, sS0);
+        }
     }
-    if (kt < slabs) compute(sA0, sB0);
+    wait_vmem<0>();
 
     // Epilogue: 32x32 D layout, lane holds column (lane & 31) and rows
     // 8 (r / 4) + 4 (lane >> 5) + (r % 4).
@@ -801,12 +882,12 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(TiledArgs p, int tiles_m,
     for (int i = 0; i < WM; ++i) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const int64_t row = row0 + wm * (BM / 2) + i * 32 + 8 * (r >> 2) + 4 * khalf + (r & 3);
+            const int64_t row = row0 + wm * (BM / kWavesM) + i * 32 + 8 * (r >> 2) + 4 * khalf + (r & 3);
             if (row >= re) continue;
             if (kGlu) {
 #pragma unroll
                 for (int j = 0; j < WN; j += 2) {
-                    const int block = wn * (BN / 64) + j;  // even: gate block
+                    const int block = wn * WN + j;  // even: gate block
                     const int64_t col = ncol0 + (block >> 1) * 32 + l32;
                     if (col >= p.n) continue;
                     float gv = acc[i][j][r], uv = acc[i][j + 1][r];
@@ -819,7 +900,7 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(TiledArgs p, int tiles_m,
             } else {
 #pragma unroll
                 for (int j = 0; j < WN; ++j) {
-                    const int64_t col = ncol0 + wn * (BN / 2) + j * 32 + l32;
+                    const int64_t col = ncol0 + wn * (BN / kWavesN) + j * 32 + l32;
                     if (col >= p.n) continue;
                     float v = acc[i][j][r];
                     if (scales) v *= scales[col];
@@ -977,13 +1058,13 @@ void launch_big_b(const TiledArgs& a, dim3 grid, int tm, int tn, int epi, hipStr
     }
 }
 
-template <int BM, int BN>
+template <int BM, int BN, int NW = 4>
 void launch_dma_b(const TiledArgs& a, dim3 grid, int tm, int tn, int epi, hipStream_t s) {
     switch (epi) {
-        case SFG_EPI_NONE: gemm_dma_kernel<BM, BN, SFG_EPI_NONE><<<grid, 256, 0, s>>>(a, tm, tn); break;
-        case SFG_EPI_RESIDUAL: gemm_dma_kernel<BM, BN, SFG_EPI_RESIDUAL><<<grid, 256, 0, s>>>(a, tm, tn); break;
-        case SFG_EPI_SWIGLU: gemm_dma_kernel<BM, BN, SFG_EPI_SWIGLU><<<grid, 256, 0, s>>>(a, tm, tn); break;
-        default: gemm_dma_kernel<BM, BN, SFG_EPI_GLU_SILU_UP><<<grid, 256, 0, s>>>(a, tm, tn); break;
+        case SFG_EPI_NONE: gemm_dma_kernel<BM, BN, NW, SFG_EPI_NONE><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
+        case SFG_EPI_RESIDUAL: gemm_dma_kernel<BM, BN, NW, SFG_EPI_RESIDUAL><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
+        case SFG_EPI_SWIGLU: gemm_dma_kernel<BM, BN, NW, SFG_EPI_SWIGLU><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
+        default: gemm_dma_kernel<BM, BN, NW, SFG_EPI_GLU_SILU_UP><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
     }
 }
 
@@ -1095,7 +1176,10 @@ int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes, h
     a.c = p.c; a.c_dtype = p.c_dtype; a.ldc = p.ldc;
     a.residual = p.residual; a.ldr = p.ldr;
     a.m = p.m; a.n = p.n; a.k = p.k; a.offsets = p.offsets; a.groups = groups;
-    if (big && p.b_dtype == SFG_BF16) {
+    // the direct-to-LDS kernel addresses each operand with 32-bit byte offsets
+    const bool fits32 = static_cast<uint64_t>(a.a_rows_limit) * p.lda * 2 <= 0xFFFFFFFFull &&
+                        static_cast<uint64_t>(glu ? 2 : 1) * p.n * p.ldb * 2 <= 0xFFFFFFFFull;
+    if (big && fits32 && p.b_dtype == SFG_BF16) {
         const DmaShape sh = pick_dma_shape(p.m, p.n, glu, groups);
         const int64_t cols = glu ? sh.bn / 2 : sh.bn;
         const int64_t tn = (p.n + cols - 1) / cols;
@@ -1103,7 +1187,10 @@ int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes, h
         const dim3 grid = p.offsets ? dim3(static_cast<unsigned>(tn), static_cast<unsigned>(tm + groups))
                                     : dim3(static_cast<unsigned>(tm * tn));
         const int itm = p.offsets ? 0 : static_cast<int>(tm);
-        if (sh.bm == 256 && sh.bn == 256) launch_dma_b<256, 256>(a, grid, itm, static_cast<int>(tn), p.epilogue, stream);
+        static const char* waves_env = std::getenv("SFG_GEMM_WAVES");
+        const bool eight = !(waves_env && std::atoi(waves_env) == 4);
+        if (sh.bm == 256 && sh.bn == 256 && eight) launch_dma_b<256, 256, 8>(a, grid, itm, static_cast<int>(tn), p.epilogue, stream);
+        else if (sh.bm == 256 && sh.bn == 256) launch_dma_b<256, 256>(a, grid, itm, static_cast<int>(tn), p.epilogue, stream);
         else if (sh.bm == 256) launch_dma_b<256, 128>(a, grid, itm, static_cast<int>(tn), p.epilogue, stream);
         else if (sh.bn == 256) launch_dma_b<128, 256>(a, grid, itm, static_cast<int>(tn), p.epilogue, stream);
         else launch_dma_b<128, 128>(a, grid, itm, static_cast<int>(tn), p.epilogue, stream);

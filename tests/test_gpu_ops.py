@@ -105,7 +105,8 @@ def _ref_epilogue(acc, epi, n, residual=None):
 
 @pytest.mark.parametrize("m,n,k", [(16, 3072, 2048), (64, 1024, 512), (5, 256, 384),
                                    (256, 512, 256), (512, 1024, 512), (300, 256, 128),
-                                   (1024, 512, 256), (1300, 256, 192), (2048, 1024, 1024)])
+                                   (1024, 512, 256), (1300, 256, 192), (2048, 1024, 1024),
+                                   (1536, 768, 320), (1100, 384, 64)])
 def test_gemm_bf16_integer_operands_exact(lib, m, n, k):
     """Small-integer operands: every product and partial sum is exact in fp32,
     so any lane-layout or indexing mistake shows as a nonzero difference."""
