@@ -385,26 +385,28 @@ void attn_prefill_fa2_kernel(Fa2Args p) {
     // --- loads: K block i = rows 4 i + (lane >> 4), slot lane & 15 holds
     // chunk slot ^ swap23(row & 15); V^T block i = dims 8 i + (lane >> 3),
     // slot lane & 7 holds chunk slot ^ (row & 7) ^ ((row >> 3) & 1).
-    int k_row[kBlk], k_chunk[kBlk];
-    int64_t v_off[kBlk];
+    // Loads go through buffer resources over this (batch, kv_head)'s K rows
+    // and V^T rows (byte offsets): key rows at or past seq_kv read as zeros
+    // and are masked out of the scores.
+    const buf_rsrc rk = make_rsrc(kb, static_cast<uint32_t>(p.seq_kv) * kFaD * 2);
+    const buf_rsrc rv = make_rsrc(vtb, static_cast<uint32_t>(p.ld_vt) * kFaD * 2);
+    uint32_t k_off[kBlk], v_off[kBlk];
 #pragma unroll
     for (int n = 0; n < kBlk; ++n) {
         const int blk = wave * kBlk + n;
         const int row = 4 * blk + (lane >> 4);
-        k_row[n] = row;
-        k_chunk[n] = ((lane & 15) ^ swap23(row & 15)) * 8;
+        k_off[n] = static_cast<uint32_t>(row * kFaD + ((lane & 15) ^ swap23(row & 15)) * 8) * 2;
         const int d = 8 * blk + (lane >> 3);
         const int vch = (lane & 7) ^ (d & 7) ^ ((d >> 3) & 1);
-        v_off[n] = static_cast<int64_t>(d) * p.ld_vt + vch * 8;
+        v_off[n] = static_cast<uint32_t>(d * p.ld_vt + vch * 8) * 2;
     }
     auto issue = [&](uint16_t* dk, uint16_t* dv, int kv0) {
 #pragma unroll
-        for (int n = 0; n < kBlk; ++n) {
-            const int key = min(kv0 + k_row[n], p.seq_kv - 1);
-            lds_dma16(kb + static_cast<int64_t>(key) * kFaD + k_chunk[n], dk + (wave * kBlk + n) * 512);
-        }
+        for (int n = 0; n < kBlk; ++n)
+            lds_dma16_buf(rk, k_off[n] + static_cast<uint32_t>(kv0) * kFaD * 2, dk + (wave * kBlk + n) * 512);
 #pragma unroll
-        for (int n = 0; n < kBlk; ++n) lds_dma16(vtb + v_off[n] + kv0, dv + (wave * kBlk + n) * 512);
+        for (int n = 0; n < kBlk; ++n)
+            lds_dma16_buf(rv, v_off[n] + static_cast<uint32_t>(kv0) * 2, dv + (wave * kBlk + n) * 512);
     };
 
     floatx16 acc_o[4];
