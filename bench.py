@@ -115,6 +115,19 @@ def decode_attention_bytes(cfg):
     return kv + q + o + pt
 
 
+def stage_tflops(cfg, work, avg):
+    """Algorithmic TFLOP/s of the MFMA stages (projection = QKV + O; FFN up and
+    down, which for MoE are both inside ffn_up; attention)."""
+    out = {"projection": work["proj_flops"] / (avg("projection") * 1e-3) / 1e12,
+           "attention": work["attn_flops"] / (avg("attention_main") * 1e-3) / 1e12}
+    if cfg.moe:
+        out["experts"] = 6 * cfg.rows * cfg.top_k * cfg.hidden * cfg.intermediate / (avg("ffn_up") * 1e-3) / 1e12
+    else:
+        out["ffn_up"] = 4 * cfg.rows * cfg.hidden * cfg.intermediate / (avg("ffn_up") * 1e-3) / 1e12
+        out["ffn_down"] = 2 * cfg.rows * cfg.hidden * cfg.intermediate / (avg("ffn_down") * 1e-3) / 1e12
+    return {k: round(v, 2) for k, v in out.items()}
+
+
 def cpu_baseline(cfg, budget_s: float):
     """Time the CPU oracle (C restatement of reference_decoder_layer) on a
     bounded sample of the workload: full-size layer steps for decode / small
@@ -186,9 +199,10 @@ def main():
         run_layer(plan, x, out)
     torch.cuda.synchronize()
 
-    # Timed region: K layer steps; for decode, two HIP events per step bracket
-    # the paged attention kernel on the layer's stream (its per-launch time).
-    marks = (_abi.MARK_ROPE, _abi.MARK_ATTN_MAIN) if cfg.decode else ()
+    # Timed region: K layer steps; two HIP events per step on the layer's
+    # stream bracket the roofline kernel: the paged attention kernel (decode)
+    # or the FFN up-projection GEMM (prefill; for MoE the grouped expert GEMMs).
+    marks = (_abi.MARK_ROPE, _abi.MARK_ATTN_MAIN) if cfg.decode else (_abi.MARK_ROUTE, _abi.MARK_FFN_UP)
     events = [StageEvents(plan.lib, marks) for _ in range(args.steps)] if marks else None
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -196,7 +210,7 @@ def main():
         run_layer(plan, x, out, events=events[i] if events else None)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3
-    att_times = [e.elapsed(_abi.MARK_ROPE, _abi.MARK_ATTN_MAIN) for e in events] if events else []
+    kern_times = [e.elapsed(*marks) for e in events] if events else []
     if events:
         for e in events:
             e.close()
@@ -217,7 +231,7 @@ def main():
 
     work = algorithmic_work(cfg)
     if cfg.decode:
-        att_ms = sum(att_times) / len(att_times)
+        att_ms = sum(kern_times) / len(kern_times)
         bytes_ = decode_attention_bytes(cfg)
         achieved = bytes_ / (att_ms * 1e-3) / 1e9
         roofline = {"bound": "hbm", "kernel": "attn_decode_split_kernel", "achieved":
@@ -226,14 +240,25 @@ def main():
                     "traffic": MEASURED_TRAFFIC.get(args.config),
                     "algorithmic_bytes": bytes_, "avg_ms": round(att_ms, 5)}
     else:
-        # prefill: the layer's algorithmic FLOPs over the measured step
+        # prefill: the FFN up-projection's algorithmic FLOPs (2 rows H 2I for
+        # the packed gate|up GEMM; 4 T k H I for the grouped W1|W3 expert GEMM
+        # plus 2 T k H I for W2) over its bracketed time
         peak = C.PEAK_F32_TFLOPS if cfg.dtype == "f32" else C.PEAK_BF16_TFLOPS
-        achieved = work["flops"] / (ms_per_step * 1e-3) / 1e12
-        roofline = {"bound": "mfma", "kernel": "decoder layer (all GEMMs + attention)",
+        ffn_ms = sum(kern_times) / len(kern_times)
+        if cfg.moe:
+            kflops = 6 * cfg.rows * cfg.top_k * cfg.hidden * cfg.intermediate
+            kname = "gemm_dma_kernel grouped expert GEMMs (W1|W3 + SwiGLU, W2)"
+        else:
+            kflops = 2 * cfg.rows * cfg.hidden * 2 * cfg.intermediate
+            kname = ("gemm_f32_kernel" if cfg.dtype == "f32" else "gemm_dma_kernel") + " (gate|up + SwiGLU)"
+        achieved = kflops / (ffn_ms * 1e-3) / 1e12
+        roofline = {"bound": "mfma", "kernel": kname,
                     "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
                     "frac": round(achieved / peak, 4),
                     "traffic": MEASURED_TRAFFIC.get(args.config),
-                    "algorithmic_flops": work["flops"]}
+                    "algorithmic_flops": kflops, "avg_ms": round(ffn_ms, 5),
+                    "layer_tflops": round(work["flops"] / (ms_per_step * 1e-3) / 1e12, 2),
+                    "layer_frac": round(work["flops"] / (ms_per_step * 1e-3) / 1e12 / peak, 4)}
     layer_gbps = work["bytes"] / (ms_per_step * 1e-3) / 1e9
     line = {
         "metric": "decoder-layer equiv. tokens/s (1 GPU)",
@@ -254,7 +279,8 @@ def main():
                    + f" D{cfg.head_dim} {'MoE E%d top%d I%d' % (cfg.experts, cfg.top_k, cfg.intermediate) if cfg.moe else 'SwiGLU I%d' % cfg.intermediate}"
                    + (f" ctx{cfg.context_sequence} paged{cfg.page_tokens}" if cfg.decode else ""),
                    "rows": cfg.rows, "layer_hbm_gbps": round(layer_gbps, 1),
-                   "stage_ms": {k: round(avg(k), 5) for k in stages[0]}},
+                   "stage_ms": {k: round(avg(k), 5) for k in stages[0]},
+                   "stage_tflops": stage_tflops(cfg, work, avg)},
         "roofline": roofline,
     }
     if not args.no_cpu_baseline:
