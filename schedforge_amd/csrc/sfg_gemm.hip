@@ -679,11 +679,13 @@ struct DmaShapeTraits {
     static constexpr int occupancy = (big && NW == 4) ? 1 : 2;
 };
 
-template <int BM, int BN, int NW, int EPI>
+template <int BM, int BN, int NW, int EPI, bool PP = false>
 __global__ __launch_bounds__(NW * 64)
 __attribute__((amdgpu_waves_per_eu(DmaShapeTraits<BM, BN, NW>::occupancy,
                                    DmaShapeTraits<BM, BN, NW>::occupancy)))
 void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
+    static_assert(!PP || (NW == 8 && DmaShapeTraits<BM, BN, NW>::stages == 4),
+                  "ping-pong pairs two four-wave groups over a four-stage ring");
     constexpr bool kGlu = EpiTraits<EPI>::glu;
     constexpr int kStages = DmaShapeTraits<BM, BN, NW>::stages;
     constexpr int kWavesM = 2, kWavesN = NW / 2;
@@ -859,6 +861,51 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
     if constexpr (kStages == 4) issue(sS2, min(int64_t(2), slabs - 1) * kRK);
     wait_vmem_lds<(kStages - 2) * kLoads>();
     barrier_no_fence();
+    if constexpr (PP) {
+        // Ping-pong: waves 0..3 (one per SIMD) lead, waves 4..7 trail by one
+        // phase; between consecutive barriers one group multiplies a whole
+        // slab while the other reads the next slab's fragments and issues its
+        // loads, so each SIMD's MFMA pipe always has one group feeding it.
+        //   leader:  mem(0) | mul(0) | mem(1) | mul(1) | ... | (idle)
+        //   trailer: (idle) | mem(0) | mul(0) | mem(1) | ... | mul(last)
+        // mem(s) reads both k-steps of slab s, issues slab s + 3 into the stage
+        // slab s - 1 used, waits for its own loads of slab s + 1 and its reads.
+        // Every read of a slab is retired (lgkmcnt(0)) before a barrier that
+        // precedes the next issue into its stage, and every wave's loads of
+        // slab s + 1 are complete before the barrier that precedes the first
+        // read of slab s + 1 (by the leader, one phase before the trailer).
+        auto mem = [&](int64_t kt, const uint16_t* cur, uint16_t* prev) {
+            load_frags(cur, 0, f0a, f0b);
+            load_frags(cur, 1, f1a, f1b);
+            issue(prev, min(kt + kStages - 1, slabs - 1) * kRK);
+            wait_vmem_lds<(kStages - 2) * kLoads>();
+            barrier_no_fence();
+        };
+        auto mul = [&](int64_t kt) {
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_setprio(1);
+            if (kt < slabs) {
+                mfmas(f0a, f0b);
+                mfmas(f1a, f1b);
+            }
+            __builtin_amdgcn_s_setprio(0);
+            __builtin_amdgcn_sched_barrier(0);
+            barrier_no_fence();
+        };
+        const bool trailer = wave >= NW / 2;
+        if (trailer) barrier_no_fence();
+        for (int64_t kt = 0; kt < slabs; kt += 4) {
+            mem(kt, sS0, sS3);
+            mul(kt);
+            mem(kt + 1, sS1, sS0);
+            mul(kt + 1);
+            mem(kt + 2, sS2, sS1);
+            mul(kt + 2);
+            mem(kt + 3, sS3, sS2);
+            mul(kt + 3);
+        }
+        if (!trailer) barrier_no_fence();
+    } else {
     load_frags(sS0, 0, f0a, f0b);
     if constexpr (kStages == 4) {
         for (int64_t kt = 0; kt < slabs; kt += 4) {
@@ -873,6 +920,7 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
             slab(kt + 1, sS1, sS0, sS2);
             slab(kt + 2, sS2, sS1, sS0);
         }
+    }
     }
     wait_vmem<0>();
 
@@ -1058,13 +1106,13 @@ void launch_big_b(const TiledArgs& a, dim3 grid, int tm, int tn, int epi, hipStr
     }
 }
 
-template <int BM, int BN, int NW = 4>
+template <int BM, int BN, int NW = 4, bool PP = false>
 void launch_dma_b(const TiledArgs& a, dim3 grid, int tm, int tn, int epi, hipStream_t s) {
     switch (epi) {
-        case SFG_EPI_NONE: gemm_dma_kernel<BM, BN, NW, SFG_EPI_NONE><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
-        case SFG_EPI_RESIDUAL: gemm_dma_kernel<BM, BN, NW, SFG_EPI_RESIDUAL><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
-        case SFG_EPI_SWIGLU: gemm_dma_kernel<BM, BN, NW, SFG_EPI_SWIGLU><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
-        default: gemm_dma_kernel<BM, BN, NW, SFG_EPI_GLU_SILU_UP><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
+        case SFG_EPI_NONE: gemm_dma_kernel<BM, BN, NW, SFG_EPI_NONE, PP><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
+        case SFG_EPI_RESIDUAL: gemm_dma_kernel<BM, BN, NW, SFG_EPI_RESIDUAL, PP><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
+        case SFG_EPI_SWIGLU: gemm_dma_kernel<BM, BN, NW, SFG_EPI_SWIGLU, PP><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
+        default: gemm_dma_kernel<BM, BN, NW, SFG_EPI_GLU_SILU_UP, PP><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
     }
 }
 
@@ -1189,7 +1237,11 @@ int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes, h
         const int itm = p.offsets ? 0 : static_cast<int>(tm);
         static const char* waves_env = std::getenv("SFG_GEMM_WAVES");
         const bool eight = !(waves_env && std::atoi(waves_env) == 4);
-        if (sh.bm == 256 && sh.bn == 256 && eight) launch_dma_b<256, 256, 8>(a, grid, itm, static_cast<int>(tn), p.epilogue, stream);
+        static const char* pp_env = std::getenv("SFG_GEMM_PINGPONG");
+        const bool pingpong = !(pp_env && std::atoi(pp_env) == 0);
+        if (sh.bm == 256 && sh.bn == 256 && eight && pingpong)
+            launch_dma_b<256, 256, 8, true>(a, grid, itm, static_cast<int>(tn), p.epilogue, stream);
+        else if (sh.bm == 256 && sh.bn == 256 && eight) launch_dma_b<256, 256, 8>(a, grid, itm, static_cast<int>(tn), p.epilogue, stream);
         else if (sh.bm == 256 && sh.bn == 256) launch_dma_b<256, 256>(a, grid, itm, static_cast<int>(tn), p.epilogue, stream);
         else if (sh.bm == 256) launch_dma_b<256, 128>(a, grid, itm, static_cast<int>(tn), p.epilogue, stream);
         else if (sh.bn == 256) launch_dma_b<128, 256>(a, grid, itm, static_cast<int>(tn), p.epilogue, stream);
