@@ -181,6 +181,27 @@ int sfg_hip_attn_decode_paged_v1(const float* q, const uint16_t* k_pool,
                                  float scale, int validate_pages, void* workspace,
                                  size_t workspace_bytes, void* stream);
 
+/* append_paged_kv (next_milestones.cpp:486-524) on the device pools: keys / values
+ * [B][Hkv][tokens][D] (SFG_F32 or SFG_BF16) are stored as bf16 at token positions
+ * start_b + t, start_b = seq_lens[b] (device) when seq_lens != NULL, else `start`,
+ * through page_table [B][pages_per_seq] into K [num_pages][Hkv][page_tokens][D] /
+ * V [num_pages][Hkv][D][page_tokens].  Pages are assigned by the caller (the host
+ * allocator, as the reference's free list); positions past the table's capacity and
+ * page ids outside [0, num_pages) are not written.  advance != 0 adds `tokens` to
+ * seq_lens afterwards.  head_dim 128, page_tokens 16.
+ * gather_paged_kv (next_milestones.cpp:554-581): the first `length` tokens of every
+ * sequence back to keys / values [B][Hkv][length][D] fp32. */
+int sfg_hip_kv_append_paged_v1(const void* keys, const void* values, int dtype, uint16_t* k_pool,
+                               uint16_t* v_pool, const int32_t* page_table, int32_t* seq_lens,
+                               int64_t start, int advance, int64_t batch, int64_t kv_heads,
+                               int64_t tokens, int64_t head_dim, int64_t page_tokens,
+                               int64_t pages_per_seq, int64_t num_pages, void* stream);
+int sfg_hip_kv_gather_paged_v1(const uint16_t* k_pool, const uint16_t* v_pool,
+                               const int32_t* page_table, int64_t batch, int64_t kv_heads,
+                               int64_t length, int64_t head_dim, int64_t page_tokens,
+                               int64_t pages_per_seq, int64_t num_pages, float* keys, float* values,
+                               void* stream);
+
 /* MoE routing: Router -> Softmax -> TopK -> Histogram -> PrefixSum -> Dispatch
  * (route_topk, moe_compiler.cpp:412-455; dispatch_tokens, 496-528).
  * x fp32 [T][H], router fp32 [H][E], bias fp32 [E] or NULL.  Logits are
@@ -237,6 +258,14 @@ typedef struct {
     int32_t kv_splits;  /* decode; <= 0: automatic */
     int32_t use_routing_trace;
     int32_t weight_layout; /* layout of every projection / expert weight */
+    int32_t kv_append;  /* decode only.  0: the reference's semantics -- RoPE at position 0
+                         * within the step, the step's K/V computed and discarded
+                         * (decoder_compiler.cpp:96-104, 238-243).  1: RoPE at the
+                         * sequence's true position (its cached length), the step's
+                         * K/V written into the pools at that position (append_paged_kv,
+                         * next_milestones.cpp:486-524; the page must already be in the
+                         * table) and attention over the cache including it.  Not a
+                         * reference mode: its outputs differ from execute_once's. */
 } sfg_layer_desc;
 
 typedef struct {
@@ -248,7 +277,7 @@ typedef struct {
     const float* router; const float* router_bias; /* MoE: [H][E], [E] or NULL */
     const void* w13; const float* s13;           /* MoE: [E][2I][H] */
     const void* w2; const float* s2;             /* MoE: [E][H][I] */
-    const uint16_t* k_pool; const uint16_t* v_pool; /* decode: paged bf16 pools */
+    uint16_t* k_pool; uint16_t* v_pool;          /* decode: paged bf16 pools (written when kv_append) */
     const int32_t* page_table;                   /* decode: [B][pages_per_seq] */
     const float* rope_table;                     /* [S][D/2][2] */
 } sfg_layer_weights;
@@ -266,6 +295,8 @@ typedef struct {
     const int32_t* trace_ids;        /* optional routing trace [rows][k] */
     const float* trace_weights;
     void** stage_events;             /* NULL or SFG_NUM_MARKS hipEvent_t */
+    int32_t* seq_lens;               /* kv_append: device [B] cached lengths, advanced by one
+                                      * after the step; NULL: every sequence holds `context` */
 } sfg_layer_io;
 
 size_t sfg_hip_decoder_layer_workspace_v1(const sfg_layer_desc* desc);

@@ -50,7 +50,7 @@ class LayerCfg(ctypes.Structure):
                                                "query_heads", "kv_heads", "head_dim")] + \
                [("rms_epsilon", ctypes.c_float), ("rope_theta", ctypes.c_float)] + \
                [(n, ctypes.c_int32) for n in ("causal", "moe", "experts", "top_k", "context",
-                                               "int8_weights", "threads")]
+                                               "int8_weights", "threads", "kv_append")]
 
 
 class LayerData(ctypes.Structure):
@@ -64,7 +64,8 @@ class LayerData(ctypes.Structure):
 
 class LayerTaps(ctypes.Structure):
     _fields_ = [("normalized1", fp), ("qkv", fp), ("attn_merged", fp), ("residual1", fp),
-                ("normalized2", fp), ("ids", ip), ("weights", fp), ("counts", ip)]
+                ("normalized2", fp), ("ids", ip), ("weights", fp), ("counts", ip),
+                ("new_k", fp), ("new_v", fp)]
 
 
 def lib() -> ctypes.CDLL:

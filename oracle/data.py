@@ -101,7 +101,7 @@ def decoder_layer(cfg, d, quant=None, taps: bool = False, threads: int = 0,
     c = LayerCfg(cfg.batch, cfg.sequence, H, cfg.intermediate, cfg.query_heads, cfg.kv_heads,
                  cfg.head_dim, cfg.rms_epsilon, cfg.rope_theta, int(cfg.causal),
                  int(cfg.ffn == "moe"), cfg.experts, cfg.top_k, cfg.context_sequence,
-                 int(cfg.dtype == "w8"), threads)
+                 int(cfg.dtype == "w8"), threads, int(getattr(cfg, "kv_append", False)))
     ld = LayerData()
     keep = []
 
@@ -147,6 +147,10 @@ def decoder_layer(cfg, d, quant=None, taps: bool = False, threads: int = 0,
         t["normalized2"] = np.empty((rows, H), np.float32)
         tp = LayerTaps(_f(t["normalized1"]), _f(t["qkv"]), _f(t["attn_merged"]),
                        _f(t["residual1"]), _f(t["normalized2"]))
+        if getattr(cfg, "kv_append", False):
+            t["new_k"] = np.empty((cfg.batch, cfg.kv_heads, cfg.sequence, cfg.head_dim), np.float32)
+            t["new_v"] = np.empty_like(t["new_k"])
+            tp.new_k, tp.new_v = _f(t["new_k"]), _f(t["new_v"])
         if cfg.ffn == "moe":
             t["ids"] = np.empty((rows, cfg.top_k), np.int32)
             t["weights"] = np.empty((rows, cfg.top_k), np.float32)

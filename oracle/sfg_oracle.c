@@ -165,12 +165,20 @@ void sfgo_concat_columns(const float* const* weights, const int64_t* widths, int
  * f = powf(theta, -(2i)/D), angle = float(pos) * f, pos = index within seq. */
 void sfgo_rope(float* t, int64_t batch, int64_t heads, int64_t seq, int64_t head_dim,
                float theta) {
+    sfgo_rope_at(t, batch, heads, seq, head_dim, theta, 0);
+}
+
+/* The same rotation with token s at position pos0 + s: the build's append mode
+ * rotates a decode step's token at its true position (the reference always uses
+ * the index within the step, decoder_compiler.cpp:96-104). */
+void sfgo_rope_at(float* t, int64_t batch, int64_t heads, int64_t seq, int64_t head_dim,
+                  float theta, int64_t pos0) {
     for (int64_t b = 0; b < batch; ++b)
         for (int64_t h = 0; h < heads; ++h)
             for (int64_t s = 0; s < seq; ++s)
                 for (int64_t d = 0; d + 1 < head_dim; d += 2) {
                     const float freq = powf(theta, -(float)d / (float)head_dim);
-                    const float angle = (float)s * freq;
+                    const float angle = (float)(pos0 + s) * freq;
                     const float cs = cosf(angle);
                     const float sn = sinf(angle);
                     float* base = t + (((b * heads + h) * seq + s) * head_dim + d);
@@ -588,16 +596,56 @@ int sfgo_decoder_layer(const sfgo_layer_cfg* c, const sfgo_layer_data* d, float*
     float* q = alloc_f(qn);
     float* k = alloc_f(kn);
     float* v = alloc_f(kn);
-    sfgo_split_qkv_rope(qkv, c->batch, c->sequence, H, c->query_heads, c->kv_heads, D,
-                        c->rope_theta, q, k, v);
-    sfgo_attn_cfg ac = {c->batch, c->query_heads, c->kv_heads, c->sequence,
-                        c->context > 0 ? c->context : c->sequence, c->head_dim, c->head_dim,
-                        c->causal, 0.0f};
+    const int append = c->context > 0 && c->kv_append;
+    if (append) {
+        /* Append mode (the build's non-reference option): the step's tokens are
+         * rotated at their true positions context + s, stored as bf16 (the pool
+         * dtype) after the cached tokens, and attended over with the cache. */
+        sfgo_split_qkv_rope(qkv, c->batch, c->sequence, H, c->query_heads, c->kv_heads, D,
+                            c->rope_theta, q, k, v);
+        /* Q and K again from the unrotated rows, rotated at the new positions */
+        for (int64_t b = 0; b < c->batch; ++b)
+            for (int64_t s = 0; s < c->sequence; ++s) {
+                const float* row = qkv + (b * c->sequence + s) * qkvw;
+                for (int64_t h = 0; h < c->query_heads; ++h)
+                    memcpy(q + ((b * c->query_heads + h) * c->sequence + s) * D, row + h * D,
+                           sizeof(float) * (size_t)D);
+                for (int64_t h = 0; h < c->kv_heads; ++h)
+                    memcpy(k + ((b * c->kv_heads + h) * c->sequence + s) * D, row + H + h * D,
+                           sizeof(float) * (size_t)D);
+            }
+        sfgo_rope_at(q, c->batch, c->query_heads, c->sequence, D, c->rope_theta, c->context);
+        sfgo_rope_at(k, c->batch, c->kv_heads, c->sequence, D, c->rope_theta, c->context);
+        sfgo_round_bf16(k, kn);
+        sfgo_round_bf16(v, kn);
+    } else {
+        sfgo_split_qkv_rope(qkv, c->batch, c->sequence, H, c->query_heads, c->kv_heads, D,
+                            c->rope_theta, q, k, v);
+    }
+    const int64_t skv = c->context > 0 ? c->context + (append ? c->sequence : 0) : c->sequence;
+    sfgo_attn_cfg ac = {c->batch, c->query_heads, c->kv_heads, c->sequence, skv, c->head_dim,
+                        c->head_dim, c->causal, 0.0f};
     float* attn = alloc_f(qn);
-    if (c->context > 0)
+    if (append) {
+        float* kc = alloc_f((int64_t)c->batch * c->kv_heads * skv * D);
+        float* vc = alloc_f((int64_t)c->batch * c->kv_heads * skv * D);
+        for (int64_t b = 0; b < c->batch; ++b)
+            for (int64_t h = 0; h < c->kv_heads; ++h) {
+                const int64_t bh = b * c->kv_heads + h;
+                memcpy(kc + bh * skv * D, d->cached_k + bh * c->context * D, sizeof(float) * (size_t)(c->context * D));
+                memcpy(vc + bh * skv * D, d->cached_v + bh * c->context * D, sizeof(float) * (size_t)(c->context * D));
+                memcpy(kc + (bh * skv + c->context) * D, k + bh * c->sequence * D, sizeof(float) * (size_t)(c->sequence * D));
+                memcpy(vc + (bh * skv + c->context) * D, v + bh * c->sequence * D, sizeof(float) * (size_t)(c->sequence * D));
+            }
+        sfgo_attention(&ac, q, kc, vc, attn);
+        if (taps && taps->new_k) memcpy(taps->new_k, k, sizeof(float) * (size_t)kn);
+        if (taps && taps->new_v) memcpy(taps->new_v, v, sizeof(float) * (size_t)kn);
+        free(kc); free(vc);
+    } else if (c->context > 0) {
         sfgo_attention(&ac, q, d->cached_k, d->cached_v, attn);
-    else
+    } else {
         sfgo_attention(&ac, q, k, v, attn);
+    }
     float* merged = alloc_f(rows * H);
     sfgo_merge_heads(attn, c->batch, c->sequence, c->query_heads, D, merged);
     float* proj = alloc_f(rows * H);

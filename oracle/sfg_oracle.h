@@ -45,6 +45,8 @@ void sfgo_rms_norm(const float* x, const float* w, float* y, int64_t rows, int64
 void sfgo_matmul(const float* a, const float* b, float* c, int64_t m, int64_t n, int64_t k);
 void sfgo_concat_columns(const float* const* weights, const int64_t* widths, int64_t count,
                          int64_t input_width, float* packed);
+void sfgo_rope_at(float* t, int64_t batch, int64_t heads, int64_t seq, int64_t head_dim,
+                  float theta, int64_t pos0);
 void sfgo_rope(float* t, int64_t batch, int64_t heads, int64_t seq, int64_t head_dim,
                float theta);
 void sfgo_split_qkv_rope(const float* qkv, int64_t batch, int64_t seq, int64_t hidden,
@@ -102,6 +104,8 @@ typedef struct {
     int32_t context;      /* 0 prefill, >0 decode over cached K/V of this length */
     int32_t int8_weights; /* 1: projections and FFN weights are weight-only int8 */
     int32_t threads;      /* OpenMP threads for the oracle (<=0: default) */
+    int32_t kv_append;    /* decode: 1 = the build's append mode (true-position RoPE, the
+                             step's bf16 K/V appended to the cache and attended over) */
 } sfgo_layer_cfg;
 
 typedef struct {
@@ -133,6 +137,7 @@ typedef struct {  /* optional intermediates for stage-level checks (each may be 
     float* residual1;    /* [rows, H] */
     float* normalized2;  /* [rows, H] */
     int32_t* ids; float* weights; int32_t* counts; /* routing */
+    float* new_k; float* new_v;  /* append mode: the step's K/V as stored [B,Hkv,S,D] */
 } sfgo_layer_taps;
 
 int sfgo_decoder_layer(const sfgo_layer_cfg* cfg, const sfgo_layer_data* d, float* out,

@@ -62,6 +62,7 @@ class LayerDesc(ctypes.Structure):
         ("context", c_i32), ("page_tokens", c_i32), ("pages_per_seq", c_i32),
         ("num_pages", c_i32), ("act_dtype", c_i32), ("weight_dtype", c_i32),
         ("kv_splits", c_i32), ("use_routing_trace", c_i32), ("weight_layout", c_i32),
+        ("kv_append", c_i32),
     ]
 
 
@@ -86,6 +87,7 @@ class LayerIO(ctypes.Structure):
         ("x", c_vp), ("out", c_vp),
         ("trace_ids", c_vp), ("trace_weights", c_vp),
         ("stage_events", ctypes.POINTER(c_vp)),
+        ("seq_lens", c_vp),
     ]
 
 
@@ -120,6 +122,11 @@ _SIGNATURES = {
                                              c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,
                                              c_i64, c_i32, c_f32, ctypes.c_int, c_vp, c_sz,
                                              c_vp]),
+    "sfg_hip_kv_append_paged_v1": (c_i32, [c_vp, c_vp, ctypes.c_int, c_vp, c_vp, c_vp, c_vp, c_i64,
+                                           ctypes.c_int, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,
+                                           c_i64, c_vp]),
+    "sfg_hip_kv_gather_paged_v1": (c_i32, [c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,
+                                           c_i64, c_vp, c_vp, c_vp]),
     "sfg_hip_moe_route_workspace_v1": (c_sz, [c_i64, c_i64, c_i64]),
     "sfg_hip_moe_route_v1": (c_i32, [c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp,
                                      c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_sz, c_vp]),

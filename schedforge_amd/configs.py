@@ -32,6 +32,11 @@ class DecoderConfig:
     dtype: str = "f32"
     page_tokens: int = 16
     router_bias_std: float = 0.0
+    # decode only: append the step's K/V into the paged cache at the true
+    # position (not the reference's semantics; see sfg_layer_desc.kv_append)
+    kv_append: bool = False
+    # page-table capacity in tokens for append plans (0: context + 1)
+    kv_capacity: int = 0
 
     @property
     def rows(self) -> int:
@@ -66,6 +71,16 @@ class DecoderConfig:
             raise ValueError("invalid decoder context sequence")
         if self.dtype not in ("f32", "bf16", "w8"):
             raise ValueError(f"unknown dtype {self.dtype}")
+        if self.kv_append and not self.decode:
+            raise ValueError("kv append needs a decode step (context > 0)")
+
+    @property
+    def capacity(self) -> int:
+        """Tokens the per-sequence page tables hold: the cached context, or for
+        append plans room for the tokens still to come."""
+        if not self.kv_append:
+            return self.context_sequence
+        return max(self.kv_capacity, self.context_sequence + self.sequence)
 
     def replace(self, **kw) -> "DecoderConfig":
         return dataclasses.replace(self, **kw)

@@ -307,7 +307,7 @@ int sfg_hip_attn_decode_paged_v1(const float* q, const uint16_t* k_pool, const u
     if (!workspace || workspace_bytes < need)
         return fail(SFG_ERR_WORKSPACE, "attn_decode_paged: workspace %zu < %zu", workspace_bytes, need);
     const int rc = sfg::launch_attn_decode_paged(
-        q, q_heads * head_dim, nullptr, 0, k_pool, v_pool, page_table, seq_lens, max_context, out,
+        q, q_heads * head_dim, nullptr, 0, k_pool, v_pool, page_table, seq_lens, max_context, 0, out,
         out_dtype, batch, q_heads,
         kv_heads, head_dim, page_tokens, pages_per_seq, num_pages, splits,
         default_scale(head_dim, scale), workspace, as_stream(stream), nullptr);
@@ -315,6 +315,46 @@ int sfg_hip_attn_decode_paged_v1(const float* q, const uint16_t* k_pool, const u
         return fail(rc, "attn_decode_paged: head_dim %lld / page_tokens %lld / group %lld not lowered",
                     (long long)head_dim, (long long)page_tokens, (long long)(q_heads / kv_heads));
     return check_launch("attn_decode_paged");
+}
+
+int sfg_hip_kv_append_paged_v1(const void* keys, const void* values, int dtype, uint16_t* k_pool,
+                               uint16_t* v_pool, const int32_t* page_table, int32_t* seq_lens,
+                               int64_t start, int advance, int64_t batch, int64_t kv_heads,
+                               int64_t tokens, int64_t head_dim, int64_t page_tokens,
+                               int64_t pages_per_seq, int64_t num_pages, void* stream) {
+    if (!keys || !values || !k_pool || !v_pool || !page_table || batch <= 0 || kv_heads <= 0 ||
+        tokens <= 0 || head_dim <= 0 || page_tokens <= 0 || pages_per_seq <= 0 || num_pages <= 0)
+        return fail(SFG_ERR_SHAPE, "kv_append_paged: invalid arguments");
+    if (dtype != SFG_F32 && dtype != SFG_BF16) return fail(SFG_ERR_UNSUPPORTED, "kv_append_paged: dtype %d", dtype);
+    if (!seq_lens && (start < 0 || start + tokens > pages_per_seq * page_tokens))
+        return fail(SFG_ERR_GUARD, "paged KV capacity exceeded (%lld + %lld > %lld)", (long long)start,
+                    (long long)tokens, (long long)(pages_per_seq * page_tokens));
+    const int rc = sfg::launch_kv_append(keys, values, dtype, kv_heads * tokens * head_dim,
+                                         tokens * head_dim, head_dim, nullptr, k_pool, v_pool, page_table,
+                                         seq_lens, start, advance, batch, kv_heads, tokens, head_dim,
+                                         page_tokens, pages_per_seq, num_pages, as_stream(stream));
+    if (rc != SFG_OK)
+        return fail(rc, "kv_append_paged: head_dim %lld / page_tokens %lld not lowered", (long long)head_dim,
+                    (long long)page_tokens);
+    return check_launch("kv_append_paged");
+}
+
+int sfg_hip_kv_gather_paged_v1(const uint16_t* k_pool, const uint16_t* v_pool,
+                               const int32_t* page_table, int64_t batch, int64_t kv_heads,
+                               int64_t length, int64_t head_dim, int64_t page_tokens,
+                               int64_t pages_per_seq, int64_t num_pages, float* keys, float* values,
+                               void* stream) {
+    if (!k_pool || !v_pool || !page_table || !keys || !values || batch <= 0 || kv_heads <= 0 ||
+        head_dim <= 0 || page_tokens <= 0 || pages_per_seq <= 0 || num_pages <= 0)
+        return fail(SFG_ERR_SHAPE, "kv_gather_paged: invalid arguments");
+    if (length <= 0) return fail(SFG_ERR_INVALID_CONFIG, "cannot gather empty paged KV cache");
+    if (length > pages_per_seq * page_tokens)
+        return fail(SFG_ERR_GUARD, "kv_gather_paged: length %lld beyond the page table", (long long)length);
+    const int rc = sfg::launch_kv_gather(k_pool, v_pool, page_table, batch, kv_heads, length, head_dim,
+                                         page_tokens, pages_per_seq, num_pages, keys, values,
+                                         as_stream(stream));
+    if (rc != SFG_OK) return fail(rc, "kv_gather_paged: head_dim %lld not lowered", (long long)head_dim);
+    return check_launch("kv_gather_paged");
 }
 
 size_t sfg_hip_moe_route_workspace_v1(int64_t tokens, int64_t experts, int64_t top_k) {
@@ -472,6 +512,14 @@ int validate_desc(const sfg_layer_desc* d) {
             return fail(SFG_ERR_INVALID_CONFIG, "invalid paged KV configuration");
         if (d->context > d->pages_per_seq * d->page_tokens)
             return fail(SFG_ERR_GUARD, "KV cache length violates compiled guard");
+        if (d->kv_append) {
+            if (d->head_dim != 128 || d->page_tokens != 16 || d->sequence != 1)
+                return fail(SFG_ERR_UNSUPPORTED, "kv append lowers head_dim 128, 16-token pages, one token");
+            if (d->context + 1 > d->pages_per_seq * d->page_tokens)
+                return fail(SFG_ERR_GUARD, "paged KV capacity exceeded by the appended token");
+        }
+    } else if (d->kv_append) {
+        return fail(SFG_ERR_INVALID_CONFIG, "kv append needs a decode step (context > 0)");
     } else if (d->causal && d->sequence <= 0) {
         return fail(SFG_ERR_INVALID_CONFIG, "invalid attention configuration");
     }
@@ -527,7 +575,7 @@ LayerBuffers plan_buffers(const sfg_layer_desc* d, void* ws) {
         b.act = c.take(rows * I * ae);
     }
     if (d->context > 0) {
-        const int splits = sfg::decode_split_count(d->batch, d->kv_heads, d->context,
+        const int splits = sfg::decode_split_count(d->batch, d->kv_heads, d->context + (d->kv_append ? 1 : 0),
                                                    d->page_tokens, d->kv_splits);
         b.attn_ws = c.take(sfg::decode_workspace_bytes(d->batch, d->query_heads, D, splits));
     }
@@ -637,17 +685,31 @@ int sfg_hip_decoder_layer_v1(const sfg_layer_desc* d, const sfg_layer_weights* w
     // 4. attention -> merged [rows][H]
     if (decode) {
         if (d->sequence != 1) return fail(SFG_ERR_UNSUPPORTED, "decode lowers one new token per sequence");
-        const int splits = sfg::decode_split_count(d->batch, d->kv_heads, d->context, d->page_tokens,
-                                                   d->kv_splits);
-        // RoPE of the new token's query (position 0 within the step, as the
-        // reference rotates it, decoder_compiler.cpp:96-104) is applied while
-        // the kernel loads Q straight from the QKV rows.
+        const bool append = d->kv_append != 0;
+        const int splits = sfg::decode_split_count(d->batch, d->kv_heads, d->context + (append ? 1 : 0),
+                                                   d->page_tokens, d->kv_splits);
+        if (append) {
+            // Append mode: the step's K (rotated at its true position, the
+            // sequence's length) and V go into the pools at that position,
+            // as append_paged_kv does (next_milestones.cpp:486-524).
+            rc = sfg::launch_kv_append(b.qkv + H, b.qkv + H + kvd, SFG_F32, qkvw, D, 0, w->rope_table,
+                                       w->k_pool, w->v_pool, w->page_table, io->seq_lens, d->context,
+                                       0, d->batch, d->kv_heads, 1, D, d->page_tokens, d->pages_per_seq,
+                                       d->num_pages, s);
+            if (rc != SFG_OK) return fail(rc, "kv append not lowered (head_dim %lld)", (long long)D);
+        }
+        // RoPE of the new token's query is applied while the kernel loads Q
+        // straight from the QKV rows: at position 0 within the step, as the
+        // reference rotates it (decoder_compiler.cpp:96-104), or in append mode
+        // at the sequence's length, over the cache including the new token.
         rc = sfg::launch_attn_decode_paged(
-            b.qkv, qkvw, w->rope_table, 0, w->k_pool, w->v_pool, w->page_table, nullptr, d->context,
+            b.qkv, qkvw, w->rope_table, append ? -1 : 0, w->k_pool, w->v_pool, w->page_table,
+            append ? io->seq_lens : nullptr, d->context, append ? 1 : 0,
             b.attn, act, d->batch, d->query_heads, d->kv_heads, D, d->page_tokens, d->pages_per_seq,
             d->num_pages, splits, scale, b.attn_ws, s,
             io->stage_events ? static_cast<hipEvent_t>(io->stage_events[SFG_MARK_ATTN_MAIN]) : nullptr);
         if (rc != SFG_OK) return fail(rc, "decode attention not lowered (head_dim %lld)", (long long)D);
+        if (append && io->seq_lens) sfg::launch_kv_advance(io->seq_lens, d->batch, 1, s);
     } else {
         if (act == SFG_F32) {
             if (D > 128) return fail(SFG_ERR_UNSUPPORTED, "fp32 attention head_dim > 128");

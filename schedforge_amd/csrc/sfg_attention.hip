@@ -588,6 +588,7 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(
     const float* __restrict__ q, int64_t q_row_stride, const float* __restrict__ rope,
     int rope_pos, const uint16_t* __restrict__ k_pool, const uint16_t* __restrict__ v_pool,
     const int32_t* __restrict__ page_table, const int32_t* __restrict__ seq_lens, int uniform_len,
+    int len_extra,
     int kv_heads, int pages_per_seq, int num_pages, int splits, float scale_log2,
     float* __restrict__ part_ml, float* __restrict__ part_acc) {
     static_assert(G >= 1 && G <= 16, "GQA group must fit the 16 MFMA columns");
@@ -596,7 +597,12 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int q_heads = kv_heads * G;
     const int lr = lane & 15, lg = lane >> 4;
-    const int len = min(seq_lens ? seq_lens[b] : uniform_len, pages_per_seq * kPageTok);
+    // Tokens this sequence attends over: its length (plus len_extra tokens just
+    // appended in place); the query rotates at rope_pos, or at the length
+    // before the append (its own position) when rope_pos < 0.
+    const int len0 = seq_lens ? seq_lens[b] : uniform_len;
+    const int len = min(len0 + len_extra, pages_per_seq * kPageTok);
+    const int q_pos = rope_pos >= 0 ? rope_pos : max(len0, 0);
     const int pages = (len + kPageTok - 1) / kPageTok;
     const int sp_begin = static_cast<int>(static_cast<int64_t>(pages) * split / splits);
     const int sp_end = static_cast<int>(static_cast<int64_t>(pages) * (split + 1) / splits);
@@ -621,7 +627,7 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(
             v[4] = c.x; v[5] = c.y; v[6] = c.z; v[7] = c.w;
             if (rope) {
                 const float2* t = reinterpret_cast<const float2*>(rope) +
-                                  static_cast<int64_t>(rope_pos) * (kDecD / 2) + d0 / 2;
+                                  static_cast<int64_t>(q_pos) * (kDecD / 2) + d0 / 2;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const float2 cs = t[e];
@@ -792,7 +798,7 @@ size_t decode_workspace_bytes(int64_t batch, int64_t q_heads, int64_t head_dim, 
 int launch_attn_decode_paged(const float* q, int64_t q_row_stride, const float* rope, int rope_pos,
                              const uint16_t* k_pool, const uint16_t* v_pool,
                              const int32_t* page_table, const int32_t* seq_lens, int64_t max_context,
-                             void* out, int out_dtype, int64_t batch, int64_t q_heads,
+                             int len_extra, void* out, int out_dtype, int64_t batch, int64_t q_heads,
                              int64_t kv_heads, int64_t head_dim, int64_t page_tokens,
                              int64_t pages_per_seq, int64_t num_pages, int splits, float scale,
                              void* workspace, hipStream_t stream, hipEvent_t mid_event) {
@@ -808,7 +814,7 @@ int launch_attn_decode_paged(const float* q, int64_t q_row_stride, const float* 
     const int len = static_cast<int>(max_context);
     const int pps = static_cast<int>(pages_per_seq);
     const int np = static_cast<int>(num_pages);
-#define SFG_DECODE(G) attn_decode_split_kernel<G><<<grid, 256, 0, stream>>>(q, q_row_stride, rope, rope_pos, k_pool, v_pool, page_table, seq_lens, len, static_cast<int>(kv_heads), pps, np, splits, scale_log2, part_ml, part_acc)
+#define SFG_DECODE(G) attn_decode_split_kernel<G><<<grid, 256, 0, stream>>>(q, q_row_stride, rope, rope_pos, k_pool, v_pool, page_table, seq_lens, len, len_extra, static_cast<int>(kv_heads), pps, np, splits, scale_log2, part_ml, part_acc)
     switch (group) {
         case 1: SFG_DECODE(1); break;
         case 2: SFG_DECODE(2); break;
@@ -826,6 +832,120 @@ int launch_attn_decode_paged(const float* q, int64_t q_row_stride, const float* 
     else
         attn_decode_combine_kernel<uint16_t><<<cgrid, kDecD, 0, stream>>>(
             part_ml, part_acc, static_cast<uint16_t*>(out), static_cast<int>(q_heads), splits);
+    return SFG_OK;
+}
+
+// ===========================================================================
+// Paged KV cache maintenance: append_paged_kv / gather_paged_kv
+// (next_milestones.cpp:486-524, 554-581) on the device pools
+// K [page][Hkv][16][128], V [page][Hkv][128][16] (bf16) through per-sequence
+// page tables [B][pages_per_seq].  Pages are assigned by the host (the plan's
+// allocator, as the reference's free list); the kernels only move data and
+// skip any position past the table's capacity or any page id outside the pool.
+// ===========================================================================
+struct KvAppendArgs {
+    const void* keys; const void* values; int src_f32;
+    int64_t sb, sh, st;           // source element strides: batch, kv head, token (dims contiguous)
+    const float2* rope;           // [positions][64] (cos, sin) or null: keys rotated at their position
+    uint16_t* k_pool; uint16_t* v_pool;
+    const int32_t* page_table; const int32_t* seq_lens; int start;
+    int kv_heads, pages_per_seq, num_pages;
+};
+
+__device__ __forceinline__ float2 load_pair(const void* base, int f32, int64_t idx) {
+    if (f32) return *reinterpret_cast<const float2*>(static_cast<const float*>(base) + idx);
+    const uint32_t w = *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(base) + idx);
+    return make_float2(bf16_to_f32(static_cast<uint16_t>(w & 0xFFFFu)), bf16_to_f32(static_cast<uint16_t>(w >> 16)));
+}
+
+// One wave per (token, kv_head, sequence); lane = dim pair (2 lane, 2 lane + 1).
+__global__ __launch_bounds__(64) void kv_append_kernel(KvAppendArgs a) {
+    const int t = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int pair = threadIdx.x;
+    const int pos = (a.seq_lens ? a.seq_lens[b] : a.start) + t;
+    if (pos < 0 || pos >= a.pages_per_seq * kPageTok) return;
+    const int phys = a.page_table[static_cast<int64_t>(b) * a.pages_per_seq + pos / kPageTok];
+    if (phys < 0 || phys >= a.num_pages) return;
+    const int slot = pos % kPageTok;
+    const int64_t src = b * a.sb + h * a.sh + t * a.st + 2 * pair;
+    float2 kv = load_pair(a.keys, a.src_f32, src);
+    if (a.rope) {
+        const float2 cs = a.rope[static_cast<int64_t>(pos) * (kDecD / 2) + pair];
+        kv = make_float2(kv.x * cs.x - kv.y * cs.y, kv.x * cs.y + kv.y * cs.x);
+    }
+    const int64_t blk = static_cast<int64_t>(phys) * a.kv_heads + h;
+    *reinterpret_cast<uint32_t*>(a.k_pool + (blk * kPageTok + slot) * kDecD + 2 * pair) = pack_bf16x2(kv.x, kv.y);
+    const float2 vv = load_pair(a.values, a.src_f32, src);
+    a.v_pool[(blk * kDecD + 2 * pair) * kPageTok + slot] = f32_to_bf16(vv.x);
+    a.v_pool[(blk * kDecD + 2 * pair + 1) * kPageTok + slot] = f32_to_bf16(vv.y);
+}
+
+__global__ __launch_bounds__(256) void kv_advance_kernel(int32_t* seq_lens, int batch, int tokens) {
+    const int b = blockIdx.x * 256 + threadIdx.x;
+    if (b < batch) seq_lens[b] += tokens;
+}
+
+// gather_paged_kv: pools -> keys / values [B][Hkv][length][128] fp32 (bf16 widened exactly).
+__global__ __launch_bounds__(64) void kv_gather_kernel(const uint16_t* __restrict__ k_pool,
+                                                       const uint16_t* __restrict__ v_pool,
+                                                       const int32_t* __restrict__ page_table,
+                                                       int kv_heads, int pages_per_seq, int num_pages,
+                                                       int length, float* __restrict__ keys,
+                                                       float* __restrict__ values) {
+    const int t = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int pair = threadIdx.x;
+    const int phys = page_table[static_cast<int64_t>(b) * pages_per_seq + t / kPageTok];
+    const int64_t dst = ((static_cast<int64_t>(b) * kv_heads + h) * length + t) * kDecD + 2 * pair;
+    float2 kk = make_float2(0.f, 0.f), vv = make_float2(0.f, 0.f);
+    if (phys >= 0 && phys < num_pages) {
+        const int slot = t % kPageTok;
+        const int64_t blk = static_cast<int64_t>(phys) * kv_heads + h;
+        const uint32_t kw = *reinterpret_cast<const uint32_t*>(k_pool + (blk * kPageTok + slot) * kDecD + 2 * pair);
+        kk = make_float2(bf16_to_f32(static_cast<uint16_t>(kw & 0xFFFFu)), bf16_to_f32(static_cast<uint16_t>(kw >> 16)));
+        vv = make_float2(bf16_to_f32(v_pool[(blk * kDecD + 2 * pair) * kPageTok + slot]),
+                         bf16_to_f32(v_pool[(blk * kDecD + 2 * pair + 1) * kPageTok + slot]));
+    }
+    *reinterpret_cast<float2*>(keys + dst) = kk;
+    *reinterpret_cast<float2*>(values + dst) = vv;
+}
+
+int launch_kv_append(const void* keys, const void* values, int src_dtype, int64_t sb, int64_t sh,
+                     int64_t st, const float* rope, uint16_t* k_pool, uint16_t* v_pool,
+                     const int32_t* page_table, int32_t* seq_lens, int64_t start, int advance,
+                     int64_t batch, int64_t kv_heads, int64_t tokens, int64_t head_dim,
+                     int64_t page_tokens, int64_t pages_per_seq, int64_t num_pages,
+                     hipStream_t stream) {
+    if (head_dim != kDecD || page_tokens != kPageTok) return SFG_ERR_UNSUPPORTED;
+    KvAppendArgs a{};
+    a.keys = keys; a.values = values; a.src_f32 = src_dtype == SFG_F32;
+    a.sb = sb; a.sh = sh; a.st = st;
+    a.rope = reinterpret_cast<const float2*>(rope);
+    a.k_pool = k_pool; a.v_pool = v_pool; a.page_table = page_table; a.seq_lens = seq_lens;
+    a.start = static_cast<int>(start);
+    a.kv_heads = static_cast<int>(kv_heads); a.pages_per_seq = static_cast<int>(pages_per_seq);
+    a.num_pages = static_cast<int>(num_pages);
+    kv_append_kernel<<<dim3(static_cast<unsigned>(tokens), static_cast<unsigned>(kv_heads),
+                            static_cast<unsigned>(batch)), 64, 0, stream>>>(a);
+    if (advance && seq_lens)
+        kv_advance_kernel<<<dim3(static_cast<unsigned>((batch + 255) / 256)), 256, 0, stream>>>(
+            seq_lens, static_cast<int>(batch), static_cast<int>(tokens));
+    return SFG_OK;
+}
+
+void launch_kv_advance(int32_t* seq_lens, int64_t batch, int64_t tokens, hipStream_t stream) {
+    kv_advance_kernel<<<dim3(static_cast<unsigned>((batch + 255) / 256)), 256, 0, stream>>>(
+        seq_lens, static_cast<int>(batch), static_cast<int>(tokens));
+}
+
+int launch_kv_gather(const uint16_t* k_pool, const uint16_t* v_pool, const int32_t* page_table,
+                     int64_t batch, int64_t kv_heads, int64_t length, int64_t head_dim,
+                     int64_t page_tokens, int64_t pages_per_seq, int64_t num_pages, float* keys,
+                     float* values, hipStream_t stream) {
+    if (head_dim != kDecD || page_tokens != kPageTok) return SFG_ERR_UNSUPPORTED;
+    kv_gather_kernel<<<dim3(static_cast<unsigned>(length), static_cast<unsigned>(kv_heads),
+                            static_cast<unsigned>(batch)), 64, 0, stream>>>(
+        k_pool, v_pool, page_table, static_cast<int>(kv_heads), static_cast<int>(pages_per_seq),
+        static_cast<int>(num_pages), static_cast<int>(length), keys, values);
     return SFG_OK;
 }
 

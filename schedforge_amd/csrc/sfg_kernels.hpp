@@ -76,10 +76,25 @@ size_t decode_workspace_bytes(int64_t batch, int64_t q_heads, int64_t head_dim, 
 int launch_attn_decode_paged(const float* q, int64_t q_row_stride, const float* rope, int rope_pos,
                              const uint16_t* k_pool, const uint16_t* v_pool,
                              const int32_t* page_table, const int32_t* seq_lens, int64_t max_context,
-                             void* out, int out_dtype, int64_t batch, int64_t q_heads,
+                             int len_extra, void* out, int out_dtype, int64_t batch, int64_t q_heads,
                              int64_t kv_heads, int64_t head_dim, int64_t page_tokens,
                              int64_t pages_per_seq, int64_t num_pages, int splits, float scale,
                              void* workspace, hipStream_t stream, hipEvent_t mid_event);
+
+// Paged KV append / gather (pages pre-assigned in the tables).  Sources are
+// [b][h][t][128] with element strides sb / sh / st; rope (optional) rotates the
+// keys at their positions; advance != 0 adds `tokens` to seq_lens afterwards.
+int launch_kv_append(const void* keys, const void* values, int src_dtype, int64_t sb, int64_t sh,
+                     int64_t st, const float* rope, uint16_t* k_pool, uint16_t* v_pool,
+                     const int32_t* page_table, int32_t* seq_lens, int64_t start, int advance,
+                     int64_t batch, int64_t kv_heads, int64_t tokens, int64_t head_dim,
+                     int64_t page_tokens, int64_t pages_per_seq, int64_t num_pages,
+                     hipStream_t stream);
+void launch_kv_advance(int32_t* seq_lens, int64_t batch, int64_t tokens, hipStream_t stream);
+int launch_kv_gather(const uint16_t* k_pool, const uint16_t* v_pool, const int32_t* page_table,
+                     int64_t batch, int64_t kv_heads, int64_t length, int64_t head_dim,
+                     int64_t page_tokens, int64_t pages_per_seq, int64_t num_pages, float* keys,
+                     float* values, hipStream_t stream);
 
 // MoE
 size_t moe_route_workspace_bytes(int64_t tokens, int64_t experts, int64_t top_k);

@@ -102,6 +102,7 @@ class DecoderExecutablePlan:
         self.weights = _abi.LayerWeights()
         self.workspace: Optional[torch.Tensor] = None
         self.trace: Optional[tuple] = None
+        self.lengths: Optional[np.ndarray] = None  # append plans: host copy of the cached lengths
         self.lib = _abi.load()
 
     # ---- helpers -------------------------------------------------------
@@ -210,16 +211,19 @@ def compile_decoder(config: DecoderConfig, data: DecoderData, device="cuda",
         plan._pack([data.gate_weight, data.up_weight], H, wdt, stream, "w_gate_up", layout)
         plan._pack([data.down_weight], I, wdt, stream, "w_down", layout)
 
-    # RoPE table [S][D/2][2], host-computed with the reference's expressions.
-    table = np.empty((cfg.sequence, D // 2, 2), dtype=np.float32)
-    check(lib.sfg_hip_rope_table_host_v1(table.ctypes.data, cfg.sequence, D,
+    # RoPE table [positions][D/2][2], host-computed with the reference's
+    # expressions: the step's positions, or for append plans every position the
+    # cache can reach (tokens rotate at their true positions there).
+    positions = max(cfg.sequence, cfg.capacity) if cfg.kv_append else cfg.sequence
+    table = np.empty((positions, D // 2, 2), dtype=np.float32)
+    check(lib.sfg_hip_rope_table_host_v1(table.ctypes.data, positions, D,
                                          ctypes.c_float(cfg.rope_theta)))
     t["rope"] = torch.from_numpy(table).to(plan.device)
 
     pages_per_seq = num_pages = 0
     if cfg.decode:
         pt = cfg.page_tokens
-        pages_per_seq = (cfg.context_sequence + pt - 1) // pt
+        pages_per_seq = (cfg.capacity + pt - 1) // pt
         num_pages = cfg.batch * pages_per_seq
         if data.page_table is not None:
             table_pages = np.asarray(data.page_table, dtype=np.int32).reshape(cfg.batch, pages_per_seq)
@@ -271,6 +275,12 @@ def compile_decoder(config: DecoderConfig, data: DecoderData, device="cuda",
     d.kv_splits = kv_splits
     d.use_routing_trace = int(data.routing_trace is not None)
     d.weight_layout = layout
+    d.kv_append = int(cfg.kv_append)
+    if cfg.kv_append:
+        # per-sequence cached lengths on the device, advanced by every step
+        t["seq_lens"] = torch.full((cfg.batch,), cfg.context_sequence, dtype=torch.int32,
+                                   device=plan.device)
+        plan.lengths = np.full(cfg.batch, cfg.context_sequence, dtype=np.int64)
 
     w = plan.weights
     w.rms1, w.rms2 = _ptr(t["rms1"]), _ptr(t["rms2"])
@@ -337,6 +347,12 @@ def run_layer(plan: DecoderExecutablePlan, x: torch.Tensor, out: torch.Tensor,
     if "trace_ids" in plan.t:
         io.trace_ids, io.trace_weights = plan.t["trace_ids"].data_ptr(), plan.t["trace_weights"].data_ptr()
     io.stage_events = events.arr if events is not None else None
+    if plan.config.kv_append:
+        # append_paged_kv's guard (next_milestones.cpp:488-489), kept on the host
+        if int(plan.lengths.max()) + plan.config.sequence > plan.config.capacity:
+            raise ValueError("paged KV capacity exceeded")
+        io.seq_lens = plan.t["seq_lens"].data_ptr()
+        plan.lengths += plan.config.sequence
     check(plan.lib.sfg_hip_decoder_layer_v1(ctypes.byref(plan.desc), ctypes.byref(plan.weights),
                                             ctypes.byref(io), plan.workspace.data_ptr(),
                                             plan.workspace.numel(), _stream_handle(stream)))

@@ -707,7 +707,7 @@ DecoderExecutablePlan DecoderCompiler::compile(const DecoderConfig& config, cons
             void* p = dev.add(name, pool.size() * 2);
             dev.upload(p, pool.data(), pool.size() * 2);
             dev.sync();  // the host pool is released at scope end
-            (is_value ? w.v_pool : w.k_pool) = static_cast<const std::uint16_t*>(p);
+            (is_value ? w.v_pool : w.k_pool) = static_cast<std::uint16_t*>(p);
             plan.constants.push_back({name, {c.batch, c.kv_heads, c.context_sequence, static_cast<int>(D)},
                                       is_value ? std::vector<int>{num_pages, c.kv_heads, static_cast<int>(D), c.page_tokens}
                                                : std::vector<int>{num_pages, c.kv_heads, c.page_tokens, static_cast<int>(D)},

@@ -194,8 +194,10 @@ def test_paged_gather_iota_round_trip():
 
 
 # ------------------------------------------------------------------ whole layer
-def _np_layer(cfg, d, quant=None):
-    """Independent float64 formulation of reference_decoder_layer."""
+def _np_layer(cfg, d, quant=None, appended=None):
+    """Independent float64 formulation of reference_decoder_layer; with
+    `appended` = (k, v) the build's append mode: the step rotates at its true
+    positions and attends over the cache followed by these stored K/V."""
     x = d.input.astype(np.float64)
     B, S, H, Hq, Hkv, D = cfg.batch, cfg.sequence, cfg.hidden, cfg.query_heads, cfg.kv_heads, cfg.head_dim
 
@@ -213,7 +215,8 @@ def _np_layer(cfg, d, quant=None):
     q = qkv[:, :H].reshape(B, S, Hq, D).transpose(0, 2, 1, 3)
     k = qkv[:, H:H + Hkv * D].reshape(B, S, Hkv, D).transpose(0, 2, 1, 3)
     v = qkv[:, H + Hkv * D:].reshape(B, S, Hkv, D).transpose(0, 2, 1, 3)
-    pos = np.arange(S)[:, None].astype(np.float32)
+    pos0 = cfg.context_sequence if appended is not None else 0
+    pos = (pos0 + np.arange(S))[:, None].astype(np.float32)
     fr = np.float32(cfg.rope_theta) ** (-np.arange(0, D, 2, dtype=np.float32) / np.float32(D))
     ang = (pos * fr).astype(np.float64)
 
@@ -225,7 +228,10 @@ def _np_layer(cfg, d, quant=None):
         return t
 
     q, k = rope(q), rope(k)
-    if cfg.context_sequence > 0:
+    if appended is not None:
+        k = np.concatenate([d.cached_key.astype(np.float64), appended[0].astype(np.float64)], 2)
+        v = np.concatenate([d.cached_value.astype(np.float64), appended[1].astype(np.float64)], 2)
+    elif cfg.context_sequence > 0:
         k, v = d.cached_key.astype(np.float64), d.cached_value.astype(np.float64)
     skv = k.shape[2]
     g = Hq // Hkv
@@ -265,6 +271,38 @@ def test_layer_matches_float64_formulation(name, overrides):
     d = oracle.make_layer_data(cfg, 4242)
     out = oracle.decoder_layer(cfg, d)
     assert rel(out, _np_layer(cfg, d)) < 2e-6
+
+
+def test_append_mode_layer_matches_float64_formulation():
+    """The build's append mode (not a reference mode): the step's Q and K rotate
+    at position `context`, its K/V are stored as bf16 and attended over with the
+    cache.  The stored K/V are the fp64 rotation rounded to bf16 (to one bf16
+    ulp: fp32 vs fp64 can straddle a rounding boundary), and the layer output
+    matches the fp64 formulation that appends exactly those values."""
+    cfg = CONFIGS["c2"].replace(batch=2, hidden=256, intermediate=512, query_heads=2, kv_heads=1,
+                                context_sequence=100, kv_append=True)
+    d = oracle.make_layer_data(cfg, 4243)
+    out, taps = oracle.decoder_layer(cfg, d, taps=True)
+    new_k, new_v = taps["new_k"], taps["new_v"]
+    assert new_k.shape == (2, 1, 1, 128)
+    # stored values are bf16
+    np.testing.assert_array_equal(oracle.round_bf16(new_k), new_k)
+    # K rotated at position 100 (not 0): compare with the unrotated / rotated fp64 projection
+    n1 = taps["normalized1"].astype(np.float64)
+    kproj = (n1 @ d.key_weight.astype(np.float64)).reshape(2, 1, 1, 128)
+    fr = np.float32(cfg.rope_theta) ** (-np.arange(0, 128, 2, dtype=np.float32) / np.float32(128))
+    ang = (np.float32(100) * fr).astype(np.float64)
+    rot = kproj.copy()
+    rot[..., 0::2] = kproj[..., 0::2] * np.cos(ang) - kproj[..., 1::2] * np.sin(ang)
+    rot[..., 1::2] = kproj[..., 0::2] * np.sin(ang) + kproj[..., 1::2] * np.cos(ang)
+    assert np.max(np.abs(new_k - rot) / np.maximum(np.abs(rot), 1e-3)) < 2 ** -7
+    assert np.max(np.abs(new_k - kproj)) > 1e-2  # position 100, not the reference's 0
+    vproj = (n1 @ d.value_weight.astype(np.float64)).reshape(2, 1, 1, 128)
+    assert np.max(np.abs(new_v - vproj) / np.maximum(np.abs(vproj), 1e-3)) < 2 ** -7
+    assert rel(out, _np_layer(cfg, d, appended=(new_k, new_v))) < 2e-6
+    # and it is not the reference's decode step
+    ref_mode = oracle.decoder_layer(cfg.replace(kv_append=False), d)
+    assert rel(out, ref_mode) > 1e-4
 
 
 def test_int8_dense_layer_matches_dequantized_float64():
