@@ -666,15 +666,33 @@ int sfg_hip_decoder_layer_v1(const sfg_layer_desc* d, const sfg_layer_weights* w
     sfg::launch_rmsnorm(io->x, w->rms1, b.xn, act, rows, H, d->rms_epsilon, s);
     mk.mark(SFG_MARK_NORM1);
     // 2. fused QKV projection -> fp32
-    if ((rc = gemm(b.xn, H, w->w_qkv, w->s_qkv, b.qkv, SFG_F32, nullptr, rows, qkvw, H, SFG_EPI_NONE)))
-        return rc;
-    mk.mark(SFG_MARK_QKV);
-    // 3. split + RoPE (decode keeps only Q: the step's K/V are discarded,
-    //    decoder_compiler.cpp:238-243)
     const float scale = default_scale(D, 0.0f);
     const bool vt = use_vt(d);
     const int64_t ld_vt = vt ? sfg::attn_vt_ld(d->sequence) : 0;
-    if (!decode) {
+    // bf16 prefill: the QKV GEMM's epilogue writes the RoPE'd Q / K and V^T
+    // itself (split_qkv + apply_rope, decoder_compiler.cpp:96-148) when the
+    // direct-to-LDS path takes the shape; otherwise the product goes to fp32
+    // rows and the split + RoPE kernels follow.
+    sfg::GemmProblem qp{};
+    qp.a = b.xn; qp.a_dtype = act; qp.lda = H;
+    qp.b = w->w_qkv; qp.b_dtype = wdt; qp.ldb = H; qp.b_scales = w->s_qkv;
+    qp.m = rows; qp.n = qkvw; qp.k = H; qp.epilogue = sfg::kEpiQkvRope; qp.groups = 1;
+    qp.b_layout = d->weight_layout;
+    qp.qkv = sfg::QkvRopeOut{reinterpret_cast<const float2*>(w->rope_table), d->sequence, d->query_heads,
+                             d->kv_heads, static_cast<uint16_t*>(b.q), static_cast<uint16_t*>(b.k),
+                             static_cast<uint16_t*>(b.v), ld_vt};
+    const bool fused_qkv = vt && !decode && sfg::gemm_qkv_rope_supported(qp);
+    if (fused_qkv) {
+        if (ld_vt != d->sequence) sfg::launch_fill_zero(b.v, static_cast<size_t>(d->batch) * kvd * ld_vt * 2, s);
+        const int r = sfg::launch_gemm(qp, b.gemm_ws, b.gemm_ws_bytes, s);
+        if (r != SFG_OK) return fail(r, "decoder layer QKV GEMM with RoPE epilogue not lowered");
+    } else if ((rc = gemm(b.xn, H, w->w_qkv, w->s_qkv, b.qkv, SFG_F32, nullptr, rows, qkvw, H, SFG_EPI_NONE))) {
+        return rc;
+    }
+    mk.mark(SFG_MARK_QKV);
+    // 3. split + RoPE (decode keeps only Q: the step's K/V are discarded,
+    //    decoder_compiler.cpp:238-243)
+    if (!decode && !fused_qkv) {
         sfg::launch_split_rope(b.qkv, w->rope_table, d->batch, d->sequence, d->query_heads,
                                d->kv_heads, D, b.q, b.k, vt ? nullptr : b.v, act, s);
         if (vt)

@@ -269,6 +269,7 @@ struct TiledArgs {
     int64_t m, n, k;
     const int32_t* offsets;   // grouped: tiles per group = ceil(rows_g / 128)
     int groups;
+    QkvRopeOut qkv;           // kEpiQkvRope only
 };
 
 constexpr int kTM = 128, kTN = 128, kTK = 32;
@@ -618,6 +619,87 @@ __global__ __launch_bounds__(256) void gemm_mfma256_kernel(TiledArgs p, int tile
 }
 
 // ===========================================================================
+// QKV epilogue for the bf16 prefill (split_qkv + apply_rope,
+// decoder_compiler.cpp:96-148, plus the transposed V the flash prefill reads):
+// the [rows][H + 2 Hkv 128] product is never stored.  Column c of the
+// accumulator lives in lane c % 32; RoPE pairs (2i, 2i+1) are neighbouring
+// lanes of one row, so one lane exchange gives each lane its partner, and the
+// rotation is split_rope_kernel's expression (same table, same float ops).
+// Every 32-column block lies inside one head, so the Q / K / V choice is
+// uniform per block.  A lane's four consecutive rows (r % 4) are four
+// consecutive tokens of one sequence (S % 4 == 0, checked on the host), so
+// V^T takes one 8-byte store per lane and block.
+// ===========================================================================
+template <int WM, int WN>
+__device__ __forceinline__ void qkv_rope_epilogue(const QkvRopeOut& o, const floatx16 (&acc)[WM][WN],
+                                                  int64_t wave_row0, int64_t wave_col0, int64_t re,
+                                                  int64_t n, int l32, int khalf) {
+    const int64_t H = static_cast<int64_t>(o.q_heads) * 128;
+    const int64_t kvd = static_cast<int64_t>(o.kv_heads) * 128;
+    const int seq = static_cast<int>(o.seq);
+#pragma unroll
+    for (int i = 0; i < WM; ++i) {
+        // One 32-row block: positions and (cos, sin) of all its rows and this
+        // lane's columns are fetched first, so the block waits for the table
+        // once instead of once per element.
+        int bq[4], sq[4];
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+            const int rr = static_cast<int>(wave_row0 + i * 32 + 8 * rq + 4 * khalf);
+            bq[rq] = rr / seq;
+            sq[rq] = rr - bq[rq] * seq;
+        }
+        float2 cs[WN][4][4];
+#pragma unroll
+        for (int j = 0; j < WN; ++j) {
+            const int64_t col = wave_col0 + j * 32 + l32;
+            const bool rot = col < H + kvd;  // uniform over the 32-column block
+            const int pr = static_cast<int>(col & 127) >> 1;
+#pragma unroll
+            for (int rq = 0; rq < 4; ++rq)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    cs[j][rq][e] = rot ? o.rope[static_cast<int64_t>(sq[rq] + e) * 64 + pr] : make_float2(1.f, 0.f);
+        }
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+            const int64_t row = wave_row0 + i * 32 + 8 * rq + 4 * khalf;  // rows row .. row + 3
+            const int b = bq[rq], s0 = sq[rq];
+#pragma unroll
+            for (int j = 0; j < WN; ++j) {
+                const int64_t col = wave_col0 + j * 32 + l32;
+                float v[4], pv[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    v[e] = acc[i][j][4 * rq + e];
+                    pv[e] = __shfl_xor(v[e], 1, 64);
+                }
+                if (col >= n || row >= re) continue;
+                const int d = static_cast<int>(col & 127);
+                if (col < H + kvd) {
+                    uint16_t* dst = col < H
+                        ? o.q + ((static_cast<int64_t>(b) * o.q_heads + (col >> 7)) * seq + s0) * 128 + d
+                        : o.k + ((static_cast<int64_t>(b) * o.kv_heads + ((col - H) >> 7)) * seq + s0) * 128 + d;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float2 c = cs[j][rq][e];
+                        // (even, odd) -> (even c - odd s, even s + odd c)
+                        const float r0 = (d & 1) ? pv[e] * c.y + v[e] * c.x : v[e] * c.x - pv[e] * c.y;
+                        dst[e * 128] = f32_to_bf16(r0);
+                    }
+                } else {
+                    const int64_t hv = (col - H - kvd) >> 7;
+                    uint2 pk;
+                    pk.x = pack_bf16x2(v[0], v[1]);
+                    pk.y = pack_bf16x2(v[2], v[3]);
+                    *reinterpret_cast<uint2*>(o.vt + ((static_cast<int64_t>(b) * o.kv_heads + hv) * 128 + d) * o.ld_vt + s0) = pk;
+                }
+            }
+        }
+    }
+}
+
+// ===========================================================================
 // Large-M MFMA GEMM, third generation (bf16 operands): BM x BN output tile per
 // workgroup, four waves in a 2 x 2 grid, each owning a (BM/2) x (BN/2) block of
 // v_mfma_f32_32x32x16_bf16 tiles (accumulators in the AccVGPRs).
@@ -930,6 +1012,7 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
     for (int i = 0; i < WM; ++i) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
+            if constexpr (EPI == kEpiQkvRope) break;
             const int64_t row = row0 + wm * (BM / kWavesM) + i * 32 + 8 * (r >> 2) + 4 * khalf + (r & 3);
             if (row >= re) continue;
             if (kGlu) {
@@ -945,7 +1028,7 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
                     }
                     store_out(p.c, p.c_dtype, row * p.ldc + col, glu_combine(EPI, gv, uv));
                 }
-            } else {
+            } else if constexpr (EPI != kEpiQkvRope) {
 #pragma unroll
                 for (int j = 0; j < WN; ++j) {
                     const int64_t col = ncol0 + wn * (BN / kWavesN) + j * 32 + l32;
@@ -958,6 +1041,9 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
             }
         }
     }
+    if constexpr (EPI == kEpiQkvRope) qkv_rope_epilogue<WM, WN>(p.qkv, acc, row0 + wm * (BM / kWavesM),
+                                                               ncol0 + wn * (BN / kWavesN), re, p.n,
+                                                               l32, khalf);
 }
 
 // ===========================================================================
@@ -1112,6 +1198,7 @@ void launch_dma_b(const TiledArgs& a, dim3 grid, int tm, int tn, int epi, hipStr
         case SFG_EPI_NONE: gemm_dma_kernel<BM, BN, NW, SFG_EPI_NONE, PP><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
         case SFG_EPI_RESIDUAL: gemm_dma_kernel<BM, BN, NW, SFG_EPI_RESIDUAL, PP><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
         case SFG_EPI_SWIGLU: gemm_dma_kernel<BM, BN, NW, SFG_EPI_SWIGLU, PP><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
+        case kEpiQkvRope: gemm_dma_kernel<BM, BN, NW, kEpiQkvRope, PP><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
         default: gemm_dma_kernel<BM, BN, NW, SFG_EPI_GLU_SILU_UP, PP><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
     }
 }
@@ -1156,6 +1243,17 @@ constexpr int64_t kBigMinRows = 1024;
 
 }  // namespace
 
+bool gemm_qkv_rope_supported(const GemmProblem& p) {
+    const QkvRopeOut& o = p.qkv;
+    return p.a_dtype == SFG_BF16 && p.b_dtype == SFG_BF16 && !p.offsets && !p.a_rows &&
+           p.b_layout == SFG_LAYOUT_NK && p.m >= kBigMinRows && p.k % kGK == 0 && o.rope && o.q &&
+           o.k && o.vt && o.seq > 0 && o.seq % 4 == 0 && p.m % o.seq == 0 && o.q_heads > 0 &&
+           o.kv_heads > 0 && p.n == (static_cast<int64_t>(o.q_heads) + 2 * o.kv_heads) * 128 &&
+           o.ld_vt % 64 == 0 && o.ld_vt >= o.seq &&
+           static_cast<uint64_t>(p.m) * p.lda * 2 <= 0xFFFFFFFFull &&
+           static_cast<uint64_t>(p.n) * p.ldb * 2 <= 0xFFFFFFFFull;
+}
+
 int gemm_preferred_layout(int64_t rows, int64_t k, bool grouped) {
     const bool skinny = k % kSkinnyChunk == 0 &&
                         (grouped ? rows <= kSkinnyGroupedMaxTotal : rows <= kSkinnyMaxRows);
@@ -1169,6 +1267,7 @@ size_t gemm_workspace_bytes(int64_t m, int64_t n, int64_t k) {
 
 int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes, hipStream_t stream) {
     const bool glu = is_glu(p.epilogue);
+    if (p.epilogue == kEpiQkvRope && !gemm_qkv_rope_supported(p)) return SFG_ERR_UNSUPPORTED;
     if (p.a_dtype == SFG_F32) {
         if (p.b_dtype != SFG_F32 || p.offsets || p.a_rows || p.b_layout != SFG_LAYOUT_NK)
             return SFG_ERR_UNSUPPORTED;
@@ -1224,6 +1323,7 @@ int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes, h
     a.c = p.c; a.c_dtype = p.c_dtype; a.ldc = p.ldc;
     a.residual = p.residual; a.ldr = p.ldr;
     a.m = p.m; a.n = p.n; a.k = p.k; a.offsets = p.offsets; a.groups = groups;
+    a.qkv = p.qkv;
     // the direct-to-LDS kernel addresses each operand with 32-bit byte offsets
     const bool fits32 = static_cast<uint64_t>(a.a_rows_limit) * p.lda * 2 <= 0xFFFFFFFFull &&
                         static_cast<uint64_t>(glu ? 2 : 1) * p.n * p.ldb * 2 <= 0xFFFFFFFFull;

@@ -25,6 +25,16 @@ void launch_quantize_weight(const float* src, int64_t k, int64_t n, int8_t* dst,
 void launch_to_bf16(const float* src, uint16_t* dst, int64_t count, hipStream_t stream);
 void launch_fill_zero(void* dst, size_t bytes, hipStream_t stream);
 
+// QKV-projection epilogue of the bf16 prefill (kEpiQkvRope): RoPE'd Q / K as
+// [B][H*][S][128] bf16 and V^T [B][Hkv][128][ld_vt] bf16, the product itself
+// never stored.  Needs the direct-to-LDS GEMM path (gemm_qkv_rope_supported).
+constexpr int kEpiQkvRope = 16;
+struct QkvRopeOut {
+    const float2* rope;          // [S][64] (cos, sin)
+    int64_t seq; int q_heads, kv_heads;
+    uint16_t* q; uint16_t* k; uint16_t* vt; int64_t ld_vt;
+};
+
 // GEMM family.  A grouped problem: `groups` independent products sharing N, K;
 // group g covers rows [row_begin(g), row_end(g)) of the (virtual) row space,
 // given by `offsets` (device, groups+1 entries) or a single dense group.  A's
@@ -43,8 +53,10 @@ struct GemmProblem {
     int b_layout;               // SFG_LAYOUT_NK or SFG_LAYOUT_TILED
     const int32_t* offsets;     // grouped: device [groups+1]; nullptr = dense
     int groups;
+    QkvRopeOut qkv;             // epilogue kEpiQkvRope only
 };
 
+bool gemm_qkv_rope_supported(const GemmProblem& p);
 size_t gemm_workspace_bytes(int64_t m, int64_t n, int64_t k);
 // The layout launch_gemm reads fastest for these rows (see sfg_layout).
 int gemm_preferred_layout(int64_t rows, int64_t k, bool grouped);

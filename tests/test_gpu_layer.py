@@ -87,3 +87,17 @@ def test_layer_reduced_w8_dense():
     err = oracle.rel_error(res.output, ref)
     print(f"c2-small w8 dense: rel_err {err:.3e}")
     assert err < TOL["w8"], err
+
+
+@pytest.mark.parametrize("batch,seq", [(2, 600), (1, 1024)])
+def test_layer_prefill_fused_qkv_rope_matches_oracle(batch, seq):
+    """Prefill with >= 1024 rows: the QKV GEMM's epilogue writes the RoPE'd Q / K
+    and V^T directly (seq 600 also exercises the zeroed key padding of V^T, whose
+    row stride rounds up to 640)."""
+    cfg = CONFIGS["c4"].replace(batch=batch, sequence=seq, hidden=1024, intermediate=2048,
+                                query_heads=8, kv_heads=2)
+    res, ref, _ = _run(cfg, CONFIG_SEEDS["c4"] + 11 + seq, reps=1)
+    err = oracle.rel_error(res.output, ref)
+    print(f"fused-qkv prefill B{batch} S{seq}: rel_err {err:.3e}")
+    assert np.isfinite(res.output).all()
+    assert err < TOL[cfg.dtype], err
