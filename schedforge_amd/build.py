@@ -74,17 +74,17 @@ def build_runtime() -> Path:
     """libsfg_decoder.so + sfg-decoder from runtime/*.cpp."""
     BUILD.mkdir(exist_ok=True)
     BINDIR.mkdir(exist_ok=True)
-    lib_obj = BUILD / "sfg_decoder.o"
+    lib_objs = [BUILD / "sfg_decoder.o", BUILD / "sfg_package.o"]
     cli_obj = BUILD / "sfg_decoder_cli.o"
-    with cf.ThreadPoolExecutor(max_workers=2) as pool:
-        jobs = [pool.submit(_run, [CXX, *HOST_FLAGS, "-c", str(RUNTIME / "sfg_decoder.cpp"), "-o",
-                                   str(lib_obj)], "g++ sfg_decoder.cpp"),
-                pool.submit(_run, [CXX, *HOST_FLAGS, "-c", str(RUNTIME / "sfg_decoder_cli.cpp"), "-o",
-                                   str(cli_obj)], "g++ sfg_decoder_cli.cpp")]
+    units = [(RUNTIME / "sfg_decoder.cpp", lib_objs[0]), (RUNTIME / "sfg_package.cpp", lib_objs[1]),
+             (RUNTIME / "sfg_decoder_cli.cpp", cli_obj)]
+    with cf.ThreadPoolExecutor(max_workers=len(units)) as pool:
+        jobs = [pool.submit(_run, [CXX, *HOST_FLAGS, "-c", str(src), "-o", str(obj)], f"g++ {src.name}")
+                for src, obj in units]
         for j in jobs:
             j.result()
     tmp = RUNTIME_LIB.with_suffix(".so.tmp")
-    _run([CXX, "-shared", "-o", str(tmp), str(lib_obj), *HIP_LINK], "link libsfg_decoder.so")
+    _run([CXX, "-shared", "-o", str(tmp), *map(str, lib_objs), *HIP_LINK], "link libsfg_decoder.so")
     os.replace(tmp, RUNTIME_LIB)
     tmp_cli = DECODER_CLI.with_suffix(".tmp")
     _run([CXX, "-o", str(tmp_cli), str(cli_obj), f"-L{LIBDIR}", "-lsfg_decoder",

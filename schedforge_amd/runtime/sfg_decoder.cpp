@@ -7,6 +7,7 @@
 //   library loading    aot_runtime.cpp:152-196, 259 (dlopen, dlsym, metadata check)
 //   paged KV           next_milestones.cpp:29-33, 472-581 (page -> physical slot)
 #include "sfg_decoder.hpp"
+#include "sfg_runtime_internal.hpp"
 
 #include <dlfcn.h>
 #include <hip/hip_runtime_api.h>
@@ -24,69 +25,6 @@
 namespace schedforge::hip {
 namespace {
 
-// ---------------------------------------------------------------- library
-
-// Function table of libsfg_hip.so, resolved once per process.
-class Library {
-public:
-    decltype(&sfg_hip_abi_version) abi_version = nullptr;
-    decltype(&sfg_hip_metadata_v1) metadata = nullptr;
-    decltype(&sfg_hip_last_error) last_error = nullptr;
-    decltype(&sfg_hip_device_info_v1) device_info = nullptr;
-    decltype(&sfg_hip_pack_weight_v1) pack_weight = nullptr;
-    decltype(&sfg_hip_quantize_weight_v1) quantize_weight = nullptr;
-    decltype(&sfg_hip_preferred_weight_layout_v1) preferred_layout = nullptr;
-    decltype(&sfg_hip_rope_table_host_v1) rope_table = nullptr;
-    decltype(&sfg_hip_decoder_layer_workspace_v1) layer_workspace = nullptr;
-    decltype(&sfg_hip_decoder_layer_v1) layer = nullptr;
-    decltype(&sfg_hip_events_create_v1) events_create = nullptr;
-    decltype(&sfg_hip_events_destroy_v1) events_destroy = nullptr;
-    decltype(&sfg_hip_event_elapsed_v1) event_elapsed = nullptr;
-    std::string path;
-
-    explicit Library(const std::filesystem::path& file) : path(file.string()) {
-        handle_ = dlopen(path.c_str(), RTLD_NOW | RTLD_LOCAL);
-        if (!handle_) throw std::runtime_error(std::string("cannot load libsfg_hip.so: ") + dlerror());
-        bind(abi_version, "sfg_hip_abi_version");
-        bind(metadata, "sfg_hip_metadata_v1");
-        bind(last_error, "sfg_hip_last_error");
-        bind(device_info, "sfg_hip_device_info_v1");
-        bind(pack_weight, "sfg_hip_pack_weight_v1");
-        bind(quantize_weight, "sfg_hip_quantize_weight_v1");
-        bind(preferred_layout, "sfg_hip_preferred_weight_layout_v1");
-        bind(rope_table, "sfg_hip_rope_table_host_v1");
-        bind(layer_workspace, "sfg_hip_decoder_layer_workspace_v1");
-        bind(layer, "sfg_hip_decoder_layer_v1");
-        bind(events_create, "sfg_hip_events_create_v1");
-        bind(events_destroy, "sfg_hip_events_destroy_v1");
-        bind(event_elapsed, "sfg_hip_event_elapsed_v1");
-        const std::string meta = metadata();
-        if (abi_version() != SFG_HIP_ABI_VERSION || meta.find("abi=1") == std::string::npos ||
-            meta.find("arch=gfx950") == std::string::npos)
-            throw std::runtime_error("libsfg_hip.so ABI or target mismatch: " + meta);
-    }
-    ~Library() {
-        if (handle_) dlclose(handle_);
-    }
-    Library(const Library&) = delete;
-    Library& operator=(const Library&) = delete;
-
-    // Status codes below 16 are the reference's std::invalid_argument class.
-    void check(int rc, const char* what) const {
-        if (rc == SFG_OK) return;
-        const std::string message = std::string(what) + ": " + last_error();
-        if (rc < SFG_ERR_DEVICE) throw std::invalid_argument(message);
-        throw std::runtime_error(message);
-    }
-
-private:
-    template <typename Fn>
-    void bind(Fn& fn, const char* name) {
-        fn = reinterpret_cast<Fn>(dlsym(handle_, name));
-        if (!fn) throw std::runtime_error(std::string("libsfg_hip.so lacks ") + name);
-    }
-    void* handle_ = nullptr;
-};
 
 // libsfg_hip.so beside the library (or executable) that holds this code.
 std::filesystem::path default_library_path() {
@@ -100,20 +38,6 @@ std::filesystem::path default_library_path() {
     throw std::runtime_error("libsfg_hip.so not found (set SFG_HIP_LIBRARY or build the package)");
 }
 
-std::shared_ptr<Library> load_library(const std::filesystem::path& requested) {
-    static std::mutex mutex;
-    static std::shared_ptr<Library> cached;
-    std::lock_guard lock(mutex);
-    const auto path = requested.empty() ? default_library_path() : requested;
-    if (cached && cached->path == path.string()) return cached;
-    cached = std::make_shared<Library>(path);
-    return cached;
-}
-
-void hip_check(hipError_t rc, const char* what) {
-    if (rc != hipSuccess)
-        throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(rc));
-}
 
 // ---------------------------------------------------------------- numerics
 
@@ -205,57 +129,16 @@ void require_size(const std::vector<float>& v, std::size_t expected, const char*
 
 }  // namespace
 
-// ---------------------------------------------------------------- device state
+std::shared_ptr<SfgHipLibrary> load_library(const std::filesystem::path& requested) {
+    static std::mutex mutex;
+    static std::shared_ptr<SfgHipLibrary> cached;
+    std::lock_guard lock(mutex);
+    const auto path = requested.empty() ? default_library_path() : requested;
+    if (cached && cached->path == path.string()) return cached;
+    cached = std::make_shared<SfgHipLibrary>(path);
+    return cached;
+}
 
-struct DeviceBuffer {
-    void* ptr = nullptr;
-    std::size_t bytes = 0;
-    DeviceBuffer() = default;
-    explicit DeviceBuffer(std::size_t n) : bytes(n) {
-        if (n) hip_check(hipMalloc(&ptr, n), "hipMalloc");
-    }
-    ~DeviceBuffer() {
-        if (ptr) (void)hipFree(ptr);
-    }
-    DeviceBuffer(DeviceBuffer&& other) noexcept : ptr(other.ptr), bytes(other.bytes) {
-        other.ptr = nullptr;
-        other.bytes = 0;
-    }
-    DeviceBuffer& operator=(DeviceBuffer&& other) noexcept {
-        std::swap(ptr, other.ptr);
-        std::swap(bytes, other.bytes);
-        return *this;
-    }
-    DeviceBuffer(const DeviceBuffer&) = delete;
-    DeviceBuffer& operator=(const DeviceBuffer&) = delete;
-    template <typename T>
-    T* as() const { return static_cast<T*>(ptr); }
-};
-
-struct DecoderExecutablePlan::Device {
-    std::shared_ptr<Library> lib;
-    int ordinal = 0;
-    hipStream_t stream = nullptr;
-    sfg_layer_desc desc{};
-    sfg_layer_weights weights{};
-    std::vector<std::pair<std::string, DeviceBuffer>> buffers;
-    DeviceBuffer workspace;
-    DeviceBuffer trace_ids, trace_weights;
-    std::mutex mutex;  // one execution of a plan at a time (shared stream and workspace)
-
-    ~Device() {
-        buffers.clear();
-        if (stream) (void)hipStreamDestroy(stream);
-    }
-    void* add(const std::string& name, std::size_t bytes) {
-        buffers.emplace_back(name, DeviceBuffer(bytes));
-        return buffers.back().second.ptr;
-    }
-    void upload(void* dst, const void* src, std::size_t bytes) {
-        hip_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream), "hipMemcpyAsync");
-    }
-    void sync() { hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize"); }
-};
 
 DecoderExecutablePlan::DecoderExecutablePlan() = default;
 DecoderExecutablePlan::~DecoderExecutablePlan() {
@@ -550,7 +433,9 @@ std::vector<std::uint16_t> build_pool(const DecoderConfig& c, const std::vector<
     return pool;
 }
 
-std::string describe_hardware(const Library& lib, int ordinal) {
+}  // namespace
+
+std::string describe_hardware(const SfgHipLibrary& lib, int ordinal) {
     hipDeviceProp_t prop{};
     hip_check(hipGetDeviceProperties(&prop, ordinal), "hipGetDeviceProperties");
     int cus = 0, xcds = 0;
@@ -562,7 +447,42 @@ std::string describe_hardware(const Library& lib, int ordinal) {
     return out.str();
 }
 
-}  // namespace
+void fill_layer_desc(sfg_layer_desc& d, const DecoderConfig& c, int kv_splits, int layout,
+                     int pages_per_seq, int num_pages, bool use_routing_trace) {
+    d = sfg_layer_desc{};
+    d.abi = SFG_HIP_ABI_VERSION;
+    d.batch = c.batch;
+    d.sequence = c.sequence;
+    d.hidden = c.hidden;
+    d.intermediate = c.intermediate;
+    d.query_heads = c.query_heads;
+    d.kv_heads = c.kv_heads;
+    d.head_dim = c.head_dim;
+    d.rms_epsilon = c.rms_epsilon;
+    d.rope_theta = c.rope_theta;
+    d.causal = c.causal ? 1 : 0;
+    d.ffn = c.ffn == DecoderFFNKind::MoE ? 1 : 0;
+    d.experts = c.experts;
+    d.top_k = c.top_k;
+    d.context = c.context_sequence;
+    d.page_tokens = c.page_tokens;
+    d.pages_per_seq = pages_per_seq;
+    d.num_pages = num_pages;
+    d.act_dtype = c.precision == DecoderPrecision::F32 ? SFG_F32 : SFG_BF16;
+    d.weight_dtype = weight_dtype(c.precision);
+    d.kv_splits = kv_splits;
+    d.use_routing_trace = use_routing_trace ? 1 : 0;
+    d.weight_layout = layout;
+}
+
+std::size_t allocate_workspace(DecoderExecutablePlan::Device& dev) {
+    const std::size_t ws = dev.lib->layer_workspace(&dev.desc);
+    if (ws == 0) dev.lib->check(SFG_ERR_INVALID_CONFIG, "decoder layer workspace");
+    dev.workspace = DeviceBuffer(ws);
+    hip_check(hipMemsetAsync(dev.workspace.ptr, 0, ws, dev.stream), "hipMemsetAsync");
+    dev.sync();
+    return ws;
+}
 
 DecoderExecutablePlan DecoderCompiler::compile(const DecoderConfig& config, const DecoderData& data,
                                                DecoderCompileOptions options) const {
@@ -726,36 +646,9 @@ DecoderExecutablePlan DecoderCompiler::compile(const DecoderConfig& config, cons
         dev.upload(dev.trace_weights.ptr, t.expert_weights.data(), t.expert_weights.size() * 4);
     }
 
-    sfg_layer_desc& d = dev.desc;
-    d.abi = SFG_HIP_ABI_VERSION;
-    d.batch = c.batch;
-    d.sequence = c.sequence;
-    d.hidden = c.hidden;
-    d.intermediate = c.intermediate;
-    d.query_heads = c.query_heads;
-    d.kv_heads = c.kv_heads;
-    d.head_dim = c.head_dim;
-    d.rms_epsilon = c.rms_epsilon;
-    d.rope_theta = c.rope_theta;
-    d.causal = c.causal ? 1 : 0;
-    d.ffn = moe ? 1 : 0;
-    d.experts = c.experts;
-    d.top_k = c.top_k;
-    d.context = c.context_sequence;
-    d.page_tokens = c.page_tokens;
-    d.pages_per_seq = pages_per_seq;
-    d.num_pages = num_pages;
-    d.act_dtype = c.precision == DecoderPrecision::F32 ? SFG_F32 : SFG_BF16;
-    d.weight_dtype = weight_dtype(c.precision);
-    d.kv_splits = options.kv_splits;
-    d.use_routing_trace = data.routing_trace ? 1 : 0;
-    d.weight_layout = layout;
-
-    const std::size_t ws = dev.lib->layer_workspace(&d);
-    if (ws == 0) dev.lib->check(SFG_ERR_INVALID_CONFIG, "decoder layer workspace");
-    dev.workspace = DeviceBuffer(ws);
-    hip_check(hipMemsetAsync(dev.workspace.ptr, 0, ws, dev.stream), "hipMemsetAsync");
-    dev.sync();
+    fill_layer_desc(dev.desc, c, options.kv_splits, layout, pages_per_seq, num_pages,
+                    data.routing_trace.has_value());
+    const std::size_t ws = allocate_workspace(dev);
 
     plan.memory.workspace_bytes = ws;
     for (const auto& constant : plan.constants) plan.memory.constant_bytes += constant.bytes;

@@ -195,6 +195,90 @@ DecoderBenchmarkResult execute_decoder_layer(const DecoderExecutablePlan& plan,
                                              int repetitions = 5,
                                              const std::vector<float>* expected = nullptr);
 
+// ---------------------------------------------------------------- .sfe packages
+//
+// A compiled plan as an inspectable directory with a .sfe suffix, after the
+// reference's AOT package format 1 (src/aot_runtime.cpp:217-316,
+// docs/AOT_DEPLOYMENT.md:6-35), carrying what a GPU plan needs:
+//   manifest.sfe      key=value: format, ABI, target, configuration, policy,
+//                     buffer table, file and code-object checksums
+//   plan.sfe          DecoderExecutablePlan::dump()
+//   libsfg_hip.so     the host + device library the plan was compiled against
+//   kernels/NN.gfx950.hsaco  the gfx950 code objects embedded in that library
+//                     (the ones the HIP runtime loads), one per translation unit
+//   constants.bin     device bytes of every plan buffer (packed weights, int8
+//                     scales, RoPE table, page table, paged K/V pools, routing
+//                     trace) at 256-byte aligned offsets
+// Checksums are FNV-1a 64-bit as 16 hex digits (aot_runtime.cpp:26-35).
+// Loading validates the format version, ABI, target, every checksum, the
+// library's embedded metadata (sfg_hip_metadata_v1 and its ABI version) and
+// that the library's embedded code objects are the packaged ones, then the
+// device architecture; any mismatch throws std::runtime_error, with no
+// fallback to recompilation.  Nothing is recompiled on load.
+struct DecoderPackageFile {
+    std::string path;  // relative to the package directory
+    std::size_t bytes = 0;
+    std::string checksum;
+};
+struct DecoderPackageCodeObject {
+    DecoderPackageFile file;
+    std::string target_id;  // offload bundle id, e.g. hipv4-amdgcn-amd-amdhsa--gfx950
+};
+struct DecoderPackageBuffer {
+    std::string name;
+    std::size_t offset = 0;
+    std::size_t bytes = 0;
+    std::string checksum;
+};
+struct DecoderPackageManifest {
+    int format_version = 1;
+    std::string schedforge_version;
+    std::string abi;     // sfg_hip_decoder_layer_v1
+    std::string symbol;  // the entry point resolved in the packaged library
+    std::string target;  // gfx950
+    int library_abi = 0;
+    std::string library_metadata;
+    DecoderConfig config;
+    int weight_layout = SFG_LAYOUT_NK;
+    int kv_splits = 0;
+    int pages_per_seq = 0;
+    int num_pages = 0;
+    bool routing_trace = false;
+    std::size_t workspace_bytes = 0;
+    std::size_t naive_bytes = 0;
+    DecoderPackageFile plan, library, constants;
+    std::vector<DecoderPackageCodeObject> code_objects;
+    std::vector<DecoderPackageBuffer> buffers;
+    std::vector<DecoderConstant> constant_table;
+
+    std::string dump() const;
+    // Throws std::runtime_error on an unknown format, ABI or a missing,
+    // duplicate or malformed field (aot_runtime.cpp:97-121, 167-199).
+    static DecoderPackageManifest parse(const std::string& text);
+};
+
+// FNV-1a 64-bit of a byte range as 16 lower-case hex digits.
+std::string package_checksum(const void* data, std::size_t bytes);
+
+// The gfx950 code objects inside a library's .hip_fatbin section, in link order
+// (ELF section table, then the clang offload bundles it holds).
+struct EmbeddedCodeObject {
+    std::string target_id;
+    std::vector<unsigned char> bytes;
+};
+std::vector<EmbeddedCodeObject> embedded_code_objects(const std::filesystem::path& library);
+
+// Writes `plan` to `path` (which must end in .sfe) through a temporary
+// directory renamed into place; returns the manifest written.
+DecoderPackageManifest save_decoder_package(const DecoderExecutablePlan& plan,
+                                            const std::filesystem::path& path);
+// Validates a package without touching a GPU: manifest, file checksums, the
+// packaged library's embedded metadata and code objects.
+DecoderPackageManifest inspect_decoder_package(const std::filesystem::path& path);
+// inspect_decoder_package, then the device's architecture, then the buffers
+// uploaded to `device` and the plan rebuilt around the packaged library.
+DecoderExecutablePlan load_decoder_package(const std::filesystem::path& path, int device = 0);
+
 // Seeded synthetic inputs: a counter-based generator (SplitMix64 keyed by
 // seed and tensor id, Box-Muller in double) with activations N(0,1), weights
 // N(0,0.02), norm gains 1, cached K/V N(0,1), router bias N(0,router_bias_std)

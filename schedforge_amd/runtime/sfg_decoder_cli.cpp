@@ -14,6 +14,12 @@
 //   --dump-output=FILE       raw fp32 output
 //   --dump-data=DIR          write the generated inputs as raw files and exit
 //                            without touching the GPU
+//   --package=DIR.sfe        also write the compiled plan as a .sfe GPU package
+//   --load-package=DIR.sfe   run a packaged plan instead of compiling (shape
+//                            options are taken from its manifest; --seed
+//                            selects the input)
+//   --inspect=DIR.sfe        validate a package without a GPU and print its
+//                            manifest and plan (schedforge-aot inspect)
 #include "sfg_decoder.hpp"
 
 #include <algorithm>
@@ -39,6 +45,7 @@ struct Options {
     int repetitions = 3;
     std::string output = "decoder_layer.sfe";
     std::string expect, dump_output, dump_data;
+    std::string package, load_package, inspect;
     double max_relative_error = 1.0e-3;
 };
 
@@ -86,6 +93,9 @@ Options parse(int argc, char** argv) {
         else if (auto v = value(a, "--max-error=")) o.max_relative_error = std::stod(*v);
         else if (auto v = value(a, "--dump-output=")) o.dump_output = *v;
         else if (auto v = value(a, "--dump-data=")) o.dump_data = *v;
+        else if (auto v = value(a, "--package=")) o.package = *v;
+        else if (auto v = value(a, "--load-package=")) o.load_package = *v;
+        else if (auto v = value(a, "--inspect=")) o.inspect = *v;
         else if (a == "--moe") c.ffn = sh::DecoderFFNKind::MoE;
         else if (a == "--non-causal") c.causal = false;
         else if (a == "-o" && i + 1 < argc) o.output = argv[++i];
@@ -95,7 +105,8 @@ Options parse(int argc, char** argv) {
                          "  [--moe --experts=4 --top-k=2 --router-bias-std=0] [--context=0 --page-tokens=16]\n"
                          "  [--precision=f32|bf16|w8 --kv-splits=0 --device=0 --seed=71]\n"
                          "  [--warmup=1 --repetitions=3 --non-causal] [-o decoder.sfe]\n"
-                         "  [--expect=FILE --max-error=1e-3 --dump-output=FILE --dump-data=DIR]\n";
+                         "  [--expect=FILE --max-error=1e-3 --dump-output=FILE --dump-data=DIR]\n"
+                         "  [--package=DIR.sfe | --load-package=DIR.sfe | --inspect=DIR.sfe]\n";
             std::exit(0);
         } else {
             throw std::invalid_argument("unknown option: " + a);
@@ -129,7 +140,21 @@ std::vector<float> read_floats(const std::string& path, std::size_t count) {
 
 int main(int argc, char** argv) {
     try {
-        const Options o = parse(argc, argv);
+        Options o = parse(argc, argv);
+        if (!o.inspect.empty()) {
+            const auto m = sh::inspect_decoder_package(o.inspect);
+            std::cout << "[Manifest]\n" << m.dump() << "\n[Plan]\n"
+                      << std::ifstream(std::filesystem::path(o.inspect) / m.plan.path).rdbuf()
+                      << "\n[Validation]\npackage valid: " << m.code_objects.size()
+                      << " code objects, " << m.buffers.size() << " buffers, " << m.constants.bytes
+                      << " constant bytes\n";
+            return 0;
+        }
+        std::optional<sh::DecoderExecutablePlan> loaded;
+        if (!o.load_package.empty()) {
+            loaded.emplace(sh::load_decoder_package(o.load_package, o.compile.device));
+            o.config = loaded->config;
+        }
         sh::validate(o.config);
         const auto data = sh::make_decoder_data(o.config, o.seed, o.router_bias_std);
         if (!o.dump_data.empty()) {
@@ -154,8 +179,13 @@ int main(int argc, char** argv) {
             std::cout << "wrote generated inputs to " << d << '\n';
             return 0;
         }
-        const auto plan = sh::DecoderCompiler{}.compile(o.config, data, o.compile);
+        const auto plan = loaded ? std::move(*loaded) : sh::DecoderCompiler{}.compile(o.config, data, o.compile);
         plan.save(o.output);
+        if (!o.package.empty()) {
+            const auto m = sh::save_decoder_package(plan, o.package);
+            std::cout << "[Package]\n" << o.package << ": " << m.code_objects.size() << " code objects, "
+                      << m.buffers.size() << " buffers, " << m.constants.bytes << " constant bytes\n\n";
+        }
         std::vector<float> expected;
         if (!o.expect.empty())
             expected = read_floats(o.expect, static_cast<std::size_t>(o.config.rows()) * o.config.hidden);
