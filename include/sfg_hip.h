@@ -64,6 +64,23 @@ enum sfg_dtype { SFG_F32 = 0, SFG_BF16 = 1, SFG_I8 = 2 };
 
 enum sfg_layout { SFG_LAYOUT_NK = 0, SFG_LAYOUT_TILED = 1 };
 
+/* Output tile of the bf16 direct-to-LDS GEMM family that runs the prefill
+ * projections and grouped expert GEMMs (bf16 weights, >= 1024 rows, k % 32 == 0).
+ * A plan policy, not a numeric choice: every tile gives bit-identical results
+ * (each output is one fp32 accumulation in k order).  Ignored by the other GEMM
+ * paths (skinny decode GEMV, fp32, int8 and small-M kernels).  The plan
+ * optimiser (ExecutablePlanOptimizer, decoder_compiler.cpp:750-861) searches it. */
+enum sfg_gemm_tile {
+    SFG_TILE_AUTO = 0,       /* the largest tile that still gives >= 512 workgroups */
+    SFG_TILE_256x256_PP = 1, /* eight waves as two ping-pong groups of four          */
+    SFG_TILE_256x256_W8 = 2, /* eight waves (2 x 4), 128 x 64 per wave               */
+    SFG_TILE_256x256_W4 = 3, /* four waves (2 x 2), 128 x 128 per wave               */
+    SFG_TILE_256x128 = 4,    /* four waves, two workgroups per CU                    */
+    SFG_TILE_128x256 = 5,
+    SFG_TILE_128x128 = 6,
+    SFG_TILE_COUNT = 7
+};
+
 enum sfg_epilogue {
     SFG_EPI_NONE = 0,      /* C = A B                                             */
     SFG_EPI_RESIDUAL = 1,  /* C = A B + R  (R fp32 [M][N]); decoder_compiler.cpp:256,277 */
@@ -123,6 +140,7 @@ typedef struct {
     int64_t m, n, k;
     int32_t epilogue;
     int32_t b_layout;   /* SFG_LAYOUT_NK or SFG_LAYOUT_TILED */
+    int32_t tile;       /* sfg_gemm_tile; SFG_TILE_AUTO (0) picks per shape */
 } sfg_gemm_args;
 size_t sfg_hip_gemm_workspace_v1(int64_t m, int64_t n, int64_t k);
 int sfg_hip_gemm_v1(const sfg_gemm_args* args, void* workspace, size_t workspace_bytes,
@@ -166,7 +184,8 @@ int sfg_hip_attn_prefill_vt_v1(const uint16_t* q, const uint16_t* k, const uint1
  * sequence), pools bf16: K [num_pages][Hkv][page_tokens][D], V
  * [num_pages][Hkv][D][page_tokens]; page_table
  * [B][pages_per_seq], seq_lens[B] (each <= pages_per_seq*page_tokens).  out
- * merged [B][Hq*D] in out_dtype.  kv_splits <= 0 picks a split count.  Page ids
+ * merged [B][Hq*D] in out_dtype.  head_dim 128 or 64, page_tokens 16, GQA group
+ * Hq/Hkv in {1, 2, 4, 8, 16}.  kv_splits <= 0 picks a split count.  Page ids
  * are validated on the host against num_pages only when validate_pages != 0
  * (this reads the table back and synchronises the stream). */
 size_t sfg_hip_attn_decode_workspace_v1(int64_t batch, int64_t q_heads, int64_t head_dim,
@@ -266,6 +285,11 @@ typedef struct {
                          * next_milestones.cpp:486-524; the page must already be in the
                          * table) and attention over the cache including it.  Not a
                          * reference mode: its outputs differ from execute_once's. */
+    int32_t gemm_tile;  /* sfg_gemm_tile of the prefill projection / expert GEMMs;
+                         * SFG_TILE_AUTO (0) picks per shape.  Same results for every
+                         * tile; a plan-policy knob searched by the plan optimiser. */
+    int32_t attn_waves; /* bf16 flash prefill (head_dim 128): 4 or 8 waves, i.e. 128 or
+                         * 256 query rows per workgroup; 0: 4.  Same results either way. */
 } sfg_layer_desc;
 
 typedef struct {

@@ -18,6 +18,9 @@ ABI_VERSION = 1
 F32, BF16, I8 = 0, 1, 2
 EPI_NONE, EPI_RESIDUAL, EPI_SWIGLU, EPI_GLU_SILU_UP = 0, 1, 2, 3
 LAYOUT_NK, LAYOUT_TILED = 0, 1
+# sfg_gemm_tile
+TILE_AUTO, TILE_256x256_PP, TILE_256x256_W8, TILE_256x256_W4, TILE_256x128, TILE_128x256, \
+    TILE_128x128, TILE_COUNT = range(8)
 
 (MARK_START, MARK_NORM1, MARK_QKV, MARK_ROPE, MARK_ATTN_MAIN, MARK_ATTN, MARK_OPROJ,
  MARK_NORM2, MARK_ROUTE, MARK_FFN_UP, MARK_FFN_DOWN, MARK_END, NUM_MARKS) = range(13)
@@ -48,7 +51,7 @@ class GemmArgs(ctypes.Structure):
         ("c", c_vp), ("c_dtype", c_i32), ("ldc", c_i64),
         ("residual", c_vp), ("ldr", c_i64),
         ("m", c_i64), ("n", c_i64), ("k", c_i64),
-        ("epilogue", c_i32), ("b_layout", c_i32),
+        ("epilogue", c_i32), ("b_layout", c_i32), ("tile", c_i32),
     ]
 
 
@@ -62,7 +65,7 @@ class LayerDesc(ctypes.Structure):
         ("context", c_i32), ("page_tokens", c_i32), ("pages_per_seq", c_i32),
         ("num_pages", c_i32), ("act_dtype", c_i32), ("weight_dtype", c_i32),
         ("kv_splits", c_i32), ("use_routing_trace", c_i32), ("weight_layout", c_i32),
-        ("kv_append", c_i32),
+        ("kv_append", c_i32), ("gemm_tile", c_i32), ("attn_waves", c_i32),
     ]
 
 

@@ -8,7 +8,7 @@ linked into schedforge_amd/lib/libsfg_hip.so.  Flags:
   -O3 -std=c++20 -fPIC
 The host runtime under runtime/ is plain C++20 (g++, the reference's own
 toolchain) against the HIP runtime API: schedforge_amd/lib/libsfg_decoder.so
-and the driver schedforge_amd/bin/sfg-decoder.
+and the drivers schedforge_amd/bin/sfg-decoder and sfg-decoder-bench.
 """
 from __future__ import annotations
 
@@ -28,6 +28,7 @@ RUNTIME = PKG / "runtime"
 BINDIR = PKG / "bin"
 RUNTIME_LIB = LIBDIR / "libsfg_decoder.so"
 DECODER_CLI = BINDIR / "sfg-decoder"
+BENCH_CLI = BINDIR / "sfg-decoder-bench"
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 CXX = os.environ.get("CXX", "g++")
 HOST_FLAGS = ["-std=c++20", "-O2", "-Wall", "-Wextra", "-fPIC", "-D__HIP_PLATFORM_AMD__",
@@ -71,25 +72,26 @@ def _run(cmd: list, what: str) -> None:
 
 
 def build_runtime() -> Path:
-    """libsfg_decoder.so + sfg-decoder from runtime/*.cpp."""
+    """libsfg_decoder.so + sfg-decoder + sfg-decoder-bench from runtime/*.cpp."""
     BUILD.mkdir(exist_ok=True)
     BINDIR.mkdir(exist_ok=True)
-    lib_objs = [BUILD / "sfg_decoder.o", BUILD / "sfg_package.o"]
-    cli_obj = BUILD / "sfg_decoder_cli.o"
-    units = [(RUNTIME / "sfg_decoder.cpp", lib_objs[0]), (RUNTIME / "sfg_package.cpp", lib_objs[1]),
-             (RUNTIME / "sfg_decoder_cli.cpp", cli_obj)]
+    lib_srcs = ["sfg_decoder", "sfg_package", "sfg_optimizer"]
+    clis = {"sfg_decoder_cli": DECODER_CLI, "sfg_decoder_bench_cli": BENCH_CLI}
+    units = [(RUNTIME / f"{n}.cpp", BUILD / f"{n}.o") for n in [*lib_srcs, *clis]]
     with cf.ThreadPoolExecutor(max_workers=len(units)) as pool:
         jobs = [pool.submit(_run, [CXX, *HOST_FLAGS, "-c", str(src), "-o", str(obj)], f"g++ {src.name}")
                 for src, obj in units]
         for j in jobs:
             j.result()
     tmp = RUNTIME_LIB.with_suffix(".so.tmp")
-    _run([CXX, "-shared", "-o", str(tmp), *map(str, lib_objs), *HIP_LINK], "link libsfg_decoder.so")
+    _run([CXX, "-shared", "-o", str(tmp), *(str(BUILD / f"{n}.o") for n in lib_srcs), *HIP_LINK],
+         "link libsfg_decoder.so")
     os.replace(tmp, RUNTIME_LIB)
-    tmp_cli = DECODER_CLI.with_suffix(".tmp")
-    _run([CXX, "-o", str(tmp_cli), str(cli_obj), f"-L{LIBDIR}", "-lsfg_decoder",
-          "-Wl,-rpath,$ORIGIN/../lib", *HIP_LINK], "link sfg-decoder")
-    os.replace(tmp_cli, DECODER_CLI)
+    for name, exe in clis.items():
+        tmp_cli = exe.with_suffix(".tmp")
+        _run([CXX, "-o", str(tmp_cli), str(BUILD / f"{name}.o"), f"-L{LIBDIR}", "-lsfg_decoder",
+              "-Wl,-rpath,$ORIGIN/../lib", *HIP_LINK], f"link {exe.name}")
+        os.replace(tmp_cli, exe)
     return DECODER_CLI
 
 

@@ -175,8 +175,11 @@ int sfg_hip_gemm_v1(const sfg_gemm_args* a, void* workspace, size_t workspace_by
     p.m = a->m; p.n = a->n; p.k = a->k; p.epilogue = a->epilogue;
     p.b_layout = a->b_layout;
     p.offsets = nullptr; p.groups = 1;
+    p.tile = a->tile;
     if (a->b_layout != SFG_LAYOUT_NK && a->b_layout != SFG_LAYOUT_TILED)
         return fail(SFG_ERR_SHAPE, "gemm: unknown weight layout %d", a->b_layout);
+    if (a->tile < SFG_TILE_AUTO || a->tile >= SFG_TILE_COUNT)
+        return fail(SFG_ERR_SHAPE, "gemm: unknown tile policy %d", a->tile);
     const int rc = sfg::launch_gemm(p, workspace, workspace_bytes, as_stream(stream));
     if (rc != SFG_OK)
         return fail(rc, "gemm: unsupported or invalid combination (a=%d b=%d m=%lld n=%lld k=%lld epi=%d)",
@@ -259,7 +262,7 @@ int sfg_hip_attn_prefill_vt_v1(const uint16_t* q, const uint16_t* k, const uint1
                     (long long)sfg::attn_vt_ld(seq_kv));
     const int rc = sfg::launch_attn_prefill_vt(q, k, vt, ld_vt, out, out_dtype, batch, q_heads,
                                                kv_heads, seq_q, seq_kv, head_dim, causal,
-                                               default_scale(head_dim, scale), as_stream(stream));
+                                               default_scale(head_dim, scale), 0, as_stream(stream));
     if (rc != SFG_OK) return fail(rc, "attn_prefill_vt: head_dim %lld not lowered", (long long)head_dim);
     return check_launch("attn_prefill_vt");
 }
@@ -406,7 +409,7 @@ size_t sfg_hip_moe_expert_workspace_v1(int64_t tokens, int64_t hidden, int64_t i
 static int moe_experts(const uint16_t* x, const int32_t* offsets, const int32_t* token_ids,
                        const void* w13, const float* s13, const void* w2, const float* s2,
                        int w_dtype, int w_layout, uint16_t* act, float* y, int64_t tokens, int64_t hidden,
-                       int64_t inter, int64_t experts, int64_t top_k, hipStream_t stream) {
+                       int64_t inter, int64_t experts, int64_t top_k, int tile, hipStream_t stream) {
     sfg::GemmProblem p{};
     p.a = x; p.a_dtype = SFG_BF16; p.lda = hidden; p.a_rows = token_ids; p.a_rows_limit = tokens;
     p.b = w13; p.b_dtype = w_dtype; p.ldb = hidden; p.b_scales = s13;
@@ -415,6 +418,7 @@ static int moe_experts(const uint16_t* x, const int32_t* offsets, const int32_t*
     p.m = tokens * top_k; p.n = inter; p.k = hidden; p.epilogue = SFG_EPI_GLU_SILU_UP;
     p.b_layout = w_layout;
     p.offsets = offsets; p.groups = static_cast<int>(experts);
+    p.tile = tile;
     int rc = sfg::launch_gemm(p, nullptr, 0, stream);
     if (rc != SFG_OK) return fail(rc, "moe experts W1/W3: shape not lowered (H=%lld I=%lld)",
                                   (long long)hidden, (long long)inter);
@@ -426,6 +430,7 @@ static int moe_experts(const uint16_t* x, const int32_t* offsets, const int32_t*
     q.m = tokens * top_k; q.n = hidden; q.k = inter; q.epilogue = SFG_EPI_NONE;
     q.b_layout = w_layout;
     q.offsets = offsets; q.groups = static_cast<int>(experts);
+    q.tile = tile;
     rc = sfg::launch_gemm(q, nullptr, 0, stream);
     if (rc != SFG_OK) return fail(rc, "moe experts W2: shape not lowered");
     return check_launch("moe_experts");
@@ -445,7 +450,7 @@ int sfg_hip_moe_experts_v1(const uint16_t* x, const int32_t* offsets, const int3
     if (w_layout != SFG_LAYOUT_NK && w_layout != SFG_LAYOUT_TILED)
         return fail(SFG_ERR_SHAPE, "moe experts: unknown weight layout %d", w_layout);
     return moe_experts(x, offsets, token_ids, w13, s13, w2, s2, w_dtype, w_layout, act, y, tokens,
-                       hidden, inter, experts, top_k, as_stream(stream));
+                       hidden, inter, experts, top_k, SFG_TILE_AUTO, as_stream(stream));
 }
 
 int sfg_hip_moe_combine_v1(const float* y, const int32_t* position, const float* weights,
@@ -527,6 +532,10 @@ int validate_desc(const sfg_layer_desc* d) {
         return fail(SFG_ERR_UNSUPPORTED, "MoE layers run with bf16 activations");
     if (d->weight_layout != SFG_LAYOUT_NK && d->weight_layout != SFG_LAYOUT_TILED)
         return fail(SFG_ERR_SHAPE, "unknown weight layout %d", d->weight_layout);
+    if (d->gemm_tile < SFG_TILE_AUTO || d->gemm_tile >= SFG_TILE_COUNT)
+        return fail(SFG_ERR_SHAPE, "unknown GEMM tile policy %d", d->gemm_tile);
+    if (d->attn_waves != 0 && d->attn_waves != 4 && d->attn_waves != 8)
+        return fail(SFG_ERR_SHAPE, "flash prefill waves %d (0, 4 or 8)", d->attn_waves);
     if (d->weight_layout == SFG_LAYOUT_TILED && d->act_dtype != SFG_BF16)
         return fail(SFG_ERR_UNSUPPORTED, "tiled weights are bf16 / int8");
     return SFG_OK;
@@ -654,6 +663,7 @@ int sfg_hip_decoder_layer_v1(const sfg_layer_desc* d, const sfg_layer_weights* w
         p.residual = res; p.ldr = n;
         p.m = m; p.n = n; p.k = k; p.epilogue = epi; p.groups = 1;
         p.b_layout = d->weight_layout;
+        p.tile = d->gemm_tile;
         const int r = sfg::launch_gemm(p, b.gemm_ws, b.gemm_ws_bytes, s);
         if (r != SFG_OK)
             return fail(r, "decoder layer GEMM %lldx%lldx%lld not lowered for dtype %d/%d",
@@ -678,6 +688,7 @@ int sfg_hip_decoder_layer_v1(const sfg_layer_desc* d, const sfg_layer_weights* w
     qp.b = w->w_qkv; qp.b_dtype = wdt; qp.ldb = H; qp.b_scales = w->s_qkv;
     qp.m = rows; qp.n = qkvw; qp.k = H; qp.epilogue = sfg::kEpiQkvRope; qp.groups = 1;
     qp.b_layout = d->weight_layout;
+    qp.tile = d->gemm_tile;
     qp.qkv = sfg::QkvRopeOut{reinterpret_cast<const float2*>(w->rope_table), d->sequence, d->query_heads,
                              d->kv_heads, static_cast<uint16_t*>(b.q), static_cast<uint16_t*>(b.k),
                              static_cast<uint16_t*>(b.v), ld_vt};
@@ -740,7 +751,7 @@ int sfg_hip_decoder_layer_v1(const sfg_layer_desc* d, const sfg_layer_weights* w
                                              static_cast<const uint16_t*>(b.k),
                                              static_cast<const uint16_t*>(b.v), ld_vt, b.attn, act,
                                              d->batch, d->query_heads, d->kv_heads, d->sequence,
-                                             d->sequence, D, d->causal, scale, s);
+                                             d->sequence, D, d->causal, scale, d->attn_waves, s);
             if (rc != SFG_OK) return fail(rc, "bf16 prefill attention not lowered (head_dim %lld)", (long long)D);
         } else {
             rc = sfg::launch_attn_prefill_bf16(static_cast<const uint16_t*>(b.q),
@@ -787,7 +798,7 @@ int sfg_hip_decoder_layer_v1(const sfg_layer_desc* d, const sfg_layer_weights* w
         const float* route_w = d->use_routing_trace ? io->trace_weights : b.wts;
         rc = moe_experts(static_cast<const uint16_t*>(b.xn), b.offsets, b.token_ids, w->w13, w->s13,
                          w->w2, w->s2, wdt, d->weight_layout, static_cast<uint16_t*>(b.act), b.y, rows,
-                         H, I, E, K, s);
+                         H, I, E, K, d->gemm_tile, s);
         if (rc != SFG_OK) return rc;
         mk.mark(SFG_MARK_FFN_UP);
         sfg::launch_moe_combine(b.y, b.position, route_w, b.r1, io->out, rows, H, K, s);

@@ -101,21 +101,25 @@ void launch_attn_prefill_f32(const float* q, const float* k, const float* v, voi
 }
 
 // ===========================================================================
-// bf16 MFMA flash prefill, head_dim 128.
+// bf16 MFMA flash prefill, head_dim 128 or 64.
 // ===========================================================================
 constexpr int kFaD = 128;
 constexpr int kFaBM = 128;          // query rows per workgroup
 constexpr int kFaBN = 64;           // keys per tile
-constexpr int kKRow = kFaD + 8;     // padded K row (bf16 elements)
 constexpr int kVRow = kFaBN + 8;    // padded V^T row
 
-template <typename OutT>
+template <typename OutT, int kD>
 __global__ __launch_bounds__(256) void attn_prefill_bf16_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, OutT* __restrict__ out, int q_heads, int kv_heads,
     int seq_q, int seq_kv, int causal, float scale_log2) {
+    static_assert(kD == 64 || kD == 128, "head_dim 64 or 128");
+    constexpr int kKRow = kD + 8;       // padded K row (bf16 elements)
+    constexpr int kQs = kD / 16;        // k-steps of S^T = K Q^T
+    constexpr int kOd = kD / 32;        // 32-dim blocks of O^T
+    constexpr int kChunks = kD / 8;     // 16-byte chunks per key row
     __shared__ __attribute__((aligned(16))) uint16_t sK[kFaBN * kKRow];
-    __shared__ __attribute__((aligned(16))) uint16_t sVt[kFaD * kVRow];
+    __shared__ __attribute__((aligned(16))) uint16_t sVt[kD * kVRow];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -132,22 +136,22 @@ __global__ __launch_bounds__(256) void attn_prefill_bf16_kernel(
 
     // Q fragments (B operand of S^T = K Q^T): lane supplies row my_q,
     // d = 16 * step + 8 * half + [0, 8).
-    bf16x8 qf[8];
+    bf16x8 qf[kQs];
     {
-        const uint16_t* qr = q + ((static_cast<int64_t>(b) * q_heads + h) * seq_q + my_q) * kFaD;
+        const uint16_t* qr = q + ((static_cast<int64_t>(b) * q_heads + h) * seq_q + my_q) * kD;
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
+        for (int s = 0; s < kQs; ++s) {
             uint4 val = make_uint4(0, 0, 0, 0);
             if (my_q < seq_q) val = *reinterpret_cast<const uint4*>(qr + s * 16 + half * 8);
             qf[s] = as_bf16x8(val);
         }
     }
-    const uint16_t* kb = k + (static_cast<int64_t>(b) * kv_heads + kvh) * seq_kv * kFaD;
-    const uint16_t* vb = v + (static_cast<int64_t>(b) * kv_heads + kvh) * seq_kv * kFaD;
+    const uint16_t* kb = k + (static_cast<int64_t>(b) * kv_heads + kvh) * seq_kv * kD;
+    const uint16_t* vb = v + (static_cast<int64_t>(b) * kv_heads + kvh) * seq_kv * kD;
 
-    floatx16 acc_o[4];
+    floatx16 acc_o[kOd];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < kOd; ++i)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc_o[i][r] = 0.f;
     float m_run = -INFINITY, l_run = 0.f;
@@ -160,16 +164,16 @@ __global__ __launch_bounds__(256) void attn_prefill_bf16_kernel(
     for (int t = 0; t < tiles; ++t) {
         const int kv0 = t * kFaBN;
         __syncthreads();
-        // Stage K [64][128] and V^T [128][64]: 1024 16-byte chunks each.
+        // Stage K [64][D] and V^T [D][64]: 8 D 16-byte chunks each.
 #pragma unroll
-        for (int it = 0; it < 4; ++it) {
+        for (int it = 0; it < kFaBN * kChunks / 256; ++it) {
             const int idx = tid + it * 256;
-            const int key = idx >> 4;
-            const int chunk = (idx & 15) * 8;
+            const int key = idx / kChunks;
+            const int chunk = (idx % kChunks) * 8;
             uint4 kv4 = make_uint4(0, 0, 0, 0), vv4 = make_uint4(0, 0, 0, 0);
             if (kv0 + key < seq_kv) {
-                kv4 = *reinterpret_cast<const uint4*>(kb + static_cast<int64_t>(kv0 + key) * kFaD + chunk);
-                vv4 = *reinterpret_cast<const uint4*>(vb + static_cast<int64_t>(kv0 + key) * kFaD + chunk);
+                kv4 = *reinterpret_cast<const uint4*>(kb + static_cast<int64_t>(kv0 + key) * kD + chunk);
+                vv4 = *reinterpret_cast<const uint4*>(vb + static_cast<int64_t>(kv0 + key) * kD + chunk);
             }
             *reinterpret_cast<uint4*>(&sK[key * kKRow + chunk]) = kv4;
             const uint16_t* ve = reinterpret_cast<const uint16_t*>(&vv4);
@@ -186,7 +190,7 @@ __global__ __launch_bounds__(256) void attn_prefill_bf16_kernel(
 #pragma unroll
             for (int r = 0; r < 16; ++r) s_acc[j][r] = 0.f;
 #pragma unroll
-            for (int s = 0; s < 8; ++s) {
+            for (int s = 0; s < kQs; ++s) {
                 const bf16x8 kf = as_bf16x8(*reinterpret_cast<const uint4*>(
                     &sK[(j * 32 + l32) * kKRow + s * 16 + half * 8]));
                 s_acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[s], s_acc[j], 0, 0, 0);
@@ -226,7 +230,7 @@ __global__ __launch_bounds__(256) void attn_prefill_bf16_kernel(
         l_run = l_run * alpha + psum;
         m_run = m_new;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < kOd; ++i)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc_o[i][r] *= alpha;
         // O^T[d][q] += V^T[d][key] P^T[key][q].  MFMA k index (8 half + jj)
@@ -238,7 +242,7 @@ __global__ __launch_bounds__(256) void attn_prefill_bf16_kernel(
             for (int tt = 0; tt < 2; ++tt) {
                 const int kbase = j * 32 + tt * 16 + 4 * half;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
+                for (int i = 0; i < kOd; ++i) {
                     const int d = i * 32 + l32;
                     const uint2 lo = *reinterpret_cast<const uint2*>(&sVt[d * kVRow + kbase]);
                     const uint2 hi = *reinterpret_cast<const uint2*>(&sVt[d * kVRow + kbase + 8]);
@@ -253,9 +257,9 @@ __global__ __launch_bounds__(256) void attn_prefill_bf16_kernel(
     const float inv = 1.0f / l_total;
     // O^T layout: lane holds query my_q, dims 32 i + 8 (r / 4) + 4 half + (r % 4).
     const int64_t row = static_cast<int64_t>(b) * seq_q + my_q;
-    OutT* orow = out + row * (static_cast<int64_t>(q_heads) * kFaD) + h * kFaD;
+    OutT* orow = out + row * (static_cast<int64_t>(q_heads) * kD) + h * kD;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < kOd; ++i)
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             const int d = i * 32 + 8 * c + 4 * half;
@@ -276,17 +280,27 @@ int launch_attn_prefill_bf16(const uint16_t* q, const uint16_t* k, const uint16_
                              int out_dtype, int64_t batch, int64_t q_heads, int64_t kv_heads,
                              int64_t seq_q, int64_t seq_kv, int64_t head_dim, int causal,
                              float scale, hipStream_t stream) {
-    if (head_dim != kFaD) return SFG_ERR_UNSUPPORTED;
+    if (head_dim != 128 && head_dim != 64) return SFG_ERR_UNSUPPORTED;
     const float scale_log2 = scale * kLog2e;
     const dim3 grid(static_cast<unsigned>((seq_q + kFaBM - 1) / kFaBM),
                     static_cast<unsigned>(q_heads), static_cast<unsigned>(batch));
-    if (out_dtype == SFG_F32)
-        attn_prefill_bf16_kernel<float><<<grid, 256, 0, stream>>>(
-            q, k, v, static_cast<float*>(out), q_heads, kv_heads, seq_q, seq_kv, causal, scale_log2);
-    else
-        attn_prefill_bf16_kernel<uint16_t><<<grid, 256, 0, stream>>>(
-            q, k, v, static_cast<uint16_t*>(out), q_heads, kv_heads, seq_q, seq_kv, causal,
-            scale_log2);
+    const int qh = static_cast<int>(q_heads), kvh = static_cast<int>(kv_heads);
+    const int sq = static_cast<int>(seq_q), skv = static_cast<int>(seq_kv);
+    if (head_dim == 128) {
+        if (out_dtype == SFG_F32)
+            attn_prefill_bf16_kernel<float, 128><<<grid, 256, 0, stream>>>(
+                q, k, v, static_cast<float*>(out), qh, kvh, sq, skv, causal, scale_log2);
+        else
+            attn_prefill_bf16_kernel<uint16_t, 128><<<grid, 256, 0, stream>>>(
+                q, k, v, static_cast<uint16_t*>(out), qh, kvh, sq, skv, causal, scale_log2);
+    } else {
+        if (out_dtype == SFG_F32)
+            attn_prefill_bf16_kernel<float, 64><<<grid, 256, 0, stream>>>(
+                q, k, v, static_cast<float*>(out), qh, kvh, sq, skv, causal, scale_log2);
+        else
+            attn_prefill_bf16_kernel<uint16_t, 64><<<grid, 256, 0, stream>>>(
+                q, k, v, static_cast<uint16_t*>(out), qh, kvh, sq, skv, causal, scale_log2);
+    }
     return SFG_OK;
 }
 
@@ -542,11 +556,10 @@ int64_t attn_vt_ld(int64_t seq_kv) { return (seq_kv + kFa2BN - 1) / kFa2BN * kFa
 int launch_attn_prefill_vt(const uint16_t* q, const uint16_t* k, const uint16_t* vt, int64_t ld_vt,
                            void* out, int out_dtype, int64_t batch, int64_t q_heads,
                            int64_t kv_heads, int64_t seq_q, int64_t seq_kv, int64_t head_dim,
-                           int causal, float scale, hipStream_t stream) {
+                           int causal, float scale, int waves_policy, hipStream_t stream) {
     if (head_dim != kFaD) return SFG_ERR_UNSUPPORTED;
     if (ld_vt % kFa2BN != 0 || ld_vt < seq_kv) return SFG_ERR_SHAPE;
-    static const char* forced = std::getenv("SFG_FA_WAVES");
-    const int waves = (forced && std::atoi(forced) == 8) ? 8 : 4;
+    const int waves = waves_policy == 8 ? 8 : 4;
     const int bm = waves * 32;
     Fa2Args a{};
     a.q = q; a.k = k; a.vt = vt; a.out = out; a.out_f32 = out_dtype == SFG_F32;
@@ -562,28 +575,28 @@ int launch_attn_prefill_vt(const uint16_t* q, const uint16_t* k, const uint16_t*
 }
 
 // ===========================================================================
-// Paged Split-KV decode on MFMA, head_dim 128, 16-token pages.
+// Paged Split-KV decode on MFMA, head_dim 128 or 64, 16-token pages.
 //
 // Pool layouts (one 4 KB run per (page, kv_head)):
-//   K [page][Hkv][16 tokens][128 dims]   V [page][Hkv][128 dims][16 tokens]
+//   K [page][Hkv][16 tokens][D dims]   V [page][Hkv][D dims][16 tokens]
 // V is token-minor inside a page so that the MFMA operand V^T (dims x tokens)
 // is read as 8-byte runs.  Per page a wave does
-//   S^T[16 tok][16 q] = K[16 tok][128] Q^T[128][16 q]   4 x mfma_16x16x32_bf16
-//   O^T[128 d][16 q] += V^T[128 d][16 tok] P^T[16 tok][16 q]  8 x mfma_16x16x16_bf16
+//   S^T[16 tok][16 q] = K[16 tok][D] Q^T[D][16 q]        D/32 x mfma_16x16x32_bf16
+//   O^T[D][16 q] += V^T[D][16 tok] P^T[16 tok][16 q]      D/16 x mfma_16x16x16_bf16
 // where the GQA group's G query heads occupy the first G columns.  In the
 // S^T accumulator lane l holds query (l & 15) and tokens 4 (l >> 4) + r, which
 // is exactly the P^T operand layout, and the O^T accumulator holds the same
 // query per lane: the online softmax needs only a 4-lane max per page and a
 // per-lane rescale.
 // ===========================================================================
-constexpr int kDecD = 128;
+constexpr int kKvD = 128;  // head_dim of the append / gather kernels
 constexpr int kPageTok = 16;
 
 typedef short short4v __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ short4v as_short4(const uint2& v) { return __builtin_bit_cast(short4v, v); }
 
-template <int G>
+template <int G, int kDecD>
 __global__ __launch_bounds__(256) void attn_decode_split_kernel(
     const float* __restrict__ q, int64_t q_row_stride, const float* __restrict__ rope,
     int rope_pos, const uint16_t* __restrict__ k_pool, const uint16_t* __restrict__ v_pool,
@@ -592,6 +605,9 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(
     int kv_heads, int pages_per_seq, int num_pages, int splits, float scale_log2,
     float* __restrict__ part_ml, float* __restrict__ part_acc) {
     static_assert(G >= 1 && G <= 16, "GQA group must fit the 16 MFMA columns");
+    static_assert(kDecD == 64 || kDecD == 128, "head_dim 64 or 128");
+    constexpr int kKs = kDecD / 32;   // k-steps of S^T = K Q^T
+    constexpr int kDt = kDecD / 16;   // 16-dim blocks of O^T
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
@@ -612,13 +628,13 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(
 
     // Q^T operand: lane supplies query head lr (zero beyond the group), dims
     // 32 s + 8 lg + [0, 8), rotated by the host table at rope_pos when given.
-    bf16x8 qf[4];
+    bf16x8 qf[kKs];
     {
         const bool has = lr < G;
         const float* qr = q + static_cast<int64_t>(b) * q_row_stride +
                           static_cast<int64_t>(kvh * G + (has ? lr : 0)) * kDecD;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
+        for (int s = 0; s < kKs; ++s) {
             const int d0 = 32 * s + 8 * lg;
             float v[8];
             const float4 a = *reinterpret_cast<const float4*>(qr + d0);
@@ -644,9 +660,9 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(
         }
     }
 
-    floatx4 acc[8];
+    floatx4 acc[kDt];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < kDt; ++i) acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
     float m_run = -INFINITY, l_run = 0.f;
 
     const int32_t* ptab = page_table + static_cast<int64_t>(b) * pages_per_seq;
@@ -656,8 +672,8 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(
     const int k_off = lr * kDecD + 8 * lg;  // + 32 s
     const int v_off = lr * kPageTok + 4 * lg;  // + 16 dt * 16
 
-    uint4 kb[4];
-    uint2 vb[8];
+    uint4 kb[kKs];
+    uint2 vb[kDt];
     bool okb = false;
     // Load page p (guarded: an id outside the pool reads nothing).
 #define SFG_LOAD_PAGE(p)                                                                   \
@@ -667,24 +683,24 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(
         const int64_t base = okb ? static_cast<int64_t>(phys) * page_stride + kvh * head_stride : 0; \
         const uint16_t* kp = k_pool + base + k_off;                                        \
         const uint16_t* vp = v_pool + base + v_off;                                        \
-        _Pragma("unroll") for (int s = 0; s < 4; ++s)                                      \
+        _Pragma("unroll") for (int s = 0; s < kKs; ++s)                                    \
             kb[s] = okb ? *reinterpret_cast<const uint4*>(kp + 32 * s) : make_uint4(0, 0, 0, 0); \
-        _Pragma("unroll") for (int dt = 0; dt < 8; ++dt)                                   \
+        _Pragma("unroll") for (int dt = 0; dt < kDt; ++dt)                                 \
             vb[dt] = okb ? *reinterpret_cast<const uint2*>(vp + dt * 16 * kPageTok) : make_uint2(0, 0); \
     }
     if (w_begin < w_end) SFG_LOAD_PAGE(w_begin);
     for (int p = w_begin; p < w_end; ++p) {
-        uint4 kc[4];
-        uint2 vc[8];
+        uint4 kc[kKs];
+        uint2 vc[kDt];
 #pragma unroll
-        for (int s = 0; s < 4; ++s) kc[s] = kb[s];
+        for (int s = 0; s < kKs; ++s) kc[s] = kb[s];
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) vc[dt] = vb[dt];
+        for (int dt = 0; dt < kDt; ++dt) vc[dt] = vb[dt];
         const bool ok = okb;
         if (p + 1 < w_end) SFG_LOAD_PAGE(p + 1);
         floatx4 st = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
+        for (int s = 0; s < kKs; ++s)
             st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kc[s]), qf[s], st, 0, 0, 0);
         // st[r]: token 16 p + 4 lg + r, query lr
         float sv[4];
@@ -709,7 +725,7 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(
             pk.y = pack_bf16x2(pv[2], pv[3]);
             const short4v pb = as_short4(pk);
 #pragma unroll
-            for (int dt = 0; dt < 8; ++dt) {
+            for (int dt = 0; dt < kDt; ++dt) {
                 acc[dt] *= alpha;
                 acc[dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(as_short4(vc[dt]), pb, acc[dt], 0, 0, 0);
             }
@@ -725,7 +741,7 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(
     __shared__ float s_acc[4][G][kDecD];
     if (lr < G) {
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt)
+        for (int dt = 0; dt < kDt; ++dt)
 #pragma unroll
             for (int r = 0; r < 4; ++r) s_acc[wave][lr][16 * dt + 4 * lg + r] = acc[dt][r];
         if (lg == 0) {
@@ -756,8 +772,8 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(
     }
 }
 
-template <typename OutT>
-__global__ __launch_bounds__(128) void attn_decode_combine_kernel(
+template <typename OutT, int kDecD>
+__global__ __launch_bounds__(kDecD) void attn_decode_combine_kernel(
     const float* __restrict__ part_ml, const float* __restrict__ part_acc, OutT* __restrict__ out,
     int q_heads, int splits) {
     const int bh = blockIdx.x;  // b * q_heads + h
@@ -802,7 +818,7 @@ int launch_attn_decode_paged(const float* q, int64_t q_row_stride, const float* 
                              int64_t kv_heads, int64_t head_dim, int64_t page_tokens,
                              int64_t pages_per_seq, int64_t num_pages, int splits, float scale,
                              void* workspace, hipStream_t stream, hipEvent_t mid_event) {
-    if (head_dim != kDecD || page_tokens != kPageTok) return SFG_ERR_UNSUPPORTED;
+    if ((head_dim != 128 && head_dim != 64) || page_tokens != kPageTok) return SFG_ERR_UNSUPPORTED;
     const int group = static_cast<int>(q_heads / kv_heads);
     const size_t slots = static_cast<size_t>(batch) * q_heads * splits;
     float* part_ml = static_cast<float*>(workspace);
@@ -814,24 +830,37 @@ int launch_attn_decode_paged(const float* q, int64_t q_row_stride, const float* 
     const int len = static_cast<int>(max_context);
     const int pps = static_cast<int>(pages_per_seq);
     const int np = static_cast<int>(num_pages);
-#define SFG_DECODE(G) attn_decode_split_kernel<G><<<grid, 256, 0, stream>>>(q, q_row_stride, rope, rope_pos, k_pool, v_pool, page_table, seq_lens, len, len_extra, static_cast<int>(kv_heads), pps, np, splits, scale_log2, part_ml, part_acc)
-    switch (group) {
-        case 1: SFG_DECODE(1); break;
-        case 2: SFG_DECODE(2); break;
-        case 4: SFG_DECODE(4); break;
-        case 8: SFG_DECODE(8); break;
-        case 16: SFG_DECODE(16); break;
-        default: return SFG_ERR_UNSUPPORTED;
+#define SFG_DECODE(G, D) attn_decode_split_kernel<G, D><<<grid, 256, 0, stream>>>(q, q_row_stride, rope, rope_pos, k_pool, v_pool, page_table, seq_lens, len, len_extra, static_cast<int>(kv_heads), pps, np, splits, scale_log2, part_ml, part_acc)
+#define SFG_DECODE_G(D)                      \
+    switch (group) {                         \
+        case 1: SFG_DECODE(1, D); break;     \
+        case 2: SFG_DECODE(2, D); break;     \
+        case 4: SFG_DECODE(4, D); break;     \
+        case 8: SFG_DECODE(8, D); break;     \
+        case 16: SFG_DECODE(16, D); break;   \
+        default: return SFG_ERR_UNSUPPORTED; \
     }
+    if (head_dim == 128) {
+        SFG_DECODE_G(128)
+    } else {
+        SFG_DECODE_G(64)
+    }
+#undef SFG_DECODE_G
 #undef SFG_DECODE
     if (mid_event) (void)hipEventRecord(mid_event, stream);
     const dim3 cgrid(static_cast<unsigned>(batch * q_heads));
-    if (out_dtype == SFG_F32)
-        attn_decode_combine_kernel<float><<<cgrid, kDecD, 0, stream>>>(
-            part_ml, part_acc, static_cast<float*>(out), static_cast<int>(q_heads), splits);
-    else
-        attn_decode_combine_kernel<uint16_t><<<cgrid, kDecD, 0, stream>>>(
-            part_ml, part_acc, static_cast<uint16_t*>(out), static_cast<int>(q_heads), splits);
+    const int qh = static_cast<int>(q_heads);
+    if (head_dim == 128) {
+        if (out_dtype == SFG_F32)
+            attn_decode_combine_kernel<float, 128><<<cgrid, 128, 0, stream>>>(part_ml, part_acc, static_cast<float*>(out), qh, splits);
+        else
+            attn_decode_combine_kernel<uint16_t, 128><<<cgrid, 128, 0, stream>>>(part_ml, part_acc, static_cast<uint16_t*>(out), qh, splits);
+    } else {
+        if (out_dtype == SFG_F32)
+            attn_decode_combine_kernel<float, 64><<<cgrid, 64, 0, stream>>>(part_ml, part_acc, static_cast<float*>(out), qh, splits);
+        else
+            attn_decode_combine_kernel<uint16_t, 64><<<cgrid, 64, 0, stream>>>(part_ml, part_acc, static_cast<uint16_t*>(out), qh, splits);
+    }
     return SFG_OK;
 }
 
@@ -870,14 +899,14 @@ __global__ __launch_bounds__(64) void kv_append_kernel(KvAppendArgs a) {
     const int64_t src = b * a.sb + h * a.sh + t * a.st + 2 * pair;
     float2 kv = load_pair(a.keys, a.src_f32, src);
     if (a.rope) {
-        const float2 cs = a.rope[static_cast<int64_t>(pos) * (kDecD / 2) + pair];
+        const float2 cs = a.rope[static_cast<int64_t>(pos) * (kKvD / 2) + pair];
         kv = make_float2(kv.x * cs.x - kv.y * cs.y, kv.x * cs.y + kv.y * cs.x);
     }
     const int64_t blk = static_cast<int64_t>(phys) * a.kv_heads + h;
-    *reinterpret_cast<uint32_t*>(a.k_pool + (blk * kPageTok + slot) * kDecD + 2 * pair) = pack_bf16x2(kv.x, kv.y);
+    *reinterpret_cast<uint32_t*>(a.k_pool + (blk * kPageTok + slot) * kKvD + 2 * pair) = pack_bf16x2(kv.x, kv.y);
     const float2 vv = load_pair(a.values, a.src_f32, src);
-    a.v_pool[(blk * kDecD + 2 * pair) * kPageTok + slot] = f32_to_bf16(vv.x);
-    a.v_pool[(blk * kDecD + 2 * pair + 1) * kPageTok + slot] = f32_to_bf16(vv.y);
+    a.v_pool[(blk * kKvD + 2 * pair) * kPageTok + slot] = f32_to_bf16(vv.x);
+    a.v_pool[(blk * kKvD + 2 * pair + 1) * kPageTok + slot] = f32_to_bf16(vv.y);
 }
 
 __global__ __launch_bounds__(256) void kv_advance_kernel(int32_t* seq_lens, int batch, int tokens) {
@@ -895,15 +924,15 @@ __global__ __launch_bounds__(64) void kv_gather_kernel(const uint16_t* __restric
     const int t = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int pair = threadIdx.x;
     const int phys = page_table[static_cast<int64_t>(b) * pages_per_seq + t / kPageTok];
-    const int64_t dst = ((static_cast<int64_t>(b) * kv_heads + h) * length + t) * kDecD + 2 * pair;
+    const int64_t dst = ((static_cast<int64_t>(b) * kv_heads + h) * length + t) * kKvD + 2 * pair;
     float2 kk = make_float2(0.f, 0.f), vv = make_float2(0.f, 0.f);
     if (phys >= 0 && phys < num_pages) {
         const int slot = t % kPageTok;
         const int64_t blk = static_cast<int64_t>(phys) * kv_heads + h;
-        const uint32_t kw = *reinterpret_cast<const uint32_t*>(k_pool + (blk * kPageTok + slot) * kDecD + 2 * pair);
+        const uint32_t kw = *reinterpret_cast<const uint32_t*>(k_pool + (blk * kPageTok + slot) * kKvD + 2 * pair);
         kk = make_float2(bf16_to_f32(static_cast<uint16_t>(kw & 0xFFFFu)), bf16_to_f32(static_cast<uint16_t>(kw >> 16)));
-        vv = make_float2(bf16_to_f32(v_pool[(blk * kDecD + 2 * pair) * kPageTok + slot]),
-                         bf16_to_f32(v_pool[(blk * kDecD + 2 * pair + 1) * kPageTok + slot]));
+        vv = make_float2(bf16_to_f32(v_pool[(blk * kKvD + 2 * pair) * kPageTok + slot]),
+                         bf16_to_f32(v_pool[(blk * kKvD + 2 * pair + 1) * kPageTok + slot]));
     }
     *reinterpret_cast<float2*>(keys + dst) = kk;
     *reinterpret_cast<float2*>(values + dst) = vv;
@@ -915,7 +944,7 @@ int launch_kv_append(const void* keys, const void* values, int src_dtype, int64_
                      int64_t batch, int64_t kv_heads, int64_t tokens, int64_t head_dim,
                      int64_t page_tokens, int64_t pages_per_seq, int64_t num_pages,
                      hipStream_t stream) {
-    if (head_dim != kDecD || page_tokens != kPageTok) return SFG_ERR_UNSUPPORTED;
+    if (head_dim != kKvD || page_tokens != kPageTok) return SFG_ERR_UNSUPPORTED;
     KvAppendArgs a{};
     a.keys = keys; a.values = values; a.src_f32 = src_dtype == SFG_F32;
     a.sb = sb; a.sh = sh; a.st = st;
@@ -941,7 +970,7 @@ int launch_kv_gather(const uint16_t* k_pool, const uint16_t* v_pool, const int32
                      int64_t batch, int64_t kv_heads, int64_t length, int64_t head_dim,
                      int64_t page_tokens, int64_t pages_per_seq, int64_t num_pages, float* keys,
                      float* values, hipStream_t stream) {
-    if (head_dim != kDecD || page_tokens != kPageTok) return SFG_ERR_UNSUPPORTED;
+    if (head_dim != kKvD || page_tokens != kPageTok) return SFG_ERR_UNSUPPORTED;
     kv_gather_kernel<<<dim3(static_cast<unsigned>(length), static_cast<unsigned>(kv_heads),
                             static_cast<unsigned>(batch)), 64, 0, stream>>>(
         k_pool, v_pool, page_table, static_cast<int>(kv_heads), static_cast<int>(pages_per_seq),

@@ -318,6 +318,8 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(TiledArgs p) {
 
     // Global -> LDS loaders: each thread moves 16 B of A and 16 B of B per slab
     // (128 rows x 32 k x 2 B = 8 KB = 256 threads x 2 x 16 B -> two per thread).
+    // Output columns at or past n (a ragged last tile) read B row 0 instead;
+    // their results are never stored.
     int64_t a_src[2];
     bool a_ok[2];
     int64_t b_src[2];
@@ -335,9 +337,11 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(TiledArgs p) {
         int64_t brow;
         if (kGlu) {
             const int local = ld_row[h];
-            brow = (local < 64) ? (ncol0 + local) : (p.n + ncol0 + local - 64);
+            const int64_t col = ncol0 + (local & 63);
+            brow = col < p.n ? ((local < 64) ? col : p.n + col) : 0;
         } else {
-            brow = ncol0 + ld_row[h];
+            const int64_t col = ncol0 + ld_row[h];
+            brow = col < p.n ? col : 0;
         }
         b_src[h] = bgroup + brow * p.ldb + ld_col[h];
     }
@@ -414,6 +418,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(TiledArgs p) {
             if (row >= re) continue;
             if (kGlu) {
                 const int64_t col = ncol0 + wn * 32 + (lane & 31);
+                if (col >= p.n) continue;
                 float gv = acc[i][0][r], uv = acc[i][1][r];
                 if (scales) {
                     gv *= scales[col];
@@ -424,6 +429,7 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(TiledArgs p) {
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
                     const int64_t col = ncol0 + wn * 64 + j * 32 + (lane & 31);
+                    if (col >= p.n) continue;
                     float v = acc[i][j][r];
                     if (scales) v *= scales[col];
                     if (EPI == SFG_EPI_RESIDUAL) v += p.residual[row * p.ldr + col];
@@ -1203,22 +1209,30 @@ void launch_dma_b(const TiledArgs& a, dim3 grid, int tm, int tn, int epi, hipStr
     }
 }
 
-// Output tile of the direct-to-LDS kernel: the largest that still gives every
-// CU two workgroups; smaller problems take smaller tiles.
-struct DmaShape { int bm, bn; };
-DmaShape pick_dma_shape(int64_t m, int64_t n_out, bool glu, int groups) {
-    static const char* forced = std::getenv("SFG_GEMM_TILE");
-    if (forced && *forced) {
-        const int bm = std::atoi(forced), bn = std::atoi(std::strchr(forced, 'x') ? std::strchr(forced, 'x') + 1 : forced);
-        if ((bm == 128 || bm == 256) && (bn == 128 || bn == 256)) return {bm, bn};
+// Output tile of the direct-to-LDS kernel.  SFG_TILE_AUTO: the largest tile
+// (256 x 256 as two ping-pong groups of four waves) that still gives at least
+// 512 workgroups (two per CU); smaller problems take smaller tiles.  A plan may
+// name the tile instead (sfg_layer_desc::gemm_tile); results do not depend on it.
+struct DmaShape { int bm, bn, waves; bool pingpong; };
+DmaShape dma_shape_of(int tile) {
+    switch (tile) {
+        case SFG_TILE_256x256_PP: return {256, 256, 8, true};
+        case SFG_TILE_256x256_W8: return {256, 256, 8, false};
+        case SFG_TILE_256x256_W4: return {256, 256, 4, false};
+        case SFG_TILE_256x128: return {256, 128, 4, false};
+        case SFG_TILE_128x256: return {128, 256, 4, false};
+        default: return {128, 128, 4, false};
     }
-    const DmaShape shapes[] = {{256, 256}, {256, 128}, {128, 128}};
-    for (const DmaShape& sh : shapes) {
+}
+DmaShape pick_dma_shape(int64_t m, int64_t n_out, bool glu, int groups, int tile) {
+    if (tile > SFG_TILE_AUTO && tile < SFG_TILE_COUNT) return dma_shape_of(tile);
+    for (const int t : {SFG_TILE_256x256_PP, SFG_TILE_256x128, SFG_TILE_128x128}) {
+        const DmaShape sh = dma_shape_of(t);
         const int64_t cols = glu ? sh.bn / 2 : sh.bn;
         const int64_t tiles = ((m + sh.bm - 1) / sh.bm + (groups > 1 ? groups : 0)) * ((n_out + cols - 1) / cols);
         if (tiles >= 512) return sh;
     }
-    return {128, 128};
+    return dma_shape_of(SFG_TILE_128x128);
 }
 
 template <int BDT>
@@ -1313,7 +1327,10 @@ int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes, h
         return SFG_OK;
     }
     if (p.b_layout == SFG_LAYOUT_TILED) return SFG_ERR_UNSUPPORTED;  // tiled weights feed the skinny kernel only
-    if (p.n % (glu ? 64 : 128) != 0 || p.k % kTK != 0) return SFG_ERR_UNSUPPORTED;
+    if (p.k % kTK != 0) return SFG_ERR_UNSUPPORTED;
+    // The direct-to-LDS and 128 x 128 kernels mask a ragged last column tile;
+    // the 256 x 128 register-staged kernel needs whole tiles.
+    const bool whole_n = p.n % (glu ? 64 : 128) == 0;
     const bool big = p.k % kGK == 0 && p.m >= kBigMinRows;
     TiledArgs a{};
     a.a = static_cast<const uint16_t*>(p.a); a.lda = p.lda; a.a_rows = p.a_rows;
@@ -1328,27 +1345,23 @@ int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes, h
     const bool fits32 = static_cast<uint64_t>(a.a_rows_limit) * p.lda * 2 <= 0xFFFFFFFFull &&
                         static_cast<uint64_t>(glu ? 2 : 1) * p.n * p.ldb * 2 <= 0xFFFFFFFFull;
     if (big && fits32 && p.b_dtype == SFG_BF16) {
-        const DmaShape sh = pick_dma_shape(p.m, p.n, glu, groups);
+        const DmaShape sh = pick_dma_shape(p.m, p.n, glu, groups, p.tile);
         const int64_t cols = glu ? sh.bn / 2 : sh.bn;
         const int64_t tn = (p.n + cols - 1) / cols;
         const int64_t tm = (p.m + sh.bm - 1) / sh.bm;
         const dim3 grid = p.offsets ? dim3(static_cast<unsigned>(tn), static_cast<unsigned>(tm + groups))
                                     : dim3(static_cast<unsigned>(tm * tn));
         const int itm = p.offsets ? 0 : static_cast<int>(tm);
-        static const char* waves_env = std::getenv("SFG_GEMM_WAVES");
-        const bool eight = !(waves_env && std::atoi(waves_env) == 4);
-        static const char* pp_env = std::getenv("SFG_GEMM_PINGPONG");
-        const bool pingpong = !(pp_env && std::atoi(pp_env) == 0);
-        if (sh.bm == 256 && sh.bn == 256 && eight && pingpong)
+        if (sh.bm == 256 && sh.bn == 256 && sh.pingpong)
             launch_dma_b<256, 256, 8, true>(a, grid, itm, static_cast<int>(tn), p.epilogue, stream);
-        else if (sh.bm == 256 && sh.bn == 256 && eight) launch_dma_b<256, 256, 8>(a, grid, itm, static_cast<int>(tn), p.epilogue, stream);
+        else if (sh.bm == 256 && sh.bn == 256 && sh.waves == 8) launch_dma_b<256, 256, 8>(a, grid, itm, static_cast<int>(tn), p.epilogue, stream);
         else if (sh.bm == 256 && sh.bn == 256) launch_dma_b<256, 256>(a, grid, itm, static_cast<int>(tn), p.epilogue, stream);
         else if (sh.bm == 256) launch_dma_b<256, 128>(a, grid, itm, static_cast<int>(tn), p.epilogue, stream);
         else if (sh.bn == 256) launch_dma_b<128, 256>(a, grid, itm, static_cast<int>(tn), p.epilogue, stream);
         else launch_dma_b<128, 128>(a, grid, itm, static_cast<int>(tn), p.epilogue, stream);
         return SFG_OK;
     }
-    if (big) {
+    if (big && whole_n) {
         const int64_t tn = glu ? p.n / 64 : p.n / 128;
         if (p.offsets) {
             const dim3 grid(static_cast<unsigned>(tn), static_cast<unsigned>((p.m + kGM - 1) / kGM + groups));
@@ -1363,7 +1376,7 @@ int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes, h
         return SFG_OK;
     }
     const int64_t row_tiles = p.offsets ? (p.m + kTM - 1) / kTM + groups : (p.m + kTM - 1) / kTM;
-    const dim3 grid(static_cast<unsigned>(glu ? p.n / 64 : p.n / 128), static_cast<unsigned>(row_tiles));
+    const dim3 grid(static_cast<unsigned>(glu ? (p.n + 63) / 64 : (p.n + 127) / 128), static_cast<unsigned>(row_tiles));
     if (p.b_dtype == SFG_I8) launch_tiled_b<SFG_I8>(a, grid, p.epilogue, stream);
     else launch_tiled_b<SFG_BF16>(a, grid, p.epilogue, stream);
     return SFG_OK;

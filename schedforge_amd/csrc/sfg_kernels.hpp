@@ -54,6 +54,7 @@ struct GemmProblem {
     const int32_t* offsets;     // grouped: device [groups+1]; nullptr = dense
     int groups;
     QkvRopeOut qkv;             // epilogue kEpiQkvRope only
+    int tile;                   // sfg_gemm_tile of the direct-to-LDS path (0: by shape)
 };
 
 bool gemm_qkv_rope_supported(const GemmProblem& p);
@@ -74,12 +75,13 @@ int launch_attn_prefill_bf16(const uint16_t* q, const uint16_t* k, const uint16_
                              int64_t seq_q, int64_t seq_kv, int64_t head_dim, int causal,
                              float scale, hipStream_t stream);
 // Flash prefill over V^T [B][Hkv][128][ld_vt] (keys >= seq_kv zero); ld_vt is
-// attn_vt_ld(seq_kv).  launch_v_transpose writes that V^T from fp32 QKV rows.
+// attn_vt_ld(seq_kv).  waves: 4 or 8 waves (128 / 256 query rows) per
+// workgroup; anything else means 4.  launch_v_transpose writes that V^T from fp32 QKV rows.
 int64_t attn_vt_ld(int64_t seq_kv);
 int launch_attn_prefill_vt(const uint16_t* q, const uint16_t* k, const uint16_t* vt, int64_t ld_vt,
                            void* out, int out_dtype, int64_t batch, int64_t q_heads,
                            int64_t kv_heads, int64_t seq_q, int64_t seq_kv, int64_t head_dim,
-                           int causal, float scale, hipStream_t stream);
+                           int causal, float scale, int waves, hipStream_t stream);
 void launch_v_transpose(const float* qkv, int64_t batch, int64_t seq, int64_t q_heads,
                         int64_t kv_heads, int64_t ld_vt, uint16_t* vt, hipStream_t stream);
 int decode_split_count(int64_t batch, int64_t kv_heads, int64_t max_context,

@@ -170,11 +170,13 @@ class DecoderExecutablePlan:
 
 
 def compile_decoder(config: DecoderConfig, data: DecoderData, device="cuda",
-                    kv_splits: int = 0, page_permutation: Optional[np.ndarray] = None
-                    ) -> DecoderExecutablePlan:
+                    kv_splits: int = 0, page_permutation: Optional[np.ndarray] = None,
+                    gemm_tile: int = 0, attn_waves: int = 0) -> DecoderExecutablePlan:
     """DecoderCompiler::compile for the gfx950 target (decoder_compiler.cpp:518-620):
     validate, pack constants on the device, build the paged KV pool, size the
-    workspace."""
+    workspace.  kv_splits, gemm_tile (sfg_gemm_tile) and attn_waves (4 or 8)
+    are the plan policy (DecoderPlanPolicy, decoder_compiler.h:55-65); 0 picks
+    per shape, and every choice computes the same layer."""
     cfg = config
     cfg.validate()
     plan = DecoderExecutablePlan(cfg, device)
@@ -273,6 +275,8 @@ def compile_decoder(config: DecoderConfig, data: DecoderData, device="cuda",
     d.page_tokens, d.pages_per_seq, d.num_pages = cfg.page_tokens, pages_per_seq, num_pages
     d.act_dtype, d.weight_dtype = act, wdt
     d.kv_splits = kv_splits
+    d.gemm_tile = gemm_tile
+    d.attn_waves = attn_waves
     d.use_routing_trace = int(data.routing_trace is not None)
     d.weight_layout = layout
     d.kv_append = int(cfg.kv_append)

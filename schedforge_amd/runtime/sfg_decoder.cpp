@@ -50,17 +50,6 @@ std::uint16_t bf16_bits(float value) {
     return static_cast<std::uint16_t>(bits >> 16);
 }
 
-std::uint64_t splitmix64(std::uint64_t x) {
-    std::uint64_t z = x + 0x9E3779B97F4A7C15ULL;
-    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
-    z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
-    return z ^ (z >> 31);
-}
-
-std::uint64_t stream_key(std::uint64_t seed, std::uint32_t tensor_id) {
-    return splitmix64(splitmix64(seed) ^ (static_cast<std::uint64_t>(tensor_id) * 0xD1B54A32D192ED03ULL));
-}
-
 unsigned worker_count() {
     const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
     return std::min(hw, 16u);
@@ -304,8 +293,7 @@ std::string DecoderExecutablePlan::dump() const {
         << " precision=" << decoder_precision_name(c.precision)
         << " page_tokens=" << c.page_tokens << '\n'
         << "library \"" << library_metadata << "\"\n"
-        << "policy weight_layout=" << (weight_layout == SFG_LAYOUT_TILED ? "tiled16x8" : "nk")
-        << " kv_splits=" << (kv_splits > 0 ? std::to_string(kv_splits) : std::string("auto"))
+        << policy.dump()
         << "\ncompile_ms=" << compile_milliseconds << "\nconstants {\n";
     for (const auto& constant : constants) out << "  " << constant.dump() << '\n';
     out << "}\n" << memory.dump() << "\nkernels {\n"
@@ -320,6 +308,56 @@ std::string DecoderExecutablePlan::dump() const {
                "  grouped_experts(w13 glu, w2)\n  combine(+residual)\n";
     out << "}\n}\n";
     return out.str();
+}
+
+std::string gemm_tile_name(int tile) {
+    switch (tile) {
+        case SFG_TILE_AUTO: return "auto";
+        case SFG_TILE_256x256_PP: return "256x256pp";
+        case SFG_TILE_256x256_W8: return "256x256w8";
+        case SFG_TILE_256x256_W4: return "256x256w4";
+        case SFG_TILE_256x128: return "256x128";
+        case SFG_TILE_128x256: return "128x256";
+        case SFG_TILE_128x128: return "128x128";
+        default: return "tile" + std::to_string(tile);
+    }
+}
+
+int parse_gemm_tile(const std::string& name) {
+    for (int t = SFG_TILE_AUTO; t < SFG_TILE_COUNT; ++t)
+        if (gemm_tile_name(t) == name) return t;
+    throw std::invalid_argument("unknown GEMM tile " + name);
+}
+
+std::string DecoderPlanPolicy::dump() const {
+    std::ostringstream out;
+    out << "policy weight_layout="
+        << (weight_layout < 0 ? "auto" : (weight_layout == SFG_LAYOUT_TILED ? "tiled16x8" : "nk"))
+        << " kv_splits=" << (kv_splits > 0 ? std::to_string(kv_splits) : std::string("auto"))
+        << " gemm_tile=" << gemm_tile_name(gemm_tile)
+        << " attn_waves=" << (attn_waves > 0 ? std::to_string(attn_waves) : std::string("auto"));
+    return out.str();
+}
+
+void DecoderExecutablePlan::apply_policy(const DecoderPlanPolicy& next) {
+    if (!device) throw std::invalid_argument("decoder plan was not compiled");
+    if (next.weight_layout >= 0 && next.weight_layout != policy.weight_layout)
+        throw std::invalid_argument("apply_policy: the weight layout is fixed at compile time");
+    if (next.kv_splits < 0 || next.gemm_tile < SFG_TILE_AUTO || next.gemm_tile >= SFG_TILE_COUNT ||
+        (next.attn_waves != 0 && next.attn_waves != 4 && next.attn_waves != 8))
+        throw std::invalid_argument("apply_policy: invalid policy " + next.dump());
+    std::lock_guard lock(device->mutex);
+    sfg_layer_desc& d = device->desc;
+    const int old_splits = d.kv_splits;
+    d.kv_splits = next.kv_splits;
+    d.gemm_tile = next.gemm_tile;
+    d.attn_waves = next.attn_waves;
+    // The split-KV count sizes the decode partials: grow the workspace if needed.
+    if (d.kv_splits != old_splits && device->lib->layer_workspace(&d) > device->workspace.bytes)
+        memory.workspace_bytes = allocate_workspace(*device);
+    policy.kv_splits = next.kv_splits;
+    policy.gemm_tile = next.gemm_tile;
+    policy.attn_waves = next.attn_waves;
 }
 
 void DecoderExecutablePlan::save(const std::filesystem::path& path) const {
@@ -447,7 +485,7 @@ std::string describe_hardware(const SfgHipLibrary& lib, int ordinal) {
     return out.str();
 }
 
-void fill_layer_desc(sfg_layer_desc& d, const DecoderConfig& c, int kv_splits, int layout,
+void fill_layer_desc(sfg_layer_desc& d, const DecoderConfig& c, const DecoderPlanPolicy& policy,
                      int pages_per_seq, int num_pages, bool use_routing_trace) {
     d = sfg_layer_desc{};
     d.abi = SFG_HIP_ABI_VERSION;
@@ -470,9 +508,11 @@ void fill_layer_desc(sfg_layer_desc& d, const DecoderConfig& c, int kv_splits, i
     d.num_pages = num_pages;
     d.act_dtype = c.precision == DecoderPrecision::F32 ? SFG_F32 : SFG_BF16;
     d.weight_dtype = weight_dtype(c.precision);
-    d.kv_splits = kv_splits;
+    d.kv_splits = policy.kv_splits;
     d.use_routing_trace = use_routing_trace ? 1 : 0;
-    d.weight_layout = layout;
+    d.weight_layout = policy.weight_layout;
+    d.gemm_tile = policy.gemm_tile;
+    d.attn_waves = policy.attn_waves;
 }
 
 std::size_t allocate_workspace(DecoderExecutablePlan::Device& dev) {
@@ -519,7 +559,14 @@ DecoderExecutablePlan DecoderCompiler::compile(const DecoderConfig& config, cons
 
     DecoderExecutablePlan plan;
     plan.config = c;
-    plan.kv_splits = options.kv_splits;
+    plan.policy = options.policy.value_or(DecoderPlanPolicy{});
+    {
+        const DecoderPlanPolicy& q = plan.policy;
+        if (q.weight_layout < -1 || q.weight_layout > SFG_LAYOUT_TILED || q.kv_splits < 0 ||
+            q.gemm_tile < SFG_TILE_AUTO || q.gemm_tile >= SFG_TILE_COUNT ||
+            (q.attn_waves != 0 && q.attn_waves != 4 && q.attn_waves != 8))
+            throw std::invalid_argument("invalid decoder plan policy: " + q.dump());
+    }
     plan.device = std::make_unique<DecoderExecutablePlan::Device>();
     auto& dev = *plan.device;
     dev.lib = load_library(options.library);
@@ -539,8 +586,15 @@ DecoderExecutablePlan DecoderCompiler::compile(const DecoderConfig& config, cons
             tiled = tiled && dev.lib->preferred_layout(rows * c.top_k, H, 1) == SFG_LAYOUT_TILED &&
                     dev.lib->preferred_layout(rows * c.top_k, I, 1) == SFG_LAYOUT_TILED;
         layout = tiled ? SFG_LAYOUT_TILED : SFG_LAYOUT_NK;
+        // A policy may ask for either layout where the decode GEMV kernels run
+        // every product; the tiled layout feeds nothing else.
+        if (plan.policy.weight_layout == SFG_LAYOUT_TILED && !tiled)
+            throw std::invalid_argument("the tiled weight layout needs every product on the decode GEMV kernels");
+        if (plan.policy.weight_layout >= 0) layout = plan.policy.weight_layout;
+    } else if (plan.policy.weight_layout == SFG_LAYOUT_TILED) {
+        throw std::invalid_argument("fp32 plans use the [N][K] weight layout");
     }
-    plan.weight_layout = layout;
+    plan.policy.weight_layout = layout;
 
     Packer pack{dev, c.precision, layout, DeviceBuffer(), plan.constants};
     sfg_layer_weights& w = dev.weights;
@@ -646,8 +700,7 @@ DecoderExecutablePlan DecoderCompiler::compile(const DecoderConfig& config, cons
         dev.upload(dev.trace_weights.ptr, t.expert_weights.data(), t.expert_weights.size() * 4);
     }
 
-    fill_layer_desc(dev.desc, c, options.kv_splits, layout, pages_per_seq, num_pages,
-                    data.routing_trace.has_value());
+    fill_layer_desc(dev.desc, c, plan.policy, pages_per_seq, num_pages, data.routing_trace.has_value());
     const std::size_t ws = allocate_workspace(dev);
 
     plan.memory.workspace_bytes = ws;

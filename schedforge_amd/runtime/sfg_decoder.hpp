@@ -111,10 +111,28 @@ struct DecoderData {
     std::optional<std::vector<int32_t>> page_table;  // [B][pages_per_seq]; default identity
 };
 
+// decoder_compiler.h:55-65.  The reference's policy picks CPU schedule knobs
+// (attention intermediate layout, schedule family, core placement, threads);
+// an MI355X plan chooses between kernel variants instead.  Every policy
+// computes the same layer: GEMM tiles and flash-prefill block heights give
+// bit-identical outputs, the weight layout only reorders bytes, and the
+// split-KV count changes the softmax merge order (fp32 rounding only).
+struct DecoderPlanPolicy {
+    int weight_layout = -1;         // SFG_LAYOUT_NK / SFG_LAYOUT_TILED; -1: per shape
+    int kv_splits = 0;              // decode split-KV count; 0: per shape
+    int gemm_tile = SFG_TILE_AUTO;  // sfg_gemm_tile of the bf16 prefill / expert GEMMs
+    int attn_waves = 0;             // bf16 flash prefill: 4 or 8 waves; 0: 4
+    std::string dump() const;
+    bool operator==(const DecoderPlanPolicy&) const = default;
+};
+std::string gemm_tile_name(int tile);
+// Inverse of gemm_tile_name; throws std::invalid_argument for an unknown name.
+int parse_gemm_tile(const std::string& name);
+
 // decoder_compiler.h:133-139, reduced to what a GPU plan uses.
 struct DecoderCompileOptions {
     int device = 0;
-    int kv_splits = 0;             // decode split-KV count; <= 0 chooses per shape
+    std::optional<DecoderPlanPolicy> policy;  // empty: every field per shape
     std::filesystem::path library; // libsfg_hip.so; empty: beside this library
 };
 
@@ -162,8 +180,7 @@ public:
     DecoderMemoryPlan memory;
     std::string hardware;
     std::string library_metadata;
-    int weight_layout = SFG_LAYOUT_NK;
-    int kv_splits = 0;
+    DecoderPlanPolicy policy;  // weight_layout resolved to the packed layout
     double compile_milliseconds = 0.0;
 
     DecoderExecutablePlan();
@@ -175,6 +192,11 @@ public:
 
     std::string dump() const;
     void save(const std::filesystem::path& path) const;
+    // Switches the kernel variants of a compiled plan without recompiling:
+    // kv_splits, gemm_tile and attn_waves change, the packed weights stay.  A
+    // policy naming another weight layout than the packed one throws
+    // std::invalid_argument (that needs DecoderCompiler::compile); -1 keeps it.
+    void apply_policy(const DecoderPlanPolicy& policy);
 
     struct Device;
     std::unique_ptr<Device> device;  // buffers, descriptor, stream
@@ -239,8 +261,7 @@ struct DecoderPackageManifest {
     int library_abi = 0;
     std::string library_metadata;
     DecoderConfig config;
-    int weight_layout = SFG_LAYOUT_NK;
-    int kv_splits = 0;
+    DecoderPlanPolicy policy;
     int pages_per_seq = 0;
     int num_pages = 0;
     bool routing_trace = false;
@@ -303,5 +324,155 @@ std::string decoder_ffn_name(DecoderFFNKind kind);
 std::string decoder_precision_name(DecoderPrecision precision);
 double max_abs_error(const std::vector<float>& a, const std::vector<float>& b);
 float round_to_bf16(float value);
+
+// ---------------------------------------------------------------- plan optimizer
+//
+// ExecutablePlanOptimizer (decoder_compiler.h:140-176, decoder_compiler.cpp:
+// 726-861) over MI355X plan policies.  The search is the reference's:
+// compile and measure the default plan (the baseline), score every candidate
+// policy with an analytical model, measure the `measurement_budget` best
+// scored, and when one beats the baseline confirm with three interleaved
+// baseline / winner measurements (medians kept); the baseline stays unless its
+// confirmed median is slower.  The analytical score is a roofline estimate of
+// the layer in microseconds on this GPU (see GpuCostModel) in place of the
+// reference's CPU penalties.  Candidates that share the packed weight layout
+// reuse one compiled plan (apply_policy): only a layout change recompiles.
+
+// decoder_compiler.h:140-147 (+ estimated_microseconds, the model's layer time).
+struct DecoderPlanCost {
+    double measured_milliseconds = 0.0;
+    double analytical_score = 0.0;
+    std::size_t workspace_bytes = 0;
+    std::size_t materialization_bytes = 0;
+    bool measured = false;
+    std::string dump() const;
+};
+
+struct DecoderPlanCandidate {
+    DecoderPlanPolicy policy;
+    DecoderPlanCost cost;
+};
+
+// decoder_compiler.h:154-162.
+struct DecoderOptimizationResult {
+    DecoderExecutablePlan plan;
+    DecoderPlanCost baseline;
+    DecoderPlanCost winner;
+    std::vector<DecoderPlanCandidate> candidates;  // [0] is the baseline
+    std::size_t hardware_measurements = 0;
+    double speedup = 1.0;
+    std::string dump() const;
+};
+
+// Machine constants of the analytical model: MI355X spec peaks, derated by
+// what this build's kernels reach on the box (calibration runs of the
+// benchmark; the values are the model's only inputs besides the shape).
+struct GpuCostModel {
+    int compute_units = 256;
+    double hbm_bytes_per_second = 8.0e12;
+    double mfma_bf16_flops = 2.5e15;
+    double valu_fp32_flops = 157.3e12;
+    double launch_microseconds = 2.5;  // per kernel on a busy stream
+    // fraction of peak a kernel family sustains inside a full wave of tiles
+    double hbm_efficiency = 0.68;
+    double gemv_tiled_efficiency = 0.48;
+    double gemv_nk_efficiency = 0.40;
+    double fp32_gemm_efficiency = 0.30;
+    double flash_efficiency = 0.42;
+    // per sfg_gemm_tile: efficiency of one full wave of tiles
+    double tile_efficiency[SFG_TILE_COUNT] = {0.0, 0.50, 0.47, 0.42, 0.44, 0.40, 0.36};
+};
+
+class ExecutablePlanOptimizer {
+public:
+    explicit ExecutablePlanOptimizer(GpuCostModel model = {});
+    // The candidate policies for a configuration (the reference enumerates its
+    // policy space the same way, decoder_compiler.cpp:754-781): weight layouts
+    // and split-KV counts for decode steps, GEMM tiles and flash-prefill block
+    // heights for bf16 prefill.  The first is the default policy.
+    std::vector<DecoderPlanPolicy> policies(const DecoderConfig& config) const;
+    // Analytical cost of a policy; needs no GPU (compile-only records use it).
+    DecoderPlanCost evaluate(const DecoderConfig& config, const DecoderPlanPolicy& policy) const;
+    DecoderPlanCost evaluate(const DecoderExecutablePlan& plan) const;
+    DecoderOptimizationResult optimize(const DecoderConfig& config, const DecoderData& data,
+                                       int measurement_budget = 8, int repetitions = 2,
+                                       const DecoderCompileOptions& options = {}) const;
+    const GpuCostModel& model() const { return model_; }
+
+private:
+    GpuCostModel model_;
+};
+
+// ---------------------------------------------------------------- profile harness
+//
+// The reference's realistic-profile harness (decoder_compiler.h:178-238,
+// decoder_compiler.cpp:863-1060) on the GPU: the same profile list, evidence
+// classes and CSV schemas, with GPU columns appended after the reference's.
+
+// moe_compiler.h (RoutingDistribution): expert draw weights 1 (uniform) or
+// 1 / (e + 1)^0.8 (moderate) or ^1.6 (heavy), top-k distinct experts per token
+// drawn by weight, each weighted 1 / k (moe_compiler.cpp:457-488).
+enum class RoutingDistribution { Uniform, ModerateSkew, HeavySkew };
+std::string routing_distribution_name(RoutingDistribution distribution);
+RoutingTrace make_routing_trace(int tokens, int experts, int top_k,
+                                RoutingDistribution distribution, std::uint64_t seed);
+
+enum class DecoderEvidenceKind { Measured, CompileOnly, Skipped };
+std::string decoder_evidence_name(DecoderEvidenceKind kind);
+
+// decoder_compiler.h:180-187.
+struct DecoderBenchmarkProfile {
+    std::string name;
+    DecoderConfig config;
+    RoutingDistribution routing = RoutingDistribution::Uniform;
+    std::uint64_t estimated_flops = 0;
+    std::size_t estimated_weight_bytes = 0;
+    std::size_t estimated_activation_bytes = 0;
+};
+
+// decoder_compiler.h:189-204 (+ the optimizer's policy spread).
+struct DecoderBenchmarkRecord {
+    DecoderBenchmarkProfile profile;
+    DecoderEvidenceKind evidence = DecoderEvidenceKind::Skipped;
+    DecoderBenchmarkResult measured;
+    DecoderPlanCost plan_cost;
+    double compile_milliseconds = 0.0;
+    double llvm_compile_milliseconds = 0.0;  // always 0: nothing is JIT-compiled
+    double memory_planning_milliseconds = 0.0;
+    double optimizer_speedup = 1.0;
+    double optimizer_baseline_milliseconds = 0.0;
+    std::size_t hardware_measurements = 0;
+    std::string selected_policy;
+    std::vector<DecoderPlanCandidate> optimizer_candidates;
+    std::string note;
+};
+
+// decoder_compiler.cpp:863-903: FLOPs (non-causal attention, as the reference
+// counts), weight bytes at the profile's precision, activation bytes.
+DecoderBenchmarkProfile make_decoder_profile(std::string name, DecoderConfig config,
+                                             RoutingDistribution routing = RoutingDistribution::Uniform);
+// decoder_compiler.cpp:905-930: tiny / medium / large dense prefill (S 128,
+// 512, 2048) and decode (KV 128, 512, 2048, 4096), and the tiny MoE layer
+// under three routing distributions, at the given precision.
+std::vector<DecoderBenchmarkProfile> realistic_decoder_profiles(
+    DecoderPrecision precision = DecoderPrecision::F32);
+// The five benchmark configurations c1..c5 as profiles.
+std::vector<DecoderBenchmarkProfile> baseline_decoder_profiles();
+// decoder_compiler.cpp:932-987: compile-only (analytical cost, no GPU) above
+// the FLOP or weight budget, else compile, optionally optimise, and measure.
+// Configurations the GPU target does not lower are recorded as Skipped with
+// the reason.
+DecoderBenchmarkRecord benchmark_decoder_profile(const DecoderBenchmarkProfile& profile,
+                                                 std::uint64_t max_real_flops,
+                                                 std::size_t max_real_weight_bytes,
+                                                 bool optimize_plan, int repetitions = 2,
+                                                 const DecoderCompileOptions& options = {});
+// decoder_compiler.cpp:989-1030 and 1032-1058: the reference's column lists,
+// then precision, layer_tflops and layer_gbps (benchmark) and the GPU policy
+// fields in place of the CPU ones (candidates).
+void write_decoder_benchmark_csv(const std::filesystem::path& path,
+                                 const std::vector<DecoderBenchmarkRecord>& records);
+void write_decoder_plan_candidates_csv(const std::filesystem::path& path,
+                                       const std::vector<DecoderBenchmarkRecord>& records);
 
 }  // namespace schedforge::hip

@@ -6,7 +6,9 @@
 //
 // Extra options:
 //   --config=c1..c5          one of the five benchmark configurations
-//   --precision=f32|bf16|w8  --context=N  --page-tokens=N  --kv-splits=N
+//   --precision=f32|bf16|w8  --context=N  --page-tokens=N
+//   --kv-splits=N --gemm-tile=NAME --attn-waves=N --weight-layout=auto|nk|tiled
+//                            the plan policy (DecoderPlanPolicy)
 //   --router-bias-std=S  --seed=N  --warmup=N  --device=N
 //   --expect=FILE            raw fp32 [rows][hidden] to compare with (max_error)
 //   --max-error=E            exit status 1 when max_error exceeds E (default 1e-3
@@ -51,6 +53,11 @@ struct Options {
 
 int to_int(const std::string& s) { return std::stoi(s); }
 
+sh::DecoderPlanPolicy& policy(Options& o) {
+    if (!o.compile.policy) o.compile.policy.emplace();
+    return *o.compile.policy;
+}
+
 Options parse(int argc, char** argv) {
     Options o;
     auto& c = o.config;
@@ -85,7 +92,15 @@ Options parse(int argc, char** argv) {
             else throw std::invalid_argument("unknown precision " + *v);
         } else if (auto v = value(a, "--router-bias-std=")) o.router_bias_std = std::stof(*v);
         else if (auto v = value(a, "--seed=")) o.seed = std::stoull(*v);
-        else if (auto v = value(a, "--kv-splits=")) o.compile.kv_splits = to_int(*v);
+        else if (auto v = value(a, "--kv-splits=")) policy(o).kv_splits = to_int(*v);
+        else if (auto v = value(a, "--gemm-tile=")) policy(o).gemm_tile = sh::parse_gemm_tile(*v);
+        else if (auto v = value(a, "--attn-waves=")) policy(o).attn_waves = to_int(*v);
+        else if (auto v = value(a, "--weight-layout=")) {
+            if (*v == "auto") policy(o).weight_layout = -1;
+            else if (*v == "nk") policy(o).weight_layout = SFG_LAYOUT_NK;
+            else if (*v == "tiled") policy(o).weight_layout = SFG_LAYOUT_TILED;
+            else throw std::invalid_argument("unknown weight layout " + *v);
+        }
         else if (auto v = value(a, "--device=")) o.compile.device = to_int(*v);
         else if (auto v = value(a, "--warmup=")) o.warmup = to_int(*v);
         else if (auto v = value(a, "--repetitions=")) o.repetitions = to_int(*v);
@@ -104,6 +119,8 @@ Options parse(int argc, char** argv) {
                          "  [--intermediate=128 --q-heads=4 --kv-heads=2 --head-dim=16]\n"
                          "  [--moe --experts=4 --top-k=2 --router-bias-std=0] [--context=0 --page-tokens=16]\n"
                          "  [--precision=f32|bf16|w8 --kv-splits=0 --device=0 --seed=71]\n"
+                         "  [--gemm-tile=auto|256x256pp|256x256w8|256x256w4|256x128|128x256|128x128]\n"
+                         "  [--attn-waves=0|4|8 --weight-layout=auto|nk|tiled]\n"
                          "  [--warmup=1 --repetitions=3 --non-causal] [-o decoder.sfe]\n"
                          "  [--expect=FILE --max-error=1e-3 --dump-output=FILE --dump-data=DIR]\n"
                          "  [--package=DIR.sfe | --load-package=DIR.sfe | --inspect=DIR.sfe]\n";
@@ -196,9 +213,8 @@ int main(int argc, char** argv) {
 
         std::cout << "[Constants]\n";
         for (const auto& constant : plan.constants) std::cout << constant.dump() << '\n';
-        std::cout << "\n[Memory]\n" << plan.memory.dump() << "\n\n[Plan Policy]\nweight_layout="
-                  << (plan.weight_layout == SFG_LAYOUT_TILED ? "tiled16x8" : "nk")
-                  << " kv_splits=" << (plan.kv_splits > 0 ? std::to_string(plan.kv_splits) : "auto")
+        std::cout << "\n[Memory]\n" << plan.memory.dump() << "\n\n[Plan Policy]\n"
+                  << plan.policy.dump()
                   << "\n\n[Runtime]\nFFN: " << sh::decoder_ffn_name(o.config.ffn)
                   << "\nprecision: " << sh::decoder_precision_name(o.config.precision)
                   << std::fixed << std::setprecision(4)

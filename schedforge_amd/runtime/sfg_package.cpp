@@ -393,8 +393,10 @@ std::string DecoderPackageManifest::dump() const {
       << "context_sequence=" << c.context_sequence << '\n'
       << "precision=" << decoder_precision_name(c.precision) << '\n'
       << "page_tokens=" << c.page_tokens << '\n'
-      << "weight_layout=" << weight_layout << '\n'
-      << "kv_splits=" << kv_splits << '\n'
+      << "weight_layout=" << policy.weight_layout << '\n'
+      << "kv_splits=" << policy.kv_splits << '\n'
+      << "gemm_tile=" << policy.gemm_tile << '\n'
+      << "attn_waves=" << policy.attn_waves << '\n'
       << "pages_per_seq=" << pages_per_seq << '\n'
       << "num_pages=" << num_pages << '\n'
       << "routing_trace=" << (routing_trace ? 1 : 0) << '\n'
@@ -459,10 +461,16 @@ DecoderPackageManifest DecoderPackageManifest::parse(const std::string& text) {
     } catch (const std::invalid_argument& e) {
         throw std::runtime_error(std::string(".sfe configuration: ") + e.what());
     }
-    m.weight_layout = number<int>(f, "weight_layout");
-    if (m.weight_layout != SFG_LAYOUT_NK && m.weight_layout != SFG_LAYOUT_TILED)
+    DecoderPlanPolicy& q = m.policy;
+    q.weight_layout = number<int>(f, "weight_layout");
+    if (q.weight_layout != SFG_LAYOUT_NK && q.weight_layout != SFG_LAYOUT_TILED)
         throw std::runtime_error("unknown .sfe weight layout");
-    m.kv_splits = number<int>(f, "kv_splits");
+    q.kv_splits = number<int>(f, "kv_splits");
+    q.gemm_tile = number<int>(f, "gemm_tile");
+    q.attn_waves = number<int>(f, "attn_waves");
+    if (q.kv_splits < 0 || q.gemm_tile < SFG_TILE_AUTO || q.gemm_tile >= SFG_TILE_COUNT ||
+        (q.attn_waves != 0 && q.attn_waves != 4 && q.attn_waves != 8))
+        throw std::runtime_error("invalid .sfe plan policy");
     m.pages_per_seq = number<int>(f, "pages_per_seq");
     m.num_pages = number<int>(f, "num_pages");
     m.routing_trace = number<int>(f, "routing_trace") != 0;
@@ -538,8 +546,7 @@ DecoderPackageManifest save_decoder_package(const DecoderExecutablePlan& plan,
         m.library_abi = dev.lib->abi_version();
         m.library_metadata = dev.lib->metadata();
         m.config = plan.config;
-        m.weight_layout = dev.desc.weight_layout;
-        m.kv_splits = dev.desc.kv_splits;
+        m.policy = plan.policy;
         m.pages_per_seq = dev.desc.pages_per_seq;
         m.num_pages = dev.desc.num_pages;
         m.routing_trace = dev.desc.use_routing_trace != 0;
@@ -645,8 +652,7 @@ DecoderExecutablePlan load_decoder_package(const std::filesystem::path& path, in
     DecoderExecutablePlan plan;
     plan.config = m.config;
     plan.constants = m.constant_table;
-    plan.weight_layout = m.weight_layout;
-    plan.kv_splits = m.kv_splits;
+    plan.policy = m.policy;
     plan.device = std::make_unique<DecoderExecutablePlan::Device>();
     auto& dev = *plan.device;
     dev.lib = load_library(std::filesystem::absolute(path / m.library.path));
@@ -694,7 +700,7 @@ DecoderExecutablePlan load_decoder_package(const std::filesystem::path& path, in
     if (m.routing_trace != (has_trace_ids && has_trace_weights))
         throw std::runtime_error(".sfe routing trace buffers do not match the manifest");
 
-    fill_layer_desc(dev.desc, m.config, m.kv_splits, m.weight_layout, m.pages_per_seq, m.num_pages,
+    fill_layer_desc(dev.desc, m.config, m.policy, m.pages_per_seq, m.num_pages,
                     m.routing_trace);
     const std::size_t ws = allocate_workspace(dev);
     if (ws != m.workspace_bytes)

@@ -7,6 +7,7 @@
 #include <dlfcn.h>
 #include <hip/hip_runtime_api.h>
 
+#include <cstdint>
 #include <filesystem>
 #include <memory>
 #include <mutex>
@@ -22,6 +23,21 @@ namespace schedforge::hip {
 inline void hip_check(hipError_t rc, const char* what) {
     if (rc != hipSuccess)
         throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(rc));
+}
+
+// ---------------------------------------------------------------- generator
+
+// SplitMix64 and the per-tensor stream key of the synthetic-data generator
+// (seed, tensor id): element i of a stream draws splitmix64(key + i).
+inline std::uint64_t splitmix64(std::uint64_t x) {
+    std::uint64_t z = x + 0x9E3779B97F4A7C15ULL;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+    return z ^ (z >> 31);
+}
+
+inline std::uint64_t stream_key(std::uint64_t seed, std::uint32_t tensor_id) {
+    return splitmix64(splitmix64(seed) ^ (static_cast<std::uint64_t>(tensor_id) * 0xD1B54A32D192ED03ULL));
 }
 
 // ---------------------------------------------------------------- library
@@ -150,7 +166,7 @@ struct DecoderExecutablePlan::Device {
 // Shared by compile and package loading.
 std::string describe_hardware(const SfgHipLibrary& lib, int ordinal);
 // The layer descriptor of a plan (everything but the device pointers).
-void fill_layer_desc(sfg_layer_desc& d, const DecoderConfig& c, int kv_splits, int layout,
+void fill_layer_desc(sfg_layer_desc& d, const DecoderConfig& c, const DecoderPlanPolicy& policy,
                      int pages_per_seq, int num_pages, bool use_routing_trace);
 // Allocates and zeroes the layer's workspace for dev.desc; returns its size.
 std::size_t allocate_workspace(DecoderExecutablePlan::Device& dev);

@@ -101,3 +101,55 @@ def test_layer_prefill_fused_qkv_rope_matches_oracle(batch, seq):
     print(f"fused-qkv prefill B{batch} S{seq}: rel_err {err:.3e}")
     assert np.isfinite(res.output).all()
     assert err < TOL[cfg.dtype], err
+
+
+@pytest.mark.parametrize("context", [512, 0])
+def test_layer_head_dim_64_bf16_matches_oracle(context):
+    """bf16 layer at head_dim 64 (the reference's tiny and medium decoder
+    profiles, decoder_compiler.cpp:920-921): paged decode, and prefill on the
+    generic bf16 flash kernel."""
+    cfg = CONFIGS["c2"].replace(batch=4, hidden=512, intermediate=1376, query_heads=8,
+                                kv_heads=2, head_dim=64, context_sequence=context)
+    if context == 0:
+        cfg = cfg.replace(batch=1, sequence=128)
+    res, ref, _ = _run(cfg, CONFIG_SEEDS["c2"] + 21)
+    err = oracle.rel_error(res.output, ref)
+    print(f"bf16 D64 context {context}: rel_err {err:.3e}")
+    assert err < TOL[cfg.dtype], err
+
+
+def _outputs_by_policy(cfg, seed, policies, trace=False):
+    """One compiled plan, executed under each (gemm_tile, attn_waves) policy."""
+    from schedforge_amd.layer import compile_decoder, execute_decoder_layer
+    d = oracle.make_layer_data(cfg, seed)
+    tr = None
+    if trace:
+        _, taps0 = oracle.decoder_layer(cfg, d, taps=True)
+        tr = (taps0["ids"], taps0["weights"])
+        d.routing_trace = tr
+    ref = oracle.decoder_layer(cfg, d, trace=tr)
+    plan = compile_decoder(cfg, decoder_data(d), "cuda", page_permutation=d.page_permutation)
+    outs = []
+    for tile, waves in policies:
+        plan.desc.gemm_tile, plan.desc.attn_waves = tile, waves
+        outs.append(execute_decoder_layer(plan, d.input, warmup=0, repetitions=1).output)
+    return outs, ref
+
+
+def test_layer_every_plan_policy_is_bit_identical():
+    """Plan policies choose kernel variants, not arithmetic: every GEMM tile and
+    both flash-prefill block heights give the same bits (dense prefill with the
+    fused QKV+RoPE epilogue, and the grouped expert GEMMs under a routing trace)."""
+    from schedforge_amd import _abi
+    policies = [(0, 0)] + [(t, 0) for t in range(1, _abi.TILE_COUNT)] + [(0, 8), (_abi.TILE_128x128, 8)]
+    dense = CONFIGS["c4"].replace(sequence=1024, hidden=1024, intermediate=2048, query_heads=8,
+                                  kv_heads=2)
+    moe = CONFIGS["c3"].replace(batch=2, sequence=512, hidden=1024, intermediate=512,
+                                query_heads=8, kv_heads=2)
+    for cfg, seed, trace in ((dense, CONFIG_SEEDS["c4"] + 31, False), (moe, CONFIG_SEEDS["c3"] + 31, True)):
+        outs, ref = _outputs_by_policy(cfg, seed, policies, trace=trace)
+        err = oracle.rel_error(outs[0], ref)
+        print(f"{'moe' if cfg.moe else 'dense'} policies: rel_err {err:.3e}")
+        assert err < TOL[cfg.dtype], err
+        for (tile, waves), out in zip(policies[1:], outs[1:]):
+            assert np.array_equal(out, outs[0]), (tile, waves)

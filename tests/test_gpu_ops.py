@@ -73,7 +73,7 @@ def test_rmsnorm_bf16_output_is_rne_of_f32(lib):
 
 # ------------------------------------------------------------------ GEMM
 def _gemm(lib, a_dev, a_dtype, b_dev, b_dtype, m, n, k, epi, c_dtype=F32, scales=None,
-          residual=None, layout=0):
+          residual=None, layout=0, tile=0):
     glu = epi in (EPI_SWIGLU, EPI_GLU_SILU_UP)
     c = torch.empty((m, n), dtype=torch.float32 if c_dtype == F32 else torch.int16, device="cuda")
     args = _abi.GemmArgs()
@@ -85,11 +85,39 @@ def _gemm(lib, a_dev, a_dtype, b_dev, b_dtype, m, n, k, epi, c_dtype=F32, scales
     args.ldr = n
     args.m, args.n, args.k, args.epilogue = m, n, k, epi
     args.b_layout = layout
+    args.tile = tile
     wsb = lib.sfg_hip_gemm_workspace_v1(m, n, k)
     ws = torch.zeros(max(wsb, 256), dtype=torch.uint8, device="cuda")
     _abi.check(lib.sfg_hip_gemm_v1(ctypes.byref(args), ws.data_ptr(), ws.numel(), stream()))
     _sync()
     return c
+
+
+@pytest.mark.parametrize("tile", list(range(1, _abi.TILE_COUNT)))
+@pytest.mark.parametrize("m,n,k,epi", [(1024, 512, 256, EPI_NONE), (1300, 768, 320, EPI_RESIDUAL),
+                                       (2048, 512, 192, EPI_SWIGLU)])
+def test_gemm_every_tile_policy_exact(lib, tile, m, n, k, epi):
+    """Each sfg_gemm_tile of the direct-to-LDS kernel, on small-integer
+    operands (every partial sum exact in fp32): a wrong fragment, swizzle or
+    edge mask shows as a difference.  Ragged M / N exercise the tile edges."""
+    rng = np.random.default_rng(tile * 131 + m)
+    glu = epi == EPI_SWIGLU
+    a = rng.integers(-3, 4, size=(m, k)).astype(np.float32)
+    b = rng.integers(-3, 4, size=((2 * n) if glu else n, k)).astype(np.float32)
+    res = rng.integers(-5, 6, size=(m, n)).astype(np.float32)
+    c = _gemm(lib, bf16_dev(a), BF16, bf16_dev(b), BF16, m, n, k, epi,
+              residual=dev(res) if epi == EPI_RESIDUAL else None, tile=tile)
+    acc = a.astype(np.float64) @ b.T.astype(np.float64)
+    if glu:
+        np.testing.assert_allclose(host(c), _ref_epilogue(acc, epi, n), rtol=1e-5, atol=1e-5)
+    else:
+        np.testing.assert_array_equal(host(c), _ref_epilogue(acc, epi, n, res).astype(np.float32))
+
+
+def test_gemm_rejects_unknown_tile(lib):
+    a = bf16_dev(np.ones((1024, 64), np.float32))
+    with pytest.raises(ValueError):
+        _gemm(lib, a, BF16, a, BF16, 1024, 1024, 64, EPI_NONE, tile=_abi.TILE_COUNT)
 
 
 def _ref_epilogue(acc, epi, n, residual=None):
@@ -126,6 +154,29 @@ def test_gemm_int8_integer_operands_exact(lib, m, n, k):
     s = np.ones(n, np.float32)
     c = _gemm(lib, bf16_dev(a), BF16, dev(q), I8, m, n, k, EPI_NONE, scales=dev(s))
     np.testing.assert_array_equal(host(c), a @ q.astype(np.float32).T)
+
+
+@pytest.mark.parametrize("m,n,k,epi", [(128, 1376, 512, EPI_SWIGLU), (700, 688, 256, EPI_NONE),
+                                       (300, 1376, 512, EPI_RESIDUAL), (1100, 1376, 256, EPI_SWIGLU),
+                                       (1100, 688, 512, EPI_RESIDUAL)])
+def test_gemm_bf16_ragged_n_integer_operands(lib, m, n, k, epi):
+    """Output widths that are not a whole number of column tiles (the
+    reference's tiny profile, intermediate 1376 = 10.75 x 128): the last tile's
+    extra columns read a valid B row, are masked at the store, and every stored
+    value is exact on small-integer operands."""
+    rng = np.random.default_rng(m + 3 * n + k)
+    glu = epi == EPI_SWIGLU
+    a = rng.integers(-3, 4, size=(m, k)).astype(np.float32)
+    b = rng.integers(-3, 4, size=((2 * n) if glu else n, k)).astype(np.float32)
+    res = rng.integers(-5, 6, size=(m, n)).astype(np.float32)
+    c = _gemm(lib, bf16_dev(a), BF16, bf16_dev(b), BF16, m, n, k, epi,
+              residual=dev(res) if epi == EPI_RESIDUAL else None)
+    acc = a.astype(np.float64) @ b.T.astype(np.float64)
+    ref = _ref_epilogue(acc, epi, n, res)
+    if glu:
+        np.testing.assert_allclose(host(c), ref, rtol=1e-5, atol=1e-5)
+    else:
+        np.testing.assert_array_equal(host(c), ref.astype(np.float32))
 
 
 @pytest.mark.parametrize("m", [16, 64, 512, 1280])
@@ -240,12 +291,12 @@ def test_attention_prefill_f32_matches_oracle(lib, causal, shape):
     assert oracle.rel_error(host(out), ref) < 1e-5
 
 
+@pytest.mark.parametrize("D", [128, 64])
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("shape", [(1, 4, 2, 256, 256), (2, 8, 2, 300, 300), (1, 2, 1, 64, 200),
                                    (1, 2, 2, 1, 77)])
-def test_attention_prefill_bf16_matches_oracle(lib, causal, shape):
+def test_attention_prefill_bf16_matches_oracle(lib, causal, shape, D):
     B, Hq, Hkv, Sq, Skv = shape
-    D = 128
     q = oracle.round_bf16(oracle.normal(81, 0, (B, Hq, Sq, D)))
     k = oracle.round_bf16(oracle.normal(81, 1, (B, Hkv, Skv, D)))
     v = oracle.round_bf16(oracle.normal(81, 2, (B, Hkv, Skv, D)))
@@ -376,8 +427,8 @@ def test_split_rope_vt_matches_split_rope(lib):
                                                     vt.data_ptr(), ld + 1, stream()))
 
 
-def _decode_case(lib, B, Hq, Hkv, ctx, seq_lens=None, splits=0, seed=91):
-    D, PT = 128, 16
+def _decode_case(lib, B, Hq, Hkv, ctx, seq_lens=None, splits=0, seed=91, D=128):
+    PT = 16
     pps = (ctx + PT - 1) // PT
     num_pages = B * pps + 3
     perm = oracle.page_permutation(seed, num_pages)[: B * pps]
@@ -412,6 +463,14 @@ def _decode_case(lib, B, Hq, Hkv, ctx, seq_lens=None, splits=0, seed=91):
                                           (2, 8, 1, 256), (1, 32, 4, 50)])
 def test_decode_paged_matches_oracle(lib, B, Hq, Hkv, ctx):
     _decode_case(lib, B, Hq, Hkv, ctx)
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,ctx", [(1, 8, 2, 512), (3, 16, 4, 100), (2, 4, 4, 2048)])
+def test_decode_paged_head_dim_64_matches_oracle(lib, B, Hq, Hkv, ctx):
+    """head_dim 64 (the reference's tiny / medium decoder profiles,
+    decoder_compiler.cpp:920-921): two S^T k-steps and four O^T blocks per page."""
+    _decode_case(lib, B, Hq, Hkv, ctx, D=64)
+    _decode_case(lib, B, Hq, Hkv, ctx, D=64, splits=3, seed=92)
 
 
 def test_decode_ragged_lengths_and_split_invariance(lib):

@@ -101,7 +101,8 @@ def _manifest_lines(root: Path, lib_meta: str, buffers, extra=None):
         "kv_heads": cfg.kv_heads, "head_dim": cfg.head_dim, "rms_epsilon": "9.99999997e-07",
         "rope_theta": "10000", "causal": 1, "ffn": "dense_swiglu", "experts": 4, "top_k": 2,
         "context_sequence": 0, "precision": "f32", "page_tokens": 16, "weight_layout": 0,
-        "kv_splits": 0, "pages_per_seq": 0, "num_pages": 0, "routing_trace": 0,
+        "kv_splits": 0, "gemm_tile": 0, "attn_waves": 0, "pages_per_seq": 0, "num_pages": 0,
+        "routing_trace": 0,
         "workspace_bytes": 4096, "naive_bytes": 1,
         "plan": f"plan.sfe,{len(plan)},{fnv1a64(plan)}",
         "library": f"libsfg_hip.so,{len(lib)},{fnv1a64(lib)}",

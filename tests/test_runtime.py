@@ -20,7 +20,7 @@ import pytest
 
 import oracle
 from schedforge_amd import CONFIGS, CONFIG_SEEDS
-from schedforge_amd.build import DECODER_CLI
+from schedforge_amd.build import BENCH_CLI, DECODER_CLI
 
 from _helpers import SMALL, TOL
 
@@ -107,6 +107,77 @@ def test_named_config_selects_shape_and_seed(tmp_path):
     np.testing.assert_array_equal(x, want)
 
 
+# The reference's benchmark CSV columns (decoder_compiler.cpp:993), which the
+# GPU harness keeps as the prefix of its own.
+REFERENCE_BENCH_COLUMNS = (
+    "profile,evidence,ffn,batch,sequence,context,hidden,intermediate,q_heads,kv_heads,head_dim,"
+    "experts,top_k,routing,estimated_flops,weight_bytes,activation_bytes,latency_ms,attention_ms,"
+    "attention_pct,projection_ms,projection_pct,norm_rope_ms,norm_rope_pct,ffn_ms,ffn_pct,"
+    "residual_ms,residual_pct,dispatch_ms,dispatch_pct,tokens_per_second,workspace_bytes,"
+    "compile_ms,llvm_compile_ms,memory_planning_ms,memory_planning_pct,optimizer_baseline_ms,"
+    "optimizer_speedup,hardware_measurements,max_error,selected_policy,note").split(",")
+
+
+def run_bench(args, timeout=600):
+    return subprocess.run([str(BENCH_CLI), *args], capture_output=True, text=True, timeout=timeout)
+
+
+def read_csv(path):
+    import csv
+    with open(path, newline="") as f:
+        return list(csv.DictReader(f))
+
+
+def test_bench_cli_options_and_errors():
+    r = run_bench(["--help"])
+    assert r.returncode == 0 and "--suite=realistic|optimizer|baseline" in r.stdout
+    r = run_bench(["--bogus"])
+    assert r.returncode == 2 and "unknown option" in r.stderr
+    r = run_bench(["--suite=nope"])
+    assert r.returncode == 2 and "unknown suite" in r.stderr
+
+
+def test_bench_compile_only_profiles_and_schema(tmp_path):
+    """Compile-only records (decoder_compiler.cpp:940-955) need no GPU: the
+    realistic profile list of the reference (905-930) with its FLOP and weight
+    estimates (865-903) and this target's analytical layer time."""
+    out = tmp_path / "r.csv"
+    r = run_bench(["--compile-only", f"--output={out}", "--precision=f32"])
+    assert r.returncode == 0, r.stderr
+    assert "[Summary] profiles=24 measured=0 compile-only=24 skipped=0" in r.stdout
+    header = out.read_text().splitlines()[0].split(",")
+    assert header[:len(REFERENCE_BENCH_COLUMNS)] == REFERENCE_BENCH_COLUMNS
+    rows = {row["profile"]: row for row in read_csv(out)}
+    names = [f"{s}-{k}" for s in ("tiny", "medium", "large")
+             for k in ("prefill-s128", "prefill-s512", "prefill-s2048",
+                       "decode-kv128", "decode-kv512", "decode-kv2048", "decode-kv4096")]
+    names += ["tiny-moe-uniform", "tiny-moe-moderate-skew", "tiny-moe-heavy-skew"]
+    assert list(rows) == names
+    assert all(row["evidence"] == "compile-only" for row in rows.values())
+    # estimate_decoder_flops (865-880), e.g. tiny prefill S128: projections
+    # 2*128*512*(512+256) + 2*128*512*512, attention 4*8*128*128*64, FFN 6*128*512*1376
+    flops = 2 * 128 * 512 * (512 + 256) + 2 * 128 * 512 * 512 + 4 * 8 * 128 * 128 * 64 + 6 * 128 * 512 * 1376
+    assert int(rows["tiny-prefill-s128"]["estimated_flops"]) == flops
+    # estimate_decoder_weights (882-890) in fp32
+    assert int(rows["tiny-prefill-s128"]["weight_bytes"]) == 4 * (512 * (512 + 256) + 512 * 512 + 3 * 512 * 1376)
+    assert int(rows["tiny-moe-heavy-skew"]["experts"]) == 16
+    est = {n: float(row["analytical_us"]) for n, row in rows.items()}
+    assert all(v > 0 for v in est.values())
+    for scale in ("tiny", "medium", "large"):
+        pre = [est[f"{scale}-prefill-s{s}"] for s in (128, 512, 2048)]
+        dec = [est[f"{scale}-decode-kv{k}"] for k in (128, 512, 2048, 4096)]
+        assert pre == sorted(pre) and dec == sorted(dec), scale
+
+
+def test_bench_baseline_suite_compile_only(tmp_path):
+    out = tmp_path / "b.csv"
+    r = run_bench(["--suite=baseline", "--compile-only", f"--output={out}"])
+    assert r.returncode == 0, r.stderr
+    rows = read_csv(out)
+    assert [row["profile"] for row in rows] == ["c1", "c2", "c3", "c4", "c5"]
+    assert [row["precision"] for row in rows] == ["f32", "bf16", "bf16", "bf16", "w8"]
+
+
 # ------------------------------------------------------------------ GPU
 
 
@@ -151,3 +222,50 @@ def test_cli_moe_layer_matches_oracle(tmp_path, name):
     rows_err = np.max(np.abs(got - ref), axis=1) / max(np.max(np.abs(ref)), 1e-6)
     bad = np.nonzero(rows_err >= TOL[cfg.dtype])[0]
     assert len(bad) <= max(1, cfg.rows // 200), bad
+
+
+@pytest.mark.gpu
+def test_cli_gemm_tile_policy_keeps_output(tmp_path):
+    """--gemm-tile / --attn-waves change kernel variants only: the output of a
+    bf16 prefill is identical, bit for bit, to the default plan's."""
+    cfg = CONFIGS["c4"].replace(sequence=1024, hidden=1024, intermediate=2048, query_heads=8,
+                                kv_heads=2)
+    outs = []
+    for extra in ([], ["--gemm-tile=128x128", "--attn-waves=8"], ["--gemm-tile=256x256w4"]):
+        out = tmp_path / f"o{len(outs)}.bin"
+        r = run_cli(cfg_args(cfg, 7) + ["--repetitions=1", f"--dump-output={out}", *extra])
+        assert r.returncode == 0, r.stderr
+        assert "gemm_tile=" + (extra[0].split("=")[1] if extra else "auto") in r.stdout
+        outs.append(load(out))
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+
+
+@pytest.mark.gpu
+def test_bench_optimizer_suite(tmp_path):
+    """ExecutablePlanOptimizer over GPU policies (decoder_compiler.cpp:750-861):
+    the baseline is candidate 0 and measured, at most six more are measured,
+    exactly one candidate is selected, and the speedup is baseline / winner
+    (>= 1 by construction: the baseline stays unless it is slower)."""
+    out = tmp_path / "opt.csv"
+    r = run_bench(["--suite=optimizer", f"--output={out}", "--repetitions=2"], timeout=600)
+    print(r.stdout[-3000:], r.stderr[-2000:])
+    assert r.returncode == 0, r.stderr
+    rows = {row["profile"]: row for row in read_csv(out)}
+    assert set(rows) == {"tiny-prefill-s128", "tiny-decode-kv512"}
+    cands = read_csv(tmp_path / "opt_candidates.csv")
+    for name, row in rows.items():
+        assert row["evidence"] == "measured", row
+        mine = [c for c in cands if c["profile"] == name]
+        assert mine[0]["candidate"] == "0" and mine[0]["measured"] == "1"
+        measured = [c for c in mine if c["measured"] == "1"]
+        assert 1 <= len(measured) <= 7
+        assert sum(c["selected"] == "1" for c in mine) == 1
+        hw = int(row["hardware_measurements"])
+        assert hw in (len(measured), len(measured) + 6)
+        assert float(row["optimizer_speedup"]) >= 1.0
+        assert float(row["latency_ms"]) > 0 and float(row["tokens_per_second"]) > 0
+    # decode candidates span split counts (the tiled weight layout needs K a
+    # multiple of 128: intermediate 1376 keeps this profile on [N][K])
+    dec = [c for c in cands if c["profile"] == "tiny-decode-kv512"]
+    assert {c["weight_layout"] for c in dec} == {"nk"}
+    assert len({c["kv_splits"] for c in dec}) >= 4
