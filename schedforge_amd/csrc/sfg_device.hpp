@@ -106,6 +106,14 @@ __device__ __forceinline__ void lds_dma16_buf(buf_rsrc r, uint32_t voffset, uint
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
         r, (__attribute__((address_space(3))) void*)(lds_block), 16, voffset, 0, 0, 0);
 }
+// The same load with a wave-uniform byte offset in the instruction's SGPR
+// operand: a loop that advances only `soffset` issues each load without any
+// per-lane address arithmetic.
+__device__ __forceinline__ void lds_dma16_buf(buf_rsrc r, uint32_t voffset, uint32_t soffset,
+                                              uint16_t* lds_block) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        r, (__attribute__((address_space(3))) void*)(lds_block), 16, voffset, soffset, 0, 0);
+}
 
 __device__ __forceinline__ void wait_vmem_all() {
     // s_waitcnt vmcnt(0), other counters untouched (gfx9 encoding: expcnt 7,

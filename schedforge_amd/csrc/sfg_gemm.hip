@@ -17,6 +17,8 @@
 //    and per-group (expert) segments read from device offsets.
 //  * gemm_f32_kernel      fp32 operands (the fp32 parity config): 64x64 LDS
 //    tiles on the VALU.
+#include <type_traits>
+
 #include "sfg_kernels.hpp"
 
 #include <cstdlib>
@@ -760,6 +762,24 @@ __device__ __forceinline__ void barrier_no_fence() { asm volatile("s_barrier" ::
 // With eight waves (2 x 4) a 256 x 256 tile keeps 128 accumulator registers
 // per lane and two waves per SIMD, so one wave's LDS waits overlap the other's
 // MFMAs.
+// Scheduling groups for one interleaved half slab: NM MFMAs; the NR LDS reads
+// of the next half go one after each of the first MFMAs (so the last has most
+// of the half to land before its MFMA needs it), and the NV VMEM loads are
+// spread over the MFMAs after them.
+template <int NM, int NR, int NV, int I = 0>
+__device__ __forceinline__ void interleave_groups() {
+    if constexpr (I < NM) {
+        constexpr int kRest = NM - (NR < NM ? NR : NM);  // MFMAs after the reads
+        constexpr int kJ = I - (NM - kRest);              // index among them
+        constexpr int kLoadsHere = (NV == 0 || kJ < 0) ? 0
+            : (kRest == 0 ? (I == NM - 1 ? NV : 0) : (kJ + 1) * NV / kRest - kJ * NV / kRest);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        if constexpr (I < NR) __builtin_amdgcn_sched_group_barrier(0x100, I == NM - 1 ? NR - I : 1, 0);  // DS read
+        if constexpr (kLoadsHere > 0) __builtin_amdgcn_sched_group_barrier(0x020, kLoadsHere, 0);  // VMEM read
+        interleave_groups<NM, NR, NV, I + 1>();
+    }
+}
+
 template <int BM, int BN, int NW>
 struct DmaShapeTraits {
     static constexpr bool big = BM * BN > 256 * 128;
@@ -788,7 +808,7 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS addresses in SGPRs
     const int wm = wave / kWavesN, wn = wave % kWavesN;
     constexpr int kOutCols = kGlu ? BN / 2 : BN;
 
@@ -875,9 +895,9 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
         uint16_t* db = da + BM * kRK;
         const uint32_t kb = static_cast<uint32_t>(k0 * 2);
 #pragma unroll
-        for (int i = 0; i < kLoadsA; ++i) lds_dma16_buf(ra, a_off[i] + kb, da + (i * NW + wave) * 512);
+        for (int i = 0; i < kLoadsA; ++i) lds_dma16_buf(ra, a_off[i], kb, da + (i * NW + wave) * 512);
 #pragma unroll
-        for (int i = 0; i < kLoadsB; ++i) lds_dma16_buf(rb_, b_off[i] + kb, db + (i * NW + wave) * 512);
+        for (int i = 0; i < kLoadsB; ++i) lds_dma16_buf(rb_, b_off[i], kb, db + (i * NW + wave) * 512);
     };
 
     floatx16 acc[WM][WN];
@@ -944,6 +964,24 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
         if (kt < slabs) mfmas(f1a, f1b);
         __builtin_amdgcn_sched_barrier(0);
     };
+    // The same slab for kt < slabs with its instructions interleaved: each
+    // half runs its MFMAs one by one with the next half's fragment reads and
+    // (first half) the slab's DMA issues placed between them, so a wave that
+    // is alone on its SIMD keeps the matrix pipe fed while it reads LDS and
+    // issues loads, and reaches the barrier with only its last MFMA in flight.
+    auto slab_il = [&](int64_t kt, const uint16_t* cur, uint16_t* prev, const uint16_t* next) {
+        load_frags(cur, 1, f1a, f1b);
+        mfmas(f0a, f0b);
+        issue(prev, min(kt + kStages - 1, slabs - 1) * kRK);
+        interleave_groups<WM * WN, WM + WN, kLoads>();
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vmem_lds<(kStages - 2) * kLoads>();
+        barrier_no_fence();
+        load_frags(next, 0, f0a, f0b);
+        mfmas(f1a, f1b);
+        interleave_groups<WM * WN, WM + WN, 0>();
+        __builtin_amdgcn_sched_barrier(0);
+    };
     issue(sS0, 0);
     issue(sS1, min(int64_t(1), slabs - 1) * kRK);
     if constexpr (kStages == 4) issue(sS2, min(int64_t(2), slabs - 1) * kRK);
@@ -996,7 +1034,15 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
     } else {
     load_frags(sS0, 0, f0a, f0b);
     if constexpr (kStages == 4) {
-        for (int64_t kt = 0; kt < slabs; kt += 4) {
+        // whole groups of four slabs interleaved, then at most one guarded group
+        int64_t kt = 0;
+        for (; kt + 4 <= slabs; kt += 4) {
+            slab_il(kt, sS0, sS3, sS1);
+            slab_il(kt + 1, sS1, sS0, sS2);
+            slab_il(kt + 2, sS2, sS1, sS3);
+            slab_il(kt + 3, sS3, sS2, sS0);
+        }
+        if (kt < slabs) {
             slab(kt, sS0, sS3, sS1);
             slab(kt + 1, sS1, sS0, sS2);
             slab(kt + 2, sS2, sS1, sS3);
@@ -1013,39 +1059,62 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
     wait_vmem<0>();
 
     // Epilogue: 32x32 D layout, lane holds column (lane & 31) and rows
-    // 8 (r / 4) + 4 (lane >> 5) + (r % 4).
+    // 8 (r / 4) + 4 (lane >> 5) + (r % 4).  The output dtype and the scales are
+    // resolved once per tile, a lane's scales (its columns are fixed) are read
+    // once, and each 32-row block issues all its residual loads (at clamped,
+    // always valid addresses) before its first store, so the block waits for
+    // memory once instead of once per element; only the stores are guarded.
+    if constexpr (EPI != kEpiQkvRope) {
+        constexpr int kCols = kGlu ? WN / 2 : WN;  // output columns per lane
+        int64_t cols[kCols];
+        float sc_lo[kCols], sc_hi[kCols];
 #pragma unroll
-    for (int i = 0; i < WM; ++i) {
+        for (int j = 0; j < kCols; ++j) {
+            cols[j] = kGlu ? ncol0 + (wn * WN / 2 + j) * 32 + l32 : ncol0 + wn * (BN / kWavesN) + j * 32 + l32;
+            const int64_t cc = min(cols[j], p.n - 1);
+            sc_lo[j] = scales ? scales[cc] : 1.f;
+            sc_hi[j] = (kGlu && scales) ? scales[p.n + cc] : 1.f;
+        }
+        auto store_tile = [&](auto* out) {
+            using OutT = std::remove_pointer_t<decltype(out)>;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            if constexpr (EPI == kEpiQkvRope) break;
-            const int64_t row = row0 + wm * (BM / kWavesM) + i * 32 + 8 * (r >> 2) + 4 * khalf + (r & 3);
-            if (row >= re) continue;
-            if (kGlu) {
+            for (int ih = 0; ih < 2 * WM; ++ih) {  // half 32-row blocks: 8 accumulator rows each
+                const int i = ih >> 1, r0 = (ih & 1) * 8;
+                const int64_t rbase = row0 + wm * (BM / kWavesM) + i * 32 + 4 * khalf;
+                float res[8][kCols];
+                if constexpr (EPI == SFG_EPI_RESIDUAL) {
 #pragma unroll
-                for (int j = 0; j < WN; j += 2) {
-                    const int block = wn * WN + j;  // even: gate block
-                    const int64_t col = ncol0 + (block >> 1) * 32 + l32;
-                    if (col >= p.n) continue;
-                    float gv = acc[i][j][r], uv = acc[i][j + 1][r];
-                    if (scales) {
-                        gv *= scales[col];
-                        uv *= scales[p.n + col];
-                    }
-                    store_out(p.c, p.c_dtype, row * p.ldc + col, glu_combine(EPI, gv, uv));
+                    for (int rr = 0; rr < 8; ++rr)
+#pragma unroll
+                        for (int j = 0; j < kCols; ++j) {
+                            const int r = r0 + rr;
+                            const int64_t row = min(rbase + 8 * (r >> 2) + (r & 3), re - 1);
+                            res[rr][j] = p.residual[row * p.ldr + min(cols[j], p.n - 1)];
+                        }
                 }
-            } else if constexpr (EPI != kEpiQkvRope) {
 #pragma unroll
-                for (int j = 0; j < WN; ++j) {
-                    const int64_t col = ncol0 + wn * (BN / kWavesN) + j * 32 + l32;
-                    if (col >= p.n) continue;
-                    float v = acc[i][j][r];
-                    if (scales) v *= scales[col];
-                    if (EPI == SFG_EPI_RESIDUAL) v += p.residual[row * p.ldr + col];
-                    store_out(p.c, p.c_dtype, row * p.ldc + col, v);
+                for (int rr = 0; rr < 8; ++rr) {
+                    const int r = r0 + rr;
+                    const int64_t row = rbase + 8 * (r >> 2) + (r & 3);
+#pragma unroll
+                    for (int j = 0; j < kCols; ++j) {
+                        float v;
+                        if constexpr (kGlu) {
+                            v = glu_combine(EPI, acc[i][2 * j][r] * sc_lo[j], acc[i][2 * j + 1][r] * sc_hi[j]);
+                        } else {
+                            v = acc[i][j][r] * sc_lo[j];
+                            if constexpr (EPI == SFG_EPI_RESIDUAL) v += res[rr][j];
+                        }
+                        if (row < re && cols[j] < p.n) {
+                            if constexpr (sizeof(OutT) == 4) out[row * p.ldc + cols[j]] = v;
+                            else out[row * p.ldc + cols[j]] = f32_to_bf16(v);
+                        }
+                    }
                 }
             }
-        }
+        };
+        if (p.c_dtype == SFG_F32) store_tile(static_cast<float*>(p.c));
+        else store_tile(static_cast<uint16_t*>(p.c));
     }
     if constexpr (EPI == kEpiQkvRope) qkv_rope_epilogue<WM, WN>(p.qkv, acc, row0 + wm * (BM / kWavesM),
                                                                ncol0 + wn * (BN / kWavesN), re, p.n,
