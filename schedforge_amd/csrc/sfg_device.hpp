@@ -106,6 +106,16 @@ __device__ __forceinline__ void lds_dma16_buf(buf_rsrc r, uint32_t voffset, uint
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
         r, (__attribute__((address_space(3))) void*)(lds_block), 16, voffset, 0, 0, 0);
 }
+// A DMA of BYTES (4 or 16) per lane, wave-uniform byte offset in the SGPR
+// operand; the wave's 64 lanes fill 64 * BYTES contiguous LDS bytes.
+template <int BYTES>
+__device__ __forceinline__ void lds_dma_buf(buf_rsrc r, uint32_t voffset, uint32_t soffset,
+                                            uint16_t* lds_block) {
+    static_assert(BYTES == 4 || BYTES == 16, "LDS DMA moves 4 or 16 bytes per lane here");
+    auto* dst = (__attribute__((address_space(3))) void*)(lds_block);
+    if constexpr (BYTES == 16) __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, voffset, soffset, 0, 0);
+    else __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 4, voffset, soffset, 0, 0);
+}
 // The same load with a wave-uniform byte offset in the instruction's SGPR
 // operand: a loop that advances only `soffset` issues each load without any
 // per-lane address arithmetic.

@@ -785,6 +785,10 @@ struct DmaShapeTraits {
     static constexpr bool big = BM * BN > 256 * 128;
     static constexpr int stages = (big || BM * BN <= 128 * 128) ? 4 : 3;
     static constexpr int occupancy = (big && NW == 4) ? 1 : 2;
+    // The four-wave 256 x 256 tile has registers for two full fragment sets
+    // (its accumulators live in AGPRs): it reads a whole slab ahead.
+    static constexpr bool slab_ahead = big && NW == 4;
+    static constexpr int dma_bytes = 16;  // per lane per LDS DMA instruction (dwordx4)
 };
 
 template <int BM, int BN, int NW, int EPI, bool PP = false>
@@ -798,7 +802,9 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
     constexpr int kStages = DmaShapeTraits<BM, BN, NW>::stages;
     constexpr int kWavesM = 2, kWavesN = NW / 2;
     constexpr int WM = BM / (32 * kWavesM), WN = BN / (32 * kWavesN);  // 32x32 tiles per wave
-    constexpr int kLoadsA = BM / 16 / NW, kLoadsB = BN / 16 / NW;      // 1 KB blocks per wave per slab
+    constexpr int kDmaBytes = DmaShapeTraits<BM, BN, NW>::dma_bytes;   // per lane per DMA instruction
+    constexpr int kDmaRows = kDmaBytes;                                 // 64-byte rows per instruction
+    constexpr int kLoadsA = BM / kDmaRows / NW, kLoadsB = BN / kDmaRows / NW;  // DMA instructions per wave per slab
     constexpr int kLoads = kLoadsA + kLoadsB;
     static_assert(!kGlu || WN % 2 == 0, "GLU tiles pair gate and up blocks");
     __shared__ __attribute__((aligned(1024))) uint16_t sS0[(BM + BN) * kRK];
@@ -861,24 +867,32 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
     // valid row instead (their results are never stored).
     // The loads go through buffer resources over A and over this group's B
     // (byte offsets; the host guarantees both fit 32 bits).
-    const int lrow = lane >> 2;
-    const int chunk8 = ((lane & 3) ^ ((lrow >> 2) & 3)) * 8;
+    // One DMA instruction fills kDmaRows rows of 64 B (kDmaBytes per lane):
+    // lane l covers row l / (64 / kDmaBytes) of its block and the 16-byte
+    // destination slot s it lands in holds global chunk s ^ ((row >> 2) & 3).
+    constexpr int kLanesPerRow = 64 / kDmaBytes;
+    const int lrow = lane / kLanesPerRow;
+    const int piece = lane % kLanesPerRow;
+    const int slot16 = piece * kDmaBytes / 16;
+    const int sub = (piece % (16 / kDmaBytes)) * (kDmaBytes / 2);  // bf16 offset inside the 16-byte slot
+    auto chunk_of = [&](int local_row) { return ((slot16 ^ ((local_row >> 2) & 3)) * 8) + sub; };
     const buf_rsrc ra = make_rsrc(p.a, static_cast<uint32_t>(p.a_rows_limit * p.lda * 2));
     uint32_t a_off[kLoadsA];
 #pragma unroll
     for (int i = 0; i < kLoadsA; ++i) {
-        const int64_t r = row0 + (i * NW + wave) * 16 + lrow;
+        const int local = (i * NW + wave) * kDmaRows + lrow;
+        const int64_t r = row0 + local;
         int64_t src = r < re ? r : row0;
         if (p.a_rows) src = p.a_rows[src];
         if (src < 0 || src >= p.a_rows_limit) src = 0;
-        a_off[i] = static_cast<uint32_t>((src * p.lda + chunk8) * 2);
+        a_off[i] = static_cast<uint32_t>((src * p.lda + chunk_of(local)) * 2);
     }
     const uint16_t* bbase = static_cast<const uint16_t*>(p.b) + bgroup;
     const buf_rsrc rb_ = make_rsrc(bbase, static_cast<uint32_t>((kGlu ? 2 : 1) * p.n * p.ldb * 2));
     uint32_t b_off[kLoadsB];
 #pragma unroll
     for (int i = 0; i < kLoadsB; ++i) {
-        const int local = (i * NW + wave) * 16 + lrow;
+        const int local = (i * NW + wave) * kDmaRows + lrow;
         int64_t brow;
         if (kGlu) {
             const int block = local >> 5;
@@ -888,16 +902,18 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
             const int64_t col = ncol0 + local;
             brow = col < p.n ? col : 0;
         }
-        b_off[i] = static_cast<uint32_t>((brow * p.ldb + chunk8) * 2);
+        b_off[i] = static_cast<uint32_t>((brow * p.ldb + chunk_of(local)) * 2);
     }
 
     auto issue = [&](uint16_t* da, int64_t k0) {
         uint16_t* db = da + BM * kRK;
         const uint32_t kb = static_cast<uint32_t>(k0 * 2);
 #pragma unroll
-        for (int i = 0; i < kLoadsA; ++i) lds_dma16_buf(ra, a_off[i], kb, da + (i * NW + wave) * 512);
+        for (int i = 0; i < kLoadsA; ++i)
+            lds_dma_buf<kDmaBytes>(ra, a_off[i], kb, da + (i * NW + wave) * kDmaRows * kRK);
 #pragma unroll
-        for (int i = 0; i < kLoadsB; ++i) lds_dma16_buf(rb_, b_off[i], kb, db + (i * NW + wave) * 512);
+        for (int i = 0; i < kLoadsB; ++i)
+            lds_dma_buf<kDmaBytes>(rb_, b_off[i], kb, db + (i * NW + wave) * kDmaRows * kRK);
     };
 
     floatx16 acc[WM][WN];
@@ -1032,6 +1048,50 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
         }
         if (!trailer) barrier_no_fence();
     } else {
+    if constexpr (DmaShapeTraits<BM, BN, NW>::slab_ahead) {
+        // A whole slab ahead in registers.  The MFMAs of slab kt use fragments
+        // read during slab kt - 1; while they run, the wave reads slab kt + 1
+        // from LDS into the other register set and issues slab kt + 4 into the
+        // stage slab kt occupied (every wave finished reading it before the
+        // barrier that opened slab kt).  One wait + barrier per slab, at its
+        // end: slab kt + 2 must have landed (kt + 3 and kt + 4 stay in flight)
+        // and this wave's reads of slab kt + 1 must be done; after it the next
+        // MFMAs start at once, their operands already in registers.
+        issue(sS3, min(int64_t(3), slabs - 1) * kRK);
+        bf16x8 ga[2][2][WM], gb[2][2][WN];  // [register set][k-step][fragment]
+        load_frags(sS0, 0, ga[0][0], gb[0][0]);
+        load_frags(sS0, 1, ga[0][1], gb[0][1]);
+        wait_vmem_lds<2 * kLoads>();
+        barrier_no_fence();
+        auto step = [&](int64_t kt, auto set_c, const uint16_t* next_stage, uint16_t* own_stage, bool live) {
+            constexpr int c = decltype(set_c)::value, n = 1 - c;
+            load_frags(next_stage, 0, ga[n][0], gb[n][0]);
+            if (live) mfmas(ga[c][0], gb[c][0]);
+            issue(own_stage, min(kt + 4, slabs - 1) * kRK);
+            interleave_groups<WM * WN, WM + WN, kLoads>();
+            __builtin_amdgcn_sched_barrier(0);
+            load_frags(next_stage, 1, ga[n][1], gb[n][1]);
+            if (live) mfmas(ga[c][1], gb[c][1]);
+            interleave_groups<WM * WN, WM + WN, 0>();
+            __builtin_amdgcn_sched_barrier(0);
+            wait_vmem_lds<2 * kLoads>();
+            barrier_no_fence();
+        };
+        using set0 = std::integral_constant<int, 0>;
+        using set1 = std::integral_constant<int, 1>;
+        int64_t kt = 0;
+        for (; kt + 4 <= slabs; kt += 4) {
+            step(kt, set0{}, sS1, sS0, true);
+            step(kt + 1, set1{}, sS2, sS1, true);
+            step(kt + 2, set0{}, sS3, sS2, true);
+            step(kt + 3, set1{}, sS0, sS3, true);
+        }
+        if (kt < slabs) {
+            step(kt, set0{}, sS1, sS0, kt < slabs);
+            step(kt + 1, set1{}, sS2, sS1, kt + 1 < slabs);
+            step(kt + 2, set0{}, sS3, sS2, kt + 2 < slabs);
+        }
+    } else {
     load_frags(sS0, 0, f0a, f0b);
     if constexpr (kStages == 4) {
         // whole groups of four slabs interleaved, then at most one guarded group
@@ -1054,6 +1114,7 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
             slab(kt + 1, sS1, sS0, sS2);
             slab(kt + 2, sS2, sS1, sS0);
         }
+    }
     }
     }
     wait_vmem<0>();
@@ -1299,7 +1360,10 @@ DmaShape pick_dma_shape(int64_t m, int64_t n_out, bool glu, int groups, int tile
         const DmaShape sh = dma_shape_of(t);
         const int64_t cols = glu ? sh.bn / 2 : sh.bn;
         const int64_t tiles = ((m + sh.bm - 1) / sh.bm + (groups > 1 ? groups : 0)) * ((n_out + cols - 1) / cols);
-        if (tiles >= 512) return sh;
+        // 256 x 256: the GLU epilogue (two accumulator blocks per output)
+        // runs best on the plain eight-wave tile, the others as ping-pong
+        // (measured on the prefill shapes).
+        if (tiles >= 512) return (t == SFG_TILE_256x256_PP && glu) ? dma_shape_of(SFG_TILE_256x256_W8) : sh;
     }
     return dma_shape_of(SFG_TILE_128x128);
 }

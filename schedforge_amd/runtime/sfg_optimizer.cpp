@@ -46,13 +46,14 @@ TileShape tile_shape(int tile) {
     }
 }
 
-// SFG_TILE_AUTO as the launcher resolves it: the largest tile with >= 512 workgroups.
+// SFG_TILE_AUTO as the launcher resolves it: the largest tile with >= 512
+// workgroups (the 256 x 256 one as W8 for GLU epilogues, else ping-pong).
 int auto_tile(std::int64_t m, std::int64_t n_out, bool glu, int groups) {
     for (const int t : {SFG_TILE_256x256_PP, SFG_TILE_256x128, SFG_TILE_128x128}) {
         const TileShape s = tile_shape(t);
         const std::int64_t cols = glu ? s.bn / 2 : s.bn;
         const std::int64_t tiles = (ceil_div(m, s.bm) + (groups > 1 ? groups : 0)) * ceil_div(n_out, cols);
-        if (tiles >= 512) return t;
+        if (tiles >= 512) return (t == SFG_TILE_256x256_PP && glu) ? SFG_TILE_256x256_W8 : t;
     }
     return SFG_TILE_128x128;
 }
