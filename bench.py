@@ -36,15 +36,18 @@ sys.path.insert(0, str(ROOT))
 # --copy-calibration 1024.  The calibration kernel reads 1 GiB and writes 1 GiB;
 # the counters read 524311.8 KiB and 1048576.0 KiB for it, so FETCH_SIZE is
 # scaled by 1048576 / 524311.8 and WRITE_SIZE by 1.  Summaries:
-# profiles/pmc_traffic_c2.md, profiles/pmc_traffic_c5.md.
+# profiles/pmc_traffic_c2.md, profiles/pmc_traffic_c5.md (decode attention),
+# profiles/pmc_traffic_prefill_gemm.md (C4 gate|up GEMM, C3 grouped experts).
 PMC_FETCH_SCALE = 1048576.0 / 524311.8
 PMC_WRITE_SCALE = 1.0
-PMC_ATTENTION_KIB = {          # attn_decode_split_kernel: (FETCH_SIZE, WRITE_SIZE)
-    "c2": (66117.8, 1088.0),
-    "c5": (1049963.6, 2112.0),
+PMC_ROOFLINE_KIB = {           # roofline kernel(s) per launch: (FETCH_SIZE, WRITE_SIZE)
+    "c2": (66117.8, 1088.0),                    # attn_decode_split_kernel
+    "c5": (1049963.6, 2112.0),                  # attn_decode_split_kernel
+    "c4": (1376849.7, 229376.0),                # gate|up GEMM + SwiGLU
+    "c3": (157089.2 + 71083.4, 11265.0 + 32768.0),  # grouped W1|W3 + W2 expert GEMMs
 }
 MEASURED_TRAFFIC = {k: round((f * PMC_FETCH_SCALE + w * PMC_WRITE_SCALE) * 1024)
-                    for k, (f, w) in PMC_ATTENTION_KIB.items()}
+                    for k, (f, w) in PMC_ROOFLINE_KIB.items()}
 
 
 def parse():
@@ -245,17 +248,22 @@ def main():
         # plus 2 T k H I for W2) over its bracketed time
         peak = C.PEAK_F32_TFLOPS if cfg.dtype == "f32" else C.PEAK_BF16_TFLOPS
         ffn_ms = sum(kern_times) / len(kern_times)
+        T, H, I, K, E = cfg.rows, cfg.hidden, cfg.intermediate, cfg.top_k, cfg.experts
+        esz = 4 if cfg.dtype == "f32" else 2
         if cfg.moe:
-            kflops = 6 * cfg.rows * cfg.top_k * cfg.hidden * cfg.intermediate
+            kflops = 6 * T * K * H * I
             kname = "gemm_dma_kernel grouped expert GEMMs (W1|W3 + SwiGLU, W2)"
+            # W1|W3: x rows gathered, weights, act out; W2: act in, weights, fp32 y out
+            kbytes = esz * (T * H + E * 2 * I * H + T * K * I) + esz * (T * K * I + E * H * I) + 4 * T * K * H
         else:
-            kflops = 2 * cfg.rows * cfg.hidden * 2 * cfg.intermediate
+            kflops = 2 * T * H * 2 * I
             kname = ("gemm_f32_kernel" if cfg.dtype == "f32" else "gemm_dma_kernel") + " (gate|up + SwiGLU)"
+            kbytes = esz * (T * H + 2 * I * H + T * I)
         achieved = kflops / (ffn_ms * 1e-3) / 1e12
         roofline = {"bound": "mfma", "kernel": kname,
                     "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
                     "frac": round(achieved / peak, 4),
-                    "traffic": MEASURED_TRAFFIC.get(args.config),
+                    "traffic": MEASURED_TRAFFIC.get(args.config), "algorithmic_bytes": kbytes,
                     "algorithmic_flops": kflops, "avg_ms": round(ffn_ms, 5),
                     "layer_tflops": round(work["flops"] / (ms_per_step * 1e-3) / 1e12, 2),
                     "layer_frac": round(work["flops"] / (ms_per_step * 1e-3) / 1e12 / peak, 4)}

@@ -769,8 +769,8 @@ int sfg_hip_decoder_layer_v1(const sfg_layer_desc* d, const sfg_layer_weights* w
         return rc;
     mk.mark(SFG_MARK_OPROJ);
     // 6. RMSNorm
-    sfg::launch_rmsnorm(b.r1, w->rms2, b.xn, act, rows, H, d->rms_epsilon, s);
-    if (moe) sfg::launch_rmsnorm(b.r1, w->rms2, b.xn2_f32, SFG_F32, rows, H, d->rms_epsilon, s);
+    // (MoE: the router reads the same rows in fp32, written by the same pass)
+    sfg::launch_rmsnorm(b.r1, w->rms2, b.xn, act, rows, H, d->rms_epsilon, s, moe ? b.xn2_f32 : nullptr);
     mk.mark(SFG_MARK_NORM2);
     if (!moe) {
         mk.mark(SFG_MARK_ROUTE);

@@ -18,7 +18,8 @@ namespace sfg {
 template <typename OutT>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x,
                                                       const float* __restrict__ w,
-                                                      OutT* __restrict__ y, int width, float eps) {
+                                                      OutT* __restrict__ y, int width, float eps,
+                                                      float* __restrict__ y32) {
     const int row = blockIdx.x;
     const float* xr = x + static_cast<int64_t>(row) * width;
     OutT* yr = y + static_cast<int64_t>(row) * width;
@@ -60,24 +61,26 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
                 packed.y = pack_bf16x2(o2, o3);
                 *reinterpret_cast<uint2*>(yr + c) = packed;
             }
+            if (y32) *reinterpret_cast<float4*>(y32 + static_cast<int64_t>(row) * width + c) = make_float4(o0, o1, o2, o3);
         }
     } else {
         for (int c = threadIdx.x; c < width; c += 256) {
             const float o = xr[c] * inv * w[c];
             if constexpr (sizeof(OutT) == 4) yr[c] = o;
             else yr[c] = f32_to_bf16(o);
+            if (y32) y32[static_cast<int64_t>(row) * width + c] = o;
         }
     }
 }
 
 void launch_rmsnorm(const float* x, const float* w, void* y, int y_dtype, int64_t rows,
-                    int64_t width, float eps, hipStream_t stream) {
+                    int64_t width, float eps, hipStream_t stream, float* y32) {
     if (y_dtype == SFG_F32)
         rmsnorm_kernel<float><<<dim3(rows), dim3(256), 0, stream>>>(x, w, static_cast<float*>(y),
-                                                                     static_cast<int>(width), eps);
+                                                                     static_cast<int>(width), eps, y32);
     else
         rmsnorm_kernel<uint16_t><<<dim3(rows), dim3(256), 0, stream>>>(
-            x, w, static_cast<uint16_t*>(y), static_cast<int>(width), eps);
+            x, w, static_cast<uint16_t*>(y), static_cast<int>(width), eps, y32);
 }
 
 // ---------------------------------------------------------------------------

@@ -13,8 +13,9 @@
 namespace sfg {
 
 // elementwise
+// y32 (optional): the same normalised rows also written as fp32.
 void launch_rmsnorm(const float* x, const float* w, void* y, int y_dtype, int64_t rows,
-                    int64_t width, float eps, hipStream_t stream);
+                    int64_t width, float eps, hipStream_t stream, float* y32 = nullptr);
 void launch_split_rope(const float* qkv, const float* table, int64_t batch, int64_t seq,
                        int64_t q_heads, int64_t kv_heads, int64_t head_dim, void* q, void* k,
                        void* v, int out_dtype, hipStream_t stream);

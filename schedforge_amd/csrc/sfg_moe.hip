@@ -21,6 +21,35 @@ namespace sfg {
 // router transposed to [e][f]) and fed to the chain from registers 16 features
 // at a time, the next 16 already in flight; the next chunk's global loads are
 // held in registers while the current chunk's chain runs.
+// Softmax over all experts (max-shifted), top-k by logit (slot 0 the largest;
+// ties to the lower expert index: a strictly larger logit replaces the pick),
+// selected probabilities renormalised to sum 1 (moe_compiler.cpp:429-452).
+__device__ void route_select(const float* lg, int experts, int top_k, int tok, int32_t* __restrict__ ids,
+                             float* __restrict__ weights) {
+    float maximum = -INFINITY;
+    for (int j = 0; j < experts; ++j) maximum = fmaxf(maximum, lg[j]);
+    float denom = 0.f;
+    for (int j = 0; j < experts; ++j) denom += expf(lg[j] - maximum);
+    uint32_t taken[8] = {0, 0, 0, 0, 0, 0, 0, 0};  // bitmask over <= 256 experts
+    int sel[8];
+    float selected = 0.f;
+    for (int s = 0; s < top_k; ++s) {
+        int best = -1;
+        for (int j = 0; j < experts; ++j) {
+            if (taken[j >> 5] & (1u << (j & 31))) continue;
+            if (best < 0 || lg[j] > lg[best]) best = j;
+        }
+        taken[best >> 5] |= 1u << (best & 31);
+        sel[s] = best;
+        selected += expf(lg[best] - maximum) / denom;
+    }
+    for (int s = 0; s < top_k; ++s) {
+        const int j = sel[s];
+        ids[static_cast<int64_t>(tok) * top_k + s] = j;
+        weights[static_cast<int64_t>(tok) * top_k + s] = (expf(lg[j] - maximum) / denom) / selected;
+    }
+}
+
 constexpr int kRouteChunk = 512;
 constexpr int kRouteTokens = 4;        // tokens per workgroup
 constexpr int kRouteMaxExperts = 8;    // staged path; larger E uses the direct chain
@@ -131,29 +160,7 @@ __global__ __launch_bounds__(256) void moe_router_kernel(
     if (threadIdx.x >= per_block) return;
     const int tok = blockIdx.x * per_block + threadIdx.x;
     if (tok >= tokens) return;
-    const float* lg = logits + threadIdx.x * experts;
-    float maximum = -INFINITY;
-    for (int j = 0; j < experts; ++j) maximum = fmaxf(maximum, lg[j]);
-    float denom = 0.f;
-    for (int j = 0; j < experts; ++j) denom += expf(lg[j] - maximum);
-    uint32_t taken[8] = {0, 0, 0, 0, 0, 0, 0, 0};  // bitmask over <= 256 experts
-    int sel[8];
-    float selected = 0.f;
-    for (int s = 0; s < top_k; ++s) {
-        int best = -1;
-        for (int j = 0; j < experts; ++j) {
-            if (taken[j >> 5] & (1u << (j & 31))) continue;
-            if (best < 0 || lg[j] > lg[best]) best = j;
-        }
-        taken[best >> 5] |= 1u << (best & 31);
-        sel[s] = best;
-        selected += expf(lg[best] - maximum) / denom;
-    }
-    for (int s = 0; s < top_k; ++s) {
-        const int j = sel[s];
-        ids[static_cast<int64_t>(tok) * top_k + s] = j;
-        weights[static_cast<int64_t>(tok) * top_k + s] = (expf(lg[j] - maximum) / denom) / selected;
-    }
+    route_select(logits + threadIdx.x * experts, experts, top_k, tok, ids, weights);
 }
 
 int launch_moe_router(const float* x, const float* router, const float* bias, int64_t tokens,
