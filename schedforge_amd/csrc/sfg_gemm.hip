@@ -1285,10 +1285,12 @@ int skinny_waves(int64_t k, int mt, int nbt) {
 template <int BDT, int MT, int NBT, int EPI>
 void launch_skinny_w(const SkinnyArgs& a, dim3 grid, int waves, bool tiled, hipStream_t s) {
     if (tiled) {
-        if (waves == 4) gemm_skinny_kernel<BDT, MT, NBT, EPI, 4, true><<<grid, 256, 0, s>>>(a);
+        if (waves == 2) gemm_skinny_kernel<BDT, MT, NBT, EPI, 2, true><<<grid, 128, 0, s>>>(a);
+        else if (waves == 4) gemm_skinny_kernel<BDT, MT, NBT, EPI, 4, true><<<grid, 256, 0, s>>>(a);
         else gemm_skinny_kernel<BDT, MT, NBT, EPI, 8, true><<<grid, 512, 0, s>>>(a);
     } else {
-        if (waves == 4) gemm_skinny_kernel<BDT, MT, NBT, EPI, 4, false><<<grid, 256, 0, s>>>(a);
+        if (waves == 2) gemm_skinny_kernel<BDT, MT, NBT, EPI, 2, false><<<grid, 128, 0, s>>>(a);
+        else if (waves == 4) gemm_skinny_kernel<BDT, MT, NBT, EPI, 4, false><<<grid, 256, 0, s>>>(a);
         else gemm_skinny_kernel<BDT, MT, NBT, EPI, 8, false><<<grid, 512, 0, s>>>(a);
     }
 }
@@ -1444,7 +1446,9 @@ int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes, h
         const int nbt = glu ? 2 : (rows_hint <= 16 ? 1 : 2);
         const int64_t tile_cols = glu ? 16 : 16 * nbt;
         if (p.n % tile_cols != 0) return SFG_ERR_UNSUPPORTED;
-        const int waves = skinny_waves(p.k, mt, nbt);
+        // A grouped launch already has groups x N/16 workgroups, several per
+        // CU: two waves each keeps the K split (and its LDS reduction) short.
+        const int waves = p.offsets ? 2 : skinny_waves(p.k, mt, nbt);
         SkinnyArgs a{};
         a.a = static_cast<const uint16_t*>(p.a); a.lda = p.lda; a.a_rows = p.a_rows;
         a.a_rows_limit = p.a_rows ? p.a_rows_limit : p.m;
