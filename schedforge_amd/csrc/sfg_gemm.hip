@@ -48,7 +48,7 @@ __device__ __forceinline__ void store_out(void* c, int c_dtype, int64_t idx, flo
 // Skinny (decode) GEMM.
 //
 // A workgroup owns NBT 16-row tiles of B (16 or 32 output columns; for GLU
-// epilogues one gate tile and the matching up tile) and ALL of K: its WAVES
+// epilogues NBT / 2 gate tiles and the matching up tiles) and ALL of K: its WAVES
 // waves split K into contiguous chunk ranges and reduce through LDS in a fixed
 // order, so no workgroup waits for or publishes to another (no device-scope
 // fences: on gfx950 they write back and invalidate the L2).  Each lane reads
@@ -76,9 +76,12 @@ constexpr int kSkinnyBatch = MT == 1 ? 4 : (MT == 2 ? 2 : 1);
 template <int BDT, int MT, int NBT, int EPI, int WAVES, bool TILED>
 __global__ __launch_bounds__(WAVES * 64) void gemm_skinny_kernel(SkinnyArgs p) {
     constexpr bool kGlu = EpiTraits<EPI>::glu;
-    constexpr int CB = kSkinnyBatch<MT>;           // chunks in flight per wave
+    // chunks in flight per wave; four B tiles keep the weight bytes in flight
+    // of two while each activation chunk feeds twice the columns
+    constexpr int CB = NBT > 2 ? (kSkinnyBatch<MT> > 1 ? kSkinnyBatch<MT> / 2 : 1) : kSkinnyBatch<MT>;
     constexpr int BQ = (BDT == SFG_I8) ? 2 : 4;    // uint4 per lane per chunk and tile
-    static_assert(!kGlu || NBT == 2, "GLU epilogues pair one gate and one up tile");
+    static_assert(!kGlu || NBT == 2 || NBT == 4, "GLU epilogues pair gate and up tiles");
+    constexpr int kGluTiles = NBT / 2;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int g = blockIdx.z;
@@ -95,9 +98,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny_kernel(SkinnyArgs p) {
     int64_t brow[NBT];
     int64_t out_col;
     if (kGlu) {
-        out_col = static_cast<int64_t>(tile) * 16;
-        brow[0] = out_col;              // gate (or W1)
-        brow[NBT - 1] = p.n + out_col;  // up (or W3)
+        out_col = static_cast<int64_t>(tile) * 16 * kGluTiles;
+#pragma unroll
+        for (int h = 0; h < kGluTiles; ++h) {
+            brow[h] = out_col + 16 * h;                    // gate (or W1)
+            brow[kGluTiles + h] = p.n + out_col + 16 * h;  // up (or W3)
+        }
     } else {
         out_col = static_cast<int64_t>(tile) * (16 * NBT);
 #pragma unroll
@@ -232,13 +238,16 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny_kernel(SkinnyArgs p) {
                     const int64_t row = pass + i * 16 + lg * 4 + r;
                     if (row >= re) continue;
                     if (kGlu) {
-                        const int64_t col = out_col + lr;
-                        float gv = acc[i][0][r], uv = acc[i][NBT - 1][r];
-                        if (scales) {
-                            gv *= scales[col];
-                            uv *= scales[p.n + col];
+#pragma unroll
+                        for (int h = 0; h < kGluTiles; ++h) {
+                            const int64_t col = out_col + 16 * h + lr;
+                            float gv = acc[i][h][r], uv = acc[i][kGluTiles + h][r];
+                            if (scales) {
+                                gv *= scales[col];
+                                uv *= scales[p.n + col];
+                            }
+                            store_out(p.c, p.c_dtype, row * p.ldc + col, glu_combine(EPI, gv, uv));
                         }
-                        store_out(p.c, p.c_dtype, row * p.ldc + col, glu_combine(EPI, gv, uv));
                     } else {
 #pragma unroll
                         for (int j = 0; j < NBT; ++j) {
@@ -1312,6 +1321,18 @@ void launch_skinny_e(const SkinnyArgs& a, dim3 grid, int nbt, int waves, int epi
     }
 }
 
+// Grouped GLU problems: two gate and two up tiles per two-wave workgroup.
+template <int BDT, int MT>
+void launch_skinny_glu4(const SkinnyArgs& a, dim3 grid, int epi, bool tiled, hipStream_t s) {
+    if (epi == SFG_EPI_SWIGLU) {
+        if (tiled) gemm_skinny_kernel<BDT, MT, 4, SFG_EPI_SWIGLU, 2, true><<<grid, 128, 0, s>>>(a);
+        else gemm_skinny_kernel<BDT, MT, 4, SFG_EPI_SWIGLU, 2, false><<<grid, 128, 0, s>>>(a);
+    } else {
+        if (tiled) gemm_skinny_kernel<BDT, MT, 4, SFG_EPI_GLU_SILU_UP, 2, true><<<grid, 128, 0, s>>>(a);
+        else gemm_skinny_kernel<BDT, MT, 4, SFG_EPI_GLU_SILU_UP, 2, false><<<grid, 128, 0, s>>>(a);
+    }
+}
+
 template <int BDT>
 void launch_skinny_b(const SkinnyArgs& a, dim3 grid, int mt, int nbt, int waves, int epi,
                      bool tiled, hipStream_t s) {
@@ -1443,8 +1464,11 @@ int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes, h
         // grouped problems: 32 rows per pass covers the typical decode expert
         const int64_t rows_hint = p.offsets ? 32 : p.m;
         const int mt = rows_hint <= 16 ? 1 : (rows_hint <= 32 ? 2 : 4);
-        const int nbt = glu ? 2 : (rows_hint <= 16 ? 1 : 2);
-        const int64_t tile_cols = glu ? 16 : 16 * nbt;
+        // grouped GLU: two gate and two up tiles per workgroup halve the
+        // activation re-reads per weight byte
+        const bool glu4 = glu && p.offsets && p.n % 32 == 0;
+        const int nbt = glu ? (glu4 ? 4 : 2) : (rows_hint <= 16 ? 1 : 2);
+        const int64_t tile_cols = glu ? 16 * nbt / 2 : 16 * nbt;
         if (p.n % tile_cols != 0) return SFG_ERR_UNSUPPORTED;
         // A grouped launch already has groups x N/16 workgroups, several per
         // CU: two waves each keeps the K split (and its LDS reduction) short.
@@ -1459,6 +1483,11 @@ int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes, h
         a.m = p.m; a.n = p.n; a.k = p.k; a.offsets = p.offsets;
         const dim3 grid(static_cast<unsigned>(p.n / tile_cols), 1u, static_cast<unsigned>(groups));
         const bool tiled = p.b_layout == SFG_LAYOUT_TILED;
+        if (glu4) {  // grouped problems always run 32 rows per pass (mt == 2)
+            if (p.b_dtype == SFG_I8) launch_skinny_glu4<SFG_I8, 2>(a, grid, p.epilogue, tiled, stream);
+            else launch_skinny_glu4<SFG_BF16, 2>(a, grid, p.epilogue, tiled, stream);
+            return SFG_OK;
+        }
         if (p.b_dtype == SFG_I8) launch_skinny_b<SFG_I8>(a, grid, mt, nbt, waves, p.epilogue, tiled, stream);
         else launch_skinny_b<SFG_BF16>(a, grid, mt, nbt, waves, p.epilogue, tiled, stream);
         return SFG_OK;

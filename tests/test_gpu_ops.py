@@ -566,8 +566,9 @@ def test_moe_route_ties_go_to_lower_expert(lib):
 
 # ------------------------------------------------------------------ MoE experts + combine
 @pytest.mark.parametrize("wdt", ["bf16", "w8"])
-@pytest.mark.parametrize("T", [256, 16, 700, 1500])
-def test_moe_experts_and_combine_match_oracle(lib, wdt, T):
+@pytest.mark.parametrize("T,layout", [(256, 0), (16, 0), (700, 0), (1500, 0), (16, 1), (256, 1)])
+def test_moe_experts_and_combine_match_oracle(lib, wdt, T, layout):
+    """Grouped expert GEMMs + combine; layout 1 = fragment-tiled weights (decode sizes only)."""
     H, I, E, k = 512, 256, 8, 2
     x = oracle.round_bf16(oracle.normal(111, 0, (T, H)))
     router = oracle.normal(111, 10, (H, E), 0.02)
@@ -581,16 +582,22 @@ def test_moe_experts_and_combine_match_oracle(lib, wdt, T):
     # device weights in [E][2I][H] / [E][H][I]
     if wdt == "bf16":
         w13 = np.concatenate([w1.transpose(0, 2, 1), w3.transpose(0, 2, 1)], axis=1)
-        w13d, w2d = bf16_dev(np.ascontiguousarray(w13)), bf16_dev(np.ascontiguousarray(w2.transpose(0, 2, 1)))
+        w2t = np.ascontiguousarray(w2.transpose(0, 2, 1))
+        if layout:
+            w13d = dev(np.stack([tile_nk(oracle.to_bf16_bits(w13[e]), "bf16") for e in range(E)]).view(np.int16))
+            w2d = dev(np.stack([tile_nk(oracle.to_bf16_bits(w2t[e]), "bf16") for e in range(E)]).view(np.int16))
+        else:
+            w13d, w2d = bf16_dev(np.ascontiguousarray(w13)), bf16_dev(w2t)
         s13d = s2d = None
         dt = BF16
     else:
         q1 = [oracle.quantize_kn(w1[e]) for e in range(E)]
         q3 = [oracle.quantize_kn(w3[e]) for e in range(E)]
         q2 = [oracle.quantize_kn(w2[e]) for e in range(E)]
-        w13d = dev(np.stack([np.concatenate([q1[e][0], q3[e][0]]) for e in range(E)]))
+        q13 = [np.concatenate([q1[e][0], q3[e][0]]) for e in range(E)]
+        w13d = dev(np.stack([tile_nk(q, "int8") if layout else q for q in q13]))
         s13d = dev(np.stack([np.concatenate([q1[e][1], q3[e][1]]) for e in range(E)]))
-        w2d = dev(np.stack([q2[e][0] for e in range(E)]))
+        w2d = dev(np.stack([tile_nk(q2[e][0], "int8") if layout else q2[e][0] for e in range(E)]))
         s2d = dev(np.stack([q2[e][1] for e in range(E)]))
         dt = I8
     act = torch.empty((T * k, I), dtype=torch.int16, device="cuda")
@@ -599,7 +606,7 @@ def test_moe_experts_and_combine_match_oracle(lib, wdt, T):
                                           dev(tok).data_ptr(), w13d.data_ptr(),
                                           s13d.data_ptr() if s13d is not None else None,
                                           w2d.data_ptr(), s2d.data_ptr() if s2d is not None else None,
-                                          dt, 0, act.data_ptr(), y.data_ptr(), T, H, I, E, k, None, 0,
+                                          dt, layout, act.data_ptr(), y.data_ptr(), T, H, I, E, k, None, 0,
                                           stream()))
     resid = oracle.normal(111, 5, (T, H))
     out = torch.empty((T, H), dtype=torch.float32, device="cuda")
