@@ -1321,15 +1321,20 @@ void launch_skinny_e(const SkinnyArgs& a, dim3 grid, int nbt, int waves, int epi
     }
 }
 
-// Grouped GLU problems: two gate and two up tiles per two-wave workgroup.
+// Grouped problems: four B tiles (GLU: two gate + two up) per two-wave
+// workgroup.
+template <int BDT, int MT, int EPI>
+void launch_skinny_g4(const SkinnyArgs& a, dim3 grid, bool tiled, hipStream_t s) {
+    if (tiled) gemm_skinny_kernel<BDT, MT, 4, EPI, 2, true><<<grid, 128, 0, s>>>(a);
+    else gemm_skinny_kernel<BDT, MT, 4, EPI, 2, false><<<grid, 128, 0, s>>>(a);
+}
 template <int BDT, int MT>
-void launch_skinny_glu4(const SkinnyArgs& a, dim3 grid, int epi, bool tiled, hipStream_t s) {
-    if (epi == SFG_EPI_SWIGLU) {
-        if (tiled) gemm_skinny_kernel<BDT, MT, 4, SFG_EPI_SWIGLU, 2, true><<<grid, 128, 0, s>>>(a);
-        else gemm_skinny_kernel<BDT, MT, 4, SFG_EPI_SWIGLU, 2, false><<<grid, 128, 0, s>>>(a);
-    } else {
-        if (tiled) gemm_skinny_kernel<BDT, MT, 4, SFG_EPI_GLU_SILU_UP, 2, true><<<grid, 128, 0, s>>>(a);
-        else gemm_skinny_kernel<BDT, MT, 4, SFG_EPI_GLU_SILU_UP, 2, false><<<grid, 128, 0, s>>>(a);
+void launch_skinny_grouped4(const SkinnyArgs& a, dim3 grid, int epi, bool tiled, hipStream_t s) {
+    switch (epi) {
+        case SFG_EPI_NONE: launch_skinny_g4<BDT, MT, SFG_EPI_NONE>(a, grid, tiled, s); break;
+        case SFG_EPI_RESIDUAL: launch_skinny_g4<BDT, MT, SFG_EPI_RESIDUAL>(a, grid, tiled, s); break;
+        case SFG_EPI_SWIGLU: launch_skinny_g4<BDT, MT, SFG_EPI_SWIGLU>(a, grid, tiled, s); break;
+        default: launch_skinny_g4<BDT, MT, SFG_EPI_GLU_SILU_UP>(a, grid, tiled, s); break;
     }
 }
 
@@ -1464,10 +1469,10 @@ int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes, h
         // grouped problems: 32 rows per pass covers the typical decode expert
         const int64_t rows_hint = p.offsets ? 32 : p.m;
         const int mt = rows_hint <= 16 ? 1 : (rows_hint <= 32 ? 2 : 4);
-        // grouped GLU: two gate and two up tiles per workgroup halve the
-        // activation re-reads per weight byte
-        const bool glu4 = glu && p.offsets && p.n % 32 == 0;
-        const int nbt = glu ? (glu4 ? 4 : 2) : (rows_hint <= 16 ? 1 : 2);
+        // grouped: four B tiles per workgroup (GLU: two gate + two up) halve
+        // the activation re-reads per weight byte
+        const bool g4 = p.offsets && p.n % (glu ? 32 : 64) == 0;
+        const int nbt = g4 ? 4 : (glu ? 2 : (rows_hint <= 16 ? 1 : 2));
         const int64_t tile_cols = glu ? 16 * nbt / 2 : 16 * nbt;
         if (p.n % tile_cols != 0) return SFG_ERR_UNSUPPORTED;
         // A grouped launch already has groups x N/16 workgroups, several per
@@ -1483,9 +1488,9 @@ int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes, h
         a.m = p.m; a.n = p.n; a.k = p.k; a.offsets = p.offsets;
         const dim3 grid(static_cast<unsigned>(p.n / tile_cols), 1u, static_cast<unsigned>(groups));
         const bool tiled = p.b_layout == SFG_LAYOUT_TILED;
-        if (glu4) {  // grouped problems always run 32 rows per pass (mt == 2)
-            if (p.b_dtype == SFG_I8) launch_skinny_glu4<SFG_I8, 2>(a, grid, p.epilogue, tiled, stream);
-            else launch_skinny_glu4<SFG_BF16, 2>(a, grid, p.epilogue, tiled, stream);
+        if (g4) {  // grouped problems always run 32 rows per pass (mt == 2)
+            if (p.b_dtype == SFG_I8) launch_skinny_grouped4<SFG_I8, 2>(a, grid, p.epilogue, tiled, stream);
+            else launch_skinny_grouped4<SFG_BF16, 2>(a, grid, p.epilogue, tiled, stream);
             return SFG_OK;
         }
         if (p.b_dtype == SFG_I8) launch_skinny_b<SFG_I8>(a, grid, mt, nbt, waves, p.epilogue, tiled, stream);
