@@ -76,9 +76,7 @@ constexpr int kSkinnyBatch = MT == 1 ? 4 : (MT == 2 ? 2 : 1);
 template <int BDT, int MT, int NBT, int EPI, int WAVES, bool TILED>
 __global__ __launch_bounds__(WAVES * 64) void gemm_skinny_kernel(SkinnyArgs p) {
     constexpr bool kGlu = EpiTraits<EPI>::glu;
-    // chunks in flight per wave; four B tiles keep the weight bytes in flight
-    // of two while each activation chunk feeds twice the columns
-    constexpr int CB = NBT > 2 ? (kSkinnyBatch<MT> > 1 ? kSkinnyBatch<MT> / 2 : 1) : kSkinnyBatch<MT>;
+    constexpr int CB = kSkinnyBatch<MT>;           // chunks in flight per wave
     constexpr int BQ = (BDT == SFG_I8) ? 2 : 4;    // uint4 per lane per chunk and tile
     static_assert(!kGlu || NBT == 2 || NBT == 4, "GLU epilogues pair gate and up tiles");
     constexpr int kGluTiles = NBT / 2;
