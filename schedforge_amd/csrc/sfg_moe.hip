@@ -54,6 +54,11 @@ constexpr int kRouteChunk = 512;
 constexpr int kRouteTokens = 4;        // tokens per workgroup
 constexpr int kRouteMaxExperts = 8;    // staged path; larger E uses the direct chain
 constexpr int kRouteBlock = 16;        // chain operands per register block
+// Floats of padding per staged row: room for one block read past the chunk,
+// and a row stride of 532 floats puts the eight expert rows of one b128 read
+// on disjoint banks.
+constexpr int kRoutePad = 20;
+static_assert(kRoutePad >= kRouteBlock && kRouteChunk % (2 * kRouteBlock) == 0, "router staging");
 constexpr int kRouteLoads = (kRouteTokens * kRouteChunk + kRouteChunk * kRouteMaxExperts) / 256 / 4;
 
 __global__ __launch_bounds__(256) void moe_router_kernel(
@@ -61,8 +66,8 @@ __global__ __launch_bounds__(256) void moe_router_kernel(
     int tokens, int hidden, int experts, int top_k, int32_t* __restrict__ ids,
     float* __restrict__ weights) {
     __shared__ float logits[256];
-    __shared__ __attribute__((aligned(16))) float sx[2][kRouteTokens][kRouteChunk];
-    __shared__ __attribute__((aligned(16))) float sw[2][kRouteMaxExperts][kRouteChunk];
+    __shared__ __attribute__((aligned(16))) float sx[2][kRouteTokens][kRouteChunk + kRoutePad];
+    __shared__ __attribute__((aligned(16))) float sw[2][kRouteMaxExperts][kRouteChunk + kRoutePad];
     const bool staged = experts <= kRouteMaxExperts && (hidden % kRouteChunk) == 0;
     const int per_block = staged ? kRouteTokens : min(kRouteTokens, 256 / experts);
     const int t_local = threadIdx.x / experts;
@@ -77,6 +82,16 @@ __global__ __launch_bounds__(256) void moe_router_kernel(
         const int x_vecs = kRouteTokens * kRouteChunk / 4;
         const int w_vecs = kRouteChunk * experts / 4;
         float4 reg[kRouteLoads];
+        // LDS destinations of the router values this thread moves: the same
+        // for every chunk, so the divisions by `experts` run once.
+        int woff[kRouteLoads][4];
+#pragma unroll
+        for (int i = 0; i < kRouteLoads; ++i) {
+            const int flat = 4 * (static_cast<int>(threadIdx.x) + 256 * i - x_vecs);  // = f * experts + e
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                woff[i][j] = flat + j >= 0 ? ((flat + j) % experts) * (kRouteChunk + kRoutePad) + (flat + j) / experts : 0;
+        }
         auto fetch = [&](int f0) {
 #pragma unroll
             for (int i = 0; i < kRouteLoads; ++i) {
@@ -100,10 +115,11 @@ __global__ __launch_bounds__(256) void moe_router_kernel(
                     const int tt = v / (kRouteChunk / 4), f4 = v % (kRouteChunk / 4);
                     *reinterpret_cast<float4*>(&sx[buf][tt][4 * f4]) = reg[i];
                 } else if (v - x_vecs < w_vecs) {
-                    const int flat = 4 * (v - x_vecs);  // = f * experts + e
-                    const float vals[4] = {reg[i].x, reg[i].y, reg[i].z, reg[i].w};
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) sw[buf][(flat + j) % experts][(flat + j) / experts] = vals[j];
+                    float* swb = &sw[buf][0][0];
+                    swb[woff[i][0]] = reg[i].x;
+                    swb[woff[i][1]] = reg[i].y;
+                    swb[woff[i][2]] = reg[i].z;
+                    swb[woff[i][3]] = reg[i].w;
                 }
             }
         };
@@ -123,6 +139,7 @@ __global__ __launch_bounds__(256) void moe_router_kernel(
                     *reinterpret_cast<float4*>(&xa[j]) = *reinterpret_cast<const float4*>(xr + j);
                     *reinterpret_cast<float4*>(&wa[j]) = *reinterpret_cast<const float4*>(wr + j);
                 }
+#pragma unroll
                 for (int f = 0; f < kRouteChunk; f += 2 * kRouteBlock) {
 #pragma unroll
                     for (int j = 0; j < kRouteBlock; j += 4) {
@@ -131,12 +148,13 @@ __global__ __launch_bounds__(256) void moe_router_kernel(
                     }
 #pragma unroll
                     for (int j = 0; j < kRouteBlock; ++j) acc = __builtin_fmaf(xa[j], wa[j], acc);
-                    if (f + 2 * kRouteBlock < kRouteChunk) {
+                    // unconditional: the last block's read lands in the row
+                    // padding and is unused, and the two register sets
+                    // alternate without copies
 #pragma unroll
-                        for (int j = 0; j < kRouteBlock; j += 4) {
-                            *reinterpret_cast<float4*>(&xa[j]) = *reinterpret_cast<const float4*>(xr + f + 2 * kRouteBlock + j);
-                            *reinterpret_cast<float4*>(&wa[j]) = *reinterpret_cast<const float4*>(wr + f + 2 * kRouteBlock + j);
-                        }
+                    for (int j = 0; j < kRouteBlock; j += 4) {
+                        *reinterpret_cast<float4*>(&xa[j]) = *reinterpret_cast<const float4*>(xr + f + 2 * kRouteBlock + j);
+                        *reinterpret_cast<float4*>(&wa[j]) = *reinterpret_cast<const float4*>(wr + f + 2 * kRouteBlock + j);
                     }
 #pragma unroll
                     for (int j = 0; j < kRouteBlock; ++j) acc = __builtin_fmaf(xb[j], wb[j], acc);
