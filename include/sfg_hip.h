@@ -131,8 +131,11 @@ int sfg_hip_rmsnorm_v1(const float* x, const float* w, void* y, int y_dtype, int
  * SFG_BF16 or SFG_I8 (then b_scales[N or 2N] per output channel).
  * c_dtype: SFG_F32 or SFG_BF16.  Replaces execute(LoopIR) (runtime.cpp:581-626)
  * for the four projections and quantized_invoke (next_milestones.cpp:50-69).
- * workspace: sfg_hip_gemm_workspace_v1 bytes (currently 0: every kernel reduces
- * inside its workgroup; the argument is kept for split-K variants). */
+ * workspace: sfg_hip_gemm_workspace_v1 bytes.  Non-zero only for 33..64 dense
+ * rows with k a multiple of 512 (>= 1024) and N (2N for GLU) a multiple of
+ * 128: those run split-K over 512-k slices with fp32 partial sums in the
+ * workspace, summed in slice order.  With a smaller workspace (or NULL) the
+ * same shapes run the single-pass decode kernel instead. */
 typedef struct {
     const void* a; int32_t a_dtype; int64_t lda;
     const void* b; int32_t b_dtype; int64_t ldb; const float* b_scales;

@@ -15,6 +15,9 @@
 //    v_mfma_f32_32x32x16_bf16, A/B staged through padded LDS with register
 //    prefetch of the next k-slab, optional A-row gather for dispatched tokens
 //    and per-group (expert) segments read from device offsets.
+//  * gemm_splitk_kernel   33..64 dense rows with a caller workspace: 512-k
+//    slices, activations staged once per workgroup in LDS, fp32 partials
+//    summed in slice order by gemm_splitk_reduce_kernel (scale + epilogue).
 //  * gemm_f32_kernel      fp32 operands (the fp32 parity config): 64x64 LDS
 //    tiles on the VALU.
 #include <type_traits>
@@ -260,6 +263,161 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny_kernel(SkinnyArgs p) {
             }
         }
         __syncthreads();
+    }
+}
+
+// ===========================================================================
+// Split-K decode GEMM for 33..64 activation rows.
+//
+// With 64 rows the activations (64 x K bf16) outweigh the int8 weight slice a
+// skinny workgroup streams, and a workgroup per 32 columns re-reads them from
+// L2 for every column tile.  Here a workgroup owns 128 B rows (4 waves x two
+// 16-row tiles) and one 512-k slice: it stages the slice's 64 activation rows
+// in LDS once (rows padded by 16 B so the 16 rows of a fragment read fall on
+// distinct banks), issues every weight load of the slice before that, and
+// writes raw fp32 partial sums [slice][m][n_b].  gemm_splitk_reduce_kernel
+// then sums the slices in order 0, 1, ... and applies the per-channel scale
+// and the epilogue, so the result does not depend on scheduling.
+// ===========================================================================
+struct SplitArgs {
+    const uint16_t* a; int64_t lda;
+    const void* b; int64_t ldb;
+    float* part;   // [slices][m][nb]
+    int64_t m, nb, k;
+};
+
+constexpr int kSplitKS = 512;                  // k per slice
+constexpr int kSplitCols = 128;                // B rows per workgroup
+constexpr int kSplitRows = 64;                 // activation rows staged
+constexpr int kSplitLdA = kSplitKS + 8;        // bf16 per staged row
+constexpr int kSplitChunks = kSplitKS / kSkinnyChunk;
+
+template <int BDT, bool TILED>
+__global__ __launch_bounds__(256) void gemm_splitk_kernel(SplitArgs p) {
+    constexpr int BQ = (BDT == SFG_I8) ? 2 : 4;    // uint4 per lane per chunk and tile
+    constexpr int kLaneK = (BDT == SFG_I8) ? 32 : 8;
+    constexpr int kStepK = (BDT == SFG_I8) ? 8 : 32;
+    __shared__ __attribute__((aligned(16))) uint16_t sa[kSplitRows * kSplitLdA];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int lr = lane & 15, lg = lane >> 4;
+    const int64_t k0 = static_cast<int64_t>(blockIdx.y) * kSplitKS;
+    const int64_t col0 = static_cast<int64_t>(blockIdx.x) * kSplitCols + wave * 32;
+
+    // 1. every weight load of this wave's two tiles over the slice
+    const char* bbase = static_cast<const char*>(p.b);
+    const int64_t chunk_count = p.k / kSkinnyChunk;
+    constexpr int64_t kTileBytes = 16 * kSkinnyChunk * ((BDT == SFG_I8) ? 1 : 2);
+    uint4 bq[kSplitChunks][2][BQ];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int64_t brow = col0 + 16 * j;
+#pragma unroll
+        for (int c = 0; c < kSplitChunks; ++c) {
+            const int64_t chunk = k0 / kSkinnyChunk + c;
+            if (TILED) {
+                const char* pj = bbase + ((brow / 16) * chunk_count + chunk) * kTileBytes + lane * 16;
+#pragma unroll
+                for (int s = 0; s < BQ; ++s) bq[c][j][s] = *reinterpret_cast<const uint4*>(pj + 1024 * s);
+            } else {
+                const int64_t belem = (BDT == SFG_I8) ? 1 : 2;
+                const char* pj = bbase + ((brow + lr) * p.ldb + chunk * kSkinnyChunk + lg * kLaneK) * belem;
+#pragma unroll
+                for (int s = 0; s < BQ; ++s)
+                    bq[c][j][s] = *reinterpret_cast<const uint4*>(pj + (BDT == SFG_I8 ? 16 * s : 2 * kStepK * s));
+            }
+        }
+    }
+    // 2. the slice's activation rows -> LDS (rows >= m read as zero)
+    constexpr int kVecsPerRow = kSplitKS / 8;
+#pragma unroll 4
+    for (int q = tid; q < kSplitRows * kVecsPerRow; q += 256) {
+        const int row = q / kVecsPerRow, v = q % kVecsPerRow;
+        uint4 val = make_uint4(0, 0, 0, 0);
+        if (row < p.m) val = *reinterpret_cast<const uint4*>(p.a + row * p.lda + k0 + 8 * v);
+        *reinterpret_cast<uint4*>(&sa[row * kSplitLdA + 8 * v]) = val;
+    }
+    __syncthreads();
+
+    // 3. MFMAs: A fragments from LDS in the k order of the weight fragments
+    floatx4 acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < kSplitChunks; ++c) {
+        bf16x8 bf[2][4];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            if (BDT == SFG_I8) {
+                bf[j][0] = as_bf16x8(i8x8_to_bf16x8(bq[c][j][0].x, bq[c][j][0].y));
+                bf[j][1] = as_bf16x8(i8x8_to_bf16x8(bq[c][j][0].z, bq[c][j][0].w));
+                bf[j][2] = as_bf16x8(i8x8_to_bf16x8(bq[c][j][1].x, bq[c][j][1].y));
+                bf[j][3] = as_bf16x8(i8x8_to_bf16x8(bq[c][j][1].z, bq[c][j][1].w));
+            } else {
+#pragma unroll
+                for (int s = 0; s < 4; ++s) bf[j][s] = as_bf16x8(bq[c][j][s]);
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int kk = c * kSkinnyChunk + lg * kLaneK + s * kStepK;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4*>(&sa[(16 * i + lr) * kSplitLdA + kk]));
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bf[j][s], acc[i][j], 0, 0, 0);
+            }
+        }
+    }
+    // 4. partial sums: lane holds column lr, rows 4 lg + r of each 16-row tile
+    float* part = p.part + static_cast<int64_t>(blockIdx.y) * p.m * p.nb;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t row = 16 * i + 4 * lg + r;
+            if (row >= p.m) continue;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) part[row * p.nb + col0 + 16 * j + lr] = acc[i][j][r];
+        }
+}
+
+struct SplitReduceArgs {
+    const float* part; int slices;
+    const float* scales;
+    void* c; int c_dtype; int64_t ldc;
+    const float* residual; int64_t ldr;
+    int64_t m, n, nb;  // n output columns; nb = B rows (2 n for GLU)
+};
+
+template <int EPI>
+__global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(SplitReduceArgs p) {
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (idx >= p.m * p.n) return;
+    const int64_t row = idx / p.n, col = idx % p.n;
+    const int64_t stride = p.m * p.nb;
+    const float* pr = p.part + row * p.nb;
+    if (EpiTraits<EPI>::glu) {
+        float g = 0.f, u = 0.f;
+        for (int s = 0; s < p.slices; ++s) {
+            g += pr[s * stride + col];
+            u += pr[s * stride + p.n + col];
+        }
+        if (p.scales) {
+            g *= p.scales[col];
+            u *= p.scales[p.n + col];
+        }
+        store_out(p.c, p.c_dtype, row * p.ldc + col, glu_combine(EPI, g, u));
+    } else {
+        float v = 0.f;
+        for (int s = 0; s < p.slices; ++s) v += pr[s * stride + col];
+        if (p.scales) v *= p.scales[col];
+        if (EPI == SFG_EPI_RESIDUAL) v += p.residual[row * p.ldr + col];
+        store_out(p.c, p.c_dtype, row * p.ldc + col, v);
     }
 }
 
@@ -1414,6 +1572,19 @@ constexpr int64_t kSkinnyGroupedMaxTotal = 512;
 // Problems with at least this many rows use the 256x128 kernel.
 constexpr int64_t kBigMinRows = 1024;
 
+// Partial-sum bytes of the split-K decode GEMM for m activation rows, nb B
+// rows and reduction length k; 0 where the shape does not take it.
+size_t splitk_bytes(int64_t m, int64_t nb, int64_t k) {
+    if (m <= 32 || m > kSplitRows || k % kSplitKS != 0 || k / kSplitKS < 2 || nb % kSplitCols != 0) return 0;
+    return static_cast<size_t>(k / kSplitKS) * m * nb * sizeof(float);
+}
+
+template <int BDT>
+void launch_splitk_b(const SplitArgs& a, dim3 grid, bool tiled, hipStream_t s) {
+    if (tiled) gemm_splitk_kernel<BDT, true><<<grid, 256, 0, s>>>(a);
+    else gemm_splitk_kernel<BDT, false><<<grid, 256, 0, s>>>(a);
+}
+
 }  // namespace
 
 bool gemm_qkv_rope_supported(const GemmProblem& p) {
@@ -1434,8 +1605,7 @@ int gemm_preferred_layout(int64_t rows, int64_t k, bool grouped) {
 }
 
 size_t gemm_workspace_bytes(int64_t m, int64_t n, int64_t k) {
-    (void)m; (void)n; (void)k;
-    return 0;  // every GEMM reduces inside its workgroup
+    return splitk_bytes(m, n, k);  // every other GEMM reduces inside its workgroup
 }
 
 int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes, hipStream_t stream) {
@@ -1460,12 +1630,36 @@ int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes, h
         return SFG_ERR_UNSUPPORTED;
     if (p.b_dtype == SFG_I8 && p.b_scales == nullptr) return SFG_ERR_SHAPE;
     const int groups = p.offsets ? p.groups : 1;
+    // 33..64 dense rows: split-K slices when the caller's workspace holds the
+    // partial sums (sized by gemm_workspace_bytes).
+    const int64_t nb = glu ? 2 * p.n : p.n;
+    const size_t split_bytes =
+        p.offsets || p.a_rows || p.epilogue == kEpiQkvRope ? 0 : splitk_bytes(p.m, nb, p.k);
+    if (split_bytes > 0 && workspace && workspace_bytes >= split_bytes) {
+        SplitArgs a{static_cast<const uint16_t*>(p.a), p.lda, p.b, p.ldb, static_cast<float*>(workspace),
+                    p.m, nb, p.k};
+        const dim3 grid(static_cast<unsigned>(nb / kSplitCols), static_cast<unsigned>(p.k / kSplitKS));
+        const bool tiled = p.b_layout == SFG_LAYOUT_TILED;
+        if (p.b_dtype == SFG_I8) launch_splitk_b<SFG_I8>(a, grid, tiled, stream);
+        else launch_splitk_b<SFG_BF16>(a, grid, tiled, stream);
+        SplitReduceArgs r{a.part, static_cast<int>(p.k / kSplitKS), p.b_scales, p.c, p.c_dtype, p.ldc,
+                          p.residual, p.ldr, p.m, p.n, nb};
+        const dim3 rgrid(static_cast<unsigned>((p.m * p.n + 255) / 256));
+        switch (p.epilogue) {
+            case SFG_EPI_NONE: gemm_splitk_reduce_kernel<SFG_EPI_NONE><<<rgrid, 256, 0, stream>>>(r); break;
+            case SFG_EPI_RESIDUAL: gemm_splitk_reduce_kernel<SFG_EPI_RESIDUAL><<<rgrid, 256, 0, stream>>>(r); break;
+            case SFG_EPI_SWIGLU: gemm_splitk_reduce_kernel<SFG_EPI_SWIGLU><<<rgrid, 256, 0, stream>>>(r); break;
+            default: gemm_splitk_reduce_kernel<SFG_EPI_GLU_SILU_UP><<<rgrid, 256, 0, stream>>>(r); break;
+        }
+        return SFG_OK;
+    }
     // The skinny kernel streams K in 128-element chunks; other K go tiled.
     const bool skinny = p.k % kSkinnyChunk == 0 &&
                         (p.offsets ? (p.m <= kSkinnyGroupedMaxTotal) : (p.m <= kSkinnyMaxRows));
     if (skinny) {
         // grouped problems: 32 rows per pass covers the typical decode expert
-        const int64_t rows_hint = p.offsets ? 32 : p.m;
+        static const char* drows = std::getenv("SFG_EXP_DROWS");  // EXPERIMENT
+        const int64_t rows_hint = p.offsets ? 32 : (drows ? std::min<int64_t>(p.m, std::atoi(drows)) : p.m);
         const int mt = rows_hint <= 16 ? 1 : (rows_hint <= 32 ? 2 : 4);
         // grouped: four B tiles per workgroup (GLU: two gate + two up) halve
         // the activation re-reads per weight byte
@@ -1475,7 +1669,8 @@ int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes, h
         if (p.n % tile_cols != 0) return SFG_ERR_UNSUPPORTED;
         // A grouped launch already has groups x N/16 workgroups, several per
         // CU: two waves each keeps the K split (and its LDS reduction) short.
-        const int waves = p.offsets ? 2 : skinny_waves(p.k, mt, nbt);
+        static const char* dw = std::getenv("SFG_EXP_DWAVES");  // EXPERIMENT
+        const int waves = p.offsets ? 2 : (dw ? std::atoi(dw) : skinny_waves(p.k, mt, nbt));
         SkinnyArgs a{};
         a.a = static_cast<const uint16_t*>(p.a); a.lda = p.lda; a.a_rows = p.a_rows;
         a.a_rows_limit = p.a_rows ? p.a_rows_limit : p.m;

@@ -73,7 +73,7 @@ def test_rmsnorm_bf16_output_is_rne_of_f32(lib):
 
 # ------------------------------------------------------------------ GEMM
 def _gemm(lib, a_dev, a_dtype, b_dev, b_dtype, m, n, k, epi, c_dtype=F32, scales=None,
-          residual=None, layout=0, tile=0):
+          residual=None, layout=0, tile=0, workspace=True):
     glu = epi in (EPI_SWIGLU, EPI_GLU_SILU_UP)
     c = torch.empty((m, n), dtype=torch.float32 if c_dtype == F32 else torch.int16, device="cuda")
     args = _abi.GemmArgs()
@@ -86,9 +86,12 @@ def _gemm(lib, a_dev, a_dtype, b_dev, b_dtype, m, n, k, epi, c_dtype=F32, scales
     args.m, args.n, args.k, args.epilogue = m, n, k, epi
     args.b_layout = layout
     args.tile = tile
-    wsb = lib.sfg_hip_gemm_workspace_v1(m, n, k)
-    ws = torch.zeros(max(wsb, 256), dtype=torch.uint8, device="cuda")
-    _abi.check(lib.sfg_hip_gemm_v1(ctypes.byref(args), ws.data_ptr(), ws.numel(), stream()))
+    if workspace:
+        wsb = lib.sfg_hip_gemm_workspace_v1(m, n, k)
+        ws = torch.zeros(max(wsb, 256), dtype=torch.uint8, device="cuda")
+        _abi.check(lib.sfg_hip_gemm_v1(ctypes.byref(args), ws.data_ptr(), ws.numel(), stream()))
+    else:
+        _abi.check(lib.sfg_hip_gemm_v1(ctypes.byref(args), None, 0, stream()))
     _sync()
     return c
 
@@ -126,9 +129,10 @@ def _ref_epilogue(acc, epi, n, residual=None):
     if epi == EPI_RESIDUAL:
         return acc + residual
     g, u = acc[:, :n], acc[:, n:]
+    # exponent clamped: large-magnitude negatives give silu = -0 without overflow
     if epi == EPI_SWIGLU:
-        return g / (1 + np.exp(-g)) * u
-    return g * (u / (1 + np.exp(-u)))
+        return g / (1 + np.exp(np.minimum(-g, 700.0))) * u
+    return g * (u / (1 + np.exp(np.minimum(-u, 700.0))))
 
 
 @pytest.mark.parametrize("m,n,k", [(16, 3072, 2048), (64, 1024, 512), (5, 256, 384),
@@ -154,6 +158,42 @@ def test_gemm_int8_integer_operands_exact(lib, m, n, k):
     s = np.ones(n, np.float32)
     c = _gemm(lib, bf16_dev(a), BF16, dev(q), I8, m, n, k, EPI_NONE, scales=dev(s))
     np.testing.assert_array_equal(host(c), a @ q.astype(np.float32).T)
+
+
+@pytest.mark.parametrize("wdt", ["bf16", "i8"])
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("m,n,k,epi", [(64, 512, 1024, EPI_NONE), (33, 256, 2048, EPI_RESIDUAL),
+                                       (48, 128, 1536, EPI_SWIGLU), (64, 384, 4096, EPI_GLU_SILU_UP)])
+def test_gemm_splitk_integer_operands(lib, wdt, layout, m, n, k, epi):
+    """33..64 rows with a workspace run split-K over 512-k slices; on
+    small-integer operands every partial sum is exact, so the result must equal
+    the exact product and the single-pass kernel's (run with no workspace)."""
+    assert lib.sfg_hip_gemm_workspace_v1(m, n, k) > 0
+    rng = np.random.default_rng(m * 5 + n + k + layout)
+    glu = epi in (EPI_SWIGLU, EPI_GLU_SILU_UP)
+    nb = 2 * n if glu else n
+    a = rng.integers(-3, 4, size=(m, k)).astype(np.float32)
+    res = rng.integers(-5, 6, size=(m, n)).astype(np.float32)
+    if wdt == "bf16":
+        b = rng.integers(-3, 4, size=(nb, k)).astype(np.float32)
+        bd = dev(tile_nk(oracle.to_bf16_bits(b), "bf16").view(np.int16)) if layout else bf16_dev(b)
+        bdt, sc = BF16, None
+    else:
+        q = rng.integers(-127, 128, size=(nb, k)).astype(np.int8)
+        b = q.astype(np.float32)
+        bd = dev(tile_nk(q, "int8")) if layout else dev(q)
+        bdt, sc = I8, dev(np.ones(nb, np.float32))
+    kw = dict(scales=sc, residual=dev(res) if epi == EPI_RESIDUAL else None, layout=layout)
+    c = _gemm(lib, bf16_dev(a), BF16, bd, bdt, m, n, k, epi, **kw)
+    c1 = _gemm(lib, bf16_dev(a), BF16, bd, bdt, m, n, k, epi, workspace=False, **kw)
+    acc = a.astype(np.float64) @ b.T.astype(np.float64)
+    ref = _ref_epilogue(acc, epi, n, res)
+    if glu:
+        np.testing.assert_allclose(host(c), ref, rtol=1e-5, atol=1e-5)
+        np.testing.assert_allclose(host(c), host(c1), rtol=1e-6, atol=1e-6)
+    else:
+        np.testing.assert_array_equal(host(c), ref.astype(np.float32))
+        np.testing.assert_array_equal(host(c), host(c1))
 
 
 @pytest.mark.parametrize("m,n,k,epi", [(128, 1376, 512, EPI_SWIGLU), (700, 688, 256, EPI_NONE),
