@@ -11,9 +11,12 @@ the reference's: equivalent tokens/s = rows * 1000 / ms (decoder_compiler.cpp:
 
 The JSON line also carries:
   roofline      the dominant kernel's achieved fraction of its MI355X peak,
-                from HIP events recorded around it on the layer's stream over
-                the timed region (decode: the paged Split-KV attention kernel,
-                HBM bound; prefill: the layer's MFMA work);
+                from HIP events recorded around it on the layer's stream in
+                every --mark-every'th step of the timed region (decode: the
+                paged Split-KV attention kernel, HBM bound; prefill: the FFN
+                up-projection GEMM).  An event record drains the queue around
+                the kernel it brackets (about 6 us per marked decode step), so
+                marking only some steps keeps that cost out of the throughput;
   cpu_baseline  the CPU oracle (a C restatement of the reference path) timed on
                 this host on a bounded sample of the same workload.
 Synthetic data: activations N(0,1), weights N(0,0.02), cached K/V N(0,1), drawn
@@ -59,6 +62,8 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="bound on the CPU-baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--mark-every", type=int, default=5,
+                   help="bracket the roofline kernel with HIP events in every N-th timed step")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="before warmup, stream MIB MiB through one elementwise kernel "
                         "(reads MIB, writes MIB): the known-size reference for the "
@@ -202,21 +207,22 @@ def main():
         run_layer(plan, x, out)
     torch.cuda.synchronize()
 
-    # Timed region: K layer steps; two HIP events per step on the layer's
-    # stream bracket the roofline kernel: the paged attention kernel (decode)
-    # or the FFN up-projection GEMM (prefill; for MoE the grouped expert GEMMs).
+    # Timed region: K layer steps; in every mark_every-th step two HIP events
+    # on the layer's stream bracket the roofline kernel: the paged attention
+    # kernel (decode) or the FFN up-projection GEMM (prefill; for MoE the
+    # grouped expert GEMMs).
     marks = (_abi.MARK_ROPE, _abi.MARK_ATTN_MAIN) if cfg.decode else (_abi.MARK_ROUTE, _abi.MARK_FFN_UP)
-    events = [StageEvents(plan.lib, marks) for _ in range(args.steps)] if marks else None
+    every = max(1, args.mark_every)
+    events = {i: StageEvents(plan.lib, marks) for i in range(0, args.steps, every)}
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        run_layer(plan, x, out, events=events[i] if events else None)
+        run_layer(plan, x, out, events=events.get(i))
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3
-    kern_times = [e.elapsed(*marks) for e in events] if events else []
-    if events:
-        for e in events:
-            e.close()
+    kern_times = [e.elapsed(*marks) for e in events.values()]
+    for e in events.values():
+        e.close()
     ms_per_step = wall_ms / args.steps
     tokens_s = cfg.rows * 1000.0 / ms_per_step
 
@@ -241,7 +247,8 @@ def main():
                     round(achieved, 1), "peak": C.PEAK_HBM_GBPS, "unit": "GB/s",
                     "frac": round(achieved / C.PEAK_HBM_GBPS, 4),
                     "traffic": MEASURED_TRAFFIC.get(args.config),
-                    "algorithmic_bytes": bytes_, "avg_ms": round(att_ms, 5)}
+                    "algorithmic_bytes": bytes_, "avg_ms": round(att_ms, 5),
+                    "timed_launches": len(kern_times)}
     else:
         # prefill: the FFN up-projection's algorithmic FLOPs (2 rows H 2I for
         # the packed gate|up GEMM; 4 T k H I for the grouped W1|W3 expert GEMM
@@ -265,6 +272,7 @@ def main():
                     "frac": round(achieved / peak, 4),
                     "traffic": MEASURED_TRAFFIC.get(args.config), "algorithmic_bytes": kbytes,
                     "algorithmic_flops": kflops, "avg_ms": round(ffn_ms, 5),
+                    "timed_launches": len(kern_times),
                     "layer_tflops": round(work["flops"] / (ms_per_step * 1e-3) / 1e12, 2),
                     "layer_frac": round(work["flops"] / (ms_per_step * 1e-3) / 1e12 / peak, 4)}
     layer_gbps = work["bytes"] / (ms_per_step * 1e-3) / 1e9
