@@ -135,7 +135,7 @@ def _ref_epilogue(acc, epi, n, residual=None):
     return g * (u / (1 + np.exp(np.minimum(-u, 700.0))))
 
 
-@pytest.mark.parametrize("m,n,k", [(16, 3072, 2048), (64, 1024, 512), (5, 256, 384),
+@pytest.mark.parametrize("m,n,k", [(16, 3072, 2048), (16, 512, 5632), (64, 1024, 512), (5, 256, 384),
                                    (256, 512, 256), (512, 1024, 512), (300, 256, 128),
                                    (1024, 512, 256), (1300, 256, 192), (2048, 1024, 1024),
                                    (1536, 768, 320), (1100, 384, 64)])
@@ -149,7 +149,7 @@ def test_gemm_bf16_integer_operands_exact(lib, m, n, k):
     np.testing.assert_array_equal(host(c), a @ b.T)
 
 
-@pytest.mark.parametrize("m,n,k", [(16, 2048, 2048), (64, 512, 1024), (200, 512, 256),
+@pytest.mark.parametrize("m,n,k", [(16, 2048, 2048), (9, 256, 8192), (64, 512, 1024), (200, 512, 256),
                                    (1100, 256, 128)])
 def test_gemm_int8_integer_operands_exact(lib, m, n, k):
     rng = np.random.default_rng(m + n + k)
