@@ -396,28 +396,49 @@ struct SplitReduceArgs {
 
 template <int EPI>
 __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(SplitReduceArgs p) {
-    const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    // four consecutive output columns per thread (n is a multiple of 64); the
+    // slices' loads are all issued before the ordered sum
+    const int64_t idx = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
     if (idx >= p.m * p.n) return;
     const int64_t row = idx / p.n, col = idx % p.n;
     const int64_t stride = p.m * p.nb;
-    const float* pr = p.part + row * p.nb;
-    if (EpiTraits<EPI>::glu) {
-        float g = 0.f, u = 0.f;
-        for (int s = 0; s < p.slices; ++s) {
-            g += pr[s * stride + col];
-            u += pr[s * stride + p.n + col];
+    const float* pr = p.part + row * p.nb + col;
+    constexpr int kBatch = 8;  // slices loaded together, then added in order
+    constexpr bool kGlu = EpiTraits<EPI>::glu;
+    float gv[4] = {0.f, 0.f, 0.f, 0.f}, uv[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < p.slices; s0 += kBatch) {
+        float4 g[kBatch], u[kGlu ? kBatch : 1];
+#pragma unroll
+        for (int s = 0; s < kBatch; ++s) {
+            if (s0 + s < p.slices) {
+                g[s] = *reinterpret_cast<const float4*>(pr + (s0 + s) * stride);
+                if constexpr (kGlu) u[s] = *reinterpret_cast<const float4*>(pr + (s0 + s) * stride + p.n);
+            }
         }
-        if (p.scales) {
-            g *= p.scales[col];
-            u *= p.scales[p.n + col];
+#pragma unroll
+        for (int s = 0; s < kBatch; ++s) {
+            if (s0 + s < p.slices) {
+                gv[0] += g[s].x; gv[1] += g[s].y; gv[2] += g[s].z; gv[3] += g[s].w;
+                if constexpr (kGlu) { uv[0] += u[s].x; uv[1] += u[s].y; uv[2] += u[s].z; uv[3] += u[s].w; }
+            }
         }
-        store_out(p.c, p.c_dtype, row * p.ldc + col, glu_combine(EPI, g, u));
-    } else {
-        float v = 0.f;
-        for (int s = 0; s < p.slices; ++s) v += pr[s * stride + col];
-        if (p.scales) v *= p.scales[col];
-        if (EPI == SFG_EPI_RESIDUAL) v += p.residual[row * p.ldr + col];
-        store_out(p.c, p.c_dtype, row * p.ldc + col, v);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int64_t cc = col + e;
+        if (kGlu) {
+            float gg = gv[e], uu = uv[e];
+            if (p.scales) {
+                gg *= p.scales[cc];
+                uu *= p.scales[p.n + cc];
+            }
+            store_out(p.c, p.c_dtype, row * p.ldc + cc, glu_combine(EPI, gg, uu));
+        } else {
+            float v = gv[e];
+            if (p.scales) v *= p.scales[cc];
+            if (EPI == SFG_EPI_RESIDUAL) v += p.residual[row * p.ldr + cc];
+            store_out(p.c, p.c_dtype, row * p.ldc + cc, v);
+        }
     }
 }
 
@@ -1644,7 +1665,7 @@ int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes, h
         else launch_splitk_b<SFG_BF16>(a, grid, tiled, stream);
         SplitReduceArgs r{a.part, static_cast<int>(p.k / kSplitKS), p.b_scales, p.c, p.c_dtype, p.ldc,
                           p.residual, p.ldr, p.m, p.n, nb};
-        const dim3 rgrid(static_cast<unsigned>((p.m * p.n + 255) / 256));
+        const dim3 rgrid(static_cast<unsigned>((p.m * p.n / 4 + 255) / 256));
         switch (p.epilogue) {
             case SFG_EPI_NONE: gemm_splitk_reduce_kernel<SFG_EPI_NONE><<<rgrid, 256, 0, stream>>>(r); break;
             case SFG_EPI_RESIDUAL: gemm_splitk_reduce_kernel<SFG_EPI_RESIDUAL><<<rgrid, 256, 0, stream>>>(r); break;
