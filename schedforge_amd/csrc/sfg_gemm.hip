@@ -1561,6 +1561,11 @@ DmaShape dma_shape_of(int tile) {
 }
 DmaShape pick_dma_shape(int64_t m, int64_t n_out, bool glu, int groups, int tile) {
     if (tile > SFG_TILE_AUTO && tile < SFG_TILE_COUNT) return dma_shape_of(tile);
+    // Grouped GLU (expert W1|W3): the eight-wave 256 x 256 tile once it has
+    // work for half the CUs -- measured faster than 256 x 128 on the MoE
+    // prefill shape although its tile count stays under 512.
+    if (groups > 1 && glu && ((m + 255) / 256 + groups) * ((n_out + 127) / 128) >= 128)
+        return dma_shape_of(SFG_TILE_256x256_W8);
     for (const int t : {SFG_TILE_256x256_PP, SFG_TILE_256x128, SFG_TILE_128x128}) {
         const DmaShape sh = dma_shape_of(t);
         const int64_t cols = glu ? sh.bn / 2 : sh.bn;
@@ -1679,8 +1684,7 @@ int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes, h
                         (p.offsets ? (p.m <= kSkinnyGroupedMaxTotal) : (p.m <= kSkinnyMaxRows));
     if (skinny) {
         // grouped problems: 32 rows per pass covers the typical decode expert
-        static const char* drows = std::getenv("SFG_EXP_DROWS");  // EXPERIMENT
-        const int64_t rows_hint = p.offsets ? 32 : (drows ? std::min<int64_t>(p.m, std::atoi(drows)) : p.m);
+        const int64_t rows_hint = p.offsets ? 32 : p.m;
         const int mt = rows_hint <= 16 ? 1 : (rows_hint <= 32 ? 2 : 4);
         // grouped: four B tiles per workgroup (GLU: two gate + two up) halve
         // the activation re-reads per weight byte
@@ -1690,8 +1694,7 @@ int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes, h
         if (p.n % tile_cols != 0) return SFG_ERR_UNSUPPORTED;
         // A grouped launch already has groups x N/16 workgroups, several per
         // CU: two waves each keeps the K split (and its LDS reduction) short.
-        static const char* dw = std::getenv("SFG_EXP_DWAVES");  // EXPERIMENT
-        const int waves = p.offsets ? 2 : (dw ? std::atoi(dw) : skinny_waves(p.k, mt, nbt));
+        const int waves = p.offsets ? 2 : skinny_waves(p.k, mt, nbt);
         SkinnyArgs a{};
         a.a = static_cast<const uint16_t*>(p.a); a.lda = p.lda; a.a_rows = p.a_rows;
         a.a_rows_limit = p.a_rows ? p.a_rows_limit : p.m;
