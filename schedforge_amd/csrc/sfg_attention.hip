@@ -779,14 +779,40 @@ __global__ __launch_bounds__(kDecD) void attn_decode_combine_kernel(
     const int bh = blockIdx.x;  // b * q_heads + h
     const int d = threadIdx.x;
     const float* ml = part_ml + static_cast<int64_t>(bh) * splits * 2;
+    const float* pa = part_acc + static_cast<int64_t>(bh) * splits * kDecD + d;
     float mm = -INFINITY;
-    for (int s = 0; s < splits; ++s) mm = fmaxf(mm, ml[2 * s]);
     float ls = 0.f, as = 0.f;
-    for (int s = 0; s < splits; ++s) {
-        const float ms = ml[2 * s];
-        const float wf = (ms == -INFINITY) ? 0.f : fast_exp2(ms - mm);
-        ls += ml[2 * s + 1] * wf;
-        as += part_acc[(static_cast<int64_t>(bh) * splits + s) * kDecD + d] * wf;
+    constexpr int kRegSplits = 16;
+    if (splits <= kRegSplits) {
+        // every split's (m, l, acc) loaded before the merge: one memory wait
+        float m_s[kRegSplits], l_s[kRegSplits], a_s[kRegSplits];
+#pragma unroll
+        for (int s = 0; s < kRegSplits; ++s) {
+            if (s < splits) {
+                m_s[s] = ml[2 * s];
+                l_s[s] = ml[2 * s + 1];
+                a_s[s] = pa[s * kDecD];
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < kRegSplits; ++s)
+            if (s < splits) mm = fmaxf(mm, m_s[s]);
+#pragma unroll
+        for (int s = 0; s < kRegSplits; ++s) {
+            if (s < splits) {
+                const float wf = (m_s[s] == -INFINITY) ? 0.f : fast_exp2(m_s[s] - mm);
+                ls += l_s[s] * wf;
+                as += a_s[s] * wf;
+            }
+        }
+    } else {
+        for (int s = 0; s < splits; ++s) mm = fmaxf(mm, ml[2 * s]);
+        for (int s = 0; s < splits; ++s) {
+            const float ms = ml[2 * s];
+            const float wf = (ms == -INFINITY) ? 0.f : fast_exp2(ms - mm);
+            ls += ml[2 * s + 1] * wf;
+            as += pa[s * kDecD] * wf;
+        }
     }
     const float o = as / ls;
     // merged layout [B][Hq * D] == [b][h * D + d]

@@ -6,6 +6,8 @@
 // the row width allows.
 #include "sfg_kernels.hpp"
 
+#include <type_traits>
+
 namespace sfg {
 
 // ---------------------------------------------------------------------------
@@ -73,8 +75,77 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
     }
 }
 
+// Rows of at most 1024 * NV floats (width a multiple of 4): the row and the
+// gains are read once into registers before the reduction, so the output pass
+// waits on no second global read.  Same accumulation order as rmsnorm_kernel
+// (thread-strided float4 runs, wave sums, four partials), so the same bits.
+template <typename OutT, int NV>
+__global__ __launch_bounds__(256) void rmsnorm_reg_kernel(const float* __restrict__ x,
+                                                          const float* __restrict__ w,
+                                                          OutT* __restrict__ y, int width, float eps,
+                                                          float* __restrict__ y32) {
+    const int row = blockIdx.x;
+    const float* xr = x + static_cast<int64_t>(row) * width;
+    OutT* yr = y + static_cast<int64_t>(row) * width;
+    __shared__ double partial[4];
+    __shared__ float inv_shared;
+    float4 v[NV], g[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c = (threadIdx.x + 256 * i) * 4;
+        v[i] = c < width ? *reinterpret_cast<const float4*>(xr + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+        g[i] = c < width ? *reinterpret_cast<const float4*>(w + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    double sum = 0.0;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        if ((threadIdx.x + 256 * i) * 4 >= width) break;
+        sum += static_cast<double>(v[i].x) * v[i].x;
+        sum += static_cast<double>(v[i].y) * v[i].y;
+        sum += static_cast<double>(v[i].z) * v[i].z;
+        sum += static_cast<double>(v[i].w) * v[i].w;
+    }
+    sum = wave_sum(sum);
+    if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = sum;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const double total = partial[0] + partial[1] + partial[2] + partial[3];
+        inv_shared = 1.0f / sqrtf(static_cast<float>(total / static_cast<double>(width)) + eps);
+    }
+    __syncthreads();
+    const float inv = inv_shared;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c = (threadIdx.x + 256 * i) * 4;
+        if (c >= width) break;
+        const float o0 = v[i].x * inv * g[i].x, o1 = v[i].y * inv * g[i].y;
+        const float o2 = v[i].z * inv * g[i].z, o3 = v[i].w * inv * g[i].w;
+        if constexpr (sizeof(OutT) == 4) {
+            *reinterpret_cast<float4*>(yr + c) = make_float4(o0, o1, o2, o3);
+        } else {
+            uint2 packed;
+            packed.x = pack_bf16x2(o0, o1);
+            packed.y = pack_bf16x2(o2, o3);
+            *reinterpret_cast<uint2*>(yr + c) = packed;
+        }
+        if (y32) *reinterpret_cast<float4*>(y32 + static_cast<int64_t>(row) * width + c) = make_float4(o0, o1, o2, o3);
+    }
+}
+
 void launch_rmsnorm(const float* x, const float* w, void* y, int y_dtype, int64_t rows,
                     int64_t width, float eps, hipStream_t stream, float* y32) {
+    if (width % 4 == 0 && width <= 1024 * 8) {
+        const int nv = width <= 1024 * 2 ? 2 : (width <= 1024 * 4 ? 4 : 8);
+        auto go = [&](auto* out) {
+            using OutT = std::remove_pointer_t<decltype(out)>;
+            if (nv == 2) rmsnorm_reg_kernel<OutT, 2><<<dim3(rows), dim3(256), 0, stream>>>(x, w, out, static_cast<int>(width), eps, y32);
+            else if (nv == 4) rmsnorm_reg_kernel<OutT, 4><<<dim3(rows), dim3(256), 0, stream>>>(x, w, out, static_cast<int>(width), eps, y32);
+            else rmsnorm_reg_kernel<OutT, 8><<<dim3(rows), dim3(256), 0, stream>>>(x, w, out, static_cast<int>(width), eps, y32);
+        };
+        if (y_dtype == SFG_F32) go(static_cast<float*>(y));
+        else go(static_cast<uint16_t*>(y));
+        return;
+    }
     if (y_dtype == SFG_F32)
         rmsnorm_kernel<float><<<dim3(rows), dim3(256), 0, stream>>>(x, w, static_cast<float*>(y),
                                                                      static_cast<int>(width), eps, y32);
