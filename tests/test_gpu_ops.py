@@ -586,7 +586,12 @@ def _route(lib, x, router, bias, top_k):
 
 
 @pytest.mark.parametrize("T,H,E,k,bias_std", [(2048, 2048, 8, 2, 0.5), (64, 4096, 8, 2, 0.0),
-                                              (100, 512, 16, 4, 1.0), (33, 256, 4, 1, 0.0)])
+                                              (100, 512, 16, 4, 1.0), (33, 256, 4, 1, 0.0),
+                                              # dispatch held in registers: 8 full chunks of
+                                              # 1024 assignments; a ragged last chunk
+                                              (4096, 128, 16, 2, 1.0), (1537, 256, 8, 2, 0.5),
+                                              # chunked dispatch: more experts / assignments
+                                              (300, 256, 32, 2, 1.0), (5000, 128, 8, 2, 0.5)])
 def test_moe_route_bit_exact(lib, T, H, E, k, bias_std):
     x = oracle.normal(101, 0, (T, H))
     router = oracle.normal(101, 10, (H, E), 0.02)
