@@ -675,10 +675,24 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(
     uint4 kb[kKs];
     uint2 vb[kDt];
     bool okb = false;
+    // Long page ranges: the wave's page ids 64 at a time (lane i holds page
+    // ids_base + i), so a page's K / V loads wait on no page-table read of
+    // their own.  Short ranges read each id through the scalar cache, which
+    // costs less than the one vector load up front.
+    const bool vec_ids = w_end - w_begin > 16;
+    int ids_vec = 0, ids_base = w_begin - 64;
+    auto phys_of = [&](int pg) {
+        if (!vec_ids) return ptab[pg];
+        if (pg - ids_base >= 64) {  // wave-uniform
+            ids_base = pg;
+            ids_vec = pg + lane < w_end ? ptab[pg + lane] : -1;
+        }
+        return __builtin_amdgcn_readlane(ids_vec, pg - ids_base);
+    };
     // Load page p (guarded: an id outside the pool reads nothing).
 #define SFG_LOAD_PAGE(p)                                                                   \
     {                                                                                      \
-        const int phys = ptab[(p)];                                                        \
+        const int phys = phys_of(p);                                                       \
         okb = phys >= 0 && phys < num_pages;                                               \
         const int64_t base = okb ? static_cast<int64_t>(phys) * page_stride + kvh * head_stride : 0; \
         const uint16_t* kp = k_pool + base + k_off;                                        \

@@ -287,7 +287,8 @@ struct SplitArgs {
 };
 
 constexpr int kSplitKS = 512;                  // k per slice
-constexpr int kSplitCols = 128;                // B rows per workgroup
+constexpr int kSplitTiles = 2;                 // 16-row B tiles per wave
+constexpr int kSplitCols = 64 * kSplitTiles;   // B rows per workgroup
 constexpr int kSplitRows = 64;                 // activation rows staged
 constexpr int kSplitLdA = kSplitKS + 8;        // bf16 per staged row
 constexpr int kSplitChunks = kSplitKS / kSkinnyChunk;
@@ -303,15 +304,15 @@ __global__ __launch_bounds__(256) void gemm_splitk_kernel(SplitArgs p) {
     const int wave = tid >> 6;
     const int lr = lane & 15, lg = lane >> 4;
     const int64_t k0 = static_cast<int64_t>(blockIdx.y) * kSplitKS;
-    const int64_t col0 = static_cast<int64_t>(blockIdx.x) * kSplitCols + wave * 32;
+    const int64_t col0 = static_cast<int64_t>(blockIdx.x) * kSplitCols + wave * 16 * kSplitTiles;
 
     // 1. every weight load of this wave's two tiles over the slice
     const char* bbase = static_cast<const char*>(p.b);
     const int64_t chunk_count = p.k / kSkinnyChunk;
     constexpr int64_t kTileBytes = 16 * kSkinnyChunk * ((BDT == SFG_I8) ? 1 : 2);
-    uint4 bq[kSplitChunks][2][BQ];
+    uint4 bq[kSplitChunks][kSplitTiles][BQ];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < kSplitTiles; ++j) {
         const int64_t brow = col0 + 16 * j;
 #pragma unroll
         for (int c = 0; c < kSplitChunks; ++c) {
@@ -341,16 +342,16 @@ __global__ __launch_bounds__(256) void gemm_splitk_kernel(SplitArgs p) {
     __syncthreads();
 
     // 3. MFMAs: A fragments from LDS in the k order of the weight fragments
-    floatx4 acc[4][2];
+    floatx4 acc[4][kSplitTiles];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < kSplitTiles; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < kSplitChunks; ++c) {
-        bf16x8 bf[2][4];
+        bf16x8 bf[kSplitTiles][4];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < kSplitTiles; ++j) {
             if (BDT == SFG_I8) {
                 bf[j][0] = as_bf16x8(i8x8_to_bf16x8(bq[c][j][0].x, bq[c][j][0].y));
                 bf[j][1] = as_bf16x8(i8x8_to_bf16x8(bq[c][j][0].z, bq[c][j][0].w));
@@ -368,7 +369,7 @@ __global__ __launch_bounds__(256) void gemm_splitk_kernel(SplitArgs p) {
             for (int i = 0; i < 4; ++i) {
                 const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4*>(&sa[(16 * i + lr) * kSplitLdA + kk]));
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
+                for (int j = 0; j < kSplitTiles; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bf[j][s], acc[i][j], 0, 0, 0);
             }
         }
@@ -382,7 +383,7 @@ __global__ __launch_bounds__(256) void gemm_splitk_kernel(SplitArgs p) {
             const int64_t row = 16 * i + 4 * lg + r;
             if (row >= p.m) continue;
 #pragma unroll
-            for (int j = 0; j < 2; ++j) part[row * p.nb + col0 + 16 * j + lr] = acc[i][j][r];
+            for (int j = 0; j < kSplitTiles; ++j) part[row * p.nb + col0 + 16 * j + lr] = acc[i][j][r];
         }
 }
 

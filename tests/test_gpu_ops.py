@@ -534,6 +534,14 @@ def test_decode_paged_head_dim_64_matches_oracle(lib, B, Hq, Hkv, ctx):
     _decode_case(lib, B, Hq, Hkv, ctx, D=64, splits=3, seed=92)
 
 
+@pytest.mark.parametrize("ctx,lens", [(4096, None), (6000, None), (6000, [6000, 1500, 17, 4097])])
+def test_decode_long_page_ranges_match_oracle(lib, ctx, lens):
+    """One split: each wave walks more than 16 pages (64 and about 94), so the
+    page ids come 64 at a time from one vector load, reloaded past 64 pages."""
+    B = 4 if lens else 2
+    _decode_case(lib, B, 8, 2, ctx, seq_lens=np.array(lens, np.int32) if lens else None, splits=1, seed=93)
+
+
 def test_decode_ragged_lengths_and_split_invariance(lib):
     lens = [1000, 1, 513, 640]
     a = _decode_case(lib, 4, 8, 2, 1000, seq_lens=lens, splits=1)
