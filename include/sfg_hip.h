@@ -130,6 +130,9 @@ int sfg_hip_rmsnorm_v1(const float* x, const float* w, void* y, int y_dtype, int
 /* C[M][N] = A[M][K] * B^T with B stored [N][K] (or [2N][K] for GLU epilogues).
  * a_dtype: SFG_F32 (only with b_dtype SFG_F32) or SFG_BF16.  b_dtype: SFG_F32,
  * SFG_BF16 or SFG_I8 (then b_scales[N or 2N] per output channel).
+ * bf16 / int8 operands: a and b 16-byte aligned, lda * 2 and ldb * (2 or 1)
+ * bytes multiples of 16 (rows are read as 16-byte vectors), else
+ * SFG_ERR_UNSUPPORTED.
  * c_dtype: SFG_F32 or SFG_BF16.  Replaces execute(LoopIR) (runtime.cpp:581-626)
  * for the four projections and quantized_invoke (next_milestones.cpp:50-69).
  * workspace: sfg_hip_gemm_workspace_v1 bytes.  Non-zero only for 33..64 dense

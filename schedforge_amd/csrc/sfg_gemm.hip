@@ -1656,6 +1656,11 @@ int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes, h
     if (p.a_dtype != SFG_BF16 || (p.b_dtype != SFG_BF16 && p.b_dtype != SFG_I8))
         return SFG_ERR_UNSUPPORTED;
     if (p.b_dtype == SFG_I8 && p.b_scales == nullptr) return SFG_ERR_SHAPE;
+    // every bf16 / int8 kernel reads A and B rows as 16-byte vectors
+    const int64_t b_elem = p.b_dtype == SFG_I8 ? 1 : 2;
+    if ((reinterpret_cast<uintptr_t>(p.a) & 15) || (reinterpret_cast<uintptr_t>(p.b) & 15) ||
+        (p.lda * 2) % 16 != 0 || (p.ldb * b_elem) % 16 != 0)
+        return SFG_ERR_UNSUPPORTED;
     const int groups = p.offsets ? p.groups : 1;
     // 33..64 dense rows: split-K slices when the caller's workspace holds the
     // partial sums (sized by gemm_workspace_bytes).
