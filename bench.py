@@ -47,7 +47,7 @@ PMC_ROOFLINE_KIB = {           # roofline kernel(s) per launch: (FETCH_SIZE, WRI
     "c2": (66117.8, 1088.0),                    # attn_decode_split_kernel
     "c5": (1049963.6, 2112.0),                  # attn_decode_split_kernel
     "c4": (1376849.7, 229376.0),                # gate|up GEMM + SwiGLU
-    "c3": (157089.2 + 71083.4, 11265.0 + 32768.0),  # grouped W1|W3 + W2 expert GEMMs
+    "c3": (143115.5 + 71003.0, 11264.0 + 32768.0),  # grouped W1|W3 + W2 expert GEMMs
 }
 MEASURED_TRAFFIC = {k: round((f * PMC_FETCH_SCALE + w * PMC_WRITE_SCALE) * 1024)
                     for k, (f, w) in PMC_ROOFLINE_KIB.items()}
