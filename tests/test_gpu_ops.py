@@ -612,6 +612,8 @@ def _route(lib, x, router, bias, top_k):
 
 @pytest.mark.parametrize("T,H,E,k,bias_std", [(2048, 2048, 8, 2, 0.5), (64, 4096, 8, 2, 0.0),
                                               (100, 512, 16, 4, 1.0), (33, 256, 4, 1, 0.0),
+                                              # six 512-feature router chunks, ragged last workgroup
+                                              (37, 3072, 8, 2, 0.5),
                                               # dispatch held in registers: 8 full chunks of
                                               # 1024 assignments; a ragged last chunk
                                               (4096, 128, 16, 2, 1.0), (1537, 256, 8, 2, 0.5),
