@@ -1700,7 +1700,10 @@ int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes, h
         if (p.n % tile_cols != 0) return SFG_ERR_UNSUPPORTED;
         // A grouped launch already has groups x N/16 workgroups, several per
         // CU: two waves each keeps the K split (and its LDS reduction) short.
-        const int waves = p.offsets ? 2 : skinny_waves(p.k, mt, nbt);
+        // So does a 16-row GLU product up to K = 2048 (two load batches per
+        // wave; measured faster than four waves on the decode gate|up).
+        const bool two = p.offsets || (glu && mt == 1 && p.k <= 2048);
+        const int waves = two ? 2 : skinny_waves(p.k, mt, nbt);
         SkinnyArgs a{};
         a.a = static_cast<const uint16_t*>(p.a); a.lda = p.lda; a.a_rows = p.a_rows;
         a.a_rows_limit = p.a_rows ? p.a_rows_limit : p.m;
