@@ -60,7 +60,7 @@ enum sfg_status {
     SFG_ERR_WORKSPACE = 17      /* workspace too small                           */
 };
 
-enum sfg_dtype { SFG_F32 = 0, SFG_BF16 = 1, SFG_I8 = 2 };
+enum sfg_dtype { SFG_F32 = 0, SFG_BF16 = 1, SFG_I8 = 2, SFG_I32 = 3 /* taps only */ };
 
 enum sfg_layout { SFG_LAYOUT_NK = 0, SFG_LAYOUT_TILED = 1 };
 
@@ -244,7 +244,10 @@ int sfg_hip_moe_route_v1(const float* x, const float* router, const float* bias,
                          int32_t* token_ids, int32_t* route_slots, float* routing_weights,
                          int32_t* position, void* workspace, size_t workspace_bytes,
                          void* stream);
-/* Same pipeline from a given routing trace (decoder_compiler.cpp:281-284). */
+/* Same pipeline from a given routing trace (decoder_compiler.cpp:281-284).  An
+ * expert id outside [0, experts) (the reference refuses one,
+ * next_milestones.cpp:427-428) is left out of counts, offsets and the segments,
+ * and its position is -1: sfg_hip_moe_combine_v1 adds nothing for it. */
 int sfg_hip_moe_dispatch_trace_v1(const int32_t* ids, const float* weights, int64_t tokens,
                                   int64_t experts, int64_t top_k, int32_t* counts,
                                   int32_t* offsets, int32_t* token_ids, int32_t* route_slots,
@@ -292,7 +295,12 @@ typedef struct {
                          * K/V written into the pools at that position (append_paged_kv,
                          * next_milestones.cpp:486-524; the page must already be in the
                          * table) and attention over the cache including it.  Not a
-                         * reference mode: its outputs differ from execute_once's. */
+                         * reference mode: its outputs differ from execute_once's.
+                         * Needs a capacity-sized rope_table (below).  A sequence already
+                         * at capacity (pages_per_seq * page_tokens) gets nothing
+                         * appended and its length stays at the capacity: the caller
+                         * must refuse such a step, as the reference's append_paged_kv
+                         * does ("paged KV capacity exceeded"). */
     int32_t gemm_tile;  /* sfg_gemm_tile of the prefill projection / expert GEMMs;
                          * SFG_TILE_AUTO (0) picks per shape.  Same results for every
                          * tile; a plan-policy knob searched by the plan optimiser. */
@@ -311,7 +319,12 @@ typedef struct {
     const void* w2; const float* s2;             /* MoE: [E][H][I] */
     uint16_t* k_pool; uint16_t* v_pool;          /* decode: paged bf16 pools (written when kv_append) */
     const int32_t* page_table;                   /* decode: [B][pages_per_seq] */
-    const float* rope_table;                     /* [S][D/2][2] */
+    const float* rope_table;                     /* [rows][D/2][2] device copy of
+                                                  * sfg_hip_rope_table_host_v1 with rows =
+                                                  * S (prefill), 1 (decode: position 0), or
+                                                  * pages_per_seq * page_tokens when
+                                                  * kv_append: the new token rotates at its
+                                                  * length, clamped to capacity - 1 */
 } sfg_layer_weights;
 
 /* Stage marks recorded into caller-created events when io->stage_events != NULL. */
@@ -332,6 +345,27 @@ typedef struct {
 } sfg_layer_io;
 
 size_t sfg_hip_decoder_layer_workspace_v1(const sfg_layer_desc* desc);
+
+/* Stage intermediates a layer call leaves in its workspace, for stage-level
+ * validation: execute_once's own intermediate buffers (decoder_compiler.cpp:
+ * 218-304 -- merged attention, the residual r1, the second RMSNorm's output and
+ * the routing of route_topk, moe_compiler.cpp:412-455).  After a call returns
+ * (once its stream has drained), bytes [offset, offset + bytes) of the same
+ * workspace hold the tap for the same descriptor:
+ *   SFG_TAP_ATTN          merged attention [rows][H], act dtype
+ *   SFG_TAP_RESIDUAL1     r1 = attn Wo + x, [rows][H] fp32
+ *   SFG_TAP_NORM2         RMSNorm(r1) * rms2, [rows][H] act dtype
+ *   SFG_TAP_ROUTE_INPUT   the router's fp32 input RMSNorm(r1) * rms2 [rows][H] (MoE)
+ *   SFG_TAP_ROUTE_IDS     top-k expert ids [rows][k] int32     } MoE routed on
+ *   SFG_TAP_ROUTE_WEIGHTS renormalised weights [rows][k] fp32  } the device only
+ * dtype receives an sfg_dtype.  No reference entry point exposes these; the
+ * reference's tests compare whole-layer outputs only. */
+enum sfg_layer_tap {
+    SFG_TAP_ATTN = 0, SFG_TAP_RESIDUAL1, SFG_TAP_NORM2, SFG_TAP_ROUTE_INPUT, SFG_TAP_ROUTE_IDS,
+    SFG_TAP_ROUTE_WEIGHTS, SFG_NUM_TAPS
+};
+int sfg_hip_decoder_layer_tap_v1(const sfg_layer_desc* desc, int tap, size_t* offset,
+                                 size_t* bytes, int* dtype);
 int sfg_hip_decoder_layer_v1(const sfg_layer_desc* desc, const sfg_layer_weights* weights,
                              const sfg_layer_io* io, void* workspace, size_t workspace_bytes,
                              void* stream);

@@ -109,6 +109,17 @@ def normal(seed: int, tensor: str | int, shape, std: float = 1.0, mean: float = 
     return out
 
 
+def normal_at(seed: int, tensor: str | int, shape, offset: int, std: float = 1.0,
+              mean: float = 0.0) -> np.ndarray:
+    """Elements [offset, offset + prod(shape)) of the tensor normal() draws:
+    normal(seed, t, (E, *shape))[e] == normal_at(seed, t, shape, e * prod(shape))."""
+    tid = TID[tensor] if isinstance(tensor, str) else int(tensor)
+    out = np.empty(shape, dtype=np.float32)
+    lib().sfgo_fill_normal_at(ctypes.c_uint64(seed), ctypes.c_uint32(tid), ctypes.c_float(mean),
+                              ctypes.c_float(std), _f(out), i64(offset), i64(out.size))
+    return out
+
+
 def page_permutation(seed: int, count: int) -> np.ndarray:
     out = np.empty(count, dtype=np.int32)
     lib().sfgo_page_permutation(ctypes.c_uint64(seed), _i(out), i64(count))
@@ -254,6 +265,24 @@ def quantized_matmul(x, q_nk, scales):
     return out
 
 
+def quantized_moe(x, e1, e3, e2, ids, weights):
+    """execute_quantized_moe_once restated (sfgo_quantized_moe): e1 / e3 / e2 are
+    per-expert (q [N][K] int8, scales [N]) pairs from quantize_kn of W1[e],
+    W3[e] ([H][I]) and W2[e] ([I][H])."""
+    x = np.ascontiguousarray(x, np.float32)
+    t, h = x.shape
+    ids = np.ascontiguousarray(ids, np.int32)
+    weights = np.ascontiguousarray(weights, np.float32)
+    top_k = ids.shape[1]
+    inter = e1[0][0].shape[0]
+    stk = [np.ascontiguousarray(np.stack([p[j] for p in e])) for e in (e1, e3, e2) for j in (0, 1)]
+    out = np.empty((t, h), np.float32)
+    lib().sfgo_quantized_moe(_f(x), _b(stk[0]), _f(stk[1]), _b(stk[2]), _f(stk[3]), _b(stk[4]),
+                             _f(stk[5]), i64(t), i64(h), i64(inter), i64(top_k), _i(ids),
+                             _f(weights), _f(out))
+    return out
+
+
 def max_abs_error(a, b):
     a = np.ascontiguousarray(a, np.float32).reshape(-1)
     b = np.ascontiguousarray(b, np.float32).reshape(-1)
@@ -268,4 +297,4 @@ def rel_error(got, ref):
     return float(np.max(np.abs(got - ref)) / max(float(np.max(np.abs(ref))), 1e-6))
 
 
-from .data import make_layer_data, quantize_layer, decoder_layer  # noqa: E402,F401
+from .data import make_layer_data, quantize_layer, decoder_layer, decoder_layer_rows  # noqa: E402,F401

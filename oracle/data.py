@@ -5,7 +5,9 @@ make_layer_data(cfg, seed) draws every tensor from the counter-based generator
 cached K/V N(0,1), router bias N(0, cfg.router_bias_std) when that is > 0.
 bf16 configs round activations, weights and the KV cache to bf16 (RNE);
 w8 configs round activations and the KV cache, and quantize projection and
-expert weights per output channel (quantize_layer).
+expert weights per output channel (quantize_layer).  lazy_experts=True leaves
+the expert weights as ExpertWeights (drawn one expert at a time on access) so a
+full-size MoE layer never holds every fp32 expert in host memory.
 """
 from __future__ import annotations
 
@@ -14,13 +16,34 @@ from types import SimpleNamespace
 
 import numpy as np
 
-from . import (LayerCfg, LayerData, LayerTaps, _b, _f, _i, lib, normal, page_permutation,
-               quantize_kn, round_bf16)
+from . import (LayerCfg, LayerData, LayerTaps, _b, _f, _i, lib, normal, normal_at,
+               page_permutation, quantize_kn, round_bf16)
 
 WEIGHT_STD = 0.02
 
 
-def make_layer_data(cfg, seed: int) -> SimpleNamespace:
+class ExpertWeights:
+    """An [E, K, N] expert weight drawn one expert at a time: w[e] generates
+    expert e's [K][N] slice of normal(seed, tensor, (E, K, N), std) (bf16-rounded
+    when asked), so only one expert is ever held in host memory."""
+
+    def __init__(self, seed, tensor, experts, k, n, std, bf16):
+        self.seed, self.tensor, self.shape = seed, tensor, (experts, k, n)
+        self.std, self.bf16 = std, bf16
+
+    def __len__(self):
+        return self.shape[0]
+
+    def __getitem__(self, e):
+        _, k, n = self.shape
+        w = normal_at(self.seed, self.tensor, (k, n), int(e) * k * n, self.std)
+        return round_bf16(w) if self.bf16 else w
+
+    def __call__(self, e):
+        return self[e]
+
+
+def make_layer_data(cfg, seed: int, lazy_experts: bool = False) -> SimpleNamespace:
     H, I, D = cfg.hidden, cfg.intermediate, cfg.head_dim
     kvd = cfg.kv_heads * D
     rows = cfg.batch * cfg.sequence
@@ -39,9 +62,15 @@ def make_layer_data(cfg, seed: int) -> SimpleNamespace:
         d.router_weight = normal(seed, "router", (H, E), WEIGHT_STD)
         if getattr(cfg, "router_bias_std", 0.0) > 0.0:
             d.router_bias = normal(seed, "router_bias", (E,), cfg.router_bias_std)
-        d.w1 = normal(seed, "w1", (E, H, I), WEIGHT_STD)
-        d.w3 = normal(seed, "w3", (E, H, I), WEIGHT_STD)
-        d.w2 = normal(seed, "w2", (E, I, H), WEIGHT_STD)
+        if lazy_experts:
+            bf = cfg.dtype == "bf16"
+            d.w1 = ExpertWeights(seed, "w1", E, H, I, WEIGHT_STD, bf)
+            d.w3 = ExpertWeights(seed, "w3", E, H, I, WEIGHT_STD, bf)
+            d.w2 = ExpertWeights(seed, "w2", E, I, H, WEIGHT_STD, bf)
+        else:
+            d.w1 = normal(seed, "w1", (E, H, I), WEIGHT_STD)
+            d.w3 = normal(seed, "w3", (E, H, I), WEIGHT_STD)
+            d.w2 = normal(seed, "w2", (E, I, H), WEIGHT_STD)
     else:
         d.gate_weight = normal(seed, "wg", (H, I), WEIGHT_STD)
         d.up_weight = normal(seed, "wu", (H, I), WEIGHT_STD)
@@ -64,7 +93,7 @@ def make_layer_data(cfg, seed: int) -> SimpleNamespace:
         for name in ("query_weight", "key_weight", "value_weight", "output_weight", "gate_weight",
                      "up_weight", "down_weight", "router_weight", "w1", "w3", "w2"):
             v = getattr(d, name)
-            if v is not None:
+            if v is not None and not isinstance(v, ExpertWeights):
                 setattr(d, name, round_bf16(v))
     return d
 
@@ -91,15 +120,10 @@ def _stack(pairs):
     return qs, ss
 
 
-def decoder_layer(cfg, d, quant=None, taps: bool = False, threads: int = 0,
-                  trace=None):
-    """reference_decoder_layer (decoder_compiler.cpp:622-673) restated; int8 mode
-    per next_milestones.cpp.  Returns out [rows, H] (and a dict of taps)."""
-    rows = cfg.batch * cfg.sequence
-    H = cfg.hidden
-    kvd = cfg.kv_heads * cfg.head_dim
-    c = LayerCfg(cfg.batch, cfg.sequence, H, cfg.intermediate, cfg.query_heads, cfg.kv_heads,
-                 cfg.head_dim, cfg.rms_epsilon, cfg.rope_theta, int(cfg.causal),
+def _layer_structs(cfg, d, quant, threads, trace):
+    """LayerCfg / LayerData for one call, plus the arrays they point into."""
+    c = LayerCfg(cfg.batch, cfg.sequence, cfg.hidden, cfg.intermediate, cfg.query_heads,
+                 cfg.kv_heads, cfg.head_dim, cfg.rms_epsilon, cfg.rope_theta, int(cfg.causal),
                  int(cfg.ffn == "moe"), cfg.experts, cfg.top_k, cfg.context_sequence,
                  int(cfg.dtype == "w8"), threads, int(getattr(cfg, "kv_append", False)))
     ld = LayerData()
@@ -116,7 +140,9 @@ def decoder_layer(cfg, d, quant=None, taps: bool = False, threads: int = 0,
     ld.wq, ld.wk, ld.wv, ld.wo = F(d.query_weight), F(d.key_weight), F(d.value_weight), F(d.output_weight)
     ld.wg, ld.wu, ld.wd = F(d.gate_weight), F(d.up_weight), F(d.down_weight)
     ld.router, ld.router_bias = F(d.router_weight), F(d.router_bias)
-    ld.w1, ld.w3, ld.w2 = F(d.w1), F(d.w3), F(d.w2)
+    if cfg.dtype != "w8":
+        ld.w1, ld.w3, ld.w2 = (F(np.stack([w[e] for e in range(len(w))]) if isinstance(w, ExpertWeights)
+                                 else w) for w in (d.w1, d.w3, d.w2))
     ld.cached_k, ld.cached_v = F(d.cached_key), F(d.cached_value)
     if trace is not None:
         ids = np.ascontiguousarray(trace[0], np.int32)
@@ -136,28 +162,63 @@ def decoder_layer(cfg, d, quant=None, taps: bool = False, threads: int = 0,
                 keep += [qs, ss]
                 setattr(ld, name + "q", _b(qs))
                 setattr(ld, name + "s", _f(ss))
-    out = np.empty((rows, H), np.float32)
-    tp = None
-    t = {}
-    if taps:
-        t["normalized1"] = np.empty((rows, H), np.float32)
-        t["qkv"] = np.empty((rows, H + 2 * kvd), np.float32)
-        t["attn_merged"] = np.empty((rows, H), np.float32)
-        t["residual1"] = np.empty((rows, H), np.float32)
-        t["normalized2"] = np.empty((rows, H), np.float32)
-        tp = LayerTaps(_f(t["normalized1"]), _f(t["qkv"]), _f(t["attn_merged"]),
-                       _f(t["residual1"]), _f(t["normalized2"]))
-        if getattr(cfg, "kv_append", False):
-            t["new_k"] = np.empty((cfg.batch, cfg.kv_heads, cfg.sequence, cfg.head_dim), np.float32)
-            t["new_v"] = np.empty_like(t["new_k"])
-            tp.new_k, tp.new_v = _f(t["new_k"]), _f(t["new_v"])
-        if cfg.ffn == "moe":
-            t["ids"] = np.empty((rows, cfg.top_k), np.int32)
-            t["weights"] = np.empty((rows, cfg.top_k), np.float32)
-            t["counts"] = np.empty(cfg.experts, np.int32)
-            tp.ids, tp.weights, tp.counts = _i(t["ids"]), _f(t["weights"]), _i(t["counts"])
+    return c, ld, keep
+
+
+def _taps(cfg, rows):
+    H = cfg.hidden
+    kvd = cfg.kv_heads * cfg.head_dim
+    t = {"normalized1": np.empty((rows, H), np.float32),
+         "qkv": np.empty((rows, H + 2 * kvd), np.float32),
+         "attn_merged": np.empty((rows, H), np.float32),
+         "residual1": np.empty((rows, H), np.float32),
+         "normalized2": np.empty((rows, H), np.float32)}
+    tp = LayerTaps(_f(t["normalized1"]), _f(t["qkv"]), _f(t["attn_merged"]),
+                   _f(t["residual1"]), _f(t["normalized2"]))
+    if getattr(cfg, "kv_append", False):
+        t["new_k"] = np.empty((cfg.batch, cfg.kv_heads, cfg.sequence, cfg.head_dim), np.float32)
+        t["new_v"] = np.empty_like(t["new_k"])
+        tp.new_k, tp.new_v = _f(t["new_k"]), _f(t["new_v"])
+    if cfg.ffn == "moe":
+        t["ids"] = np.empty((rows, cfg.top_k), np.int32)
+        t["weights"] = np.empty((rows, cfg.top_k), np.float32)
+        t["counts"] = np.empty(cfg.experts, np.int32)
+        tp.ids, tp.weights, tp.counts = _i(t["ids"]), _f(t["weights"]), _i(t["counts"])
+    return t, tp
+
+
+def decoder_layer(cfg, d, quant=None, taps: bool = False, threads: int = 0,
+                  trace=None):
+    """reference_decoder_layer (decoder_compiler.cpp:622-673) restated; int8 mode
+    per next_milestones.cpp.  Returns out [rows, H] (and a dict of taps)."""
+    rows = cfg.batch * cfg.sequence
+    c, ld, keep = _layer_structs(cfg, d, quant, threads, trace)
+    out = np.empty((rows, cfg.hidden), np.float32)
+    t, tp = _taps(cfg, rows) if taps else ({}, None)
     rc = lib().sfgo_decoder_layer(ctypes.byref(c), ctypes.byref(ld), _f(out),
                                   ctypes.byref(tp) if tp is not None else None)
+    del keep
     if rc != 0:
         raise ValueError("invalid decoder configuration")
+    return (out, t) if taps else out
+
+
+def decoder_layer_rows(cfg, d, sample, quant=None, taps: bool = False, threads: int = 0,
+                       trace=None):
+    """The prefill layer at rows `sample` only (row = b * S + s): K / V of every
+    row, everything else for the sampled rows (sfgo_decoder_layer_rows).  Equal
+    bit for bit to those rows of decoder_layer.  Returns out [n, H] (and n-row
+    taps; "counts" covers the sampled rows)."""
+    sample = np.ascontiguousarray(sample, np.int64)
+    n = sample.size
+    c, ld, keep = _layer_structs(cfg, d, quant, threads, trace)
+    out = np.empty((n, cfg.hidden), np.float32)
+    t, tp = _taps(cfg, n) if taps else ({}, None)
+    rc = lib().sfgo_decoder_layer_rows(ctypes.byref(c), ctypes.byref(ld),
+                                       sample.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
+                                       ctypes.c_int64(n), _f(out),
+                                       ctypes.byref(tp) if tp is not None else None)
+    del keep
+    if rc != 0:
+        raise ValueError("invalid row-sampled decoder configuration")
     return (out, t) if taps else out

@@ -53,16 +53,24 @@ static uint64_t stream_key(uint64_t seed, uint32_t tensor_id) {
  * 53-bit uniforms drawn from the counter stream at 2i and 2i+1. */
 void sfgo_fill_normal(uint64_t seed, uint32_t tensor_id, float mean, float stddev,
                       float* out, int64_t count) {
+    sfgo_fill_normal_at(seed, tensor_id, mean, stddev, out, 0, count);
+}
+
+/* Elements [offset, offset + count) of the same tensor (one expert's slice of an
+ * [E, ...] weight, drawn without materialising the others). */
+void sfgo_fill_normal_at(uint64_t seed, uint32_t tensor_id, float mean, float stddev,
+                         float* out, int64_t offset, int64_t count) {
     const uint64_t key = stream_key(seed, tensor_id);
     const double two_pi = 6.283185307179586476925286766559;
 #pragma omp parallel for schedule(static)
-    for (int64_t i = 0; i < count; ++i) {
-        const uint64_t r1 = sfgo_splitmix64(key + 2 * (uint64_t)i);
-        const uint64_t r2 = sfgo_splitmix64(key + 2 * (uint64_t)i + 1);
+    for (int64_t n = 0; n < count; ++n) {
+        const uint64_t i = (uint64_t)(offset + n);
+        const uint64_t r1 = sfgo_splitmix64(key + 2 * i);
+        const uint64_t r2 = sfgo_splitmix64(key + 2 * i + 1);
         const double u1 = ((double)(r1 >> 11) + 1.0) * (1.0 / 9007199254740992.0);
         const double u2 = (double)(r2 >> 11) * (1.0 / 9007199254740992.0);
         const double z = sqrt(-2.0 * log(u1)) * cos(two_pi * u2);
-        out[i] = (float)((double)mean + (double)stddev * z);
+        out[n] = (float)((double)mean + (double)stddev * z);
     }
 }
 
@@ -244,9 +252,37 @@ void sfgo_add(const float* a, const float* b, float* out, int64_t count) {
 /* reference_attention (attention_compiler.cpp:742-781): two-pass softmax per
  * (batch, head, query); causal alignment j <= Skv - Sq + i (68-72); GQA
  * kv_head = h * Hkv / Hq; scale 1/sqrt(D) unless cfg->scale > 0 (43-46). */
+/* One query row: qr [D] against keys / values kb, vb ([seq_kv][D], [seq_kv][Dv]
+ * of its kv head) up to key `limit`; scores is scratch of seq_kv floats. */
+static void attention_row(const float* qr, const float* kb, const float* vb, int64_t seq_kv,
+                          int64_t limit, int64_t D, int64_t Dv, float scale, float* scores,
+                          float* orow) {
+    float maximum = -INFINITY;
+    for (int64_t j = 0; j <= limit && j < seq_kv; ++j) {
+        const float* kr = kb + j * D;
+        float dot = 0.0f;
+        for (int64_t d = 0; d < D; ++d) dot = fmaf(qr[d], kr[d], dot);
+        scores[j] = dot * scale;
+        if (scores[j] > maximum) maximum = scores[j];
+    }
+    for (int64_t d = 0; d < Dv; ++d) orow[d] = 0.0f;
+    float denom = 0.0f;
+    for (int64_t j = 0; j <= limit && j < seq_kv; ++j) {
+        const float p = expf(scores[j] - maximum);
+        denom += p;
+        const float* vr = vb + j * Dv;
+        for (int64_t d = 0; d < Dv; ++d) orow[d] = fmaf(p, vr[d], orow[d]);
+    }
+    for (int64_t d = 0; d < Dv; ++d) orow[d] /= denom;
+}
+
+static float attention_scale(const sfgo_attn_cfg* c) {
+    return c->scale > 0.0f ? c->scale : 1.0f / sqrtf((float)c->head_dim);
+}
+
 void sfgo_attention(const sfgo_attn_cfg* c, const float* q, const float* k, const float* v,
                     float* out) {
-    const float scale = c->scale > 0.0f ? c->scale : 1.0f / sqrtf((float)c->head_dim);
+    const float scale = attention_scale(c);
     const int64_t D = c->head_dim, Dv = c->head_dim_value;
     const int64_t pairs = (int64_t)c->batch * c->query_heads;
 #pragma omp parallel for schedule(dynamic, 1)
@@ -254,27 +290,13 @@ void sfgo_attention(const sfgo_attn_cfg* c, const float* q, const float* k, cons
         const int64_t b = bh / c->query_heads, h = bh % c->query_heads;
         const int64_t kvh = h * c->kv_heads / c->query_heads;
         float* scores = (float*)malloc(sizeof(float) * (size_t)c->seq_kv);
+        const float* kb = k + (b * c->kv_heads + kvh) * c->seq_kv * D;
+        const float* vb = v + (b * c->kv_heads + kvh) * c->seq_kv * Dv;
         for (int64_t i = 0; i < c->seq_q; ++i) {
-            const float* qr = q + ((b * c->query_heads + h) * c->seq_q + i) * D;
-            float* orow = out + ((b * c->query_heads + h) * c->seq_q + i) * Dv;
             const int64_t limit = c->causal ? (c->seq_kv - c->seq_q + i) : (c->seq_kv - 1);
-            float maximum = -INFINITY;
-            for (int64_t j = 0; j <= limit && j < c->seq_kv; ++j) {
-                const float* kr = k + ((b * c->kv_heads + kvh) * c->seq_kv + j) * D;
-                float dot = 0.0f;
-                for (int64_t d = 0; d < D; ++d) dot = fmaf(qr[d], kr[d], dot);
-                scores[j] = dot * scale;
-                if (scores[j] > maximum) maximum = scores[j];
-            }
-            for (int64_t d = 0; d < Dv; ++d) orow[d] = 0.0f;
-            float denom = 0.0f;
-            for (int64_t j = 0; j <= limit && j < c->seq_kv; ++j) {
-                const float p = expf(scores[j] - maximum);
-                denom += p;
-                const float* vr = v + ((b * c->kv_heads + kvh) * c->seq_kv + j) * Dv;
-                for (int64_t d = 0; d < Dv; ++d) orow[d] = fmaf(p, vr[d], orow[d]);
-            }
-            for (int64_t d = 0; d < Dv; ++d) orow[d] /= denom;
+            attention_row(q + ((b * c->query_heads + h) * c->seq_q + i) * D, kb, vb, c->seq_kv,
+                          limit, D, Dv, scale, scores,
+                          out + ((b * c->query_heads + h) * c->seq_q + i) * Dv);
         }
         free(scores);
     }
@@ -472,17 +494,29 @@ void sfgo_quantize_nk(const float* w_nk, int64_t n, int64_t k, int8_t* q, float*
 }
 
 /* quantized_invoke (next_milestones.cpp:50-69), no bias / relu:
- * y[m,n] = sum_k x[m,k] * (float(q[n,k]) * s_n), sequential over k, fp32
- * activations.  The dequantised weight is formed exactly as the reference
- * forms it, then laid out [K,N] so the chain vectorises across n. */
+ * y[m,n] = sum_k (x[m,k] * float(q[n,k])) * s_n, sequential over k, fp32
+ * activations.  The reference's `acc += x * float(q - zp) * scale` multiplies
+ * left to right and, compiled with FMA contraction, adds the scaled product
+ * into the accumulator with one fused step: acc = fma(x * q, s, acc).  That
+ * is what each output does here; q is laid out [K][N] as exact floats so the
+ * chain vectorises across n. */
 void sfgo_quantized_matmul(const float* x, const int8_t* q_nk, const float* scales,
                            int64_t m, int64_t n, int64_t k, float* out) {
-    float* deq = (float*)malloc(sizeof(float) * (size_t)(n * k));
+    float* qf = (float*)malloc(sizeof(float) * (size_t)(n * k));
 #pragma omp parallel for schedule(static)
     for (int64_t c = 0; c < n; ++c)
-        for (int64_t d = 0; d < k; ++d) deq[d * n + c] = (float)q_nk[c * k + d] * scales[c];
-    sfgo_matmul(x, deq, out, m, n, k);
-    free(deq);
+        for (int64_t d = 0; d < k; ++d) qf[d * n + c] = (float)q_nk[c * k + d];
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int64_t i = 0; i < m; ++i) {
+        float* crow = out + i * n;
+        for (int64_t j = 0; j < n; ++j) crow[j] = 0.0f;
+        for (int64_t kk = 0; kk < k; ++kk) {
+            const float xik = x[i * k + kk];
+            const float* qrow = qf + kk * n;
+            for (int64_t j = 0; j < n; ++j) crow[j] = fmaf(xik * qrow[j], scales[j], crow[j]);
+        }
+    }
+    free(qf);
 }
 
 /* execute_quantized_moe_once (next_milestones.cpp:418-460): per token and slot,
@@ -537,11 +571,14 @@ void sfgo_quantized_moe(const float* x, const int8_t* w1q, const float* s1,
     free(y_all);
 }
 
+/* max_abs_error (runtime.cpp:628-635): |float(a - b)| in double, folded with
+ * std::max(error, d) = (error < d ? d : error), so a NaN difference leaves the
+ * running value unchanged. */
 double sfgo_max_abs_error(const float* a, const float* b, int64_t count) {
     double err = 0.0;
     for (int64_t i = 0; i < count; ++i) {
         const double d = fabs((double)(a[i] - b[i]));
-        if (d > err || d != d) err = d;
+        err = err < d ? d : err;
     }
     return err;
 }
@@ -712,5 +749,177 @@ int sfgo_decoder_layer(const sfgo_layer_cfg* c, const sfgo_layer_data* d, float*
     }
     free(n1); free(qkv); free(q); free(k); free(v); free(attn); free(merged); free(proj);
     free(r1); free(n2); free(ffn);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------- */
+/* The whole layer at a sample of query rows (prefill).  Same arithmetic as   */
+/* sfgo_decoder_layer restricted to rows sample[0..n) (row = b * S + s):      */
+/* RMSNorm and the K / V projections run for every row (a query attends over  */
+/* every earlier key), Q, attention, O-projection, residual, RMSNorm and FFN  */
+/* only for the sampled rows.  Each output element is the same chain as in    */
+/* the full layer (products are per-column FMA chains over k; attention and   */
+/* the FFN are per row), so every sampled row of `out` and of the taps (n     */
+/* rows each) equals that row of sfgo_decoder_layer bit for bit.              */
+/* ------------------------------------------------------------------------- */
+
+static void gather_rows(const float* src, const int64_t* sample, int64_t n, int64_t width,
+                        float* dst) {
+    for (int64_t i = 0; i < n; ++i)
+        memcpy(dst + i * width, src + sample[i] * width, sizeof(float) * (size_t)width);
+}
+
+int sfgo_decoder_layer_rows(const sfgo_layer_cfg* c, const sfgo_layer_data* d,
+                            const int64_t* sample, int64_t n, float* out,
+                            sfgo_layer_taps* taps) {
+#ifdef _OPENMP
+    if (c->threads > 0) omp_set_num_threads(c->threads);
+#endif
+    if (c->batch <= 0 || c->sequence <= 0 || c->hidden <= 0 || c->intermediate <= 0 ||
+        c->query_heads <= 0 || c->kv_heads <= 0 || c->head_dim <= 0 ||
+        c->hidden != c->query_heads * c->head_dim || c->query_heads % c->kv_heads != 0 ||
+        c->rms_epsilon <= 0.0f || c->context != 0 || c->kv_append || n <= 0)
+        return 1;
+    if (c->moe && (c->experts <= 0 || c->top_k <= 0 || c->top_k > c->experts)) return 1;
+    const int64_t B = c->batch, S = c->sequence;
+    const int64_t rows = B * S;
+    for (int64_t i = 0; i < n; ++i)
+        if (sample[i] < 0 || sample[i] >= rows) return 1;
+    const int64_t H = c->hidden, I = c->intermediate, D = c->head_dim;
+    const int64_t Hq = c->query_heads, Hkv = c->kv_heads;
+    const int64_t kvd = Hkv * D;
+
+    /* every row: normalised input, K and V (RoPE on K at the index within S) */
+    float* n1 = alloc_f(rows * H);
+    sfgo_rms_norm(d->input, d->rms1, n1, rows, H, c->rms_epsilon);
+    float* kvp = alloc_f(rows * 2 * kvd);
+    if (c->int8_weights) {
+        float* part = alloc_f(rows * kvd);
+        for (int j = 0; j < 2; ++j) {
+            sfgo_quantized_matmul(n1, d->q8[1 + j], d->s8[1 + j], rows, kvd, H, part);
+            for (int64_t r = 0; r < rows; ++r)
+                memcpy(kvp + r * 2 * kvd + j * kvd, part + r * kvd, sizeof(float) * (size_t)kvd);
+        }
+        free(part);
+    } else {
+        float* packed = alloc_f(H * 2 * kvd);
+        const float* ws[2] = {d->wk, d->wv};
+        const int64_t widths[2] = {kvd, kvd};
+        sfgo_concat_columns(ws, widths, 2, H, packed);
+        sfgo_matmul(n1, packed, kvp, rows, 2 * kvd, H);
+        free(packed);
+    }
+    float* k = alloc_f(rows * kvd);
+    float* v = alloc_f(rows * kvd);
+    for (int64_t b = 0; b < B; ++b)
+        for (int64_t s = 0; s < S; ++s)
+            for (int64_t h = 0; h < Hkv; ++h) {
+                const float* row = kvp + (b * S + s) * 2 * kvd;
+                memcpy(k + ((b * Hkv + h) * S + s) * D, row + h * D, sizeof(float) * (size_t)D);
+                memcpy(v + ((b * Hkv + h) * S + s) * D, row + kvd + h * D, sizeof(float) * (size_t)D);
+            }
+    sfgo_rope(k, B, Hkv, S, D, c->rope_theta);
+
+    /* sampled rows: Q (RoPE at the row's index within S) and attention */
+    float* n1s = alloc_f(n * H);
+    gather_rows(n1, sample, n, H, n1s);
+    float* qs = alloc_f(n * H);
+    if (c->int8_weights)
+        sfgo_quantized_matmul(n1s, d->q8[0], d->s8[0], n, H, H, qs);
+    else
+        sfgo_matmul(n1s, d->wq, qs, n, H, H);
+    float* qrot = alloc_f(n * H);
+    memcpy(qrot, qs, sizeof(float) * (size_t)(n * H));
+    for (int64_t i = 0; i < n; ++i)  /* row i holds [Hq][D] of one token */
+        sfgo_rope_at(qrot + i * H, 1, Hq, 1, D, c->rope_theta, sample[i] % S);
+    sfgo_attn_cfg ac = {c->batch, c->query_heads, c->kv_heads, c->sequence, c->sequence,
+                        c->head_dim, c->head_dim, c->causal, 0.0f};
+    const float scale = attention_scale(&ac);
+    float* merged = alloc_f(n * H);
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int64_t ih = 0; ih < n * Hq; ++ih) {
+        const int64_t i = ih / Hq, h = ih % Hq;
+        const int64_t b = sample[i] / S, s = sample[i] % S;
+        const int64_t kvh = h * Hkv / Hq;
+        float* scores = (float*)malloc(sizeof(float) * (size_t)S);
+        attention_row(qrot + i * H + h * D, k + (b * Hkv + kvh) * S * D, v + (b * Hkv + kvh) * S * D,
+                      S, c->causal ? s : S - 1, D, D, scale, scores, merged + i * H + h * D);
+        free(scores);
+    }
+    /* O-projection, residual, RMSNorm, FFN on the sampled rows */
+    float* proj = alloc_f(n * H);
+    if (c->int8_weights)
+        sfgo_quantized_matmul(merged, d->q8[3], d->s8[3], n, H, H, proj);
+    else
+        sfgo_matmul(merged, d->wo, proj, n, H, H);
+    float* xs = alloc_f(n * H);
+    gather_rows(d->input, sample, n, H, xs);
+    float* r1 = alloc_f(n * H);
+    sfgo_add(proj, xs, r1, n * H);
+    float* n2 = alloc_f(n * H);
+    sfgo_rms_norm(r1, d->rms2, n2, n, H, c->rms_epsilon);
+    float* ffn = alloc_f(n * H);
+    if (!c->moe) {
+        float* act = alloc_f(n * I);
+        if (c->int8_weights) {
+            float* g = alloc_f(n * I);
+            float* u = alloc_f(n * I);
+            sfgo_quantized_matmul(n2, d->q8[4], d->s8[4], n, I, H, g);
+            sfgo_quantized_matmul(n2, d->q8[5], d->s8[5], n, I, H, u);
+            for (int64_t i = 0; i < n * I; ++i) act[i] = (g[i] / (1.0f + expf(-g[i]))) * u[i];
+            sfgo_quantized_matmul(act, d->q8[6], d->s8[6], n, H, I, ffn);
+            free(g); free(u);
+        } else {
+            float* packed = alloc_f(H * 2 * I);
+            const float* ws[2] = {d->wg, d->wu};
+            const int64_t widths[2] = {I, I};
+            sfgo_concat_columns(ws, widths, 2, H, packed);
+            float* gu = alloc_f(n * 2 * I);
+            sfgo_matmul(n2, packed, gu, n, 2 * I, H);
+            sfgo_swiglu(gu, n, I, act);
+            sfgo_matmul(act, d->wd, ffn, n, H, I);
+            free(packed); free(gu);
+        }
+        free(act);
+    } else {
+        const int64_t K = c->top_k;
+        int32_t* ids = (int32_t*)malloc(sizeof(int32_t) * (size_t)(n * K));
+        float* wts = alloc_f(n * K);
+        int32_t* counts = (int32_t*)calloc((size_t)c->experts, sizeof(int32_t));
+        if (d->trace_ids) {
+            for (int64_t i = 0; i < n; ++i)
+                for (int64_t j = 0; j < K; ++j) {
+                    ids[i * K + j] = d->trace_ids[sample[i] * K + j];
+                    wts[i * K + j] = d->trace_weights[sample[i] * K + j];
+                    counts[ids[i * K + j]] += 1;
+                }
+        } else {
+            sfgo_route_topk(n2, d->router, d->router_bias, n, H, c->experts, K, ids, wts, counts);
+        }
+        if (c->int8_weights)
+            sfgo_quantized_moe(n2, d->e1q, d->e1s, d->e3q, d->e3s, d->e2q, d->e2s, n, H, I, K, ids,
+                               wts, ffn);
+        else
+            sfgo_moe_reference(n2, d->w1, d->w3, d->w2, n, H, I, K, ids, wts, ffn);
+        if (taps && taps->ids) memcpy(taps->ids, ids, sizeof(int32_t) * (size_t)(n * K));
+        if (taps && taps->weights) memcpy(taps->weights, wts, sizeof(float) * (size_t)(n * K));
+        if (taps && taps->counts) memcpy(taps->counts, counts, sizeof(int32_t) * (size_t)c->experts);
+        free(ids); free(wts); free(counts);
+    }
+    sfgo_add(r1, ffn, out, n * H);
+    if (taps) {
+        if (taps->normalized1) memcpy(taps->normalized1, n1s, sizeof(float) * (size_t)(n * H));
+        if (taps->qkv)
+            for (int64_t i = 0; i < n; ++i) {
+                float* row = taps->qkv + i * (H + 2 * kvd);
+                memcpy(row, qs + i * H, sizeof(float) * (size_t)H);
+                memcpy(row + H, kvp + sample[i] * 2 * kvd, sizeof(float) * (size_t)(2 * kvd));
+            }
+        if (taps->attn_merged) memcpy(taps->attn_merged, merged, sizeof(float) * (size_t)(n * H));
+        if (taps->residual1) memcpy(taps->residual1, r1, sizeof(float) * (size_t)(n * H));
+        if (taps->normalized2) memcpy(taps->normalized2, n2, sizeof(float) * (size_t)(n * H));
+    }
+    free(n1); free(kvp); free(k); free(v); free(n1s); free(qs); free(qrot); free(merged);
+    free(proj); free(xs); free(r1); free(n2); free(ffn);
     return 0;
 }

@@ -32,6 +32,8 @@ extern "C" {
 uint64_t sfgo_splitmix64(uint64_t x);
 void sfgo_fill_normal(uint64_t seed, uint32_t tensor_id, float mean, float stddev,
                       float* out, int64_t count);
+void sfgo_fill_normal_at(uint64_t seed, uint32_t tensor_id, float mean, float stddev,
+                         float* out, int64_t offset, int64_t count);
 void sfgo_page_permutation(uint64_t seed, int32_t* perm, int64_t count);
 
 /* ---- bf16 (compiler.cpp:34-52) ---- */
@@ -142,6 +144,10 @@ typedef struct {  /* optional intermediates for stage-level checks (each may be 
 
 int sfgo_decoder_layer(const sfgo_layer_cfg* cfg, const sfgo_layer_data* d, float* out,
                        sfgo_layer_taps* taps);
+/* Prefill layer at the rows sample[0..n) only (row = b * S + s): out [n][H] and
+ * n-row taps equal those rows of sfgo_decoder_layer bit for bit. */
+int sfgo_decoder_layer_rows(const sfgo_layer_cfg* cfg, const sfgo_layer_data* d,
+                            const int64_t* sample, int64_t n, float* out, sfgo_layer_taps* taps);
 
 double sfgo_max_abs_error(const float* a, const float* b, int64_t count);
 int sfgo_num_threads(void);

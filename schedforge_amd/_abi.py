@@ -15,12 +15,14 @@ LIB_PATH = Path(__file__).resolve().parent / "lib" / "libsfg_hip.so"
 
 ABI_VERSION = 1
 
-F32, BF16, I8 = 0, 1, 2
+F32, BF16, I8, I32 = 0, 1, 2, 3
 EPI_NONE, EPI_RESIDUAL, EPI_SWIGLU, EPI_GLU_SILU_UP = 0, 1, 2, 3
 LAYOUT_NK, LAYOUT_TILED = 0, 1
 # sfg_gemm_tile
 TILE_AUTO, TILE_256x256_PP, TILE_256x256_W8, TILE_256x256_W4, TILE_256x128, TILE_128x256, \
     TILE_128x128, TILE_COUNT = range(8)
+
+TAP_ATTN, TAP_RESIDUAL1, TAP_NORM2, TAP_ROUTE_INPUT, TAP_ROUTE_IDS, TAP_ROUTE_WEIGHTS, NUM_TAPS = range(7)
 
 (MARK_START, MARK_NORM1, MARK_QKV, MARK_ROPE, MARK_ATTN_MAIN, MARK_ATTN, MARK_OPROJ,
  MARK_NORM2, MARK_ROUTE, MARK_FFN_UP, MARK_FFN_DOWN, MARK_END, NUM_MARKS) = range(13)
@@ -141,6 +143,9 @@ _SIGNATURES = {
                                        c_sz, c_vp]),
     "sfg_hip_moe_combine_v1": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp]),
     "sfg_hip_decoder_layer_workspace_v1": (c_sz, [ctypes.POINTER(LayerDesc)]),
+    "sfg_hip_decoder_layer_tap_v1": (c_i32, [ctypes.POINTER(LayerDesc), ctypes.c_int,
+                                             ctypes.POINTER(c_sz), ctypes.POINTER(c_sz),
+                                             ctypes.POINTER(ctypes.c_int)]),
     "sfg_hip_decoder_layer_v1": (c_i32, [ctypes.POINTER(LayerDesc), ctypes.POINTER(LayerWeights),
                                          ctypes.POINTER(LayerIO), c_vp, c_sz, c_vp]),
     "sfg_hip_events_create_v1": (c_i32, [ctypes.c_int, ctypes.POINTER(c_vp)]),

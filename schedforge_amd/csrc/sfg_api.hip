@@ -619,6 +619,50 @@ size_t sfg_hip_decoder_layer_workspace_v1(const sfg_layer_desc* desc) {
     return plan_buffers(desc, nullptr).total;
 }
 
+int sfg_hip_decoder_layer_tap_v1(const sfg_layer_desc* d, int tap, size_t* offset, size_t* bytes,
+                                 int* dtype) {
+    int rc = validate_desc(d);
+    if (rc != SFG_OK) return rc;
+    if (!offset || !bytes || !dtype) return fail(SFG_ERR_SHAPE, "decoder layer tap: null output");
+    // Offsets are the carve-up of a workspace based at a non-null sentinel.
+    char* const base = reinterpret_cast<char*>(static_cast<uintptr_t>(1) << 20);
+    const LayerBuffers b = plan_buffers(d, base);
+    const int64_t rows = static_cast<int64_t>(d->batch) * d->sequence;
+    const int64_t H = d->hidden;
+    const bool routed = d->ffn == 1 && !d->use_routing_trace;
+    const void* p = nullptr;
+    size_t n = 0;
+    int dt = SFG_F32;
+    switch (tap) {
+    case SFG_TAP_ATTN:
+        p = b.attn; dt = d->act_dtype; n = static_cast<size_t>(rows * H) * (dt == SFG_F32 ? 4 : 2);
+        break;
+    case SFG_TAP_RESIDUAL1:
+        p = b.r1; n = static_cast<size_t>(rows * H) * 4;
+        break;
+    case SFG_TAP_NORM2:
+        p = b.xn; dt = d->act_dtype; n = static_cast<size_t>(rows * H) * (dt == SFG_F32 ? 4 : 2);
+        break;
+    case SFG_TAP_ROUTE_INPUT:
+        if (d->ffn != 1) return fail(SFG_ERR_UNSUPPORTED, "the router input tap needs a MoE layer");
+        p = b.xn2_f32; n = static_cast<size_t>(rows * H) * 4;
+        break;
+    case SFG_TAP_ROUTE_IDS:
+    case SFG_TAP_ROUTE_WEIGHTS:
+        if (!routed) return fail(SFG_ERR_UNSUPPORTED, "routing taps need a MoE layer routed on the device");
+        p = tap == SFG_TAP_ROUTE_IDS ? static_cast<const void*>(b.ids) : static_cast<const void*>(b.wts);
+        dt = tap == SFG_TAP_ROUTE_IDS ? SFG_I32 : SFG_F32;
+        n = static_cast<size_t>(rows * d->top_k) * 4;
+        break;
+    default:
+        return fail(SFG_ERR_SHAPE, "unknown decoder layer tap %d", tap);
+    }
+    *offset = static_cast<size_t>(static_cast<const char*>(p) - base);
+    *bytes = n;
+    *dtype = dt;
+    return SFG_OK;
+}
+
 int sfg_hip_decoder_layer_v1(const sfg_layer_desc* d, const sfg_layer_weights* w,
                              const sfg_layer_io* io, void* workspace, size_t workspace_bytes,
                              void* stream_ptr) {
@@ -738,7 +782,9 @@ int sfg_hip_decoder_layer_v1(const sfg_layer_desc* d, const sfg_layer_weights* w
             d->num_pages, splits, scale, b.attn_ws, s,
             io->stage_events ? static_cast<hipEvent_t>(io->stage_events[SFG_MARK_ATTN_MAIN]) : nullptr);
         if (rc != SFG_OK) return fail(rc, "decode attention not lowered (head_dim %lld)", (long long)D);
-        if (append && io->seq_lens) sfg::launch_kv_advance(io->seq_lens, d->batch, 1, s);
+        if (append && io->seq_lens)
+            sfg::launch_kv_advance(io->seq_lens, d->batch, 1,
+                                   static_cast<int64_t>(d->pages_per_seq) * d->page_tokens, s);
     } else {
         if (act == SFG_F32) {
             if (D > 128) return fail(SFG_ERR_UNSUPPORTED, "fp32 attention head_dim > 128");

@@ -614,11 +614,15 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(
     const int q_heads = kv_heads * G;
     const int lr = lane & 15, lg = lane >> 4;
     // Tokens this sequence attends over: its length (plus len_extra tokens just
-    // appended in place); the query rotates at rope_pos, or at the length
-    // before the append (its own position) when rope_pos < 0.
+    // appended in place), at most the table's capacity; the query rotates at
+    // rope_pos, or at the length before the append (its own position) when
+    // rope_pos < 0 -- clamped to the capacity's last row, the last row a
+    // capacity-sized RoPE table holds (a step past the capacity appended
+    // nothing and is refused by the host mirror).
+    const int capacity = pages_per_seq * kPageTok;
     const int len0 = seq_lens ? seq_lens[b] : uniform_len;
-    const int len = min(len0 + len_extra, pages_per_seq * kPageTok);
-    const int q_pos = rope_pos >= 0 ? rope_pos : max(len0, 0);
+    const int len = min(len0 + len_extra, capacity);
+    const int q_pos = rope_pos >= 0 ? rope_pos : min(max(len0, 0), capacity - 1);
     const int pages = (len + kPageTok - 1) / kPageTok;
     const int sp_begin = static_cast<int>(static_cast<int64_t>(pages) * split / splits);
     const int sp_end = static_cast<int>(static_cast<int64_t>(pages) * (split + 1) / splits);
@@ -949,9 +953,13 @@ __global__ __launch_bounds__(64) void kv_append_kernel(KvAppendArgs a) {
     a.v_pool[(blk * kKvD + 2 * pair + 1) * kPageTok + slot] = f32_to_bf16(vv.y);
 }
 
-__global__ __launch_bounds__(256) void kv_advance_kernel(int32_t* seq_lens, int batch, int tokens) {
+// Lengths advance by the appended tokens and saturate at the capacity: tokens
+// past it were not written (kv_append_kernel skips them), so they are not
+// counted either.
+__global__ __launch_bounds__(256) void kv_advance_kernel(int32_t* seq_lens, int batch, int tokens,
+                                                         int capacity) {
     const int b = blockIdx.x * 256 + threadIdx.x;
-    if (b < batch) seq_lens[b] += tokens;
+    if (b < batch) seq_lens[b] = min(seq_lens[b] + tokens, capacity);
 }
 
 // gather_paged_kv: pools -> keys / values [B][Hkv][length][128] fp32 (bf16 widened exactly).
@@ -997,13 +1005,15 @@ int launch_kv_append(const void* keys, const void* values, int src_dtype, int64_
                             static_cast<unsigned>(batch)), 64, 0, stream>>>(a);
     if (advance && seq_lens)
         kv_advance_kernel<<<dim3(static_cast<unsigned>((batch + 255) / 256)), 256, 0, stream>>>(
-            seq_lens, static_cast<int>(batch), static_cast<int>(tokens));
+            seq_lens, static_cast<int>(batch), static_cast<int>(tokens),
+            static_cast<int>(pages_per_seq * page_tokens));
     return SFG_OK;
 }
 
-void launch_kv_advance(int32_t* seq_lens, int64_t batch, int64_t tokens, hipStream_t stream) {
+void launch_kv_advance(int32_t* seq_lens, int64_t batch, int64_t tokens, int64_t capacity,
+                       hipStream_t stream) {
     kv_advance_kernel<<<dim3(static_cast<unsigned>((batch + 255) / 256)), 256, 0, stream>>>(
-        seq_lens, static_cast<int>(batch), static_cast<int>(tokens));
+        seq_lens, static_cast<int>(batch), static_cast<int>(tokens), static_cast<int>(capacity));
 }
 
 int launch_kv_gather(const uint16_t* k_pool, const uint16_t* v_pool, const int32_t* page_table,

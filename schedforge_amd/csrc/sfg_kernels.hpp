@@ -105,7 +105,8 @@ int launch_kv_append(const void* keys, const void* values, int src_dtype, int64_
                      int64_t batch, int64_t kv_heads, int64_t tokens, int64_t head_dim,
                      int64_t page_tokens, int64_t pages_per_seq, int64_t num_pages,
                      hipStream_t stream);
-void launch_kv_advance(int32_t* seq_lens, int64_t batch, int64_t tokens, hipStream_t stream);
+void launch_kv_advance(int32_t* seq_lens, int64_t batch, int64_t tokens, int64_t capacity,
+                       hipStream_t stream);
 int launch_kv_gather(const uint16_t* k_pool, const uint16_t* v_pool, const int32_t* page_table,
                      int64_t batch, int64_t kv_heads, int64_t length, int64_t head_dim,
                      int64_t page_tokens, int64_t pages_per_seq, int64_t num_pages, float* keys,

@@ -264,6 +264,8 @@ __global__ __launch_bounds__(1024) void moe_dispatch_kernel(
             route_slots[dst] = a % top_k;
             routing_weights[dst] = weights[a];
             position[a] = dst;
+        } else if (active) {
+            position[a] = -1;  // expert id out of range: the combine skips it
         }
         __syncthreads();
     }
@@ -363,8 +365,12 @@ __global__ __launch_bounds__(1024) void moe_dispatch_reg_kernel(
 #pragma unroll
     for (int c = 0; c < kDispChunks; ++c) {
         const int e = e_c[c];
-        if (c >= chunks || e < 0 || e >= experts) continue;
         const int a = c * 1024 + tid;
+        if (c >= chunks || a >= total) continue;
+        if (e < 0 || e >= experts) {
+            position[a] = -1;  // expert id out of range: the combine skips it
+            continue;
+        }
         const int dst = s_base[e] + s_chunk_off[c][e] + s_wave[c][wave][e] + rank_c[c];
         token_ids[dst] = a / top_k;
         route_slots[dst] = a % top_k;

@@ -65,7 +65,7 @@ class DecoderBenchmarkResult:
     residual_milliseconds: float = 0.0
     dispatch_overhead_milliseconds: float = 0.0
     tokens_per_second: float = 0.0
-    max_error: float = 0.0
+    max_error: float = float("nan")   # NaN unless expected outputs were given
     output: Any = None
     stages: dict = field(default_factory=dict)
 
@@ -304,7 +304,8 @@ def compile_decoder(config: DecoderConfig, data: DecoderData, device="cuda",
     ws = lib.sfg_hip_decoder_layer_workspace_v1(ctypes.byref(d))
     if ws == 0:
         check(_abi.ERR_INVALID_CONFIG)
-    # zero-filled once: split-K tile counters must start at zero
+    # zero-filled once so that a stage tap read before the first call is
+    # defined; every call writes each buffer before reading it
     plan.workspace = torch.zeros(ws, dtype=torch.uint8, device=plan.device)
     torch.cuda.synchronize(plan.device)
     return plan
@@ -377,11 +378,58 @@ def stage_times(ev: StageEvents) -> dict:
     }
 
 
+def layer_taps(plan: DecoderExecutablePlan) -> dict:
+    """The stage intermediates the last layer call left in the plan's workspace
+    (sfg_hip_decoder_layer_tap_v1), as host arrays: "attn" merged attention
+    [rows][H], "residual1" r1 [rows][H], "normalized2" [rows][H] (fp32 views of
+    bf16 values when the activations are bf16); for a MoE layer "route_input"
+    (the router's fp32 rows) and, routed on the device, "ids" / "weights"
+    [rows][k]."""
+    cfg = plan.config
+    torch.cuda.synchronize(plan.device)
+    shapes = {_abi.TAP_ATTN: ("attn", cfg.hidden), _abi.TAP_RESIDUAL1: ("residual1", cfg.hidden),
+              _abi.TAP_NORM2: ("normalized2", cfg.hidden)}
+    if cfg.moe:
+        shapes[_abi.TAP_ROUTE_INPUT] = ("route_input", cfg.hidden)
+    if cfg.moe and not plan.desc.use_routing_trace:
+        shapes[_abi.TAP_ROUTE_IDS] = ("ids", cfg.top_k)
+        shapes[_abi.TAP_ROUTE_WEIGHTS] = ("weights", cfg.top_k)
+    out = {}
+    for tap, (name, width) in shapes.items():
+        off, nbytes, dt = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_int()
+        check(plan.lib.sfg_hip_decoder_layer_tap_v1(ctypes.byref(plan.desc), tap, ctypes.byref(off),
+                                                    ctypes.byref(nbytes), ctypes.byref(dt)))
+        raw = plan.workspace[off.value:off.value + nbytes.value].cpu().numpy()
+        if dt.value == BF16:
+            a = (raw.view(np.uint16).astype(np.uint32) << 16).view(np.float32)
+        elif dt.value == _abi.I32:
+            a = raw.view(np.int32)
+        else:
+            a = raw.view(np.float32)
+        out[name] = a.reshape(cfg.rows, width)
+    return out
+
+
+def max_abs_error(output: np.ndarray, expected: np.ndarray) -> float:
+    """max_abs_error (runtime.cpp:628-635): the largest |float(a - b)| taken in
+    double; infinity on a size mismatch.  As there, std::max keeps the running
+    value when a difference is NaN, so NaNs are not reported here."""
+    a = np.asarray(output, np.float32).reshape(-1)
+    b = np.asarray(expected, np.float32).reshape(-1)
+    if a.size != b.size:
+        return float("inf")
+    d = np.abs((a - b).astype(np.float64))
+    d = d[~np.isnan(d)]
+    return float(d.max(initial=0.0))
+
+
 def execute_decoder_layer(plan: DecoderExecutablePlan, x, warmup: int = 1,
-                          repetitions: int = 5) -> DecoderBenchmarkResult:
+                          repetitions: int = 5, expected=None) -> DecoderBenchmarkResult:
     """execute_decoder_layer (decoder_compiler.cpp:675-692): warmup, timed
-    repetitions, median by time, tokens/s = rows * 1000 / ms.  The scalar
-    max_error validation of the reference is left to the caller's checker."""
+    repetitions, median by time, tokens/s = rows * 1000 / ms.  The reference
+    sets max_error against its scalar reference_decoder_layer (690); here the
+    caller passes the expected [rows][H] output (from any checker) and
+    max_error is max |output - expected|, or NaN when none is given."""
     cfg = plan.config
     xd = _dev(x, plan.device)
     out = torch.empty((cfg.rows, cfg.hidden), dtype=torch.float32, device=plan.device)
@@ -410,4 +458,6 @@ def execute_decoder_layer(plan: DecoderExecutablePlan, x, warmup: int = 1,
     r.tokens_per_second = cfg.rows * 1000.0 / r.milliseconds if r.milliseconds > 0 else 0.0
     r.output = out.cpu().numpy()
     r.stages = med
+    if expected is not None:
+        r.max_error = max_abs_error(r.output, expected)
     return r

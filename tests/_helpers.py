@@ -95,3 +95,78 @@ def tile_nk(w_nk, kind):
     nt = np.arange(n // 16)[:, None, None, None, None] * 16
     kc = np.arange(k // 128)[None, :, None, None, None] * 128
     return np.ascontiguousarray(w_nk[nt + rows[None, None], kc + kk[None, None]])
+
+
+# ---------------------------------------------------------------- layer checks
+def _rel(got, ref):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return float(np.max(np.abs(got - ref)) / max(float(np.max(np.abs(ref))), 1e-6))
+
+
+def branch_errors(x, out, taps, ref_out, ref_taps):
+    """Relative errors of the layer output and of each of its branches, each
+    against its own largest magnitude (max|got - ref| / max|ref|):
+      out          the layer output;
+      attn         the merged attention output (the attention kernel alone);
+      attn_branch  r1 - x, what the attention block adds to the residual stream;
+      ffn_branch   out - r1, what the FFN block adds.
+    With N(0, 0.02) weights the residual stream dominates the output, so the
+    whole-output error alone barely sees a broken attention; each branch is
+    checked on its own scale."""
+    x = np.asarray(x, np.float64)
+    r1, rr1 = np.asarray(taps["residual1"], np.float64), np.asarray(ref_taps["residual1"], np.float64)
+    return {"out": _rel(out, ref_out),
+            "attn": _rel(taps["attn"], ref_taps["attn_merged"]),
+            "attn_branch": _rel(r1 - x, rr1 - x),
+            "ffn_branch": _rel(np.asarray(out, np.float64) - r1, np.asarray(ref_out, np.float64) - rr1)}
+
+
+def assert_branches(x, out, taps, ref_out, ref_taps, tol, label=""):
+    err = branch_errors(x, out, taps, ref_out, ref_taps)
+    print(f"{label} " + " ".join(f"{k} {v:.3e}" for k, v in err.items()))
+    bad = {k: v for k, v in err.items() if not v < tol}
+    assert not bad, f"{label}: over tolerance {tol}: {bad}"
+    return err
+
+
+# Router logits are O(1) here (N(0, 0.02) router weights over H >= 2048
+# features, plus the bias); a token is a near tie when two adjacent logits among
+# its top k + 1 are closer than this.  The device's router input is checked to
+# be within a quarter of it, so only a near tie can flip its routing.
+ROUTE_TIE_EPS = 1e-2
+
+
+def route_logits(route_input, router, bias):
+    lg = np.asarray(route_input, np.float64) @ np.asarray(router, np.float64)
+    return lg + (0.0 if bias is None else np.asarray(bias, np.float64))
+
+
+def near_tie_rows(logits, top_k, eps=ROUTE_TIE_EPS):
+    """Rows whose top k + 1 sorted logits have an adjacent gap below eps: the
+    only rows whose top-k set or slot order can change under a perturbation of
+    the logits smaller than eps / 2."""
+    srt = -np.sort(-logits, axis=1)[:, :top_k + 1]
+    return np.nonzero(np.min(srt[:, :-1] - srt[:, 1:], axis=1) < eps)[0]
+
+
+def check_device_routing(dev_taps, ref_taps, router, bias, top_k, eps=ROUTE_TIE_EPS):
+    """Device routing against the oracle's: the device's router input is close
+    (logit deviation < eps / 4), every row whose ids differ from the oracle's
+    is a near tie of the oracle's logits, and rows that agree carry the same
+    weights.  Returns the rows that differ (the only rows the caller may
+    exempt from the output tolerance)."""
+    dev_logits = route_logits(dev_taps["route_input"], router, bias)
+    ref_logits = route_logits(ref_taps["normalized2"], router, bias)
+    dev_dev = float(np.max(np.abs(dev_logits - ref_logits)))
+    assert dev_dev < eps / 4, f"router input deviates: logit error {dev_dev:.3e}"
+    differ = np.nonzero(np.any(dev_taps["ids"] != ref_taps["ids"], axis=1))[0]
+    ties = near_tie_rows(ref_logits, top_k, eps)
+    assert set(differ.tolist()) <= set(ties.tolist()), (differ, ties)
+    # renormalised top-k weights move by at most half the logit deviation
+    same = np.setdiff1d(np.arange(len(ref_logits)), differ)
+    wdev = float(np.max(np.abs(dev_taps["weights"][same] - ref_taps["weights"][same]), initial=0.0))
+    assert wdev <= dev_dev / 2 + 1e-6, (wdev, dev_dev)
+    print(f"routing: logit deviation {dev_dev:.2e}, near ties (eps {eps}) {len(ties)}, "
+          f"rows routed differently {len(differ)}")
+    return differ

@@ -143,3 +143,38 @@ def test_rope_table_matches_reference_expressions(lib):
     np.testing.assert_allclose(t[..., 1], np.sin(ang.astype(np.float64)), atol=2e-7)
     np.testing.assert_array_equal(t[0, :, 0], 1.0)
     np.testing.assert_array_equal(t[0, :, 1], 0.0)
+
+
+def test_layer_taps_lie_inside_the_workspace(lib):
+    """sfg_hip_decoder_layer_tap_v1 (host-only query): every stage tap is a
+    distinct region inside the layer workspace, with its documented size and
+    dtype; routing taps exist only for a MoE layer routed on the device."""
+    def tap(d, t):
+        off, nb, dt = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_int()
+        rc = lib.sfg_hip_decoder_layer_tap_v1(ctypes.byref(d), t, ctypes.byref(off), ctypes.byref(nb),
+                                              ctypes.byref(dt))
+        return rc, off.value, nb.value, dt.value
+    for kw in (dict(), dict(context=0, sequence=64), dict(ffn=1), dict(ffn=1, use_routing_trace=1)):
+        d = _desc(**kw)
+        ws = lib.sfg_hip_decoder_layer_workspace_v1(ctypes.byref(d))
+        rows, H, k = d.batch * d.sequence, d.hidden, d.top_k
+        expect = {_abi.TAP_ATTN: (rows * H * 2, _abi.BF16), _abi.TAP_RESIDUAL1: (rows * H * 4, _abi.F32),
+                  _abi.TAP_NORM2: (rows * H * 2, _abi.BF16)}
+        if d.ffn == 1:
+            expect[_abi.TAP_ROUTE_INPUT] = (rows * H * 4, _abi.F32)
+        if d.ffn == 1 and not d.use_routing_trace:
+            expect[_abi.TAP_ROUTE_IDS] = (rows * k * 4, _abi.I32)
+            expect[_abi.TAP_ROUTE_WEIGHTS] = (rows * k * 4, _abi.F32)
+        spans = []
+        for t in range(_abi.NUM_TAPS):
+            rc, off, nb, dt = tap(d, t)
+            if t not in expect:
+                assert rc == _abi.ERR_UNSUPPORTED, (kw, t)
+                continue
+            assert rc == 0 and (nb, dt) == expect[t], (kw, t, nb, dt)
+            assert off % 256 == 0 and off + nb <= ws
+            spans.append((off, off + nb))
+        spans.sort()
+        assert all(a[1] <= b[0] for a, b in zip(spans, spans[1:])), spans
+    assert tap(_desc(), 99)[0] == _abi.ERR_SHAPE
+    assert tap(_desc(hidden=250), 0)[0] == _abi.ERR_INVALID_CONFIG

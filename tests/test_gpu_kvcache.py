@@ -124,3 +124,30 @@ def test_layer_append_mode_steps_match_oracle():
     assert (plan.t["seq_lens"].cpu().numpy() == ctx + 3).all()
     with pytest.raises(ValueError, match="capacity"):
         run_layer(plan, x, out)
+
+
+def test_append_at_capacity_writes_nothing_and_lengths_saturate():
+    """Device guard at the capacity boundary (the host mirror refuses the step,
+    as append_paged_kv does, next_milestones.cpp:498): a sequence already at
+    pages_per_seq * 16 tokens gets no K/V written and keeps its length; one
+    token short appends its last token and reaches the capacity."""
+    lib = _abi.load()
+    B, Hkv, D, PT, pps = 2, 2, 128, 16, 2
+    cap = pps * PT
+    pages = B * pps
+    table = np.arange(pages, dtype=np.int32).reshape(B, pps)
+    k_pool = torch.zeros((pages, Hkv, PT, D), dtype=torch.int16, device="cuda")
+    v_pool = torch.zeros((pages, Hkv, D, PT), dtype=torch.int16, device="cuda")
+    lens = dev(np.array([cap, cap - 1], np.int32))
+    keys = np.full((B, Hkv, 1, D), 3.0, np.float32)
+    _abi.check(lib.sfg_hip_kv_append_paged_v1(
+        dev(keys).data_ptr(), dev(keys + 1).data_ptr(), _abi.F32, k_pool.data_ptr(),
+        v_pool.data_ptr(), dev(table).data_ptr(), lens.data_ptr(), 0, 1, B, Hkv, 1, D, PT, pps,
+        pages, torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(lens.cpu().numpy(), [cap, cap])
+    kp = k_pool.cpu().numpy()
+    # sequence 0 (full): untouched; sequence 1: its last slot holds bf16(3.0) = 0x4040
+    assert not kp[table[0]].any()
+    assert (kp[table[1, 1], :, PT - 1].view(np.uint16) == 0x4040).all()
+    assert not kp[table[1, 1], :, :PT - 1].any() and not kp[table[1, 0]].any()

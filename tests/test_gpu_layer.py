@@ -1,9 +1,12 @@
 """Whole-layer parity: libsfg_hip.so's decoder layer vs the CPU oracle on
 identical seeded inputs (GPU only).
 
-C1 runs at its full BASELINE size; C2 at full size; C3/C4/C5 at reduced sizes
-with the same structure (SMALL in _helpers.py).  Tolerance: max|got - ref| /
-max|ref| below 1e-4 (fp32), 2e-2 (bf16), 1e-2 (int8 weights).
+C1 and C2 run at their full BASELINE sizes here (C3, C4 and C5 at full size in
+test_gpu_layer_full.py); reduced variants with the same structure (SMALL in
+_helpers.py) cover more seeds and paths.  Every layer check compares the output
+and, each on its own scale, the merged attention output and the two residual
+branches (branch_errors in _helpers.py).  Tolerance: max|got - ref| / max|ref|
+below 1e-4 (fp32), 2e-2 (bf16), 1e-2 (int8 weights).
 """
 from __future__ import annotations
 
@@ -13,14 +16,14 @@ import pytest
 import oracle
 from schedforge_amd import CONFIGS, CONFIG_SEEDS
 
-from _helpers import SMALL, TOL, decoder_data
+from _helpers import SMALL, TOL, assert_branches, check_device_routing, decoder_data
 
 pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
 
 
 def _run(cfg, seed, trace=False, reps=2):
-    from schedforge_amd.layer import compile_decoder, execute_decoder_layer
+    from schedforge_amd.layer import compile_decoder, execute_decoder_layer, layer_taps
     d = oracle.make_layer_data(cfg, seed)
     tr = None
     if trace:
@@ -29,27 +32,36 @@ def _run(cfg, seed, trace=False, reps=2):
         d.routing_trace = tr
     ref, taps = oracle.decoder_layer(cfg, d, taps=True, trace=tr)
     plan = compile_decoder(cfg, decoder_data(d), "cuda", page_permutation=d.page_permutation)
-    res = execute_decoder_layer(plan, d.input, warmup=1, repetitions=reps)
+    res = execute_decoder_layer(plan, d.input, warmup=1, repetitions=reps, expected=ref)
+    res.taps = layer_taps(plan)
+    res.x = d.input
+    res.data = d
     return res, ref, taps
+
+
+def _check(res, ref, taps, tol, label, rows=None):
+    if rows is None:
+        return assert_branches(res.x, res.output, res.taps, ref, taps, tol, label)
+    sel = lambda t: {k: v[rows] for k, v in t.items() if k != "counts"}
+    return assert_branches(res.x[rows], res.output[rows], sel(res.taps), ref[rows], sel(taps), tol,
+                           label)
 
 
 @pytest.mark.parametrize("name", ["c1", "c2"])
 def test_layer_full_size_matches_oracle(name):
     cfg = CONFIGS[name]
-    res, ref, _ = _run(cfg, CONFIG_SEEDS[name])
-    err = oracle.rel_error(res.output, ref)
-    print(f"{name}: {res.milliseconds:.4f} ms/layer, rel_err {err:.3e}")
+    res, ref, taps = _run(cfg, CONFIG_SEEDS[name])
+    print(f"{name}: {res.milliseconds:.4f} ms/layer, max_error {res.max_error:.3e}")
     assert np.isfinite(res.output).all()
-    assert err < TOL[cfg.dtype], err
+    assert res.max_error == pytest.approx(oracle.max_abs_error(res.output, ref), rel=0, abs=0)
+    _check(res, ref, taps, TOL[cfg.dtype], name)
 
 
 @pytest.mark.parametrize("name", ["c2", "c4"])
 def test_layer_reduced_dense_matches_oracle(name):
     cfg = SMALL[name]
-    res, ref, _ = _run(cfg, CONFIG_SEEDS[name] + 1)
-    err = oracle.rel_error(res.output, ref)
-    print(f"{name}-small: rel_err {err:.3e}")
-    assert err < TOL[cfg.dtype], err
+    res, ref, taps = _run(cfg, CONFIG_SEEDS[name] + 1)
+    _check(res, ref, taps, TOL[cfg.dtype], f"{name}-small")
 
 
 @pytest.mark.parametrize("name", ["c3", "c5"])
@@ -57,36 +69,31 @@ def test_layer_reduced_moe_with_routing_trace(name):
     """Routing fixed by the oracle's trace (decoder_compiler.cpp:281-284): every
     expert receives exactly the oracle's rows, so the tolerance applies to all."""
     cfg = SMALL[name]
-    res, ref, _ = _run(cfg, CONFIG_SEEDS[name] + 2, trace=True)
-    err = oracle.rel_error(res.output, ref)
-    print(f"{name}-small (trace): rel_err {err:.3e}")
-    assert err < TOL[cfg.dtype], err
+    res, ref, taps = _run(cfg, CONFIG_SEEDS[name] + 2, trace=True)
+    _check(res, ref, taps, TOL[cfg.dtype], f"{name}-small (trace)")
 
 
 @pytest.mark.parametrize("name", ["c3", "c5"])
 def test_layer_reduced_moe_device_routing(name):
-    """Routing on the device from the layer's own normalized activations.  A
-    token whose logits are a near-tie can legitimately pick another expert when
-    the GPU's residual stream differs in the last bits; such tokens (if any)
-    are reported and excluded, and must stay rare."""
+    """Routing on the device from the layer's own normalized activations.  The
+    device's router input must be within a quarter of the near-tie margin of
+    the oracle's; a token routed differently must be a near tie of the oracle's
+    logits (ROUTE_TIE_EPS in _helpers.py), and every other row meets the
+    tolerance on every branch."""
     cfg = SMALL[name]
     res, ref, taps = _run(cfg, CONFIG_SEEDS[name] + 3)
-    # recompute the device's choice from the oracle's normalized2: tokens
-    # whose top-k logit gap is tiny are the only ones allowed to differ
-    rows_err = np.max(np.abs(res.output - ref), axis=1) / max(np.max(np.abs(ref)), 1e-6)
-    bad = np.nonzero(rows_err >= TOL[cfg.dtype])[0]
-    print(f"{name}-small (device routing): max rel {rows_err.max():.3e}, rows over tol {len(bad)}")
-    assert len(bad) <= max(1, cfg.rows // 200), bad
+    differ = check_device_routing(res.taps, taps, res.data.router_weight, res.data.router_bias,
+                                  cfg.top_k)
+    same = np.setdiff1d(np.arange(cfg.rows), differ)
+    _check(res, ref, taps, TOL[cfg.dtype], f"{name}-small (device routing)", rows=same)
 
 
 def test_layer_reduced_w8_dense():
     """Weight-only int8 dense decode layer (execute_quantized_decoder_layer,
     next_milestones.cpp:339-385, 676-697) against the oracle's int8 path."""
     cfg = SMALL["c2"].replace(dtype="w8")
-    res, ref, _ = _run(cfg, CONFIG_SEEDS["c2"] + 5)
-    err = oracle.rel_error(res.output, ref)
-    print(f"c2-small w8 dense: rel_err {err:.3e}")
-    assert err < TOL["w8"], err
+    res, ref, taps = _run(cfg, CONFIG_SEEDS["c2"] + 5)
+    _check(res, ref, taps, TOL["w8"], "c2-small w8 dense")
 
 
 @pytest.mark.parametrize("batch,seq", [(2, 600), (1, 1024)])
@@ -96,11 +103,9 @@ def test_layer_prefill_fused_qkv_rope_matches_oracle(batch, seq):
     row stride rounds up to 640)."""
     cfg = CONFIGS["c4"].replace(batch=batch, sequence=seq, hidden=1024, intermediate=2048,
                                 query_heads=8, kv_heads=2)
-    res, ref, _ = _run(cfg, CONFIG_SEEDS["c4"] + 11 + seq, reps=1)
-    err = oracle.rel_error(res.output, ref)
-    print(f"fused-qkv prefill B{batch} S{seq}: rel_err {err:.3e}")
+    res, ref, taps = _run(cfg, CONFIG_SEEDS["c4"] + 11 + seq, reps=1)
     assert np.isfinite(res.output).all()
-    assert err < TOL[cfg.dtype], err
+    _check(res, ref, taps, TOL[cfg.dtype], f"fused-qkv prefill B{batch} S{seq}")
 
 
 @pytest.mark.parametrize("context", [512, 0])
@@ -112,10 +117,8 @@ def test_layer_head_dim_64_bf16_matches_oracle(context):
                                 kv_heads=2, head_dim=64, context_sequence=context)
     if context == 0:
         cfg = cfg.replace(batch=1, sequence=128)
-    res, ref, _ = _run(cfg, CONFIG_SEEDS["c2"] + 21)
-    err = oracle.rel_error(res.output, ref)
-    print(f"bf16 D64 context {context}: rel_err {err:.3e}")
-    assert err < TOL[cfg.dtype], err
+    res, ref, taps = _run(cfg, CONFIG_SEEDS["c2"] + 21)
+    _check(res, ref, taps, TOL[cfg.dtype], f"bf16 D64 context {context}")
 
 
 def _outputs_by_policy(cfg, seed, policies, trace=False):

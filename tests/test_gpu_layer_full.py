@@ -1,0 +1,135 @@
+"""Whole-layer parity at the full BASELINE sizes of C3, C4 and C5 (GPU only).
+
+The reference checks execute_once against reference_decoder_layer at any shape
+(decoder_compiler.cpp:622-673, tests/test_schedforge.cpp:822-900).  Here:
+  C3  MoE prefill, 2048 tokens: the whole oracle layer (a few seconds), once
+      with routing on the device (rows routed differently must be near ties of
+      the oracle's logits) and once under the oracle's own routing trace;
+  C4  Llama-3-8B-shaped prefill, S 8192: the GPU runs the whole layer; the
+      oracle runs sfgo_decoder_layer_rows (K / V of every row, the rest for a
+      sample of 272 query rows spread over the whole causal range, first and
+      last included), pinned bit-exact against the full oracle on the CPU;
+  C5  Mixtral-shaped int8 decode, 64 sequences over 8192 cached tokens: the
+      GPU runs all 64 rows; decode rows are independent (each attends over its
+      own cache and is routed alone), so the oracle runs a subset of eight
+      sequences, first and last included, under a skewed routing trace and
+      with routing on the device.
+Every check compares the output and, on their own scales, the attention
+output and both residual branches (tests/_helpers.py branch_errors).
+Tolerances: bf16 2e-2, int8 weights 1e-2 (max|got - ref| / max|ref|).
+"""
+from __future__ import annotations
+
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+
+import oracle
+from schedforge_amd import CONFIGS, CONFIG_SEEDS
+
+from _helpers import TOL, assert_branches, check_device_routing, decoder_data
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+
+def _rows(taps, rows):
+    return {k: v[rows] for k, v in taps.items() if k != "counts"}
+
+
+def _compile_and_run(cfg, d, trace=None):
+    from schedforge_amd.layer import compile_decoder, execute_decoder_layer, layer_taps
+    data = decoder_data(d)
+    data.routing_trace = trace
+    plan = compile_decoder(cfg, data, "cuda", page_permutation=d.page_permutation)
+    res = execute_decoder_layer(plan, d.input, warmup=1, repetitions=1)
+    assert np.isfinite(res.output).all()
+    return plan, res, layer_taps(plan)
+
+
+def _rerun(plan, x, trace):
+    """The same plan under a routing trace (ids, weights) or, with None, routed
+    on the device (decoder_compiler.cpp:281-284)."""
+    from schedforge_amd.layer import execute_decoder_layer, layer_taps
+    if trace is None:
+        plan.t.pop("trace_ids", None)
+        plan.t.pop("trace_weights", None)
+        plan.desc.use_routing_trace = 0
+    else:
+        plan.t["trace_ids"] = torch.from_numpy(np.ascontiguousarray(trace[0], np.int32)).cuda()
+        plan.t["trace_weights"] = torch.from_numpy(np.ascontiguousarray(trace[1], np.float32)).cuda()
+        plan.desc.use_routing_trace = 1
+    res = execute_decoder_layer(plan, x, warmup=0, repetitions=1)
+    return res, layer_taps(plan)
+
+
+def test_c3_full_size_matches_oracle():
+    cfg = CONFIGS["c3"]
+    d = oracle.make_layer_data(cfg, CONFIG_SEEDS["c3"])
+    ref, rt = oracle.decoder_layer(cfg, d, taps=True)
+    plan, res, taps = _compile_and_run(cfg, d)
+    print(f"c3 full: {res.milliseconds:.4f} ms/layer")
+    differ = check_device_routing(taps, rt, d.router_weight, d.router_bias, cfg.top_k)
+    same = np.setdiff1d(np.arange(cfg.rows), differ)
+    assert_branches(d.input[same], res.output[same], _rows(taps, same), ref[same], _rows(rt, same),
+                    TOL["bf16"], "c3 full, device routing (rows routed alike)")
+    # the oracle's own routing as a trace: every row within tolerance
+    res2, taps2 = _rerun(plan, d.input, (rt["ids"], rt["weights"]))
+    assert_branches(d.input, res2.output, taps2, ref, rt, TOL["bf16"], "c3 full, routing trace")
+
+
+def test_c4_full_size_matches_row_sampled_oracle():
+    cfg = CONFIGS["c4"]
+    d = oracle.make_layer_data(cfg, CONFIG_SEEDS["c4"])
+    plan, res, taps = _compile_and_run(cfg, d)
+    print(f"c4 full: {res.milliseconds:.4f} ms/layer")
+    S = cfg.sequence
+    edges = [0, 1, 2, 31, 32, 63, 64, 127, 128, 255, 256, 1023, 1024, 4095, 4096, S - 129, S - 128,
+             S - 65, S - 64, S - 2, S - 1]
+    rng = np.random.default_rng(CONFIG_SEEDS["c4"])
+    sample = np.unique(np.r_[edges, rng.choice(S, 256, replace=False)])
+    del plan
+    torch.cuda.empty_cache()
+    ref, rt = oracle.decoder_layer_rows(cfg, d, sample, taps=True)
+    assert_branches(d.input[sample], res.output[sample], _rows(taps, sample), ref, rt, TOL["bf16"],
+                    f"c4 full, {sample.size} sampled rows")
+
+
+def _skewed_trace(rows, experts, top_k, seed):
+    """k distinct experts per token drawn with probability (e + 1)^-0.8 (the
+    reference's moderate profile, moe_compiler.cpp:457-488) and random
+    renormalised weights."""
+    rng = np.random.default_rng(seed)
+    p = (np.arange(experts) + 1.0) ** -0.8
+    p /= p.sum()
+    ids = np.stack([rng.choice(experts, top_k, replace=False, p=p) for _ in range(rows)])
+    w = rng.random((rows, top_k)) + 0.1
+    return ids.astype(np.int32), (w / w.sum(1, keepdims=True)).astype(np.float32)
+
+
+def test_c5_full_size_matches_oracle_on_a_sequence_subset():
+    cfg = CONFIGS["c5"]
+    d = oracle.make_layer_data(cfg, CONFIG_SEEDS["c5"], lazy_experts=True)
+    trace = _skewed_trace(cfg.rows, cfg.experts, cfg.top_k, CONFIG_SEEDS["c5"])
+    plan, res, taps = _compile_and_run(cfg, d, trace)
+    print(f"c5 full: {res.milliseconds:.4f} ms/layer")
+    res2, taps2 = _rerun(plan, d.input, None)
+    del plan
+    torch.cuda.empty_cache()
+    sub = np.array([0, 9, 18, 27, 36, 45, 54, 63])
+    ds = SimpleNamespace(**vars(d))
+    ds.input = d.input[sub]
+    ds.cached_key, ds.cached_value = d.cached_key[sub], d.cached_value[sub]
+    d.cached_key = d.cached_value = None
+    cs = cfg.replace(batch=sub.size)
+    quant = oracle.quantize_layer(cfg, d)
+    ref, rt = oracle.decoder_layer(cs, ds, quant=quant, taps=True, trace=(trace[0][sub], trace[1][sub]))
+    assert_branches(ds.input, res.output[sub], _rows(taps, sub), ref, rt, TOL["w8"],
+                    "c5 full, routing trace, 8 sequences")
+    ref2, rt2 = oracle.decoder_layer(cs, ds, quant=quant, taps=True)
+    t2 = _rows(taps2, sub)
+    differ = check_device_routing(t2, rt2, d.router_weight, d.router_bias, cfg.top_k)
+    same = np.setdiff1d(np.arange(sub.size), differ)
+    assert_branches(ds.input[same], res2.output[sub][same], _rows(t2, same), ref2[same],
+                    _rows(rt2, same), TOL["w8"], "c5 full, device routing")

@@ -473,6 +473,40 @@ def test_attention_prefill_vt_equal_keys_is_prefix_mean(lib):
         assert np.max(np.abs(got[:, h] - prefix)) < 2e-2
 
 
+def test_attention_prefill_vt_s8192_matches_oracle_rows(lib):
+    """C4's sequence length (8192) with few heads: the flash kernel over the
+    whole causal range, checked on the first, a middle and the last 256 query
+    rows.  Causal alignment (j <= Skv - Sq + i, attention_compiler.cpp:68-72)
+    lets the oracle run a row block against exactly the key prefix it sees."""
+    B, Hq, Hkv, S, D = 1, 4, 1, 8192, 128
+    q = oracle.round_bf16(oracle.normal(86, 0, (B, Hq, S, D)))
+    k = oracle.round_bf16(oracle.normal(86, 1, (B, Hkv, S, D)))
+    v = oracle.round_bf16(oracle.normal(86, 2, (B, Hkv, S, D)))
+    got = _prefill_vt(lib, q, k, v, True).reshape(S, Hq, D)
+    assert np.isfinite(got).all()
+    for r0 in (0, 4000, S - 256):
+        r1 = r0 + 256
+        ref = oracle.attention(q[:, :, r0:r1], k[:, :, :r1], v[:, :, :r1], True)[0].transpose(1, 0, 2)
+        err = oracle.rel_error(got[r0:r1], ref)
+        print(f"S8192 rows [{r0}, {r1}): rel_err {err:.3e}")
+        assert err < 2e-2
+
+
+def test_attention_prefill_vt_s8192_equal_keys_is_prefix_mean(lib):
+    """Closed form at S 8192: equal keys give every allowed key probability
+    exactly 1 before normalisation, so row i is the mean of V[0..i]."""
+    B, Hq, Hkv, S, D = 1, 2, 1, 8192, 128
+    q = oracle.round_bf16(oracle.normal(87, 0, (B, Hq, S, D)))
+    k = np.broadcast_to(oracle.round_bf16(oracle.normal(87, 1, (D,))), (B, Hkv, S, D)).copy()
+    v = oracle.round_bf16(oracle.normal(87, 2, (B, Hkv, S, D)))
+    got = _prefill_vt(lib, q, k, v, True).reshape(S, Hq, D)
+    prefix = np.cumsum(v[0, 0].astype(np.float64), axis=0) / np.arange(1, S + 1)[:, None]
+    for h in range(Hq):
+        err = np.max(np.abs(got[:, h] - prefix))
+        print(f"S8192 equal keys head {h}: max abs err {err:.2e}")
+        assert err < 1e-3
+
+
 def test_split_rope_vt_matches_split_rope(lib):
     """split_qkv + RoPE writing V^T: q and k bit-equal to the plain split, vt
     the exact transpose of its v with zero key padding."""
@@ -655,6 +689,50 @@ def test_moe_route_ties_go_to_lower_expert(lib):
             assert 2 in chosen
         if 7 in chosen:
             assert 2 in chosen and 5 in chosen
+
+
+@pytest.mark.parametrize("T,E", [(300, 8), (300, 32)])   # register and chunked dispatch
+def test_moe_dispatch_trace_skips_out_of_range_experts(lib, T, E):
+    """A caller-supplied routing trace with expert ids outside [0, E) (the
+    reference refuses them, next_milestones.cpp:427-428): such an assignment is
+    left out of the histogram and the segments, its position is -1, and the
+    combine adds nothing for it (the token keeps its other slots)."""
+    k, H = 2, 256
+    rng = np.random.default_rng(7)
+    ids = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
+    ids[5, 0], ids[77, 1], ids[299, 0] = E, -1, E + 100
+    w = rng.random((T, k)).astype(np.float32)
+    counts = torch.empty(E, dtype=torch.int32, device="cuda")
+    offsets = torch.empty(E + 1, dtype=torch.int32, device="cuda")
+    tok = torch.full((T * k,), -7, dtype=torch.int32, device="cuda")
+    slots = torch.empty(T * k, dtype=torch.int32, device="cuda")
+    rw = torch.empty(T * k, dtype=torch.float32, device="cuda")
+    pos = torch.full((T * k,), 12345, dtype=torch.int32, device="cuda")  # stale contents
+    _abi.check(lib.sfg_hip_moe_dispatch_trace_v1(dev(ids).data_ptr(), dev(w).data_ptr(), T, E, k,
+                                                 counts.data_ptr(), offsets.data_ptr(),
+                                                 tok.data_ptr(), slots.data_ptr(), rw.data_ptr(),
+                                                 pos.data_ptr(), stream()))
+    _sync()
+    valid = (ids >= 0) & (ids < E)
+    np.testing.assert_array_equal(host(counts), np.bincount(ids[valid], minlength=E))
+    p = host(pos).reshape(T, k)
+    assert p[5, 0] == -1 and p[77, 1] == -1 and p[299, 0] == -1
+    n_valid = int(valid.sum())
+    assert host(offsets)[E] == n_valid
+    np.testing.assert_array_equal(np.sort(p[valid]), np.arange(n_valid))
+    y = oracle.normal(112, 0, (T * k, H))
+    resid = oracle.normal(112, 5, (T, H))
+    out = torch.empty((T, H), dtype=torch.float32, device="cuda")
+    _abi.check(lib.sfg_hip_moe_combine_v1(dev(y).data_ptr(), pos.data_ptr(), dev(w).data_ptr(),
+                                          dev(resid).data_ptr(), out.data_ptr(), T, H, k, stream()))
+    _sync()
+    ref = resid.copy()
+    for t in range(T):
+        for s in range(k):
+            if valid[t, s]:
+                ref[t] = np.float32(ref[t] + w[t, s] * y[p[t, s]])
+    assert oracle.rel_error(host(out), ref) < 1e-6
+    np.testing.assert_allclose(host(out)[5] - resid[5], w[5, 1] * y[p[5, 1]], rtol=1e-5, atol=1e-6)
 
 
 # ------------------------------------------------------------------ MoE experts + combine
