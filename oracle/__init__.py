@@ -109,17 +109,6 @@ def normal(seed: int, tensor: str | int, shape, std: float = 1.0, mean: float = 
     return out
 
 
-def normal_at(seed: int, tensor: str | int, shape, offset: int, std: float = 1.0,
-              mean: float = 0.0) -> np.ndarray:
-    """Elements [offset, offset + prod(shape)) of the tensor normal() draws:
-    normal(seed, t, (E, *shape))[e] == normal_at(seed, t, shape, e * prod(shape))."""
-    tid = TID[tensor] if isinstance(tensor, str) else int(tensor)
-    out = np.empty(shape, dtype=np.float32)
-    lib().sfgo_fill_normal_at(ctypes.c_uint64(seed), ctypes.c_uint32(tid), ctypes.c_float(mean),
-                              ctypes.c_float(std), _f(out), i64(offset), i64(out.size))
-    return out
-
-
 def page_permutation(seed: int, count: int) -> np.ndarray:
     out = np.empty(count, dtype=np.int32)
     lib().sfgo_page_permutation(ctypes.c_uint64(seed), _i(out), i64(count))

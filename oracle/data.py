@@ -5,9 +5,7 @@ make_layer_data(cfg, seed) draws every tensor from the counter-based generator
 cached K/V N(0,1), router bias N(0, cfg.router_bias_std) when that is > 0.
 bf16 configs round activations, weights and the KV cache to bf16 (RNE);
 w8 configs round activations and the KV cache, and quantize projection and
-expert weights per output channel (quantize_layer).  lazy_experts=True leaves
-the expert weights as ExpertWeights (drawn one expert at a time on access) so a
-full-size MoE layer never holds every fp32 expert in host memory.
+expert weights per output channel (quantize_layer).
 """
 from __future__ import annotations
 
@@ -16,34 +14,13 @@ from types import SimpleNamespace
 
 import numpy as np
 
-from . import (LayerCfg, LayerData, LayerTaps, _b, _f, _i, lib, normal, normal_at,
-               page_permutation, quantize_kn, round_bf16)
+from . import (LayerCfg, LayerData, LayerTaps, _b, _f, _i, lib, normal, page_permutation,
+               quantize_kn, round_bf16)
 
 WEIGHT_STD = 0.02
 
 
-class ExpertWeights:
-    """An [E, K, N] expert weight drawn one expert at a time: w[e] generates
-    expert e's [K][N] slice of normal(seed, tensor, (E, K, N), std) (bf16-rounded
-    when asked), so only one expert is ever held in host memory."""
-
-    def __init__(self, seed, tensor, experts, k, n, std, bf16):
-        self.seed, self.tensor, self.shape = seed, tensor, (experts, k, n)
-        self.std, self.bf16 = std, bf16
-
-    def __len__(self):
-        return self.shape[0]
-
-    def __getitem__(self, e):
-        _, k, n = self.shape
-        w = normal_at(self.seed, self.tensor, (k, n), int(e) * k * n, self.std)
-        return round_bf16(w) if self.bf16 else w
-
-    def __call__(self, e):
-        return self[e]
-
-
-def make_layer_data(cfg, seed: int, lazy_experts: bool = False) -> SimpleNamespace:
+def make_layer_data(cfg, seed: int) -> SimpleNamespace:
     H, I, D = cfg.hidden, cfg.intermediate, cfg.head_dim
     kvd = cfg.kv_heads * D
     rows = cfg.batch * cfg.sequence
@@ -62,15 +39,9 @@ def make_layer_data(cfg, seed: int, lazy_experts: bool = False) -> SimpleNamespa
         d.router_weight = normal(seed, "router", (H, E), WEIGHT_STD)
         if getattr(cfg, "router_bias_std", 0.0) > 0.0:
             d.router_bias = normal(seed, "router_bias", (E,), cfg.router_bias_std)
-        if lazy_experts:
-            bf = cfg.dtype == "bf16"
-            d.w1 = ExpertWeights(seed, "w1", E, H, I, WEIGHT_STD, bf)
-            d.w3 = ExpertWeights(seed, "w3", E, H, I, WEIGHT_STD, bf)
-            d.w2 = ExpertWeights(seed, "w2", E, I, H, WEIGHT_STD, bf)
-        else:
-            d.w1 = normal(seed, "w1", (E, H, I), WEIGHT_STD)
-            d.w3 = normal(seed, "w3", (E, H, I), WEIGHT_STD)
-            d.w2 = normal(seed, "w2", (E, I, H), WEIGHT_STD)
+        d.w1 = normal(seed, "w1", (E, H, I), WEIGHT_STD)
+        d.w3 = normal(seed, "w3", (E, H, I), WEIGHT_STD)
+        d.w2 = normal(seed, "w2", (E, I, H), WEIGHT_STD)
     else:
         d.gate_weight = normal(seed, "wg", (H, I), WEIGHT_STD)
         d.up_weight = normal(seed, "wu", (H, I), WEIGHT_STD)
@@ -93,7 +64,7 @@ def make_layer_data(cfg, seed: int, lazy_experts: bool = False) -> SimpleNamespa
         for name in ("query_weight", "key_weight", "value_weight", "output_weight", "gate_weight",
                      "up_weight", "down_weight", "router_weight", "w1", "w3", "w2"):
             v = getattr(d, name)
-            if v is not None and not isinstance(v, ExpertWeights):
+            if v is not None:
                 setattr(d, name, round_bf16(v))
     return d
 
@@ -141,8 +112,7 @@ def _layer_structs(cfg, d, quant, threads, trace):
     ld.wg, ld.wu, ld.wd = F(d.gate_weight), F(d.up_weight), F(d.down_weight)
     ld.router, ld.router_bias = F(d.router_weight), F(d.router_bias)
     if cfg.dtype != "w8":
-        ld.w1, ld.w3, ld.w2 = (F(np.stack([w[e] for e in range(len(w))]) if isinstance(w, ExpertWeights)
-                                 else w) for w in (d.w1, d.w3, d.w2))
+        ld.w1, ld.w3, ld.w2 = F(d.w1), F(d.w3), F(d.w2)
     ld.cached_k, ld.cached_v = F(d.cached_key), F(d.cached_value)
     if trace is not None:
         ids = np.ascontiguousarray(trace[0], np.int32)

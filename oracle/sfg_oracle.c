@@ -53,24 +53,16 @@ static uint64_t stream_key(uint64_t seed, uint32_t tensor_id) {
  * 53-bit uniforms drawn from the counter stream at 2i and 2i+1. */
 void sfgo_fill_normal(uint64_t seed, uint32_t tensor_id, float mean, float stddev,
                       float* out, int64_t count) {
-    sfgo_fill_normal_at(seed, tensor_id, mean, stddev, out, 0, count);
-}
-
-/* Elements [offset, offset + count) of the same tensor (one expert's slice of an
- * [E, ...] weight, drawn without materialising the others). */
-void sfgo_fill_normal_at(uint64_t seed, uint32_t tensor_id, float mean, float stddev,
-                         float* out, int64_t offset, int64_t count) {
     const uint64_t key = stream_key(seed, tensor_id);
     const double two_pi = 6.283185307179586476925286766559;
 #pragma omp parallel for schedule(static)
-    for (int64_t n = 0; n < count; ++n) {
-        const uint64_t i = (uint64_t)(offset + n);
-        const uint64_t r1 = sfgo_splitmix64(key + 2 * i);
-        const uint64_t r2 = sfgo_splitmix64(key + 2 * i + 1);
+    for (int64_t i = 0; i < count; ++i) {
+        const uint64_t r1 = sfgo_splitmix64(key + 2 * (uint64_t)i);
+        const uint64_t r2 = sfgo_splitmix64(key + 2 * (uint64_t)i + 1);
         const double u1 = ((double)(r1 >> 11) + 1.0) * (1.0 / 9007199254740992.0);
         const double u2 = (double)(r2 >> 11) * (1.0 / 9007199254740992.0);
         const double z = sqrt(-2.0 * log(u1)) * cos(two_pi * u2);
-        out[n] = (float)((double)mean + (double)stddev * z);
+        out[i] = (float)((double)mean + (double)stddev * z);
     }
 }
 

@@ -32,8 +32,6 @@ extern "C" {
 uint64_t sfgo_splitmix64(uint64_t x);
 void sfgo_fill_normal(uint64_t seed, uint32_t tensor_id, float mean, float stddev,
                       float* out, int64_t count);
-void sfgo_fill_normal_at(uint64_t seed, uint32_t tensor_id, float mean, float stddev,
-                         float* out, int64_t offset, int64_t count);
 void sfgo_page_permutation(uint64_t seed, int32_t* perm, int64_t count);
 
 /* ---- bf16 (compiler.cpp:34-52) ---- */

@@ -131,10 +131,11 @@ def assert_branches(x, out, taps, ref_out, ref_taps, tol, label=""):
 
 
 # Router logits are O(1) here (N(0, 0.02) router weights over H >= 2048
-# features, plus the bias); a token is a near tie when two adjacent logits among
-# its top k + 1 are closer than this.  The device's router input is checked to
-# be within a quarter of it, so only a near tie can flip its routing.
-ROUTE_TIE_EPS = 1e-2
+# features, plus the bias).  The device's router input (its fp32 RMSNorm rows)
+# may move the logits by at most this much against the oracle's; measured
+# deviations are 1e-4 (decode) to 5e-3 (C3 prefill, whose attention branch
+# carries bf16 rounding into the residual stream).
+ROUTE_LOGIT_DEV_MAX = 1e-2
 
 
 def route_logits(route_input, router, bias):
@@ -142,31 +143,35 @@ def route_logits(route_input, router, bias):
     return lg + (0.0 if bias is None else np.asarray(bias, np.float64))
 
 
-def near_tie_rows(logits, top_k, eps=ROUTE_TIE_EPS):
-    """Rows whose top k + 1 sorted logits have an adjacent gap below eps: the
-    only rows whose top-k set or slot order can change under a perturbation of
-    the logits smaller than eps / 2."""
+def near_tie_rows(logits, top_k, gap):
+    """Rows whose top k + 1 sorted logits have an adjacent gap below `gap`: the
+    only rows whose top-k set or slot order can change when every logit moves by
+    less than gap / 2."""
     srt = -np.sort(-logits, axis=1)[:, :top_k + 1]
-    return np.nonzero(np.min(srt[:, :-1] - srt[:, 1:], axis=1) < eps)[0]
+    return np.nonzero(np.min(srt[:, :-1] - srt[:, 1:], axis=1) < gap)[0]
 
 
-def check_device_routing(dev_taps, ref_taps, router, bias, top_k, eps=ROUTE_TIE_EPS):
-    """Device routing against the oracle's: the device's router input is close
-    (logit deviation < eps / 4), every row whose ids differ from the oracle's
-    is a near tie of the oracle's logits, and rows that agree carry the same
-    weights.  Returns the rows that differ (the only rows the caller may
-    exempt from the output tolerance)."""
+def check_device_routing(dev_taps, ref_taps, router, bias, top_k):
+    """Device routing against the oracle's.  With delta the largest logit
+    deviation between the two router inputs (asserted below
+    ROUTE_LOGIT_DEV_MAX), two experts can swap order only if the oracle's logits
+    are closer than 2 delta: every row whose ids differ must be such a near tie,
+    and rows that agree carry the same weights to within delta / 2.  Returns
+    the rows that differ (the only rows the caller may exempt from the output
+    tolerance)."""
     dev_logits = route_logits(dev_taps["route_input"], router, bias)
     ref_logits = route_logits(ref_taps["normalized2"], router, bias)
-    dev_dev = float(np.max(np.abs(dev_logits - ref_logits)))
-    assert dev_dev < eps / 4, f"router input deviates: logit error {dev_dev:.3e}"
+    delta = float(np.max(np.abs(dev_logits - ref_logits)))
+    assert delta < ROUTE_LOGIT_DEV_MAX, f"router input deviates: logit error {delta:.3e}"
+    # slack for the device's own fp32 logit chains against this fp64 product
+    margin = 2 * delta + 1e-5
     differ = np.nonzero(np.any(dev_taps["ids"] != ref_taps["ids"], axis=1))[0]
-    ties = near_tie_rows(ref_logits, top_k, eps)
+    ties = near_tie_rows(ref_logits, top_k, margin)
     assert set(differ.tolist()) <= set(ties.tolist()), (differ, ties)
     # renormalised top-k weights move by at most half the logit deviation
     same = np.setdiff1d(np.arange(len(ref_logits)), differ)
     wdev = float(np.max(np.abs(dev_taps["weights"][same] - ref_taps["weights"][same]), initial=0.0))
-    assert wdev <= dev_dev / 2 + 1e-6, (wdev, dev_dev)
-    print(f"routing: logit deviation {dev_dev:.2e}, near ties (eps {eps}) {len(ties)}, "
+    assert wdev <= delta / 2 + 1e-6, (wdev, delta)
+    print(f"routing: logit deviation {delta:.2e}, near ties (gap < {margin:.2e}) {len(ties)}, "
           f"rows routed differently {len(differ)}")
     return differ

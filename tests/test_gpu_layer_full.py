@@ -9,18 +9,13 @@ The reference checks execute_once against reference_decoder_layer at any shape
       oracle runs sfgo_decoder_layer_rows (K / V of every row, the rest for a
       sample of 272 query rows spread over the whole causal range, first and
       last included), pinned bit-exact against the full oracle on the CPU;
-  C5  Mixtral-shaped int8 decode, 64 sequences over 8192 cached tokens: the
-      GPU runs all 64 rows; decode rows are independent (each attends over its
-      own cache and is routed alone), so the oracle runs a subset of eight
-      sequences, first and last included, under a skewed routing trace and
-      with routing on the device.
+  C5  Mixtral-shaped int8 decode, 64 sequences over 8192 cached tokens, every
+      row on both sides, routed on the device and under the oracle's trace.
 Every check compares the output and, on their own scales, the attention
 output and both residual branches (tests/_helpers.py branch_errors).
 Tolerances: bf16 2e-2, int8 weights 1e-2 (max|got - ref| / max|ref|).
 """
 from __future__ import annotations
-
-from types import SimpleNamespace
 
 import numpy as np
 import pytest
@@ -96,40 +91,19 @@ def test_c4_full_size_matches_row_sampled_oracle():
                     f"c4 full, {sample.size} sampled rows")
 
 
-def _skewed_trace(rows, experts, top_k, seed):
-    """k distinct experts per token drawn with probability (e + 1)^-0.8 (the
-    reference's moderate profile, moe_compiler.cpp:457-488) and random
-    renormalised weights."""
-    rng = np.random.default_rng(seed)
-    p = (np.arange(experts) + 1.0) ** -0.8
-    p /= p.sum()
-    ids = np.stack([rng.choice(experts, top_k, replace=False, p=p) for _ in range(rows)])
-    w = rng.random((rows, top_k)) + 0.1
-    return ids.astype(np.int32), (w / w.sum(1, keepdims=True)).astype(np.float32)
-
-
-def test_c5_full_size_matches_oracle_on_a_sequence_subset():
+def test_c5_full_size_matches_oracle():
+    """All 64 decode rows on both sides: routed on the device, then under the
+    oracle's own routing as a trace."""
     cfg = CONFIGS["c5"]
-    d = oracle.make_layer_data(cfg, CONFIG_SEEDS["c5"], lazy_experts=True)
-    trace = _skewed_trace(cfg.rows, cfg.experts, cfg.top_k, CONFIG_SEEDS["c5"])
-    plan, res, taps = _compile_and_run(cfg, d, trace)
+    d = oracle.make_layer_data(cfg, CONFIG_SEEDS["c5"])
+    plan, res, taps = _compile_and_run(cfg, d)
     print(f"c5 full: {res.milliseconds:.4f} ms/layer")
-    res2, taps2 = _rerun(plan, d.input, None)
-    del plan
-    torch.cuda.empty_cache()
-    sub = np.array([0, 9, 18, 27, 36, 45, 54, 63])
-    ds = SimpleNamespace(**vars(d))
-    ds.input = d.input[sub]
-    ds.cached_key, ds.cached_value = d.cached_key[sub], d.cached_value[sub]
-    d.cached_key = d.cached_value = None
-    cs = cfg.replace(batch=sub.size)
     quant = oracle.quantize_layer(cfg, d)
-    ref, rt = oracle.decoder_layer(cs, ds, quant=quant, taps=True, trace=(trace[0][sub], trace[1][sub]))
-    assert_branches(ds.input, res.output[sub], _rows(taps, sub), ref, rt, TOL["w8"],
-                    "c5 full, routing trace, 8 sequences")
-    ref2, rt2 = oracle.decoder_layer(cs, ds, quant=quant, taps=True)
-    t2 = _rows(taps2, sub)
-    differ = check_device_routing(t2, rt2, d.router_weight, d.router_bias, cfg.top_k)
-    same = np.setdiff1d(np.arange(sub.size), differ)
-    assert_branches(ds.input[same], res2.output[sub][same], _rows(t2, same), ref2[same],
-                    _rows(rt2, same), TOL["w8"], "c5 full, device routing")
+    d.w1 = d.w3 = d.w2 = None
+    ref, rt = oracle.decoder_layer(cfg, d, quant=quant, taps=True)
+    differ = check_device_routing(taps, rt, d.router_weight, d.router_bias, cfg.top_k)
+    same = np.setdiff1d(np.arange(cfg.rows), differ)
+    assert_branches(d.input[same], res.output[same], _rows(taps, same), ref[same], _rows(rt, same),
+                    TOL["w8"], "c5 full, device routing (rows routed alike)")
+    res2, taps2 = _rerun(plan, d.input, (rt["ids"], rt["weights"]))
+    assert_branches(d.input, res2.output, taps2, ref, rt, TOL["w8"], "c5 full, routing trace")

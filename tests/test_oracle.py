@@ -31,7 +31,6 @@ known-answer tests, and an independent float64 formulation of the whole layer.
   sfgo_decoder_layer_rows  bit-exact against the sampled rows (and taps) of
                            sfgo_decoder_layer: dense bf16, MoE with bias and
                            with a trace, int8 dense, two sequences
-  sfgo_fill_normal_at      equals the matching slice of sfgo_fill_normal
   generators               determinism, moments, permutation property
 """
 from __future__ import annotations
@@ -438,33 +437,6 @@ def test_row_sampled_layer_equals_full_layer_rows(name, overrides, trace):
     if cfg.ffn == "moe":
         np.testing.assert_array_equal(gt["ids"], taps["ids"][sample])
         np.testing.assert_array_equal(gt["weights"], taps["weights"][sample])
-
-
-def test_fill_normal_at_is_a_slice_of_the_full_draw():
-    full = oracle.normal(77, "w1", (3, 40, 24), 0.02)
-    for e in range(3):
-        np.testing.assert_array_equal(oracle.normal_at(77, "w1", (40, 24), e * 40 * 24, 0.02), full[e])
-    cfg = CONFIGS["c3"].replace(batch=1, sequence=8, hidden=128, intermediate=64, query_heads=2,
-                                kv_heads=1, head_dim=64)
-    eager = oracle.make_layer_data(cfg, 3)
-    lazy = oracle.make_layer_data(cfg, 3, lazy_experts=True)
-    for name in ("w1", "w3", "w2"):
-        for e in range(cfg.experts):
-            np.testing.assert_array_equal(getattr(lazy, name)[e], getattr(eager, name)[e])
-    np.testing.assert_array_equal(oracle.decoder_layer(cfg, lazy), oracle.decoder_layer(cfg, eager))
-
-
-def test_max_abs_error_follows_std_max():
-    """runtime.cpp:628-635: float difference, abs in double, std::max fold (a
-    NaN difference is skipped); the host mirror's max_abs_error agrees."""
-    from schedforge_amd.layer import max_abs_error
-    a = np.array([1.0, 2.0, np.nan, 4.0, 1e8], np.float32)
-    b = np.array([1.5, 2.0, 0.0, 1.0, 1e8 + 4], np.float32)
-    assert oracle.max_abs_error(a, b) == 3.0
-    assert max_abs_error(a, b) == 3.0
-    x = np.float32(1.0) + np.float32(2 ** -23)
-    assert oracle.max_abs_error(np.array([x]), np.array([1.0], np.float32)) == 2.0 ** -23
-    assert max_abs_error(np.zeros(3), np.zeros(4)) == float("inf")
 
 
 # ------------------------------------------------------------------ generators
