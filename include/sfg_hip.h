@@ -208,6 +208,30 @@ int sfg_hip_attn_decode_paged_v1(const float* q, const uint16_t* k_pool,
                                  float scale, int validate_pages, void* workspace,
                                  size_t workspace_bytes, void* stream);
 
+/* The same paged Split-KV decode with no workspace argument and no allocation.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory or pass a workspace (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  The split partials live in
+ * a library-held device array of SFG_DECODE_SCRATCH_BYTES (16 MiB) per device,
+ * resident from the first call on a device until the process ends; a call
+ * whose partials, batch * q_heads * splits * (head_dim + 2) * 4 bytes (each
+ * part rounded up to 256), exceed it returns SFG_ERR_WORKSPACE.  Every call on
+ * one device shares that device's array: calls that overlap on one GPU (other
+ * streams, other host threads) race and must be serialised by the caller.
+ * Nothing in the array needs clearing: each call writes every partial before
+ * reading it.  Page ids outside [0, num_pages) are skipped on the device (no
+ * host-side table validation: it would synchronise the stream).  Results are
+ * bit-identical to sfg_hip_attn_decode_paged_v1 with the same split count. */
+#define SFG_DECODE_SCRATCH_BYTES ((size_t)16 << 20)
+int sfg_hip_attn_decode_paged_noalloc_v1(const float* q, const uint16_t* k_pool,
+                                         const uint16_t* v_pool, const int32_t* page_table,
+                                         const int32_t* seq_lens, void* out, int out_dtype,
+                                         int64_t batch, int64_t q_heads, int64_t kv_heads,
+                                         int64_t head_dim, int64_t page_tokens,
+                                         int64_t pages_per_seq, int64_t num_pages,
+                                         int64_t max_context, int32_t kv_splits, float scale,
+                                         void* stream);
+
 /* append_paged_kv (next_milestones.cpp:486-524) on the device pools: keys / values
  * [B][Hkv][tokens][D] (SFG_F32 or SFG_BF16) are stored as bf16 at token positions
  * start_b + t, start_b = seq_lens[b] (device) when seq_lens != NULL, else `start`,

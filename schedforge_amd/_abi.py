@@ -127,6 +127,9 @@ _SIGNATURES = {
                                              c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,
                                              c_i64, c_i32, c_f32, ctypes.c_int, c_vp, c_sz,
                                              c_vp]),
+    "sfg_hip_attn_decode_paged_noalloc_v1": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, ctypes.c_int,
+                                                     c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,
+                                                     c_i64, c_i32, c_f32, c_vp]),
     "sfg_hip_kv_append_paged_v1": (c_i32, [c_vp, c_vp, ctypes.c_int, c_vp, c_vp, c_vp, c_vp, c_i64,
                                            ctypes.c_int, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,
                                            c_i64, c_vp]),

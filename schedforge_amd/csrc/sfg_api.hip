@@ -11,10 +11,18 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
 #include <string>
 #include <vector>
 
 #include "sfg_kernels.hpp"
+
+// Library-held split partials of the paged decode, for callers that cannot
+// allocate (sfg_hip_attn_decode_paged_noalloc_v1).  Each device holds its own
+// copy from the library's load until the process ends.  Host code never uses
+// this name as an address: the per-device address comes from
+// hipGetSymbolAddress (scratch_on_current_device below).
+static __device__ __align__(256) unsigned char scratch[SFG_DECODE_SCRATCH_BYTES];
 
 namespace {
 
@@ -43,6 +51,62 @@ size_t align256(size_t v) { return (v + 255) / 256 * 256; }
 
 float default_scale(int64_t head_dim, float scale) {
     return scale > 0.0f ? scale : 1.0f / sqrtf(static_cast<float>(head_dim));
+}
+
+// Argument checks shared by the two paged-decode entry points.
+int check_decode_args(const float* q, const uint16_t* k_pool, const uint16_t* v_pool,
+                      const int32_t* page_table, const void* out, int64_t batch, int64_t q_heads,
+                      int64_t kv_heads, int64_t head_dim, int64_t page_tokens, int64_t pages_per_seq,
+                      int64_t num_pages, int64_t max_context) {
+    if (!q || !k_pool || !v_pool || !page_table || !out || batch <= 0 || q_heads <= 0 ||
+        kv_heads <= 0 || q_heads % kv_heads || head_dim <= 0 || page_tokens <= 0 ||
+        pages_per_seq <= 0 || num_pages <= 0 || max_context <= 0)
+        return fail(SFG_ERR_INVALID_CONFIG, "attn_decode_paged: invalid configuration");
+    if (max_context > pages_per_seq * page_tokens)
+        return fail(SFG_ERR_GUARD, "paged KV length violates compiled guard (%lld > %lld)",
+                    (long long)max_context, (long long)(pages_per_seq * page_tokens));
+    return SFG_OK;
+}
+
+// The split kernel + merge of both paged-decode entry points, partials in ws.
+int launch_decode(const float* q, const uint16_t* k_pool, const uint16_t* v_pool,
+                  const int32_t* page_table, const int32_t* seq_lens, void* out, int out_dtype,
+                  int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                  int64_t page_tokens, int64_t pages_per_seq, int64_t num_pages, int64_t max_context,
+                  int splits, float scale, void* ws, void* stream) {
+    const int rc = sfg::launch_attn_decode_paged(
+        q, q_heads * head_dim, nullptr, 0, k_pool, v_pool, page_table, seq_lens, max_context, 0, out,
+        out_dtype, batch, q_heads, kv_heads, head_dim, page_tokens, pages_per_seq, num_pages, splits,
+        default_scale(head_dim, scale), ws, as_stream(stream), nullptr);
+    if (rc != SFG_OK)
+        return fail(rc, "attn_decode_paged: head_dim %lld / page_tokens %lld / group %lld not lowered",
+                    (long long)head_dim, (long long)page_tokens, (long long)(q_heads / kv_heads));
+    return check_launch("attn_decode_paged");
+}
+
+// The device address of `scratch` on the current device, looked up once per
+// device (with that device current) and kept.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_on_current_device(void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(SFG_ERR_DEVICE, "hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices)
+        return fail(SFG_ERR_UNSUPPORTED, "device %d beyond the %d the library tracks", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr)
+            return fail(SFG_ERR_DEVICE, "hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                        hipGetErrorString(e));
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return SFG_OK;
 }
 
 // Bump allocator over the caller's workspace.
@@ -283,13 +347,9 @@ int sfg_hip_attn_decode_paged_v1(const float* q, const uint16_t* k_pool, const u
                                  int64_t num_pages, int64_t max_context, int32_t kv_splits,
                                  float scale, int validate_pages, void* workspace,
                                  size_t workspace_bytes, void* stream) {
-    if (!q || !k_pool || !v_pool || !page_table || !out || batch <= 0 || q_heads <= 0 ||
-        kv_heads <= 0 || q_heads % kv_heads || head_dim <= 0 || page_tokens <= 0 ||
-        pages_per_seq <= 0 || num_pages <= 0 || max_context <= 0)
-        return fail(SFG_ERR_INVALID_CONFIG, "attn_decode_paged: invalid configuration");
-    if (max_context > pages_per_seq * page_tokens)
-        return fail(SFG_ERR_GUARD, "paged KV length violates compiled guard (%lld > %lld)",
-                    (long long)max_context, (long long)(pages_per_seq * page_tokens));
+    int rc = check_decode_args(q, k_pool, v_pool, page_table, out, batch, q_heads, kv_heads, head_dim,
+                               page_tokens, pages_per_seq, num_pages, max_context);
+    if (rc != SFG_OK) return rc;
     if (validate_pages) {
         std::vector<int32_t> table(static_cast<size_t>(batch * pages_per_seq));
         hipError_t e = hipMemcpyAsync(table.data(), page_table, table.size() * sizeof(int32_t),
@@ -309,15 +369,35 @@ int sfg_hip_attn_decode_paged_v1(const float* q, const uint16_t* k_pool, const u
     const size_t need = sfg::decode_workspace_bytes(batch, q_heads, head_dim, splits);
     if (!workspace || workspace_bytes < need)
         return fail(SFG_ERR_WORKSPACE, "attn_decode_paged: workspace %zu < %zu", workspace_bytes, need);
-    const int rc = sfg::launch_attn_decode_paged(
-        q, q_heads * head_dim, nullptr, 0, k_pool, v_pool, page_table, seq_lens, max_context, 0, out,
-        out_dtype, batch, q_heads,
-        kv_heads, head_dim, page_tokens, pages_per_seq, num_pages, splits,
-        default_scale(head_dim, scale), workspace, as_stream(stream), nullptr);
-    if (rc != SFG_OK)
-        return fail(rc, "attn_decode_paged: head_dim %lld / page_tokens %lld / group %lld not lowered",
-                    (long long)head_dim, (long long)page_tokens, (long long)(q_heads / kv_heads));
-    return check_launch("attn_decode_paged");
+    return launch_decode(q, k_pool, v_pool, page_table, seq_lens, out, out_dtype, batch, q_heads,
+                         kv_heads, head_dim, page_tokens, pages_per_seq, num_pages, max_context, splits,
+                         scale, workspace, stream);
+}
+
+int sfg_hip_attn_decode_paged_noalloc_v1(const float* q, const uint16_t* k_pool,
+                                         const uint16_t* v_pool, const int32_t* page_table,
+                                         const int32_t* seq_lens, void* out, int out_dtype,
+                                         int64_t batch, int64_t q_heads, int64_t kv_heads,
+                                         int64_t head_dim, int64_t page_tokens,
+                                         int64_t pages_per_seq, int64_t num_pages,
+                                         int64_t max_context, int32_t kv_splits, float scale,
+                                         void* stream) {
+    int rc = check_decode_args(q, k_pool, v_pool, page_table, out, batch, q_heads, kv_heads, head_dim,
+                               page_tokens, pages_per_seq, num_pages, max_context);
+    if (rc != SFG_OK) return rc;
+    const int splits = sfg::decode_split_count(batch, kv_heads, max_context, page_tokens, kv_splits);
+    const size_t need = sfg::decode_workspace_bytes(batch, q_heads, head_dim, splits);
+    if (need > SFG_DECODE_SCRATCH_BYTES)
+        return fail(SFG_ERR_WORKSPACE,
+                    "attn_decode_paged_noalloc: %zu bytes of split partials (batch %lld x %lld heads x "
+                    "%d splits) exceed the library's %zu-byte scratch; use sfg_hip_attn_decode_paged_v1 "
+                    "with a workspace",
+                    need, (long long)batch, (long long)q_heads, splits, (size_t)SFG_DECODE_SCRATCH_BYTES);
+    void* ws = nullptr;
+    if ((rc = scratch_on_current_device(&ws)) != SFG_OK) return rc;
+    return launch_decode(q, k_pool, v_pool, page_table, seq_lens, out, out_dtype, batch, q_heads,
+                         kv_heads, head_dim, page_tokens, pages_per_seq, num_pages, max_context, splits,
+                         scale, ws, stream);
 }
 
 int sfg_hip_kv_append_paged_v1(const void* keys, const void* values, int dtype, uint16_t* k_pool,
