@@ -1,24 +1,34 @@
 """Decoder-layer benchmark on one MI355X.
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c4] [--decode-config c5]
 
 A step is one execution of the whole decoder layer (execute_once,
 decoder_compiler.cpp:218-304) on one batch of synthetic input, inputs resident in
-HBM.  The default workload is BASELINE config 2 (medium dense decode, bf16,
-paged KV) -- the configuration the headline metric is quoted on.  The metric is
-the reference's: equivalent tokens/s = rows * 1000 / ms (decoder_compiler.cpp:
-301-302, 688-689), rows = batch * sequence.
+HBM.  The metric is the reference's: equivalent tokens/s = rows * 1000 / ms
+(decoder_compiler.cpp:301-302, 688-689), rows = batch * sequence.
 
-The JSON line also carries:
-  roofline      the dominant kernel's achieved fraction of its MI355X peak,
-                from HIP events recorded around it on the layer's stream in
-                every --mark-every'th step of the timed region (decode: the
-                paged Split-KV attention kernel, HBM bound; prefill: the FFN
-                up-projection GEMM).  An event record drains the queue around
-                the kernel it brackets (about 6 us per marked decode step), so
-                marking only some steps keeps that cost out of the throughput;
-  cpu_baseline  the CPU oracle (a C restatement of the reference path) timed on
-                this host on a bounded sample of the same workload.
+BASELINE.json's metric names no configuration, so the headline is the largest
+single-GPU configuration: config 4 (Llama-3-8B-shaped prefill, S 8192, bf16),
+MFMA-bound.  The same line nests, under "decode", config 5 (Mixtral-shaped int8
+decode over a paged 8192-token cache), HBM-bound, with its own value and
+roofline; --decode-config none leaves it out, --config picks another headline.
+
+Each measured block carries:
+  roofline      the dominant kernel's achieved fraction of its MI355X peak:
+                algorithmic FLOPs (prefill: the FFN up-projection GEMM) or bytes
+                (decode: the paged Split-KV attention kernel) per launch over
+                the launch's average duration, from HIP events recorded around
+                it on the layer's stream in every --mark-every'th timed step (an
+                event record drains the queue, so only some steps are marked);
+                "traffic" is the kernel's HBM bytes per launch from the
+                rocprofv3 FETCH_SIZE / WRITE_SIZE passes in
+                profiles/pmc_traffic.txt, scaled by the same counters' reading
+                for a 1 GiB copy (--copy-calibration);
+  cpu_baseline  the CPU oracle (oracle/sfg_oracle.c, a C restatement of the
+                reference path) on this host's cores, on a bounded sample of the
+                same workload: prefill as the layer at sampled query rows
+                (K / V for every row, the rest for rows spread over the whole
+                causal range), decode as whole layer steps.
 Synthetic data: activations N(0,1), weights N(0,0.02), cached K/V N(0,1), drawn
 on the device; norm gains 1; random page table.
 """
@@ -26,7 +36,6 @@ from __future__ import annotations
 
 import argparse
 import json
-import os
 import sys
 import time
 from pathlib import Path
@@ -34,33 +43,19 @@ from pathlib import Path
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
-# HBM traffic per launch of the roofline kernel, from two rocprofv3 --pmc runs
-# of this script (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch) with
-# --copy-calibration 1024.  The calibration kernel reads 1 GiB and writes 1 GiB;
-# the counters read 524311.8 KiB and 1048576.0 KiB for it, so FETCH_SIZE is
-# scaled by 1048576 / 524311.8 and WRITE_SIZE by 1.  Summaries:
-# profiles/pmc_traffic_c2.md, profiles/pmc_traffic_c5.md (decode attention),
-# profiles/pmc_traffic_prefill_gemm.md (C4 gate|up GEMM, C3 grouped experts).
-PMC_FETCH_SCALE = 1048576.0 / 524311.8
-PMC_WRITE_SCALE = 1.0
-PMC_ROOFLINE_KIB = {           # roofline kernel(s) per launch: (FETCH_SIZE, WRITE_SIZE)
-    "c2": (66117.8, 1088.0),                    # attn_decode_split_kernel
-    "c5": (1049963.6, 2112.0),                  # attn_decode_split_kernel
-    "c4": (1376849.7, 229376.0),                # gate|up GEMM + SwiGLU
-    "c3": (143115.5 + 71003.0, 11264.0 + 32768.0),  # grouped W1|W3 + W2 expert GEMMs
-}
-MEASURED_TRAFFIC = {k: round((f * PMC_FETCH_SCALE + w * PMC_WRITE_SCALE) * 1024)
-                    for k, (f, w) in PMC_ROOFLINE_KIB.items()}
+TRAFFIC_FILE = ROOT / "profiles" / "pmc_traffic.txt"
 
 
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=5)
-    p.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
+    p.add_argument("--config", default="c4", choices=["c1", "c2", "c3", "c4", "c5"])
+    p.add_argument("--decode-config", default="c5", choices=["c2", "c5", "none"],
+                   help="decode configuration nested under 'decode' when the headline is a prefill")
     p.add_argument("--cpu-seconds", type=float, default=12.0,
-                   help="bound on the CPU-baseline sample")
+                   help="bound on each CPU-baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--mark-every", type=int, default=5,
                    help="bracket the roofline kernel with HIP events in every N-th timed step")
@@ -71,6 +66,7 @@ def parse():
     return p.parse_args()
 
 
+# ---------------------------------------------------------------- data
 def make_device_data(cfg, seed, device):
     """Synthetic DecoderData drawn on the device (reference layouts, fp32)."""
     import torch
@@ -112,6 +108,64 @@ def make_device_data(cfg, seed, device):
     return d, perm
 
 
+def timing_data(cfg, seed):
+    """Host data in the oracle's layouts for timing only, and for int8 configs
+    the quantized weights: each tensor is a random 1 Mi-element block repeated
+    to its shape (the oracle's cost does not depend on the values, and drawing
+    and quantizing 10^9 values would dominate the sample)."""
+    import numpy as np
+    from types import SimpleNamespace
+    rng = np.random.default_rng(seed)
+    block = rng.standard_normal(1 << 20, dtype=np.float32)
+    qblock = rng.integers(-127, 128, size=1 << 20, dtype=np.int8)
+
+    def fill(shape, src):
+        out = np.empty(int(np.prod(shape)), src.dtype)
+        whole = out.size // src.size * src.size
+        out[:whole].reshape(-1, src.size)[:] = src
+        out[whole:] = src[:out.size - whole]
+        return out.reshape(shape)
+
+    def t(shape, std=1.0):
+        return fill(shape, block * np.float32(std))
+
+    def q8(n, k):  # int8 [N][K] and per-channel scales, as quantize_kn returns
+        return fill((n, k), qblock), np.full(n, 0.02 / 127 * 4, np.float32)
+
+    H, I, D, E = cfg.hidden, cfg.intermediate, cfg.head_dim, cfg.experts
+    kvd = cfg.kv_heads * D
+    w8 = cfg.dtype == "w8"
+    d = SimpleNamespace(routing_trace=None, router_bias=None, gate_weight=None, up_weight=None,
+                        down_weight=None, router_weight=None, w1=None, w3=None, w2=None,
+                        cached_key=None, cached_value=None, query_weight=None, key_weight=None,
+                        value_weight=None, output_weight=None)
+    d.input = t((cfg.rows, H))
+    d.rms1_weight = d.rms2_weight = np.ones(H, np.float32)
+    quant = None
+    if w8:
+        quant = SimpleNamespace(dense=[q8(H, H), q8(kvd, H), q8(kvd, H), q8(H, H)])
+        if cfg.moe:
+            quant.e1 = [q8(I, H) for _ in range(E)]
+            quant.e3 = [q8(I, H) for _ in range(E)]
+            quant.e2 = [q8(H, I) for _ in range(E)]
+        else:
+            quant.dense += [q8(I, H), q8(I, H), q8(H, I)]
+    else:
+        d.query_weight, d.output_weight = t((H, H), 0.02), t((H, H), 0.02)
+        d.key_weight, d.value_weight = t((H, kvd), 0.02), t((H, kvd), 0.02)
+    if cfg.moe:
+        d.router_weight = t((H, E), 0.02)
+        if not w8:
+            d.w1, d.w3, d.w2 = t((E, H, I), 0.02), t((E, H, I), 0.02), t((E, I, H), 0.02)
+    elif not w8:
+        d.gate_weight, d.up_weight, d.down_weight = t((H, I), 0.02), t((H, I), 0.02), t((I, H), 0.02)
+    if cfg.decode:
+        d.cached_key = t((cfg.batch, cfg.kv_heads, cfg.context_sequence, D))
+        d.cached_value = t((cfg.batch, cfg.kv_heads, cfg.context_sequence, D))
+    return d, quant
+
+
+# ---------------------------------------------------------------- roofline inputs
 def decode_attention_bytes(cfg):
     """Algorithmic HBM bytes of one paged decode-attention launch: K + V pages
     (bf16), Q (fp32), the merged output (bf16) and the page table."""
@@ -121,6 +175,33 @@ def decode_attention_bytes(cfg):
     o = cfg.batch * cfg.query_heads * cfg.head_dim * 2
     pt = cfg.batch * pps * 4
     return kv + q + o + pt
+
+
+def measured_traffic(config: str):
+    """HBM bytes per launch of the config's roofline kernel from
+    profiles/pmc_traffic.txt: FETCH_SIZE and WRITE_SIZE (KiB per dispatch),
+    each scaled by copy_mib * 1024 / (the counter's KiB for the calibration
+    copy, which reads copy_mib MiB and writes copy_mib MiB).  None when the file
+    holds no entry for the config."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    cal, rows = None, {}
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        parts = line.split()
+        if not parts or line.startswith("#"):
+            continue
+        kv = dict(p.split("=", 1) for p in parts[1:] if "=" in p)
+        if parts[0] == "calibration":
+            cal = kv
+        else:
+            rows[parts[0]] = kv
+    if cal is None or config not in rows:
+        return None
+    moved_kib = float(cal["copy_mib"]) * 1024.0
+    fs, ws = moved_kib / float(cal["fetch_kib"]), moved_kib / float(cal["write_kib"])
+    r = rows[config]
+    return {"bytes": round((float(r["fetch_kib"]) * fs + float(r["write_kib"]) * ws) * 1024),
+            "kernel": r.get("kernel", "")}
 
 
 def stage_tflops(cfg, work, avg):
@@ -136,72 +217,92 @@ def stage_tflops(cfg, work, avg):
     return {k: round(v, 2) for k, v in out.items()}
 
 
+# ---------------------------------------------------------------- CPU baseline
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(cfg, budget_s: float):
-    """Time the CPU oracle (C restatement of reference_decoder_layer) on a
-    bounded sample of the workload: full-size layer steps for decode / small
-    prefill configs, a row-sliced prefill for the large ones."""
+    """Time the CPU oracle on a bounded sample of the workload.
+
+    Decode: whole layer steps (rows are few).  Prefill with more than 256 rows:
+    the layer at n sampled query rows (sfgo_decoder_layer_rows: RMSNorm and K / V
+    for every row, then Q, attention, O-projection and FFN for rows spread
+    evenly over the sequence, so their causal lengths average the full range),
+    timed at two sample sizes n1 < n2; t(n) = a + n c separates the all-row part
+    a from the per-row cost c, and a full layer costs a + rows c."""
     import numpy as np
     import oracle
     threads = oracle.lib().sfgo_num_threads()
-    sample = cfg
-    note = "full layer step"
-    if not cfg.decode and cfg.rows > 256:
-        # the prefill's cost is dominated by the GEMMs and attention over all
-        # rows; sample a prefix of the sequence and scale by rows
-        seq = 256 if cfg.sequence > 256 else cfg.sequence
-        sample = cfg.replace(batch=1, sequence=seq)
-        note = f"prefill sample batch 1 seq {seq} (scaled per row)"
-    t0 = time.time()
-    d = oracle.make_layer_data(sample, 99)
-    gen_s = time.time() - t0
-    q = oracle.quantize_layer(sample, d) if sample.dtype == "w8" else None
-    reps, spent = 0, 0.0
-    while True:
-        t = time.time()
-        oracle.decoder_layer(sample, d, quant=q)
-        spent += time.time() - t
-        reps += 1
-        if spent > budget_s or reps >= 1000:  # the time budget governs
-            break
-    per_step = spent / reps
-    tok_s = sample.rows / per_step
-    return {"value": round(tok_s, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{note}: {reps} x {sample.rows} rows in {spent:.1f} s "
-                      f"({per_step * 1e3:.1f} ms/step; data generation {gen_s:.1f} s untimed)"}
+    d, q = timing_data(cfg, 99)
+    base = {"unit": "tokens/s", "cores": threads, "kind": "port",
+            "what": "oracle/sfg_oracle.c: C restatement of reference_decoder_layer (OpenMP)",
+            "cpu_model": cpu_model(), "threads": threads}
+    if cfg.decode or cfg.rows <= 256:
+        reps, spent = 0, 0.0
+        while True:
+            t = time.time()
+            oracle.decoder_layer(cfg, d, quant=q)
+            spent += time.time() - t
+            reps += 1
+            if spent > budget_s or reps >= 1000:
+                break
+        per_step = spent / reps
+        return {"value": round(cfg.rows / per_step, 3), **base,
+                "sample": f"full layer step: {reps} x {cfg.rows} rows in {spent:.1f} s "
+                          f"({per_step * 1e3:.1f} ms/step)"}
+    times = {}
+    for n in (32, 96):
+        sample = np.linspace(0, cfg.rows - 1, n).round().astype(np.int64)
+        reps, spent = 0, 0.0
+        while True:
+            t = time.time()
+            oracle.decoder_layer_rows(cfg, d, sample, quant=q)
+            spent += time.time() - t
+            reps += 1
+            if spent > budget_s / 2 or reps >= 50:
+                break
+        times[n] = spent / reps
+    c = max((times[96] - times[32]) / 64, 0.0)
+    a = max(times[32] - 32 * c, 0.0)
+    per_layer = a + cfg.rows * c
+    return {"value": round(cfg.rows / per_layer, 3), **base,
+            "sample": f"layer at 32 and 96 evenly spaced query rows of {cfg.rows}: "
+                      f"{times[32]:.2f} s and {times[96]:.2f} s per call -> all-row part "
+                      f"{a:.2f} s + {c * 1e3:.2f} ms per row -> {per_layer:.1f} s per layer"}
 
 
-def main():
-    args = parse()
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported here "
-              "(multi-GPU sharding is design-only for this backend).", file=sys.stderr)
-        sys.exit(2)
+# ---------------------------------------------------------------- one configuration
+def workload_name(name, cfg):
+    return (f"BASELINE config {name[1]}: " + ("decode" if cfg.decode else "prefill")
+            + f" B{cfg.batch} S{cfg.sequence} H{cfg.hidden} Hq{cfg.query_heads}/Hkv{cfg.kv_heads}"
+            + f" D{cfg.head_dim} "
+            + (f"MoE E{cfg.experts} top{cfg.top_k} I{cfg.intermediate}" if cfg.moe
+               else f"SwiGLU I{cfg.intermediate}")
+            + (f" ctx{cfg.context_sequence} paged{cfg.page_tokens}" if cfg.decode else "")
+            + {"f32": " fp32", "bf16": " bf16", "w8": " int8 weights / bf16 activations"}[cfg.dtype])
+
+
+def measure(name, args, device="cuda:0"):
     import torch
-    from schedforge_amd import CONFIGS, CONFIG_SEEDS, algorithmic_work, load
+    from schedforge_amd import CONFIGS, CONFIG_SEEDS, algorithmic_work
     from schedforge_amd import configs as C
     from schedforge_amd import _abi
     from schedforge_amd.layer import StageEvents, compile_decoder, run_layer, stage_times
 
-    load()
-    device = "cuda:0"
-    cfg = CONFIGS[args.config]
-    data, perm = make_device_data(cfg, CONFIG_SEEDS[args.config], device)
+    cfg = CONFIGS[name]
+    data, perm = make_device_data(cfg, CONFIG_SEEDS[name], device)
     plan = compile_decoder(cfg, data, device, page_permutation=perm)
     x = data.input.contiguous()
     del data
     torch.cuda.empty_cache()
     out = torch.empty((cfg.rows, cfg.hidden), dtype=torch.float32, device=device)
-    stream = torch.cuda.current_stream()
-
-    if args.copy_calibration > 0:
-        n = args.copy_calibration * (1 << 20) // 4
-        src = torch.ones(n, dtype=torch.float32, device=device)
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        torch.mul(src, 1.0, out=dst)   # one launch: n*4 bytes read, n*4 written
-        torch.cuda.synchronize()
-        del src, dst
-        torch.cuda.empty_cache()
 
     for _ in range(args.warmup):
         run_layer(plan, x, out)
@@ -234,27 +335,29 @@ def main():
     stages = [stage_times(e) for e in full]
     for e in full:
         e.close()
+    del plan, x, out
+    torch.cuda.empty_cache()
 
     def avg(key):
         return sum(s[key] for s in stages) / len(stages)
 
     work = algorithmic_work(cfg)
+    traffic = measured_traffic(name)
+    kern_ms = sum(kern_times) / len(kern_times)
     if cfg.decode:
-        att_ms = sum(kern_times) / len(kern_times)
         bytes_ = decode_attention_bytes(cfg)
-        achieved = bytes_ / (att_ms * 1e-3) / 1e9
+        achieved = bytes_ / (kern_ms * 1e-3) / 1e9
         roofline = {"bound": "hbm", "kernel": "attn_decode_split_kernel", "achieved":
                     round(achieved, 1), "peak": C.PEAK_HBM_GBPS, "unit": "GB/s",
                     "frac": round(achieved / C.PEAK_HBM_GBPS, 4),
-                    "traffic": MEASURED_TRAFFIC.get(args.config),
-                    "algorithmic_bytes": bytes_, "avg_ms": round(att_ms, 5),
+                    "traffic": traffic["bytes"] if traffic else None,
+                    "algorithmic_bytes": bytes_, "avg_ms": round(kern_ms, 5),
                     "timed_launches": len(kern_times)}
     else:
         # prefill: the FFN up-projection's algorithmic FLOPs (2 rows H 2I for
         # the packed gate|up GEMM; 4 T k H I for the grouped W1|W3 expert GEMM
         # plus 2 T k H I for W2) over its bracketed time
         peak = C.PEAK_F32_TFLOPS if cfg.dtype == "f32" else C.PEAK_BF16_TFLOPS
-        ffn_ms = sum(kern_times) / len(kern_times)
         T, H, I, K, E = cfg.rows, cfg.hidden, cfg.intermediate, cfg.top_k, cfg.experts
         esz = 4 if cfg.dtype == "f32" else 2
         if cfg.moe:
@@ -266,41 +369,74 @@ def main():
             kflops = 2 * T * H * 2 * I
             kname = ("gemm_f32_kernel" if cfg.dtype == "f32" else "gemm_dma_kernel") + " (gate|up + SwiGLU)"
             kbytes = esz * (T * H + 2 * I * H + T * I)
-        achieved = kflops / (ffn_ms * 1e-3) / 1e12
+        achieved = kflops / (kern_ms * 1e-3) / 1e12
+        layer_tf = work["flops"] / (ms_per_step * 1e-3) / 1e12
         roofline = {"bound": "mfma", "kernel": kname,
                     "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
                     "frac": round(achieved / peak, 4),
-                    "traffic": MEASURED_TRAFFIC.get(args.config), "algorithmic_bytes": kbytes,
-                    "algorithmic_flops": kflops, "avg_ms": round(ffn_ms, 5),
+                    "traffic": traffic["bytes"] if traffic else None, "algorithmic_bytes": kbytes,
+                    "algorithmic_flops": kflops, "avg_ms": round(kern_ms, 5),
                     "timed_launches": len(kern_times),
-                    "layer_tflops": round(work["flops"] / (ms_per_step * 1e-3) / 1e12, 2),
-                    "layer_frac": round(work["flops"] / (ms_per_step * 1e-3) / 1e12 / peak, 4)}
-    layer_gbps = work["bytes"] / (ms_per_step * 1e-3) / 1e9
-    line = {
-        "metric": "decoder-layer equiv. tokens/s (1 GPU)",
+                    "layer_tflops": round(layer_tf, 2), "layer_frac": round(layer_tf / peak, 4)}
+    block = {
         "value": round(tokens_s, 2),
-        "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
         "dtype": {"f32": "f32", "bf16": "bf16", "w8": "int8-weight/bf16"}[cfg.dtype],
-        "data": "synthetic (device-drawn N(0,1) activations / KV, N(0,0.02) weights)",
-        "config": {"workload": f"BASELINE config {args.config[1]}: "
-                   + ("decode" if cfg.decode else "prefill")
-                   + f" B{cfg.batch} S{cfg.sequence} H{cfg.hidden} Hq{cfg.query_heads}/Hkv{cfg.kv_heads}"
-                   + f" D{cfg.head_dim} {'MoE E%d top%d I%d' % (cfg.experts, cfg.top_k, cfg.intermediate) if cfg.moe else 'SwiGLU I%d' % cfg.intermediate}"
-                   + (f" ctx{cfg.context_sequence} paged{cfg.page_tokens}" if cfg.decode else ""),
-                   "rows": cfg.rows, "layer_hbm_gbps": round(layer_gbps, 1),
+        "config": {"workload": workload_name(name, cfg), "rows": cfg.rows,
+                   "layer_hbm_gbps": round(work["bytes"] / (ms_per_step * 1e-3) / 1e9, 1),
                    "stage_ms": {k: round(avg(k), 5) for k in stages[0]},
                    "stage_tflops": stage_tflops(cfg, work, avg)},
         "roofline": roofline,
     }
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds)
+        block["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds)
+    return block
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported here "
+              "(multi-GPU sharding is design-only for this backend).", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from schedforge_amd import CONFIGS, load
+
+    load()
+    device = "cuda:0"
+    if args.copy_calibration > 0:
+        n = args.copy_calibration * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=device)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        torch.mul(src, 1.0, out=dst)   # one launch: n*4 bytes read, n*4 written
+        torch.cuda.synchronize()
+        del src, dst
+        torch.cuda.empty_cache()
+
+    head = measure(args.config, args, device)
+    line = {
+        "metric": "decoder-layer equiv. tokens/s (1 GPU)",
+        "value": head["value"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": head["dtype"],
+        "data": "synthetic (device-drawn N(0,1) activations / KV, N(0,0.02) weights)",
+        "config": head["config"],
+        "roofline": head["roofline"],
+    }
+    if "cpu_baseline" in head:
+        line["cpu_baseline"] = head["cpu_baseline"]
+    if not CONFIGS[args.config].decode and args.decode_config != "none":
+        dec = measure(args.decode_config, args, device)
+        line["decode"] = {"metric": line["metric"], "unit": "tokens/s", "steps": args.steps,
+                          "warmup": args.warmup, **dec}
     print(json.dumps(line), flush=True)
 
 
