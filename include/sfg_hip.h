@@ -96,7 +96,32 @@ enum sfg_epilogue {
 int sfg_hip_abi_version(void);
 const char* sfg_hip_metadata_v1(void);
 const char* sfg_hip_last_error(void);
+/* CUs, XCDs (hipDeviceAttributeNumberOfXccs) and HBM bytes of a device. */
 int sfg_hip_device_info_v1(int device, int* cu_count, int* xcd_count, int64_t* hbm_bytes);
+
+/* The GPU target a plan compiles for: the counterpart of the reference's
+ * TargetInfo (include/schedforge/schedforge.h:15-34, TargetInfo::detect in
+ * src/target.cpp:8-17), which describes the CPU the LoopIR schedules target.
+ * Queried from the device (architecture, CUs, XCDs, LDS, L2, clocks, HBM);
+ * peaks follow from the queried counts and clock with gfx950's per-CU rates
+ * (bf16 dense MFMA 4096 FLOP / clock / CU, fp32 VALU 256 FLOP / clock / CU);
+ * HBM bandwidth is gfx950's published 8 TB/s (HIP's memory clock and bus
+ * width understate HBM3E's data rate), else estimated from them. */
+typedef struct {
+    char architecture[64];        /* gcnArchName, e.g. gfx950:sramecc+:xnack- */
+    int32_t wavefront;            /* 64 */
+    int32_t compute_units;        /* 256 on MI355X */
+    int32_t xcds;                 /* accelerator complex dies, workgroups dealt round-robin */
+    int32_t simds_per_cu;         /* 4 */
+    int64_t lds_bytes_per_cu;     /* 160 KiB on gfx950 */
+    int64_t l2_bytes_per_xcd;     /* 4 MiB on gfx950 */
+    int64_t hbm_bytes;            /* device memory */
+    double engine_clock_ghz;      /* max engine clock */
+    double hbm_gbps;              /* peak HBM bandwidth, GB/s */
+    double mfma_bf16_tflops;      /* dense bf16 MFMA peak at engine_clock_ghz */
+    double valu_fp32_tflops;      /* fp32 VALU peak (no packed math) */
+} sfg_target_info;
+int sfg_hip_target_info_v1(int device, sfg_target_info* info);
 
 /* ---------------- constant packing (DecoderCompiler::compile constant
  * specialisation, decoder_compiler.cpp:535-552; quantize_matmul_weights,

@@ -46,6 +46,16 @@ class SfgInvalidArgument(ValueError):
         self.code = code
 
 
+class TargetInfo(ctypes.Structure):
+    _fields_ = [
+        ("architecture", ctypes.c_char * 64), ("wavefront", c_i32), ("compute_units", c_i32),
+        ("xcds", c_i32), ("simds_per_cu", c_i32), ("lds_bytes_per_cu", c_i64),
+        ("l2_bytes_per_xcd", c_i64), ("hbm_bytes", c_i64), ("engine_clock_ghz", ctypes.c_double),
+        ("hbm_gbps", ctypes.c_double), ("mfma_bf16_tflops", ctypes.c_double),
+        ("valu_fp32_tflops", ctypes.c_double),
+    ]
+
+
 class GemmArgs(ctypes.Structure):
     _fields_ = [
         ("a", c_vp), ("a_dtype", c_i32), ("lda", c_i64),
@@ -102,6 +112,7 @@ _SIGNATURES = {
     "sfg_hip_last_error": (ctypes.c_char_p, []),
     "sfg_hip_device_info_v1": (c_i32, [ctypes.c_int, ctypes.POINTER(ctypes.c_int),
                                        ctypes.POINTER(ctypes.c_int), ctypes.POINTER(c_i64)]),
+    "sfg_hip_target_info_v1": (c_i32, [ctypes.c_int, ctypes.POINTER(TargetInfo)]),
     "sfg_hip_pack_weight_v1": (c_i32, [c_vp, c_i64, c_i64, c_i64, c_vp, ctypes.c_int, ctypes.c_int,
                                        c_vp]),
     "sfg_hip_quantize_weight_v1": (c_i32, [c_vp, c_i64, c_i64, c_vp, c_vp, ctypes.c_int, c_vp]),

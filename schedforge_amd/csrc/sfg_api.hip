@@ -109,6 +109,28 @@ int scratch_on_current_device(void** out) {
     return SFG_OK;
 }
 
+}  // namespace
+
+namespace sfg {
+
+int device_xcds() {
+    static std::mutex mu;
+    static int cache[kMaxDevices] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 1;
+    std::lock_guard<std::mutex> lock(mu);
+    if (cache[dev] == 0) {
+        int x = 0;
+        if (hipDeviceGetAttribute(&x, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess || x <= 0) x = 1;
+        cache[dev] = x;
+    }
+    return cache[dev];
+}
+
+}  // namespace sfg
+
+namespace {
+
 // Bump allocator over the caller's workspace.
 struct Carve {
     char* base;
@@ -136,12 +158,45 @@ const char* sfg_hip_metadata_v1(void) {
 const char* sfg_hip_last_error(void) { return g_last_error.c_str(); }
 
 int sfg_hip_device_info_v1(int device, int* cu_count, int* xcd_count, int64_t* hbm_bytes) {
+    sfg_target_info t;
+    const int rc = sfg_hip_target_info_v1(device, &t);
+    if (rc != SFG_OK) return rc;
+    if (cu_count) *cu_count = t.compute_units;
+    if (xcd_count) *xcd_count = t.xcds;
+    if (hbm_bytes) *hbm_bytes = t.hbm_bytes;
+    return SFG_OK;
+}
+
+int sfg_hip_target_info_v1(int device, sfg_target_info* info) {
+    if (!info) return fail(SFG_ERR_SHAPE, "target_info: null output");
     hipDeviceProp_t prop;
-    const hipError_t e = hipGetDeviceProperties(&prop, device);
+    hipError_t e = hipGetDeviceProperties(&prop, device);
     if (e != hipSuccess) return fail(SFG_ERR_DEVICE, "hipGetDeviceProperties: %s", hipGetErrorString(e));
-    if (cu_count) *cu_count = prop.multiProcessorCount;
-    if (xcd_count) *xcd_count = 8;
-    if (hbm_bytes) *hbm_bytes = static_cast<int64_t>(prop.totalGlobalMem);
+    int xcds = 0;
+    e = hipDeviceGetAttribute(&xcds, hipDeviceAttributeNumberOfXccs, device);
+    if (e != hipSuccess) return fail(SFG_ERR_DEVICE, "hipDeviceGetAttribute(XCCs): %s", hipGetErrorString(e));
+    sfg_target_info t{};
+    snprintf(t.architecture, sizeof t.architecture, "%s", prop.gcnArchName);
+    t.wavefront = prop.warpSize;
+    t.compute_units = prop.multiProcessorCount;
+    t.xcds = xcds > 0 ? xcds : 1;
+    t.simds_per_cu = 4;
+    t.lds_bytes_per_cu = static_cast<int64_t>(prop.maxSharedMemoryPerMultiProcessor);
+    // HIP reports no L2 size for this architecture (prop.l2CacheSize is 0 or
+    // the whole device's); gfx950 has 4 MiB per XCD.
+    t.l2_bytes_per_xcd = prop.l2CacheSize > 0 && prop.l2CacheSize / t.xcds >= (1 << 20)
+                             ? prop.l2CacheSize / t.xcds : (int64_t(4) << 20);
+    t.hbm_bytes = static_cast<int64_t>(prop.totalGlobalMem);
+    t.engine_clock_ghz = prop.clockRate / 1.0e6;
+    // HIP's memory clock times two transfers per clock over the bus width
+    // understates HBM3E (on MI355X it reads 4.1 TB/s, half the 8 GT/s pin
+    // rate), so gfx950 takes its published 8 TB/s; other parts the estimate.
+    t.hbm_gbps = strncmp(prop.gcnArchName, "gfx950", 6) == 0
+                     ? 8000.0
+                     : 2.0 * prop.memoryClockRate * 1.0e3 * (prop.memoryBusWidth / 8.0) / 1.0e9;
+    t.mfma_bf16_tflops = t.compute_units * 4096.0 * t.engine_clock_ghz / 1.0e3;
+    t.valu_fp32_tflops = t.compute_units * 256.0 * t.engine_clock_ghz / 1.0e3;
+    *info = t;
     return SFG_OK;
 }
 

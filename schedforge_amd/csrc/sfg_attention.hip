@@ -324,7 +324,7 @@ int launch_attn_prefill_bf16(const uint16_t* q, const uint16_t* k, const uint16_
 // Online softmax in the exp2 domain with a lazy rescale: a row keeps its
 // running max until a tile's max exceeds it by more than 8 (p <= 2^8), so the
 // O^T rescale runs only when some row of the wave moved that far.
-// Work order: consecutive workgroup ids go to the 8 XCDs in turn; each XCD
+// Work order: consecutive workgroup ids go to the XCDs in turn; each XCD
 // gets a contiguous run of (batch, kv_head) groups -- the Q heads sharing one
 // K/V stay in one L2 -- and within a group the longest causal blocks first.
 // ===========================================================================
@@ -338,6 +338,7 @@ struct Fa2Args {
     int out_f32;
     int q_heads, kv_heads, seq_q, seq_kv, ld_vt, causal, nqb;
     float scale_log2;
+    int xcds;
 };
 
 __device__ __forceinline__ int swap23(int i) {
@@ -364,8 +365,9 @@ void attn_prefill_fa2_kernel(Fa2Args p) {
     const int G = p.q_heads / p.kv_heads;
     const int total = static_cast<int>(gridDim.x);
     const int bid = static_cast<int>(blockIdx.x);
-    const int full = total - total % 8;
-    const int L = bid < full ? (bid % 8) * (full / 8) + bid / 8 : bid;
+    const int x = p.xcds;
+    const int full = total - total % x;
+    const int L = bid < full ? (bid % x) * (full / x) + bid / x : bid;
     const int per_group = p.nqb * G;
     const int grp = L / per_group;
     const int rem = L - grp * per_group;
@@ -568,6 +570,7 @@ int launch_attn_prefill_vt(const uint16_t* q, const uint16_t* k, const uint16_t*
     a.ld_vt = static_cast<int>(ld_vt); a.causal = causal;
     a.nqb = static_cast<int>((seq_q + bm - 1) / bm);
     a.scale_log2 = scale * kLog2e;
+    a.xcds = device_xcds();
     const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.nqb) * q_heads * batch));
     if (waves == 8) attn_prefill_fa2_kernel<8><<<grid, 512, 0, stream>>>(a);
     else attn_prefill_fa2_kernel<4><<<grid, 256, 0, stream>>>(a);

@@ -459,6 +459,7 @@ struct TiledArgs {
     const int32_t* offsets;   // grouped: tiles per group = ceil(rows_g / 128)
     int groups;
     QkvRopeOut qkv;           // kEpiQkvRope only
+    int xcds;                 // XCDs the dispatcher deals workgroups over
 };
 
 constexpr int kTM = 128, kTN = 128, kTK = 32;
@@ -677,9 +678,10 @@ __global__ __launch_bounds__(256) void gemm_mfma256_kernel(TiledArgs p, int tile
     } else {
         const int64_t total = static_cast<int64_t>(tiles_m) * tiles_n;
         const int64_t i = blockIdx.x;
-        const int64_t full = total - total % 8;
+        const int64_t x = p.xcds;
+        const int64_t full = total - total % x;
         int64_t L = i;
-        if (i < full) L = (i % 8) * (full / 8) + i / 8;
+        if (i < full) L = (i % x) * (full / x) + i / x;
         constexpr int64_t kGroupM = 8;
         const int64_t group = L / (kGroupM * tiles_n);
         const int64_t first_m = group * kGroupM;
@@ -1027,13 +1029,14 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
         tm = t;
     } else {
         // XCD-aware order: the dispatcher deals consecutive workgroup ids to
-        // the 8 XCDs in turn, so hand each XCD a contiguous run of tiles and
+        // the XCDs in turn, so hand each XCD a contiguous run of tiles and
         // walk them in groups of 8 M-tiles (A and B tiles shared in one L2).
         const int64_t total = static_cast<int64_t>(tiles_m) * tiles_n;
         const int64_t i = blockIdx.x;
-        const int64_t full = total - total % 8;
+        const int64_t x = p.xcds;
+        const int64_t full = total - total % x;
         int64_t L = i;
-        if (i < full) L = (i % 8) * (full / 8) + i / 8;
+        if (i < full) L = (i % x) * (full / x) + i / x;
         constexpr int64_t kGroupM = 8;
         const int64_t group = L / (kGroupM * tiles_n);
         const int64_t first_m = group * kGroupM;
@@ -1635,7 +1638,10 @@ size_t gemm_workspace_bytes(int64_t m, int64_t n, int64_t k) {
     return splitk_bytes(m, n, k);  // every other GEMM reduces inside its workgroup
 }
 
-int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+int launch_gemm(const GemmProblem& problem, void* workspace, size_t workspace_bytes,
+                hipStream_t stream) {
+    GemmProblem p = problem;
+    p.xcds = device_xcds();
     const bool glu = is_glu(p.epilogue);
     if (p.epilogue == kEpiQkvRope && !gemm_qkv_rope_supported(p)) return SFG_ERR_UNSUPPORTED;
     if (p.a_dtype == SFG_F32) {
@@ -1738,6 +1744,7 @@ int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes, h
     a.residual = p.residual; a.ldr = p.ldr;
     a.m = p.m; a.n = p.n; a.k = p.k; a.offsets = p.offsets; a.groups = groups;
     a.qkv = p.qkv;
+    a.xcds = p.xcds;
     // the direct-to-LDS kernel addresses each operand with 32-bit byte offsets
     const bool fits32 = static_cast<uint64_t>(a.a_rows_limit) * p.lda * 2 <= 0xFFFFFFFFull &&
                         static_cast<uint64_t>(glu ? 2 : 1) * p.n * p.ldb * 2 <= 0xFFFFFFFFull;

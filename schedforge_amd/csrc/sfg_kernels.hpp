@@ -56,7 +56,13 @@ struct GemmProblem {
     int groups;
     QkvRopeOut qkv;             // epilogue kEpiQkvRope only
     int tile;                   // sfg_gemm_tile of the direct-to-LDS path (0: by shape)
+    int xcds;                   // XCDs workgroups are dealt over (launch_gemm fills it)
 };
+
+// XCDs of the current device (hipDeviceAttributeNumberOfXccs), queried once per
+// device: the dispatcher deals consecutive workgroup ids over them in turn,
+// which the XCD-aware tile orders undo.
+int device_xcds();
 
 bool gemm_qkv_rope_supported(const GemmProblem& p);
 size_t gemm_workspace_bytes(int64_t m, int64_t n, int64_t k);

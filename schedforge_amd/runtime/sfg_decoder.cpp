@@ -17,6 +17,7 @@
 #include <cmath>
 #include <cstring>
 #include <fstream>
+#include <iomanip>
 #include <limits>
 #include <sstream>
 #include <stdexcept>
@@ -473,16 +474,29 @@ std::vector<std::uint16_t> build_pool(const DecoderConfig& c, const std::vector<
 
 }  // namespace
 
+GpuTargetInfo query_target(const SfgHipLibrary& lib, int ordinal) {
+    sfg_target_info t{};
+    lib.check(lib.target_info(ordinal, &t), "target info");
+    GpuTargetInfo g;
+    g.architecture = t.architecture;
+    g.wavefront = t.wavefront;
+    g.compute_units = t.compute_units;
+    g.xcds = t.xcds;
+    g.simds_per_cu = t.simds_per_cu;
+    g.lds_bytes_per_cu = static_cast<std::size_t>(t.lds_bytes_per_cu);
+    g.l2_bytes_per_xcd = static_cast<std::size_t>(t.l2_bytes_per_xcd);
+    g.hbm_bytes = static_cast<std::size_t>(t.hbm_bytes);
+    g.engine_clock_ghz = t.engine_clock_ghz;
+    g.hbm_gbps = t.hbm_gbps;
+    g.mfma_bf16_tflops = t.mfma_bf16_tflops;
+    g.valu_fp32_tflops = t.valu_fp32_tflops;
+    return g;
+}
+
 std::string describe_hardware(const SfgHipLibrary& lib, int ordinal) {
     hipDeviceProp_t prop{};
     hip_check(hipGetDeviceProperties(&prop, ordinal), "hipGetDeviceProperties");
-    int cus = 0, xcds = 0;
-    std::int64_t hbm = 0;
-    lib.check(lib.device_info(ordinal, &cus, &xcds, &hbm), "device info");
-    std::ostringstream out;
-    out << prop.name << ' ' << prop.gcnArchName << ' ' << cus << " CUs " << xcds << " XCDs "
-        << (hbm >> 30) << " GiB HBM";
-    return out.str();
+    return std::string(prop.name) + ' ' + query_target(lib, ordinal).str();
 }
 
 void fill_layer_desc(sfg_layer_desc& d, const DecoderConfig& c, const DecoderPlanPolicy& policy,
@@ -798,6 +812,21 @@ DecoderBenchmarkResult execute_decoder_layer(const DecoderExecutablePlan& plan, 
     dev.sync();
     r.max_error = expected ? max_abs_error(r.output, *expected) : std::numeric_limits<double>::quiet_NaN();
     return r;
+}
+
+
+GpuTargetInfo GpuTargetInfo::detect(int device, const std::filesystem::path& library) {
+    const auto lib = load_library(library);
+    return query_target(*lib, device);
+}
+
+std::string GpuTargetInfo::str() const {
+    std::ostringstream out;
+    out << architecture << " wave" << wavefront << ' ' << compute_units << " CUs " << xcds << " XCDs "
+        << (lds_bytes_per_cu >> 10) << " KiB LDS/CU " << (l2_bytes_per_xcd >> 20) << " MiB L2/XCD "
+        << (hbm_bytes >> 30) << " GiB HBM " << std::fixed << std::setprecision(2) << engine_clock_ghz
+        << " GHz";
+    return out.str();
 }
 
 }  // namespace schedforge::hip

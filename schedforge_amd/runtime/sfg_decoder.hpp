@@ -28,6 +28,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <filesystem>
+#include <limits>
 #include <memory>
 #include <mutex>
 #include <optional>
@@ -164,8 +165,31 @@ struct DecoderBenchmarkResult {
     double residual_milliseconds = 0.0;
     double dispatch_overhead_milliseconds = 0.0;
     double tokens_per_second = 0.0;
-    double max_error = 0.0;
+    double max_error = std::numeric_limits<double>::quiet_NaN();  // NaN: nothing to compare with
     std::vector<float> output;
+};
+
+// The GPU target of a plan: the counterpart of the reference's TargetInfo
+// (include/schedforge/schedforge.h:15-34), which TargetInfo::detect() fills
+// for the host CPU (src/target.cpp:8-17).  detect() queries the device through
+// sfg_hip_target_info_v1: architecture, CUs, XCDs, LDS, L2, clock, HBM, and
+// the peaks those imply.
+struct GpuTargetInfo {
+    std::string architecture;
+    int wavefront = 64;
+    int compute_units = 0;
+    int xcds = 0;
+    int simds_per_cu = 4;
+    std::size_t lds_bytes_per_cu = 0;
+    std::size_t l2_bytes_per_xcd = 0;
+    std::size_t hbm_bytes = 0;
+    double engine_clock_ghz = 0.0;
+    double hbm_gbps = 0.0;
+    double mfma_bf16_tflops = 0.0;
+    double valu_fp32_tflops = 0.0;
+    // `library`: libsfg_hip.so to query (empty: beside this library).
+    static GpuTargetInfo detect(int device = 0, const std::filesystem::path& library = {});
+    std::string str() const;
 };
 
 class SfgHipLibrary;
@@ -368,6 +392,9 @@ struct DecoderOptimizationResult {
 // what this build's kernels reach on the box (calibration runs of the
 // benchmark; the values are the model's only inputs besides the shape).
 struct GpuCostModel {
+    // Spec figures of the target; for_target() takes them from a detected
+    // GpuTargetInfo (CUs, published HBM bandwidth, MFMA and VALU peaks).
+    static GpuCostModel for_target(const GpuTargetInfo& target);
     int compute_units = 256;
     double hbm_bytes_per_second = 8.0e12;
     double mfma_bf16_flops = 2.5e15;
@@ -462,11 +489,14 @@ std::vector<DecoderBenchmarkProfile> baseline_decoder_profiles();
 // the FLOP or weight budget, else compile, optionally optimise, and measure.
 // Configurations the GPU target does not lower are recorded as Skipped with
 // the reason.
+// `expected` (optional, rows x hidden) fills the record's max_error; without
+// it max_error is NaN.
 DecoderBenchmarkRecord benchmark_decoder_profile(const DecoderBenchmarkProfile& profile,
                                                  std::uint64_t max_real_flops,
                                                  std::size_t max_real_weight_bytes,
                                                  bool optimize_plan, int repetitions = 2,
-                                                 const DecoderCompileOptions& options = {});
+                                                 const DecoderCompileOptions& options = {},
+                                                 const std::vector<float>* expected = nullptr);
 // decoder_compiler.cpp:989-1030 and 1032-1058: the reference's column lists,
 // then precision, layer_tflops and layer_gbps (benchmark) and the GPU policy
 // fields in place of the CPU ones (candidates).

@@ -215,6 +215,15 @@ std::string DecoderOptimizationResult::dump() const {
     return out.str();
 }
 
+GpuCostModel GpuCostModel::for_target(const GpuTargetInfo& target) {
+    GpuCostModel m;
+    if (target.compute_units > 0) m.compute_units = target.compute_units;
+    if (target.hbm_gbps > 0.0) m.hbm_bytes_per_second = target.hbm_gbps * 1.0e9;
+    if (target.mfma_bf16_tflops > 0.0) m.mfma_bf16_flops = target.mfma_bf16_tflops * 1.0e12;
+    if (target.valu_fp32_tflops > 0.0) m.valu_fp32_flops = target.valu_fp32_tflops * 1.0e12;
+    return m;
+}
+
 ExecutablePlanOptimizer::ExecutablePlanOptimizer(GpuCostModel model) : model_(model) {}
 
 std::vector<DecoderPlanPolicy> ExecutablePlanOptimizer::policies(const DecoderConfig& c) const {
@@ -520,12 +529,17 @@ std::vector<DecoderBenchmarkProfile> baseline_decoder_profiles() {
 DecoderBenchmarkRecord benchmark_decoder_profile(const DecoderBenchmarkProfile& profile,
                                                  std::uint64_t max_real_flops,
                                                  std::size_t max_real_weight_bytes, bool optimize_plan,
-                                                 int repetitions, const DecoderCompileOptions& options) {
+                                                 int repetitions, const DecoderCompileOptions& options,
+                                                 const std::vector<float>* expected) {
     DecoderBenchmarkRecord record;
     record.profile = profile;
-    const ExecutablePlanOptimizer optimizer;
     const bool feasible = profile.estimated_flops <= max_real_flops &&
                           profile.estimated_weight_bytes <= max_real_weight_bytes;
+    // Analytical scores of measured profiles use the device's own figures;
+    // compile-only records (no GPU touched) the spec defaults.
+    const ExecutablePlanOptimizer optimizer(
+        feasible ? GpuCostModel::for_target(GpuTargetInfo::detect(options.device, options.library))
+                 : GpuCostModel{});
     if (!feasible) {
         record.evidence = DecoderEvidenceKind::CompileOnly;
         record.plan_cost = optimizer.evaluate(profile.config, options.policy.value_or(DecoderPlanPolicy{}));
@@ -565,7 +579,10 @@ DecoderBenchmarkRecord benchmark_decoder_profile(const DecoderBenchmarkProfile& 
             record.plan_cost = optimizer.evaluate(plan);
         }
         record.selected_policy = plan.policy.dump();
-        record.measured = execute_decoder_layer(plan, data, 1, repetitions);
+        if (expected && expected->size() != static_cast<std::size_t>(profile.config.rows()) *
+                                                 static_cast<std::size_t>(profile.config.hidden))
+            throw std::invalid_argument("expected output of " + profile.name + " has the wrong size");
+        record.measured = execute_decoder_layer(plan, data, 1, repetitions, expected);
         record.measured.output.clear();
         record.measured.output.shrink_to_fit();
         record.evidence = DecoderEvidenceKind::Measured;

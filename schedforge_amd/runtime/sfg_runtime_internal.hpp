@@ -49,6 +49,7 @@ public:
     decltype(&sfg_hip_metadata_v1) metadata = nullptr;
     decltype(&sfg_hip_last_error) last_error = nullptr;
     decltype(&sfg_hip_device_info_v1) device_info = nullptr;
+    decltype(&sfg_hip_target_info_v1) target_info = nullptr;
     decltype(&sfg_hip_pack_weight_v1) pack_weight = nullptr;
     decltype(&sfg_hip_quantize_weight_v1) quantize_weight = nullptr;
     decltype(&sfg_hip_preferred_weight_layout_v1) preferred_layout = nullptr;
@@ -67,6 +68,7 @@ public:
         bind(metadata, "sfg_hip_metadata_v1");
         bind(last_error, "sfg_hip_last_error");
         bind(device_info, "sfg_hip_device_info_v1");
+        bind(target_info, "sfg_hip_target_info_v1");
         bind(pack_weight, "sfg_hip_pack_weight_v1");
         bind(quantize_weight, "sfg_hip_quantize_weight_v1");
         bind(preferred_layout, "sfg_hip_preferred_weight_layout_v1");
@@ -164,6 +166,7 @@ struct DecoderExecutablePlan::Device {
 };
 
 // Shared by compile and package loading.
+GpuTargetInfo query_target(const SfgHipLibrary& lib, int ordinal);
 std::string describe_hardware(const SfgHipLibrary& lib, int ordinal);
 // The layer descriptor of a plan (everything but the device pointers).
 void fill_layer_desc(sfg_layer_desc& d, const DecoderConfig& c, const DecoderPlanPolicy& policy,

@@ -853,3 +853,28 @@ def test_gemm_tiled_rejects_prefill_shapes(lib):
     b = torch.zeros((256 * 256,), dtype=torch.int16, device="cuda")
     with pytest.raises(ValueError):
         _gemm(lib, a, BF16, b, BF16, 2048, 256, 256, EPI_NONE, layout=1)
+
+
+# ------------------------------------------------------------------ target descriptor
+def test_target_info_describes_the_device(lib):
+    """sfg_hip_target_info_v1 (the GPU counterpart of TargetInfo::detect,
+    target.cpp:8-17): queried counts are consistent with each other and with
+    torch's view of the device; peaks follow from them."""
+    t = _abi.TargetInfo()
+    _abi.check(lib.sfg_hip_target_info_v1(0, ctypes.byref(t)))
+    arch = t.architecture.decode()
+    props = torch.cuda.get_device_properties(0)
+    print(f"{arch}: wave {t.wavefront}, {t.compute_units} CUs, {t.xcds} XCDs, LDS {t.lds_bytes_per_cu} B/CU, "
+          f"L2 {t.l2_bytes_per_xcd} B/XCD, {t.hbm_bytes >> 30} GiB, {t.engine_clock_ghz:.2f} GHz, "
+          f"HBM {t.hbm_gbps:.0f} GB/s, bf16 {t.mfma_bf16_tflops:.0f} TFLOP/s, fp32 {t.valu_fp32_tflops:.1f}")
+    assert arch.startswith("gfx950")
+    assert t.wavefront == 64 and t.simds_per_cu == 4
+    assert t.compute_units == props.multi_processor_count
+    assert t.xcds >= 1 and t.compute_units % t.xcds == 0
+    assert t.lds_bytes_per_cu == 160 * 1024
+    assert t.hbm_bytes == props.total_memory
+    assert t.mfma_bf16_tflops == pytest.approx(t.compute_units * 4096 * t.engine_clock_ghz / 1e3)
+    assert t.hbm_gbps == 8000.0
+    cus, xcds, hbm = ctypes.c_int(), ctypes.c_int(), ctypes.c_int64()
+    _abi.check(lib.sfg_hip_device_info_v1(0, ctypes.byref(cus), ctypes.byref(xcds), ctypes.byref(hbm)))
+    assert (cus.value, xcds.value, hbm.value) == (t.compute_units, t.xcds, t.hbm_bytes)

@@ -23,10 +23,11 @@ from pathlib import Path
 import numpy as np
 import pytest
 
+import oracle
 from schedforge_amd import CONFIG_SEEDS
 from schedforge_amd.build import DECODER_CLI, LIB
 
-from _helpers import SMALL
+from _helpers import SMALL, TOL
 from test_runtime import cfg_args, load, run_cli
 
 pytestmark = pytest.mark.skipif(not DECODER_CLI.exists() or not LIB.exists(),
@@ -237,11 +238,21 @@ def test_package_round_trip_is_bit_exact(tmp_path, name):
     manifest = (pkg / "manifest.sfe").read_text()
     assert f"precision={cfg.dtype}" in manifest and "target=gfx950" in manifest
     assert (pkg / "plan.sfe").read_text() == (tmp_path / "plan.sfe").read_text()
+    # the oracle's output for the same seeded inputs: the loaded plan is checked
+    # against it (benchmark_aot_package validates against the reference,
+    # aot_runtime.cpp:346-350), not only against the plan it was saved from
+    ref = oracle.decoder_layer(cfg, oracle.make_layer_data(cfg, seed))
+    expect = tmp_path / "expect.bin"
+    ref.astype(np.float32).tofile(expect)
     print("sfg-decoder load-package", name, flush=True)
     r = run_cli([f"--load-package={pkg}", f"--seed={seed}", "--repetitions=1",
                  f"--router-bias-std={cfg.router_bias_std!r}", f"--dump-output={b}",
+                 f"--expect={expect}", f"--max-error={TOL[cfg.dtype]}",
                  "-o", str(tmp_path / "plan2.sfe")], timeout=240)
-    assert r.returncode == 0, r.stderr
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr
+    assert "max relative error" in r.stdout
+    loaded = load(b).reshape(ref.shape)
+    assert oracle.rel_error(loaded, ref) < TOL[cfg.dtype]
     np.testing.assert_array_equal(load(a).view(np.uint32), load(b).view(np.uint32))
     compiled = (tmp_path / "plan.sfe").read_text().splitlines()
     reloaded = (tmp_path / "plan2.sfe").read_text().splitlines()

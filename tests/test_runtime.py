@@ -22,7 +22,7 @@ import oracle
 from schedforge_amd import CONFIGS, CONFIG_SEEDS
 from schedforge_amd.build import BENCH_CLI, DECODER_CLI
 
-from _helpers import SMALL, TOL
+from _helpers import ROUTE_LOGIT_DEV_MAX, SMALL, TOL, near_tie_rows, route_logits
 
 pytestmark = pytest.mark.skipif(not DECODER_CLI.exists(), reason="sfg-decoder not built")
 
@@ -212,16 +212,22 @@ def test_cli_dense_layer_matches_oracle(tmp_path, name):
 @pytest.mark.gpu
 @pytest.mark.parametrize("name", ["c3", "c5"])
 def test_cli_moe_layer_matches_oracle(tmp_path, name):
-    """Device routing: a near-tie token may pick another expert when the
-    residual stream differs in its last bits, so rows are checked one by one
-    and at most a handful may exceed the tolerance (the driver's own exit
-    status uses the whole-tensor bound and is not asserted here)."""
+    """Device routing through the C++ runtime.  The driver reports no router
+    input, so the deviation bound that the layer tests measure
+    (ROUTE_LOGIT_DEV_MAX) stands in: a row may exceed the tolerance only if it
+    is a near tie of the oracle's logits within twice that bound (the driver's
+    own exit status uses the whole-tensor bound and is not asserted here)."""
     cfg = SMALL[name]
     r, ref, got, _ = _gpu_case(tmp_path, cfg, CONFIG_SEEDS[name] + 23)
     assert got is not None, r.stderr
+    d = oracle.make_layer_data(cfg, CONFIG_SEEDS[name] + 23)
+    _, taps = oracle.decoder_layer(cfg, d, taps=True)
+    ties = near_tie_rows(route_logits(taps["normalized2"], d.router_weight, d.router_bias),
+                         cfg.top_k, 2 * ROUTE_LOGIT_DEV_MAX)
     rows_err = np.max(np.abs(got - ref), axis=1) / max(np.max(np.abs(ref)), 1e-6)
     bad = np.nonzero(rows_err >= TOL[cfg.dtype])[0]
-    assert len(bad) <= max(1, cfg.rows // 200), bad
+    print(f"{name}: rows over tolerance {bad.tolist()}, near ties {len(ties)}")
+    assert set(bad.tolist()) <= set(ties.tolist()), (bad, ties)
 
 
 @pytest.mark.gpu
@@ -269,3 +275,36 @@ def test_bench_optimizer_suite(tmp_path):
     dec = [c for c in cands if c["profile"] == "tiny-decode-kv512"]
     assert {c["weight_layout"] for c in dec} == {"nk"}
     assert len({c["kv_splits"] for c in dec}) >= 4
+
+
+@pytest.mark.gpu
+def test_bench_harness_fills_max_error_from_expected_outputs(tmp_path):
+    """benchmark_decoder_profile with expected outputs (--expect-dir): a measured
+    profile with DIR/PROFILE.f32 reports max_error against it (the reference's
+    max_error column, decoder_compiler.cpp:1016); the others report NaN.  The
+    expected outputs are the oracle's on the harness's own inputs (seed 101,
+    bit-identical generators) for two tiny bf16 profiles of
+    realistic_decoder_profiles."""
+    tiny = dict(batch=1, hidden=512, intermediate=1376, query_heads=8, kv_heads=2, head_dim=64,
+                dtype="bf16")
+    cfgs = {"tiny-prefill-s128": CONFIGS["c2"].replace(sequence=128, context_sequence=0, **tiny),
+            "tiny-decode-kv512": CONFIGS["c2"].replace(sequence=1, context_sequence=512, **tiny)}
+    exp = tmp_path / "expect"
+    exp.mkdir()
+    refs = {}
+    for name, cfg in cfgs.items():
+        refs[name] = oracle.decoder_layer(cfg, oracle.make_layer_data(cfg, 101))
+        refs[name].astype(np.float32).tofile(exp / f"{name}.f32")
+    out = tmp_path / "h.csv"
+    r = run_bench(["--filter=tiny-", "--repetitions=1", f"--expect-dir={exp}", f"--output={out}"],
+                  timeout=300)
+    print(r.stdout[-3000:], r.stderr[-2000:])
+    assert r.returncode == 0, r.stderr
+    rows = {row["profile"]: row for row in read_csv(out)}
+    for name, ref in refs.items():
+        assert rows[name]["evidence"] == "measured"
+        err = float(rows[name]["max_error"])
+        assert np.isfinite(err) and err / np.max(np.abs(ref)) < TOL["bf16"], (name, err)
+        assert f"max_error=" in next(l for l in r.stdout.splitlines() if f"] {name} " in l)
+    measured_others = [n for n, row in rows.items() if n not in refs and row["evidence"] == "measured"]
+    assert measured_others and all(np.isnan(float(rows[n]["max_error"])) for n in measured_others)
