@@ -72,15 +72,17 @@ enum sfg_layout { SFG_LAYOUT_NK = 0, SFG_LAYOUT_TILED = 1 };
  * optimiser (ExecutablePlanOptimizer, decoder_compiler.cpp:750-861) searches it. */
 enum sfg_gemm_tile {
     SFG_TILE_AUTO = 0,       /* the largest tile that still gives >= 512 workgroups
-                                (256 x 256: W8 for GLU epilogues, else PP); grouped
-                                GLU products take W8 from 128 workgroups up         */
+                                (256 x 256 as V); grouped GLU products take V from
+                                128 workgroups up                                   */
     SFG_TILE_256x256_PP = 1, /* eight waves as two ping-pong groups of four          */
     SFG_TILE_256x256_W8 = 2, /* eight waves (2 x 4), 128 x 64 per wave               */
     SFG_TILE_256x256_W4 = 3, /* four waves (2 x 2), 128 x 128 per wave               */
     SFG_TILE_256x128 = 4,    /* four waves, two workgroups per CU                    */
     SFG_TILE_128x256 = 5,
     SFG_TILE_128x128 = 6,
-    SFG_TILE_COUNT = 7
+    SFG_TILE_256x256_V = 7,  /* four waves (2 x 2), 64-k slabs prefetched two ahead
+                                through registers into two LDS stages               */
+    SFG_TILE_COUNT = 8
 };
 
 enum sfg_epilogue {

@@ -20,7 +20,7 @@ EPI_NONE, EPI_RESIDUAL, EPI_SWIGLU, EPI_GLU_SILU_UP = 0, 1, 2, 3
 LAYOUT_NK, LAYOUT_TILED = 0, 1
 # sfg_gemm_tile
 TILE_AUTO, TILE_256x256_PP, TILE_256x256_W8, TILE_256x256_W4, TILE_256x128, TILE_128x256, \
-    TILE_128x128, TILE_COUNT = range(8)
+    TILE_128x128, TILE_256x256_V, TILE_COUNT = range(9)
 
 TAP_ATTN, TAP_RESIDUAL1, TAP_NORM2, TAP_ROUTE_INPUT, TAP_ROUTE_IDS, TAP_ROUTE_WEIGHTS, NUM_TAPS = range(7)
 

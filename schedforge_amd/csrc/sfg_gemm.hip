@@ -969,6 +969,26 @@ __device__ __forceinline__ void interleave_groups() {
     }
 }
 
+// Scheduling groups for a run of NM MFMAs that also moves data, spread so the
+// four waves of a CU never queue more than one LDS access per MFMA each: LDS
+// fragment reads after MFMAs 0, RS, 2 RS, ... (NR of them), and LDS writes,
+// each followed by the VMEM load that refills its registers, after MFMAs
+// WS0, WS0 + 2, ... (NW of them).
+template <int NM, int NR, int RS, int NW, int WS0, int I = 0>
+__device__ __forceinline__ void spread_moves() {
+    if constexpr (I < NM) {
+        constexpr bool read = I % RS == 0 && I / RS < NR;
+        constexpr bool write = I >= WS0 && (I - WS0) % 2 == 0 && (I - WS0) / 2 < NW;
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                    // MFMA
+        if constexpr (read) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
+        if constexpr (write) {
+            __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);                // DS write
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                // VMEM load
+        }
+        spread_moves<NM, NR, RS, NW, WS0, I + 1>();
+    }
+}
+
 template <int BM, int BN, int NW>
 struct DmaShapeTraits {
     static constexpr bool big = BM * BN > 256 * 128;
@@ -980,13 +1000,19 @@ struct DmaShapeTraits {
     static constexpr int dma_bytes = 16;  // per lane per LDS DMA instruction (dwordx4)
 };
 
-template <int BM, int BN, int NW, int EPI, bool PP = false>
+// s_waitcnt lgkmcnt(0), vmcnt and expcnt untouched: this wave's LDS accesses
+// (reads and writes) are done.
+__device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+template <int BM, int BN, int NW, int EPI, bool PP = false, bool VPF = false>
 __global__ __launch_bounds__(NW * 64)
 __attribute__((amdgpu_waves_per_eu(DmaShapeTraits<BM, BN, NW>::occupancy,
                                    DmaShapeTraits<BM, BN, NW>::occupancy)))
 void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
     static_assert(!PP || (NW == 8 && DmaShapeTraits<BM, BN, NW>::stages == 4),
                   "ping-pong pairs two four-wave groups over a four-stage ring");
+    static_assert(!VPF || (BM == 256 && BN == 256 && NW == 4 && !PP),
+                  "the register-prefetch loop runs the four-wave 256 x 256 tile");
     constexpr bool kGlu = EpiTraits<EPI>::glu;
     constexpr int kStages = DmaShapeTraits<BM, BN, NW>::stages;
     constexpr int kWavesM = 2, kWavesN = NW / 2;
@@ -1188,6 +1214,161 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
         interleave_groups<WM * WN, WM + WN, 0>();
         __builtin_amdgcn_sched_barrier(0);
     };
+    if constexpr (VPF) {
+        // Register prefetch, 64-k slabs, one barrier per slab.  Each wave owns
+        // 128 x 128 of the tile (4 x 4 MFMA tiles, accumulators in AGPRs).
+        // The four 32 KB arrays hold two stages of one 256 x 64 slab per
+        // operand: stage 0 = (sS0 A, sS1 B), stage 1 = (sS2 A, sS3 B), rows of
+        // 128 B with chunk c of row r at slot c ^ ((r >> 1) & 7), so the 16
+        // lanes of one ds_read_b128 / ds_write_b128 pass touch 16 distinct
+        // 16-byte bank groups.  Global loads go to registers two slabs ahead:
+        // thread t fetches chunk t & 7 of rows (t >> 3) + 32 i (i < 8) of A
+        // and of B, 16 dwordx4 loads per slab.  Slab s runs its four 16-k
+        // steps of 16 MFMAs each; under each step's MFMAs the wave reads the
+        // next step's fragments, writes a quarter of slab s + 1 from registers
+        // into the other stage (whose last readers passed the barrier that
+        // opened slab s) and reloads those registers with slab s + 3.  After
+        // the fourth step: wait for this wave's LDS writes, barrier, read the
+        // first fragments of slab s + 1.
+        // Every slab issues exactly one load group (past the end it re-fetches
+        // the last slab), so the compiler's vmcnt waits see one pattern.
+        constexpr int kBK = 64;
+        constexpr int kRowB = kBK * 2;           // bytes per LDS row
+        constexpr int kRows32 = 32 * kRowB;      // bytes of 32 rows
+        const int64_t nslab = p.k / kBK;
+        const int grow = tid >> 3, gch = tid & 7;
+        uint32_t va[8], vb[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int local = grow + 32 * i;
+            const int64_t r = row0 + local;
+            int64_t src = r < re ? r : row0;
+            if (p.a_rows) src = p.a_rows[src];
+            if (src < 0 || src >= p.a_rows_limit) src = 0;
+            va[i] = static_cast<uint32_t>((src * p.lda + gch * 8) * 2);
+            int64_t brow;
+            if (kGlu) {
+                const int block = local >> 5;
+                const int64_t col = ncol0 + (block >> 1) * 32 + (local & 31);
+                brow = col < p.n ? ((block & 1) ? p.n + col : col) : 0;
+            } else {
+                const int64_t col = ncol0 + local;
+                brow = col < p.n ? col : 0;
+            }
+            vb[i] = static_cast<uint32_t>((brow * p.ldb + gch * 8) * 2);
+        }
+        // rows grow + 32 i share (row >> 1) & 7, so one swizzled offset serves all i
+        const uint32_t wr = static_cast<uint32_t>(grow * kRowB + ((gch ^ ((grow >> 1) & 7)) * 16));
+        const int fsw = (l32 >> 1) & 7;
+        uint32_t ra_off[4], rb_off[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            ra_off[j] = static_cast<uint32_t>((wm * 128 + l32) * kRowB + (((2 * j + khalf) ^ fsw) * 16));
+            rb_off[j] = static_cast<uint32_t>((wn * 128 + l32) * kRowB + (((2 * j + khalf) ^ fsw) * 16));
+        }
+        char* const stA[2] = {reinterpret_cast<char*>(sS0), reinterpret_cast<char*>(sS2)};
+        char* const stB[2] = {reinterpret_cast<char*>(sS1), reinterpret_cast<char*>(sS3)};
+        uint4 pf[2][16];
+        // slab kt's chunks i in [i0, i1) of A and of B into registers / from
+        // registers into stage st
+        auto gload = [&](uint4 (&r)[16], int64_t kt, int i0, int i1) {
+            const int soff = static_cast<int>(min(kt, nslab - 1) * kBK * 2);
+#pragma unroll
+            for (int i = i0; i < i1; ++i) {
+                r[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ra, va[i], soff, 0));
+                r[8 + i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rb_, vb[i], soff, 0));
+            }
+        };
+        auto lwrite = [&](const uint4 (&r)[16], int st, int i0, int i1) {
+#pragma unroll
+            for (int i = i0; i < i1; ++i) {
+                *reinterpret_cast<uint4*>(stA[st] + wr + i * kRows32) = r[i];
+                *reinterpret_cast<uint4*>(stB[st] + wr + i * kRows32) = r[8 + i];
+            }
+        };
+        bf16x8 fa[2][4], fb[2][4];
+        // in the order the row-major MFMAs consume them: a0, b0..b3, a1..a3
+        auto frags = [&](int st, int j, bf16x8 (&a)[4], bf16x8 (&b)[4]) {
+            a[0] = as_bf16x8(*reinterpret_cast<const uint4*>(stA[st] + ra_off[j]));
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                b[i] = as_bf16x8(*reinterpret_cast<const uint4*>(stB[st] + rb_off[j] + i * kRows32));
+#pragma unroll
+            for (int i = 1; i < 4; ++i)
+                a[i] = as_bf16x8(*reinterpret_cast<const uint4*>(stA[st] + ra_off[j] + i * kRows32));
+        };
+        auto mfma_rows = [&](const bf16x8 (&a)[4], const bf16x8 (&b)[4], int i0, int i1) {
+#pragma unroll
+            for (int i = i0; i < i1; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+        };
+        auto mfma16 = [&](const bf16x8 (&a)[4], const bf16x8 (&b)[4]) { mfma_rows(a, b, 0, 4); };
+        auto mfma_at = [&](const bf16x8 (&a)[4], const bf16x8 (&b)[4], int i, int j) {
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+        };
+        // One slab; stage `cur`, the registers of slab s + 1 in set `rs`.
+        // k-steps 0..2 read the next step's fragments (8 LDS reads); k-steps 0
+        // and 1 also move chunks 0-3 and 4-7 of slab s + 1 into the other
+        // stage (8 LDS writes each, every one followed by the load of slab
+        // s + 3 into the registers it freed), reads and writes alternating
+        // over the step's 16 MFMAs; k-step 2 issues its reads under its first
+        // 8 MFMAs.  k-step 3 starts with two MFMAs, waits for this wave's LDS
+        // accesses and meets the other waves at the barrier, then reads the
+        // first fragments of slab s + 1 under its remaining 14 MFMAs.
+        auto slab64 = [&](int64_t s, int cur, auto rs_c) {
+            constexpr int rs = decltype(rs_c)::value;
+            frags(cur, 1, fa[1], fb[1]);
+            lwrite(pf[rs], cur ^ 1, 0, 4);
+            gload(pf[rs], s + 3, 0, 4);
+            mfma16(fa[0], fb[0]);
+            spread_moves<16, 8, 2, 8, 1>();
+            __builtin_amdgcn_sched_barrier(0);
+            frags(cur, 2, fa[0], fb[0]);
+            lwrite(pf[rs], cur ^ 1, 4, 8);
+            gload(pf[rs], s + 3, 4, 8);
+            mfma16(fa[1], fb[1]);
+            spread_moves<16, 8, 2, 8, 1>();
+            __builtin_amdgcn_sched_barrier(0);
+            frags(cur, 3, fa[1], fb[1]);
+            mfma16(fa[0], fb[0]);
+            spread_moves<16, 8, 1, 0, 0>();
+            __builtin_amdgcn_sched_barrier(0);
+            mfma_at(fa[1], fb[1], 0, 0);
+            mfma_at(fa[1], fb[1], 0, 1);
+            __builtin_amdgcn_sched_barrier(0);
+            wait_lds();
+            barrier_no_fence();
+            frags(cur ^ 1, 0, fa[0], fb[0]);
+            mfma_at(fa[1], fb[1], 0, 2);
+            mfma_at(fa[1], fb[1], 0, 3);
+            mfma_rows(fa[1], fb[1], 1, 4);
+            spread_moves<14, 8, 1, 0, 0>();
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        using rs0 = std::integral_constant<int, 0>;
+        using rs1 = std::integral_constant<int, 1>;
+        // the prologue keeps the steady state's load order (slab 1, then slab
+        // 2) so the compiler's vmcnt waits in the loop stay partial
+        gload(pf[0], 0, 0, 8);
+        __builtin_amdgcn_sched_barrier(0);
+        gload(pf[1], 1, 0, 8);
+        __builtin_amdgcn_sched_barrier(0);
+        lwrite(pf[0], 0, 0, 8);
+        __builtin_amdgcn_sched_barrier(0);
+        gload(pf[0], 2, 0, 8);
+        __builtin_amdgcn_sched_barrier(0);
+        wait_lds();
+        barrier_no_fence();
+        frags(0, 0, fa[0], fb[0]);
+        int64_t s = 0;
+        for (; s + 2 <= nslab; s += 2) {
+            slab64(s, 0, rs1{});
+            slab64(s + 1, 1, rs0{});
+        }
+        if (s < nslab) slab64(s, 0, rs1{});
+    } else {
     issue(sS0, 0);
     issue(sS1, min(int64_t(1), slabs - 1) * kRK);
     if constexpr (kStages == 4) issue(sS2, min(int64_t(2), slabs - 1) * kRK);
@@ -1304,6 +1485,7 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
             slab(kt + 1, sS1, sS0, sS2);
             slab(kt + 2, sS2, sS1, sS0);
         }
+    }
     }
     }
     }
@@ -1537,27 +1719,29 @@ void launch_big_b(const TiledArgs& a, dim3 grid, int tm, int tn, int epi, hipStr
     }
 }
 
-template <int BM, int BN, int NW = 4, bool PP = false>
+template <int BM, int BN, int NW = 4, bool PP = false, bool VPF = false>
 void launch_dma_b(const TiledArgs& a, dim3 grid, int tm, int tn, int epi, hipStream_t s) {
     switch (epi) {
-        case SFG_EPI_NONE: gemm_dma_kernel<BM, BN, NW, SFG_EPI_NONE, PP><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
-        case SFG_EPI_RESIDUAL: gemm_dma_kernel<BM, BN, NW, SFG_EPI_RESIDUAL, PP><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
-        case SFG_EPI_SWIGLU: gemm_dma_kernel<BM, BN, NW, SFG_EPI_SWIGLU, PP><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
-        case kEpiQkvRope: gemm_dma_kernel<BM, BN, NW, kEpiQkvRope, PP><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
-        default: gemm_dma_kernel<BM, BN, NW, SFG_EPI_GLU_SILU_UP, PP><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
+        case SFG_EPI_NONE: gemm_dma_kernel<BM, BN, NW, SFG_EPI_NONE, PP, VPF><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
+        case SFG_EPI_RESIDUAL: gemm_dma_kernel<BM, BN, NW, SFG_EPI_RESIDUAL, PP, VPF><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
+        case SFG_EPI_SWIGLU: gemm_dma_kernel<BM, BN, NW, SFG_EPI_SWIGLU, PP, VPF><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
+        case kEpiQkvRope: gemm_dma_kernel<BM, BN, NW, kEpiQkvRope, PP, VPF><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
+        default: gemm_dma_kernel<BM, BN, NW, SFG_EPI_GLU_SILU_UP, PP, VPF><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
     }
 }
 
 // Output tile of the direct-to-LDS kernel.  SFG_TILE_AUTO: the largest tile
-// (256 x 256 as two ping-pong groups of four waves) that still gives at least
-// 512 workgroups (two per CU); smaller problems take smaller tiles.  A plan may
-// name the tile instead (sfg_layer_desc::gemm_tile); results do not depend on it.
-struct DmaShape { int bm, bn, waves; bool pingpong; };
+// (256 x 256 on the four-wave register-prefetch loop) that still gives at
+// least 512 workgroups (two per CU); smaller problems take smaller tiles.  A
+// plan may name the tile instead (sfg_layer_desc::gemm_tile); results do not
+// depend on it.
+struct DmaShape { int bm, bn, waves; bool pingpong; bool vpf = false; };
 DmaShape dma_shape_of(int tile) {
     switch (tile) {
         case SFG_TILE_256x256_PP: return {256, 256, 8, true};
         case SFG_TILE_256x256_W8: return {256, 256, 8, false};
         case SFG_TILE_256x256_W4: return {256, 256, 4, false};
+        case SFG_TILE_256x256_V: return {256, 256, 4, false, true};
         case SFG_TILE_256x128: return {256, 128, 4, false};
         case SFG_TILE_128x256: return {128, 256, 4, false};
         default: return {128, 128, 4, false};
@@ -1565,19 +1749,16 @@ DmaShape dma_shape_of(int tile) {
 }
 DmaShape pick_dma_shape(int64_t m, int64_t n_out, bool glu, int groups, int tile) {
     if (tile > SFG_TILE_AUTO && tile < SFG_TILE_COUNT) return dma_shape_of(tile);
-    // Grouped GLU (expert W1|W3): the eight-wave 256 x 256 tile once it has
-    // work for half the CUs -- measured faster than 256 x 128 on the MoE
-    // prefill shape although its tile count stays under 512.
+    // Grouped GLU (expert W1|W3): the 256 x 256 tile once it has work for half
+    // the CUs -- measured faster than 256 x 128 on the MoE prefill shape
+    // although its tile count stays under 512.
     if (groups > 1 && glu && ((m + 255) / 256 + groups) * ((n_out + 127) / 128) >= 128)
-        return dma_shape_of(SFG_TILE_256x256_W8);
-    for (const int t : {SFG_TILE_256x256_PP, SFG_TILE_256x128, SFG_TILE_128x128}) {
+        return dma_shape_of(SFG_TILE_256x256_V);
+    for (const int t : {SFG_TILE_256x256_V, SFG_TILE_256x128, SFG_TILE_128x128}) {
         const DmaShape sh = dma_shape_of(t);
         const int64_t cols = glu ? sh.bn / 2 : sh.bn;
         const int64_t tiles = ((m + sh.bm - 1) / sh.bm + (groups > 1 ? groups : 0)) * ((n_out + cols - 1) / cols);
-        // 256 x 256: the GLU epilogue (two accumulator blocks per output)
-        // runs best on the plain eight-wave tile, the others as ping-pong
-        // (measured on the prefill shapes).
-        if (tiles >= 512) return (t == SFG_TILE_256x256_PP && glu) ? dma_shape_of(SFG_TILE_256x256_W8) : sh;
+        if (tiles >= 512) return sh;
     }
     return dma_shape_of(SFG_TILE_128x128);
 }
@@ -1756,7 +1937,10 @@ int launch_gemm(const GemmProblem& problem, void* workspace, size_t workspace_by
         const dim3 grid = p.offsets ? dim3(static_cast<unsigned>(tn), static_cast<unsigned>(tm + groups))
                                     : dim3(static_cast<unsigned>(tm * tn));
         const int itm = p.offsets ? 0 : static_cast<int>(tm);
-        if (sh.bm == 256 && sh.bn == 256 && sh.pingpong)
+        static_assert(kGK % 64 == 0, "the register-prefetch loop walks 64-k slabs");
+        if (sh.vpf)
+            launch_dma_b<256, 256, 4, false, true>(a, grid, itm, static_cast<int>(tn), p.epilogue, stream);
+        else if (sh.bm == 256 && sh.bn == 256 && sh.pingpong)
             launch_dma_b<256, 256, 8, true>(a, grid, itm, static_cast<int>(tn), p.epilogue, stream);
         else if (sh.bm == 256 && sh.bn == 256 && sh.waves == 8) launch_dma_b<256, 256, 8>(a, grid, itm, static_cast<int>(tn), p.epilogue, stream);
         else if (sh.bm == 256 && sh.bn == 256) launch_dma_b<256, 256>(a, grid, itm, static_cast<int>(tn), p.epilogue, stream);

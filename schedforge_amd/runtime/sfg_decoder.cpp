@@ -320,6 +320,7 @@ std::string gemm_tile_name(int tile) {
         case SFG_TILE_256x128: return "256x128";
         case SFG_TILE_128x256: return "128x256";
         case SFG_TILE_128x128: return "128x128";
+        case SFG_TILE_256x256_V: return "256x256v";
         default: return "tile" + std::to_string(tile);
     }
 }

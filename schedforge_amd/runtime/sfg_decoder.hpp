@@ -407,7 +407,7 @@ struct GpuCostModel {
     double fp32_gemm_efficiency = 0.30;
     double flash_efficiency = 0.42;
     // per sfg_gemm_tile: efficiency of one full wave of tiles
-    double tile_efficiency[SFG_TILE_COUNT] = {0.0, 0.50, 0.47, 0.42, 0.44, 0.40, 0.36};
+    double tile_efficiency[SFG_TILE_COUNT] = {0.0, 0.43, 0.45, 0.42, 0.44, 0.40, 0.36, 0.49};
 };
 
 class ExecutablePlanOptimizer {

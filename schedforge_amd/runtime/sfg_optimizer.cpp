@@ -39,7 +39,8 @@ TileShape tile_shape(int tile) {
     switch (tile) {
         case SFG_TILE_256x256_PP:
         case SFG_TILE_256x256_W8:
-        case SFG_TILE_256x256_W4: return {256, 256, 1};
+        case SFG_TILE_256x256_W4:
+        case SFG_TILE_256x256_V: return {256, 256, 1};
         case SFG_TILE_256x128: return {256, 128, 2};
         case SFG_TILE_128x256: return {128, 256, 2};
         default: return {128, 128, 2};
@@ -47,13 +48,16 @@ TileShape tile_shape(int tile) {
 }
 
 // SFG_TILE_AUTO as the launcher resolves it: the largest tile with >= 512
-// workgroups (the 256 x 256 one as W8 for GLU epilogues, else ping-pong).
+// workgroups (256 x 256 on the register-prefetch loop), and that tile for
+// grouped GLU products from 128 workgroups up.
 int auto_tile(std::int64_t m, std::int64_t n_out, bool glu, int groups) {
-    for (const int t : {SFG_TILE_256x256_PP, SFG_TILE_256x128, SFG_TILE_128x128}) {
+    if (groups > 1 && glu && (ceil_div(m, 256) + groups) * ceil_div(n_out, 128) >= 128)
+        return SFG_TILE_256x256_V;
+    for (const int t : {SFG_TILE_256x256_V, SFG_TILE_256x128, SFG_TILE_128x128}) {
         const TileShape s = tile_shape(t);
         const std::int64_t cols = glu ? s.bn / 2 : s.bn;
         const std::int64_t tiles = (ceil_div(m, s.bm) + (groups > 1 ? groups : 0)) * ceil_div(n_out, cols);
-        if (tiles >= 512) return (t == SFG_TILE_256x256_PP && glu) ? SFG_TILE_256x256_W8 : t;
+        if (tiles >= 512) return t;
     }
     return SFG_TILE_128x128;
 }

@@ -117,20 +117,24 @@ def test_gemm_every_tile_policy_exact(lib, tile, m, n, k, epi):
         np.testing.assert_array_equal(host(c), _ref_epilogue(acc, epi, n, res).astype(np.float32))
 
 
+@pytest.mark.parametrize("tile,k", [(_abi.TILE_256x256_PP, 64), (_abi.TILE_256x256_V, 64),
+                                    (_abi.TILE_256x256_V, 128)])
 @pytest.mark.parametrize("epi", [EPI_NONE, EPI_RESIDUAL, EPI_SWIGLU, EPI_GLU_SILU_UP])
-def test_gemm_many_tiles_exact(lib, epi):
-    """More 256 x 256 ping-pong tiles than the CUs hold at once, ragged in both
-    directions, K shorter than the LDS ring: small-integer operands keep every
-    sum exact, so a tile mapped twice, skipped, or read from a stale stage shows
-    as a difference."""
-    m, n, k = 4400, 4360, 96
+def test_gemm_many_tiles_exact(lib, epi, tile, k):
+    """More 256 x 256 tiles than the CUs hold at once, ragged in both
+    directions, K shorter than the LDS ring (ping-pong: two 32-k slabs in a
+    four-stage ring; register prefetch: one or two 64-k slabs, fewer than the
+    three it keeps in flight): small-integer operands keep every sum exact, so
+    a tile mapped twice, skipped, or read from a stale stage shows as a
+    difference."""
+    m, n = 4400, 4360
     glu = epi in (EPI_SWIGLU, EPI_GLU_SILU_UP)
-    rng = np.random.default_rng(977 + epi)
+    rng = np.random.default_rng(977 + epi + k)
     a = rng.integers(-3, 4, size=(m, k)).astype(np.float32)
     b = rng.integers(-3, 4, size=((2 * n) if glu else n, k)).astype(np.float32)
     res = rng.integers(-5, 6, size=(m, n)).astype(np.float32)
     c = _gemm(lib, bf16_dev(a), BF16, bf16_dev(b), BF16, m, n, k, epi,
-              residual=dev(res) if epi == EPI_RESIDUAL else None, tile=_abi.TILE_256x256_PP)
+              residual=dev(res) if epi == EPI_RESIDUAL else None, tile=tile)
     acc = a.astype(np.float64) @ b.T.astype(np.float64)
     if glu:
         np.testing.assert_allclose(host(c), _ref_epilogue(acc, epi, n), rtol=1e-5, atol=1e-5)
