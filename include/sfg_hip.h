@@ -80,8 +80,8 @@ enum sfg_gemm_tile {
     SFG_TILE_256x128 = 4,    /* four waves, two workgroups per CU                    */
     SFG_TILE_128x256 = 5,
     SFG_TILE_128x128 = 6,
-    SFG_TILE_256x256_V = 7,  /* four waves (2 x 2), 64-k slabs prefetched two ahead
-                                through registers into two LDS stages               */
+    SFG_TILE_256x256_V = 7,  /* four waves (2 x 2), 64-k slabs by LDS DMA, A in two
+                                stages and B in three (160 KB of LDS)               */
     SFG_TILE_COUNT = 8
 };
 

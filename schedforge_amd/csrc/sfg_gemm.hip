@@ -969,23 +969,18 @@ __device__ __forceinline__ void interleave_groups() {
     }
 }
 
-// Scheduling groups for a run of NM MFMAs that also moves data, spread so the
-// four waves of a CU never queue more than one LDS access per MFMA each: LDS
-// fragment reads after MFMAs 0, RS, 2 RS, ... (NR of them), and LDS writes,
-// each followed by the VMEM load that refills its registers, after MFMAs
-// WS0, WS0 + 2, ... (NW of them).
-template <int NM, int NR, int RS, int NW, int WS0, int I = 0>
-__device__ __forceinline__ void spread_moves() {
+// Scheduling groups for a run of NM MFMAs that also reads fragments and
+// issues loads: one LDS fragment read after each of the first NR MFMAs, and NV
+// VMEM instructions (LDS DMA) spread evenly over all NM, so the four waves of
+// a CU never queue a burst of LDS reads or of DMA requests.
+template <int NM, int NR, int NV, int I = 0>
+__device__ __forceinline__ void spread_reads_loads() {
     if constexpr (I < NM) {
-        constexpr bool read = I % RS == 0 && I / RS < NR;
-        constexpr bool write = I >= WS0 && (I - WS0) % 2 == 0 && (I - WS0) / 2 < NW;
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                    // MFMA
-        if constexpr (read) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
-        if constexpr (write) {
-            __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);                // DS write
-            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                // VMEM load
-        }
-        spread_moves<NM, NR, RS, NW, WS0, I + 1>();
+        constexpr int loads = (I + 1) * NV / NM - I * NV / NM;
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                          // MFMA
+        if constexpr (I < NR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);       // DS read
+        if constexpr (loads > 0) __builtin_amdgcn_sched_group_barrier(0x020, loads, 0);  // VMEM
+        spread_reads_loads<NM, NR, NV, I + 1>();
     }
 }
 
@@ -1004,15 +999,15 @@ struct DmaShapeTraits {
 // (reads and writes) are done.
 __device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
-template <int BM, int BN, int NW, int EPI, bool PP = false, bool VPF = false>
+template <int BM, int BN, int NW, int EPI, bool PP = false, bool S64 = false>
 __global__ __launch_bounds__(NW * 64)
 __attribute__((amdgpu_waves_per_eu(DmaShapeTraits<BM, BN, NW>::occupancy,
                                    DmaShapeTraits<BM, BN, NW>::occupancy)))
 void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
     static_assert(!PP || (NW == 8 && DmaShapeTraits<BM, BN, NW>::stages == 4),
                   "ping-pong pairs two four-wave groups over a four-stage ring");
-    static_assert(!VPF || (BM == 256 && BN == 256 && NW == 4 && !PP),
-                  "the register-prefetch loop runs the four-wave 256 x 256 tile");
+    static_assert(!S64 || (BM == 256 && BN == 256 && NW == 4 && !PP),
+                  "the 64-k slab loop runs the four-wave 256 x 256 tile");
     constexpr bool kGlu = EpiTraits<EPI>::glu;
     constexpr int kStages = DmaShapeTraits<BM, BN, NW>::stages;
     constexpr int kWavesM = 2, kWavesN = NW / 2;
@@ -1214,38 +1209,45 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
         interleave_groups<WM * WN, WM + WN, 0>();
         __builtin_amdgcn_sched_barrier(0);
     };
-    if constexpr (VPF) {
-        // Register prefetch, 64-k slabs, one barrier per slab.  Each wave owns
-        // 128 x 128 of the tile (4 x 4 MFMA tiles, accumulators in AGPRs).
-        // The four 32 KB arrays hold two stages of one 256 x 64 slab per
-        // operand: stage 0 = (sS0 A, sS1 B), stage 1 = (sS2 A, sS3 B), rows of
-        // 128 B with chunk c of row r at slot c ^ ((r >> 1) & 7), so the 16
-        // lanes of one ds_read_b128 / ds_write_b128 pass touch 16 distinct
-        // 16-byte bank groups.  Global loads go to registers two slabs ahead:
-        // thread t fetches chunk t & 7 of rows (t >> 3) + 32 i (i < 8) of A
-        // and of B, 16 dwordx4 loads per slab.  Slab s runs its four 16-k
-        // steps of 16 MFMAs each; under each step's MFMAs the wave reads the
-        // next step's fragments, writes a quarter of slab s + 1 from registers
-        // into the other stage (whose last readers passed the barrier that
-        // opened slab s) and reloads those registers with slab s + 3.  After
-        // the fourth step: wait for this wave's LDS writes, barrier, read the
-        // first fragments of slab s + 1.
-        // Every slab issues exactly one load group (past the end it re-fetches
-        // the last slab), so the compiler's vmcnt waits see one pattern.
+    if constexpr (S64) {
+        // 64-k slabs, one barrier per slab.  Each wave owns 128 x 128 of the
+        // tile (4 x 4 MFMA tiles, accumulators in AGPRs).  Both operands go
+        // global -> LDS by DMA, A into a two-stage ring (sS0, sS2) and B into a
+        // three-stage ring (sS1, sS3, sS4): the whole 160 KB.  LDS rows are
+        // 128 B with chunk c of row r in slot c ^ ((r >> 1) & 7), so the 16
+        // lanes of one ds_read_b128 pass touch 16 distinct 16-byte bank
+        // groups; a DMA instruction fills 8 rows (lane l: row l >> 3, slot
+        // l & 7), each lane fetching the global chunk its slot holds.
+        //   B of slab s + 2 is issued during k-steps 0..2 of slab s into the
+        //   stage slab s - 1 used (free since the barrier that ended it);
+        //   A of slab s + 2 can go only into the stage slab s uses, so half of
+        //   it is issued right after slab s's barrier and half under the next
+        //   slab's first k-step.
+        // Slab s runs four 16-k steps of 16 MFMAs; under each the wave reads
+        // the next step's 8 fragments and issues its share of DMA.  Two MFMAs
+        // into k-step 3 it waits for its own DMA of slab s + 1 (all but the 8 B
+        // instructions of slab s + 2, which are the newest) and its LDS reads,
+        // meets the other waves at the barrier, and reads slab s + 1's first
+        // fragments under the remaining 14 MFMAs.  Every slab issues the same
+        // DMA pattern (past the end it re-fetches the last slab into a free
+        // stage), so the vmcnt accounting is uniform.
+        __shared__ __attribute__((aligned(1024))) uint16_t sS4[(BM + BN) * kRK];
         constexpr int kBK = 64;
-        constexpr int kRowB = kBK * 2;           // bytes per LDS row
-        constexpr int kRows32 = 32 * kRowB;      // bytes of 32 rows
+        constexpr int kRowB = kBK * 2;        // bytes per LDS row
+        constexpr int kRows32 = 32 * kRowB;   // bytes of 32 rows
+        constexpr int kPre = 2;               // MFMAs of k-step 3 before the barrier
         const int64_t nslab = p.k / kBK;
-        const int grow = tid >> 3, gch = tid & 7;
-        uint32_t va[8], vb[8];
+        // DMA instruction i (< 8) of this wave fills rows (4 i + wave) * 8 ..+8
+        uint32_t dma_a[8], dma_b[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const int local = grow + 32 * i;
+            const int local = (4 * i + wave) * 8 + (lane >> 3);
+            const int chunk = (lane & 7) ^ ((local >> 1) & 7);
             const int64_t r = row0 + local;
             int64_t src = r < re ? r : row0;
             if (p.a_rows) src = p.a_rows[src];
             if (src < 0 || src >= p.a_rows_limit) src = 0;
-            va[i] = static_cast<uint32_t>((src * p.lda + gch * 8) * 2);
+            dma_a[i] = static_cast<uint32_t>((src * p.lda + chunk * 8) * 2);
             int64_t brow;
             if (kGlu) {
                 const int block = local >> 5;
@@ -1255,10 +1257,8 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
                 const int64_t col = ncol0 + local;
                 brow = col < p.n ? col : 0;
             }
-            vb[i] = static_cast<uint32_t>((brow * p.ldb + gch * 8) * 2);
+            dma_b[i] = static_cast<uint32_t>((brow * p.ldb + chunk * 8) * 2);
         }
-        // rows grow + 32 i share (row >> 1) & 7, so one swizzled offset serves all i
-        const uint32_t wr = static_cast<uint32_t>(grow * kRowB + ((gch ^ ((grow >> 1) & 7)) * 16));
         const int fsw = (l32 >> 1) & 7;
         uint32_t ra_off[4], rb_off[4];
 #pragma unroll
@@ -1267,107 +1267,98 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
             rb_off[j] = static_cast<uint32_t>((wn * 128 + l32) * kRowB + (((2 * j + khalf) ^ fsw) * 16));
         }
         char* const stA[2] = {reinterpret_cast<char*>(sS0), reinterpret_cast<char*>(sS2)};
-        char* const stB[2] = {reinterpret_cast<char*>(sS1), reinterpret_cast<char*>(sS3)};
-        uint4 pf[2][16];
-        // slab kt's chunks i in [i0, i1) of A and of B into registers / from
-        // registers into stage st
-        auto gload = [&](uint4 (&r)[16], int64_t kt, int i0, int i1) {
-            const int soff = static_cast<int>(min(kt, nslab - 1) * kBK * 2);
-#pragma unroll
-            for (int i = i0; i < i1; ++i) {
-                r[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ra, va[i], soff, 0));
-                r[8 + i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rb_, vb[i], soff, 0));
-            }
-        };
-        auto lwrite = [&](const uint4 (&r)[16], int st, int i0, int i1) {
-#pragma unroll
-            for (int i = i0; i < i1; ++i) {
-                *reinterpret_cast<uint4*>(stA[st] + wr + i * kRows32) = r[i];
-                *reinterpret_cast<uint4*>(stB[st] + wr + i * kRows32) = r[8 + i];
-            }
-        };
-        bf16x8 fa[2][4], fb[2][4];
-        // in the order the row-major MFMAs consume them: a0, b0..b3, a1..a3
-        auto frags = [&](int st, int j, bf16x8 (&a)[4], bf16x8 (&b)[4]) {
-            a[0] = as_bf16x8(*reinterpret_cast<const uint4*>(stA[st] + ra_off[j]));
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                b[i] = as_bf16x8(*reinterpret_cast<const uint4*>(stB[st] + rb_off[j] + i * kRows32));
-#pragma unroll
-            for (int i = 1; i < 4; ++i)
-                a[i] = as_bf16x8(*reinterpret_cast<const uint4*>(stA[st] + ra_off[j] + i * kRows32));
-        };
-        auto mfma_rows = [&](const bf16x8 (&a)[4], const bf16x8 (&b)[4], int i0, int i1) {
+        char* const stB[3] = {reinterpret_cast<char*>(sS1), reinterpret_cast<char*>(sS3),
+                              reinterpret_cast<char*>(sS4)};
+        auto dma = [&](char* const* stages, const buf_rsrc& rs, const uint32_t (&off)[8], int st,
+                       int64_t kt, int i0, int i1) {
+            const uint32_t soff = static_cast<uint32_t>(min(kt, nslab - 1) * kBK * 2);
 #pragma unroll
             for (int i = i0; i < i1; ++i)
+                lds_dma16_buf(rs, off[i], soff, reinterpret_cast<uint16_t*>(stages[st] + (4 * i + wave) * 8 * kRowB));
+        };
+        auto dma_A = [&](int st, int64_t kt, int i0, int i1) { dma(stA, ra, dma_a, st, kt, i0, i1); };
+        auto dma_B = [&](int st, int64_t kt, int i0, int i1) { dma(stB, rb_, dma_b, st, kt, i0, i1); };
+        bf16x8 fa[2][4], fb[2][4];
+        // in the order the row-major MFMAs consume them: a0, b0..b3, a1..a3
+        auto frags = [&](int sa, int sb, int j, bf16x8 (&a)[4], bf16x8 (&b)[4]) {
+            a[0] = as_bf16x8(*reinterpret_cast<const uint4*>(stA[sa] + ra_off[j]));
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+            for (int i = 0; i < 4; ++i)
+                b[i] = as_bf16x8(*reinterpret_cast<const uint4*>(stB[sb] + rb_off[j] + i * kRows32));
+#pragma unroll
+            for (int i = 1; i < 4; ++i)
+                a[i] = as_bf16x8(*reinterpret_cast<const uint4*>(stA[sa] + ra_off[j] + i * kRows32));
         };
-        auto mfma16 = [&](const bf16x8 (&a)[4], const bf16x8 (&b)[4]) { mfma_rows(a, b, 0, 4); };
-        auto mfma_at = [&](const bf16x8 (&a)[4], const bf16x8 (&b)[4], int i, int j) {
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+        // MFMAs q0 .. q1 - 1 of a k-step, row-major over the 4 x 4 tiles
+        auto mfmas = [&](const bf16x8 (&a)[4], const bf16x8 (&b)[4], int q0, int q1) {
+#pragma unroll
+            for (int q = q0; q < q1; ++q)
+                acc[q / 4][q % 4] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[q / 4], b[q % 4], acc[q / 4][q % 4], 0, 0, 0);
         };
-        // One slab; stage `cur`, the registers of slab s + 1 in set `rs`.
-        // k-steps 0..2 read the next step's fragments (8 LDS reads); k-steps 0
-        // and 1 also move chunks 0-3 and 4-7 of slab s + 1 into the other
-        // stage (8 LDS writes each, every one followed by the load of slab
-        // s + 3 into the registers it freed), reads and writes alternating
-        // over the step's 16 MFMAs; k-step 2 issues its reads under its first
-        // 8 MFMAs.  k-step 3 starts with two MFMAs, waits for this wave's LDS
-        // accesses and meets the other waves at the barrier, then reads the
-        // first fragments of slab s + 1 under its remaining 14 MFMAs.
-        auto slab64 = [&](int64_t s, int cur, auto rs_c) {
-            constexpr int rs = decltype(rs_c)::value;
-            frags(cur, 1, fa[1], fb[1]);
-            lwrite(pf[rs], cur ^ 1, 0, 4);
-            gload(pf[rs], s + 3, 0, 4);
-            mfma16(fa[0], fb[0]);
-            spread_moves<16, 8, 2, 8, 1>();
+        // Slab s (s % 6 == C): A stage s % 2, B stage s % 3.
+        auto slab64 = [&](int64_t s, auto c_c) {
+            constexpr int C = decltype(c_c)::value;
+            constexpr int sa = C % 2, sb = C % 3, nb = (sb + 2) % 3;
+            frags(sa, sb, 1, fa[1], fb[1]);
+            dma_A(sa ^ 1, s + 1, 4, 8);  // second half of A's slab s + 1
+            mfmas(fa[0], fb[0], 0, 4);
+            spread_reads_loads<4, 4, 4>();
             __builtin_amdgcn_sched_barrier(0);
-            frags(cur, 2, fa[0], fb[0]);
-            lwrite(pf[rs], cur ^ 1, 4, 8);
-            gload(pf[rs], s + 3, 4, 8);
-            mfma16(fa[1], fb[1]);
-            spread_moves<16, 8, 2, 8, 1>();
+            // every A instruction of slab s + 1 precedes every B one of slab s + 2
+            dma_B(nb, s + 2, 0, 3);
+            mfmas(fa[0], fb[0], 4, 16);
+            spread_reads_loads<12, 4, 3>();
             __builtin_amdgcn_sched_barrier(0);
-            frags(cur, 3, fa[1], fb[1]);
-            mfma16(fa[0], fb[0]);
-            spread_moves<16, 8, 1, 0, 0>();
+            frags(sa, sb, 2, fa[0], fb[0]);
+            dma_B(nb, s + 2, 3, 6);
+            mfmas(fa[1], fb[1], 0, 16);
+            spread_reads_loads<16, 8, 3>();
             __builtin_amdgcn_sched_barrier(0);
-            mfma_at(fa[1], fb[1], 0, 0);
-            mfma_at(fa[1], fb[1], 0, 1);
+            frags(sa, sb, 3, fa[1], fb[1]);
+            dma_B(nb, s + 2, 6, 8);
+            mfmas(fa[0], fb[0], 0, 16);
+            spread_reads_loads<16, 8, 2>();
             __builtin_amdgcn_sched_barrier(0);
-            wait_lds();
+            mfmas(fa[1], fb[1], 0, kPre);
+            __builtin_amdgcn_sched_barrier(0);
+            wait_vmem_lds<8>();
             barrier_no_fence();
-            frags(cur ^ 1, 0, fa[0], fb[0]);
-            mfma_at(fa[1], fb[1], 0, 2);
-            mfma_at(fa[1], fb[1], 0, 3);
-            mfma_rows(fa[1], fb[1], 1, 4);
-            spread_moves<14, 8, 1, 0, 0>();
+            dma_A(sa, s + 2, 0, 4);      // first half of A's slab s + 2
+            frags(sa ^ 1, (sb + 1) % 3, 0, fa[0], fb[0]);
+            mfmas(fa[1], fb[1], kPre, 16);
+            spread_reads_loads<16 - kPre, 8, 4>();
             __builtin_amdgcn_sched_barrier(0);
         };
-        using rs0 = std::integral_constant<int, 0>;
-        using rs1 = std::integral_constant<int, 1>;
-        // the prologue keeps the steady state's load order (slab 1, then slab
-        // 2) so the compiler's vmcnt waits in the loop stay partial
-        gload(pf[0], 0, 0, 8);
+        // prologue: A and B of slab 0, B of slab 1, then the first half of A's slab 1
+        dma_A(0, 0, 0, 8);
+        dma_B(0, 0, 0, 8);
+        dma_B(1, 1, 0, 8);
         __builtin_amdgcn_sched_barrier(0);
-        gload(pf[1], 1, 0, 8);
-        __builtin_amdgcn_sched_barrier(0);
-        lwrite(pf[0], 0, 0, 8);
-        __builtin_amdgcn_sched_barrier(0);
-        gload(pf[0], 2, 0, 8);
-        __builtin_amdgcn_sched_barrier(0);
-        wait_lds();
+        wait_vmem_lds<8>();
         barrier_no_fence();
-        frags(0, 0, fa[0], fb[0]);
+        dma_A(1, 1, 0, 4);
+        frags(0, 0, 0, fa[0], fb[0]);
+        using c0 = std::integral_constant<int, 0>;
+        using c1 = std::integral_constant<int, 1>;
+        using c2 = std::integral_constant<int, 2>;
+        using c3 = std::integral_constant<int, 3>;
+        using c4 = std::integral_constant<int, 4>;
+        using c5 = std::integral_constant<int, 5>;
+        // unrolled by 6 (stage periods 2 and 3), so every stage is a fixed array
         int64_t s = 0;
-        for (; s + 2 <= nslab; s += 2) {
-            slab64(s, 0, rs1{});
-            slab64(s + 1, 1, rs0{});
+        for (; s + 6 <= nslab; s += 6) {
+            slab64(s, c0{});
+            slab64(s + 1, c1{});
+            slab64(s + 2, c2{});
+            slab64(s + 3, c3{});
+            slab64(s + 4, c4{});
+            slab64(s + 5, c5{});
         }
-        if (s < nslab) slab64(s, 0, rs1{});
+        if (s < nslab) slab64(s, c0{});
+        if (s + 1 < nslab) slab64(s + 1, c1{});
+        if (s + 2 < nslab) slab64(s + 2, c2{});
+        if (s + 3 < nslab) slab64(s + 3, c3{});
+        if (s + 4 < nslab) slab64(s + 4, c4{});
     } else {
     issue(sS0, 0);
     issue(sS1, min(int64_t(1), slabs - 1) * kRK);
@@ -1719,23 +1710,23 @@ void launch_big_b(const TiledArgs& a, dim3 grid, int tm, int tn, int epi, hipStr
     }
 }
 
-template <int BM, int BN, int NW = 4, bool PP = false, bool VPF = false>
+template <int BM, int BN, int NW = 4, bool PP = false, bool S64 = false>
 void launch_dma_b(const TiledArgs& a, dim3 grid, int tm, int tn, int epi, hipStream_t s) {
     switch (epi) {
-        case SFG_EPI_NONE: gemm_dma_kernel<BM, BN, NW, SFG_EPI_NONE, PP, VPF><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
-        case SFG_EPI_RESIDUAL: gemm_dma_kernel<BM, BN, NW, SFG_EPI_RESIDUAL, PP, VPF><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
-        case SFG_EPI_SWIGLU: gemm_dma_kernel<BM, BN, NW, SFG_EPI_SWIGLU, PP, VPF><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
-        case kEpiQkvRope: gemm_dma_kernel<BM, BN, NW, kEpiQkvRope, PP, VPF><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
-        default: gemm_dma_kernel<BM, BN, NW, SFG_EPI_GLU_SILU_UP, PP, VPF><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
+        case SFG_EPI_NONE: gemm_dma_kernel<BM, BN, NW, SFG_EPI_NONE, PP, S64><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
+        case SFG_EPI_RESIDUAL: gemm_dma_kernel<BM, BN, NW, SFG_EPI_RESIDUAL, PP, S64><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
+        case SFG_EPI_SWIGLU: gemm_dma_kernel<BM, BN, NW, SFG_EPI_SWIGLU, PP, S64><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
+        case kEpiQkvRope: gemm_dma_kernel<BM, BN, NW, kEpiQkvRope, PP, S64><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
+        default: gemm_dma_kernel<BM, BN, NW, SFG_EPI_GLU_SILU_UP, PP, S64><<<grid, NW * 64, 0, s>>>(a, tm, tn); break;
     }
 }
 
 // Output tile of the direct-to-LDS kernel.  SFG_TILE_AUTO: the largest tile
-// (256 x 256 on the four-wave register-prefetch loop) that still gives at
-// least 512 workgroups (two per CU); smaller problems take smaller tiles.  A
+// (256 x 256 on the four-wave 64-k slab loop) that still gives at least 512
+// workgroups (two per CU); smaller problems take smaller tiles.  A
 // plan may name the tile instead (sfg_layer_desc::gemm_tile); results do not
 // depend on it.
-struct DmaShape { int bm, bn, waves; bool pingpong; bool vpf = false; };
+struct DmaShape { int bm, bn, waves; bool pingpong; bool slab64 = false; };
 DmaShape dma_shape_of(int tile) {
     switch (tile) {
         case SFG_TILE_256x256_PP: return {256, 256, 8, true};
@@ -1937,8 +1928,8 @@ int launch_gemm(const GemmProblem& problem, void* workspace, size_t workspace_by
         const dim3 grid = p.offsets ? dim3(static_cast<unsigned>(tn), static_cast<unsigned>(tm + groups))
                                     : dim3(static_cast<unsigned>(tm * tn));
         const int itm = p.offsets ? 0 : static_cast<int>(tm);
-        static_assert(kGK % 64 == 0, "the register-prefetch loop walks 64-k slabs");
-        if (sh.vpf)
+        static_assert(kGK % 64 == 0, "the 256 x 256 V tile walks 64-k slabs");
+        if (sh.slab64)
             launch_dma_b<256, 256, 4, false, true>(a, grid, itm, static_cast<int>(tn), p.epilogue, stream);
         else if (sh.bm == 256 && sh.bn == 256 && sh.pingpong)
             launch_dma_b<256, 256, 8, true>(a, grid, itm, static_cast<int>(tn), p.epilogue, stream);

@@ -48,7 +48,7 @@ TileShape tile_shape(int tile) {
 }
 
 // SFG_TILE_AUTO as the launcher resolves it: the largest tile with >= 512
-// workgroups (256 x 256 on the register-prefetch loop), and that tile for
+// workgroups (256 x 256 on the 64-k slab loop), and that tile for
 // grouped GLU products from 128 workgroups up.
 int auto_tile(std::int64_t m, std::int64_t n_out, bool glu, int groups) {
     if (groups > 1 && glu && (ceil_div(m, 256) + groups) * ceil_div(n_out, 128) >= 128)
