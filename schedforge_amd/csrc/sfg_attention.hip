@@ -313,8 +313,9 @@ int launch_attn_prefill_bf16(const uint16_t* q, const uint16_t* k, const uint16_
 // a wave owns 32 rows.  Per tile of 64 keys:
 //   S^T[64 keys][32 q] = K Q^T      2 x 8 mfma_f32_32x32x16_bf16 (Q in VGPRs)
 //   O^T[128 d][32 q] += V^T P^T     4 x 4 mfma_f32_32x32x16_bf16
-// K and V^T tiles go global -> LDS directly (global_load_lds_dwordx4), two
-// stages: the next tile is in flight while the current one is multiplied.
+// K and V^T tiles go global -> LDS directly (LDS DMA), in two stages for four
+// waves (the next tile in flight while the current one is multiplied) and
+// three for eight (the next two).
 // Key order: the K fragment of lane l is key row swap23(l & 31) of its 32-key
 // block (bits 2 and 3 of the index exchanged), so accumulator register r of
 // lane l holds key 16 (r / 8) + 8 (l / 32) + r % 8 -- eight consecutive keys
@@ -350,10 +351,16 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2
 void attn_prefill_fa2_kernel(Fa2Args p) {
     constexpr int BM = WAVES * 32;
     constexpr int kBlk = 16 / WAVES;  // 1 KB blocks of K (and of V^T) per wave per tile
+    // Four waves: two stages (two workgroups per CU); eight waves: three
+    // stages (96 KB, one workgroup per CU), the next two tiles in flight.
+    constexpr int kStages = WAVES == 8 ? 3 : 2;
+    constexpr int kStage2 = kStages == 3 ? kFa2BN * kFaD : 8;
     __shared__ __attribute__((aligned(1024))) uint16_t sK0[kFa2BN * kFaD];
     __shared__ __attribute__((aligned(1024))) uint16_t sK1[kFa2BN * kFaD];
+    __shared__ __attribute__((aligned(1024))) uint16_t sK2[kStage2];
     __shared__ __attribute__((aligned(1024))) uint16_t sV0[kFaD * kFa2BN];
     __shared__ __attribute__((aligned(1024))) uint16_t sV1[kFaD * kFa2BN];
+    __shared__ __attribute__((aligned(1024))) uint16_t sV2[kStage2];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -514,19 +521,49 @@ void attn_prefill_fa2_kernel(Fa2Args p) {
             }
     };
 
-    issue(sK0, sV0, 0);
-    wait_vmem_all();
-    __syncthreads();
-    for (int t = 0; t < tiles; t += 2) {
-        if (t + 1 < tiles) issue(sK1, sV1, (t + 1) * kFa2BN);
-        compute(sK0, sV0, t * kFa2BN);
+    if constexpr (kStages == 2) {
+        issue(sK0, sV0, 0);
         wait_vmem_all();
         __syncthreads();
-        if (t + 1 >= tiles) break;
-        if (t + 2 < tiles) issue(sK0, sV0, (t + 2) * kFa2BN);
-        compute(sK1, sV1, (t + 1) * kFa2BN);
+        for (int t = 0; t < tiles; t += 2) {
+            if (t + 1 < tiles) issue(sK1, sV1, (t + 1) * kFa2BN);
+            compute(sK0, sV0, t * kFa2BN);
+            wait_vmem_all();
+            __syncthreads();
+            if (t + 1 >= tiles) break;
+            if (t + 2 < tiles) issue(sK0, sV0, (t + 2) * kFa2BN);
+            compute(sK1, sV1, (t + 1) * kFa2BN);
+            wait_vmem_all();
+            __syncthreads();
+        }
+    } else {
+        // Tile t issues tile t + 2 into the stage tile t - 1 used (retired by
+        // the barrier that ended tile t - 1), then waits for its own loads of
+        // tile t + 1 only (the 2 kBlk loads of tile t + 2 stay in flight).
+        // Every tile issues one load group (past the end it re-fetches the
+        // last tile into a stage nobody reads again), so the count is uniform.
+        const int last = (tiles - 1) * kFa2BN;
+        issue(sK0, sV0, 0);
+        issue(sK1, sV1, min(kFa2BN, last));
+        wait_vmem_lds<2 * kBlk>();
+        barrier_no_fence();
+        for (int t = 0; t < tiles; t += 3) {
+            issue(sK2, sV2, min((t + 2) * kFa2BN, last));
+            compute(sK0, sV0, t * kFa2BN);
+            wait_vmem_lds<2 * kBlk>();
+            barrier_no_fence();
+            if (t + 1 >= tiles) break;
+            issue(sK0, sV0, min((t + 3) * kFa2BN, last));
+            compute(sK1, sV1, (t + 1) * kFa2BN);
+            wait_vmem_lds<2 * kBlk>();
+            barrier_no_fence();
+            if (t + 2 >= tiles) break;
+            issue(sK1, sV1, min((t + 4) * kFa2BN, last));
+            compute(sK2, sV2, (t + 2) * kFa2BN);
+            wait_vmem_lds<2 * kBlk>();
+            barrier_no_fence();
+        }
         wait_vmem_all();
-        __syncthreads();
     }
 
     if (my_q >= p.seq_q) return;

@@ -131,6 +131,33 @@ __device__ __forceinline__ void wait_vmem_all() {
     __builtin_amdgcn_s_waitcnt(0x0F70);
 }
 
+// s_waitcnt vmcnt(N), expcnt and lgkmcnt untouched (gfx9 encoding: vmcnt in
+// bits 3:0 and 15:14).
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+
+// s_waitcnt vmcnt(N) lgkmcnt(0): this wave's older loads and all its LDS
+// accesses are done.
+template <int N>
+__device__ __forceinline__ void wait_vmem_lds() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0070);
+}
+
+// Workgroup barrier without __syncthreads()'s release fence, which would wait
+// for every outstanding load (vmcnt(0)) including the LDS DMA of the stages
+// still meant to be in flight.  The memory clobber keeps the compiler from
+// moving LDS accesses across it; each wave has already waited for its own
+// loads of the stage about to be read, and LDS is coherent inside the CU.
+__device__ __forceinline__ void barrier_no_fence() { asm volatile("s_barrier" ::: "memory"); }
+
+// s_waitcnt lgkmcnt(0), vmcnt and expcnt untouched: this wave's LDS accesses
+// (reads and writes) are done.
+__device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
 // Two fp32 -> packed bf16 pair with the hardware converter
 // (v_cvt_pk_bf16_f32, round to nearest even: the same bits as pack_bf16x2 for
 // finite values).

@@ -921,29 +921,6 @@ __device__ __forceinline__ void qkv_rope_epilogue(const QkvRopeOut& o, const flo
 // ===========================================================================
 constexpr int kRK = 32;
 
-// s_waitcnt vmcnt(N), expcnt and lgkmcnt untouched (gfx9 encoding: vmcnt in
-// bits 3:0 and 15:14).
-template <int N>
-__device__ __forceinline__ void wait_vmem() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
-}
-
-// s_waitcnt vmcnt(N) lgkmcnt(0): this wave's older loads and all its LDS
-// accesses are done.
-template <int N>
-__device__ __forceinline__ void wait_vmem_lds() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0070);
-}
-
-// Workgroup barrier without __syncthreads()'s release fence, which would wait
-// for every outstanding load (vmcnt(0)) including the LDS DMA of the slabs
-// still meant to be in flight.  The memory clobber keeps the compiler from
-// moving LDS accesses across it; each wave has already waited for its own
-// loads of the slab about to be read, and LDS is coherent inside the CU.
-__device__ __forceinline__ void barrier_no_fence() { asm volatile("s_barrier" ::: "memory"); }
-
 // Stages and workgroups per CU by tile: 256 x 256 holds 256 accumulator
 // registers per lane (one workgroup per CU, four stages = 128 KB of LDS);
 // smaller tiles leave room for two workgroups per CU, so one's barriers and
@@ -994,10 +971,6 @@ struct DmaShapeTraits {
     static constexpr bool slab_ahead = big && NW == 4;
     static constexpr int dma_bytes = 16;  // per lane per LDS DMA instruction (dwordx4)
 };
-
-// s_waitcnt lgkmcnt(0), vmcnt and expcnt untouched: this wave's LDS accesses
-// (reads and writes) are done.
-__device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
 template <int BM, int BN, int NW, int EPI, bool PP = false, bool S64 = false>
 __global__ __launch_bounds__(NW * 64)
@@ -1485,9 +1458,10 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
     // Epilogue: 32x32 D layout, lane holds column (lane & 31) and rows
     // 8 (r / 4) + 4 (lane >> 5) + (r % 4).  The output dtype and the scales are
     // resolved once per tile, a lane's scales (its columns are fixed) are read
-    // once, and each 32-row block issues all its residual loads (at clamped,
-    // always valid addresses) before its first store, so the block waits for
-    // memory once instead of once per element; only the stores are guarded.
+    // once, and the residual loads of a group of half blocks (at clamped,
+    // always valid addresses) all precede the group's first store, so the
+    // group waits for memory once instead of once per element; only the
+    // stores are guarded.
     if constexpr (EPI != kEpiQkvRope) {
         constexpr int kCols = kGlu ? WN / 2 : WN;  // output columns per lane
         int64_t cols[kCols];
@@ -1499,39 +1473,80 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
             sc_lo[j] = scales ? scales[cc] : 1.f;
             sc_hi[j] = (kGlu && scales) ? scales[p.n + cc] : 1.f;
         }
+        // Residual rows [0, m) addressable with 32-bit byte offsets: loads go
+        // through a buffer resource (reads past its end return 0, and every
+        // load of a column >= n feeds only an output that is not stored).
+        const bool res_rsrc_ok = EPI == SFG_EPI_RESIDUAL && p.residual &&
+                                 static_cast<uint64_t>(p.m) * p.ldr * 4 <= 0xFFFFFFFFull;
+        const buf_rsrc res_rsrc = make_rsrc(p.residual, res_rsrc_ok ? static_cast<uint32_t>(p.m * p.ldr * 4) : 0u);
         auto store_tile = [&](auto* out) {
             using OutT = std::remove_pointer_t<decltype(out)>;
+            // Residual epilogues load the residual of kGroup half blocks before
+            // the first of their stores (each element is still read before it
+            // is written, so an in-place residual stays correct): the tile
+            // waits for memory 2 WM / kGroup times instead of 2 WM.
+            // (four-wave 256 x 256 tiles only: the others have no registers for it).
+            constexpr int kGroup = (EPI == SFG_EPI_RESIDUAL && NW == 4 && BM == 256 && BN == 256) ? 4 : 1;
 #pragma unroll
-            for (int ih = 0; ih < 2 * WM; ++ih) {  // half 32-row blocks: 8 accumulator rows each
-                const int i = ih >> 1, r0 = (ih & 1) * 8;
-                const int64_t rbase = row0 + wm * (BM / kWavesM) + i * 32 + 4 * khalf;
-                float res[8][kCols];
+            for (int g0 = 0; g0 < 2 * WM; g0 += kGroup) {
+                float res[kGroup][8][kCols];
                 if constexpr (EPI == SFG_EPI_RESIDUAL) {
+                    if (kGroup > 1 && res_rsrc_ok) {
+                        // 32-bit offsets through a buffer resource over the
+                        // residual rows [0, m): one offset per row, the column
+                        // blocks 128 B apart as immediate offsets
 #pragma unroll
-                    for (int rr = 0; rr < 8; ++rr)
+                        for (int h = 0; h < kGroup; ++h) {
+                            const int ih = g0 + h, i = ih >> 1, r0 = (ih & 1) * 8;
+                            const int64_t rbase = row0 + wm * (BM / kWavesM) + i * 32 + 4 * khalf;
 #pragma unroll
-                        for (int j = 0; j < kCols; ++j) {
-                            const int r = r0 + rr;
-                            const int64_t row = min(rbase + 8 * (r >> 2) + (r & 3), re - 1);
-                            res[rr][j] = p.residual[row * p.ldr + min(cols[j], p.n - 1)];
+                            for (int rr = 0; rr < 8; ++rr) {
+                                const int r = r0 + rr;
+                                const int64_t row = min(rbase + 8 * (r >> 2) + (r & 3), re - 1);
+                                const uint32_t off = static_cast<uint32_t>((row * p.ldr + cols[0]) * 4);
+#pragma unroll
+                                for (int j = 0; j < kCols; ++j)
+                                    res[h][rr][j] = __builtin_bit_cast(
+                                        float, __builtin_amdgcn_raw_buffer_load_b32(res_rsrc, off + j * 128, 0, 0));
+                            }
                         }
+                    } else {
+#pragma unroll
+                        for (int h = 0; h < kGroup; ++h) {
+                            const int ih = g0 + h, i = ih >> 1, r0 = (ih & 1) * 8;
+                            const int64_t rbase = row0 + wm * (BM / kWavesM) + i * 32 + 4 * khalf;
+#pragma unroll
+                            for (int rr = 0; rr < 8; ++rr)
+#pragma unroll
+                                for (int j = 0; j < kCols; ++j) {
+                                    const int r = r0 + rr;
+                                    const int64_t row = min(rbase + 8 * (r >> 2) + (r & 3), re - 1);
+                                    res[h][rr][j] = p.residual[row * p.ldr + min(cols[j], p.n - 1)];
+                                }
+                        }
+                    }
                 }
 #pragma unroll
-                for (int rr = 0; rr < 8; ++rr) {
-                    const int r = r0 + rr;
-                    const int64_t row = rbase + 8 * (r >> 2) + (r & 3);
+                for (int h = 0; h < kGroup; ++h) {  // half 32-row blocks: 8 accumulator rows each
+                    const int ih = g0 + h, i = ih >> 1, r0 = (ih & 1) * 8;
+                    const int64_t rbase = row0 + wm * (BM / kWavesM) + i * 32 + 4 * khalf;
 #pragma unroll
-                    for (int j = 0; j < kCols; ++j) {
-                        float v;
-                        if constexpr (kGlu) {
-                            v = glu_combine(EPI, acc[i][2 * j][r] * sc_lo[j], acc[i][2 * j + 1][r] * sc_hi[j]);
-                        } else {
-                            v = acc[i][j][r] * sc_lo[j];
-                            if constexpr (EPI == SFG_EPI_RESIDUAL) v += res[rr][j];
-                        }
-                        if (row < re && cols[j] < p.n) {
-                            if constexpr (sizeof(OutT) == 4) out[row * p.ldc + cols[j]] = v;
-                            else out[row * p.ldc + cols[j]] = f32_to_bf16(v);
+                    for (int rr = 0; rr < 8; ++rr) {
+                        const int r = r0 + rr;
+                        const int64_t row = rbase + 8 * (r >> 2) + (r & 3);
+#pragma unroll
+                        for (int j = 0; j < kCols; ++j) {
+                            float v;
+                            if constexpr (kGlu) {
+                                v = glu_combine(EPI, acc[i][2 * j][r] * sc_lo[j], acc[i][2 * j + 1][r] * sc_hi[j]);
+                            } else {
+                                v = acc[i][j][r] * sc_lo[j];
+                                if constexpr (EPI == SFG_EPI_RESIDUAL) v += res[h][rr][j];
+                            }
+                            if (row < re && cols[j] < p.n) {
+                                if constexpr (sizeof(OutT) == 4) out[row * p.ldc + cols[j]] = v;
+                                else out[row * p.ldc + cols[j]] = f32_to_bf16(v);
+                            }
                         }
                     }
                 }
