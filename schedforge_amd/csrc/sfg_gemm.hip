@@ -880,8 +880,9 @@ __device__ __forceinline__ void qkv_rope_epilogue(const QkvRopeOut& o, const flo
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const float2 c = cs[j][rq][e];
-                        // (even, odd) -> (even c - odd s, even s + odd c)
-                        const float r0 = (d & 1) ? pv[e] * c.y + v[e] * c.x : v[e] * c.x - pv[e] * c.y;
+                        // (even, odd) -> (even c - odd s, odd c + even s), the same
+                        // fused operations as qkv_rope_epilogue_staged
+                        const float r0 = (d & 1) ? fmaf(v[e], c.x, pv[e] * c.y) : fmaf(v[e], c.x, -(pv[e] * c.y));
                         dst[e * 128] = f32_to_bf16(r0);
                     }
                 } else {
@@ -892,6 +893,178 @@ __device__ __forceinline__ void qkv_rope_epilogue(const QkvRopeOut& o, const flo
                     *reinterpret_cast<uint2*>(o.vt + ((static_cast<int64_t>(b) * o.kv_heads + hv) * 128 + d) * o.ld_vt + s0) = pk;
                 }
             }
+        }
+    }
+}
+
+// The same epilogue for a wave's 128 x 128 block of the four-wave 256 x 256
+// tile, through a 16 KB LDS region of its own: for each 32-row block the
+// accumulators go to LDS as fp32 [32][128] (column c of row r at c ^ ((r & 4)
+// << 3), so the two row halves of a write use different banks), then every
+// lane reads 8 consecutive columns of one row, rotates its 4 pairs with a
+// 32-byte read of the (cos, sin) table (issued one row block ahead) and writes
+// 16 bytes of Q or K.  A V^T block is staged transposed and leaves as 16-byte
+// runs of positions; a block that is not a whole head, or V^T when the
+// sequence length is not a multiple of 8, takes the per-lane path.
+template <int WM, int WN>
+__device__ __forceinline__ void qkv_rope_epilogue_staged(const QkvRopeOut& o, const floatx16 (&acc)[WM][WN],
+                                                         int64_t wave_row0, int64_t wave_col0, int64_t re,
+                                                         int64_t n, int lane, float* stage) {
+    static_assert(WM == 4 && WN == 4, "a 128 x 128 block per wave");
+    const int l32 = lane & 31, khalf = lane >> 5;
+    const int64_t H = static_cast<int64_t>(o.q_heads) * 128;
+    const int64_t kvd = static_cast<int64_t>(o.kv_heads) * 128;
+    const int64_t seq = o.seq;
+    if (wave_col0 + 128 > n || (wave_col0 >= H + kvd && seq % 8 != 0)) {
+        qkv_rope_epilogue<WM, WN>(o, acc, wave_row0, wave_col0, re, n, l32, khalf);
+        return;
+    }
+    if (wave_col0 >= H + kvd) {
+        // V^T block: bf16 [128 d][128 s] in LDS, 8-byte granule g of row d at
+        // g ^ (d & 31) (the 32 rows of a write hit 32 distinct granules), then
+        // 16-byte runs of 8 positions of one d row go out whole.
+        uint16_t* const st = reinterpret_cast<uint16_t*>(stage);
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+#pragma unroll
+            for (int j = 0; j < WN; ++j)
+#pragma unroll
+                for (int rq = 0; rq < 4; ++rq) {
+                    const int d = j * 32 + l32;
+                    const int g = i * 8 + 2 * rq + khalf;  // positions 4 g .. 4 g + 3
+                    uint2 pk;
+                    pk.x = pack_bf16x2(acc[i][j][4 * rq + 0], acc[i][j][4 * rq + 1]);
+                    pk.y = pack_bf16x2(acc[i][j][4 * rq + 2], acc[i][j][4 * rq + 3]);
+                    *reinterpret_cast<uint2*>(st + d * 128 + (g ^ (d & 31)) * 4) = pk;
+                }
+        const int64_t hv = (wave_col0 - H - kvd) >> 7;
+        const int c = lane & 15;  // positions 8 c .. 8 c + 7 of a d row
+#pragma unroll
+        for (int t = 0; t < 32; ++t) {
+            const int d = 4 * t + (lane >> 4);
+            const int x = d & 31;
+            uint4 v = *reinterpret_cast<const uint4*>(st + d * 128 + ((2 * c) ^ (x & ~1)) * 4);
+            if (x & 1) v = make_uint4(v.z, v.w, v.x, v.y);  // the two granules of the run swapped
+            const int64_t grow = wave_row0 + 8 * c;         // first of the 8 rows
+            const int64_t b = grow / seq, sp = grow - b * seq;
+            uint16_t* const dst = o.vt + ((b * o.kv_heads + hv) * 128 + d) * o.ld_vt + sp;
+            if (grow + 8 <= re && sp + 8 <= seq) {
+                *reinterpret_cast<uint4*>(dst) = v;
+            } else {
+                const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int64_t r = grow + e;
+                    if (r >= re) break;
+                    const int64_t be = r / seq, se = r - be * seq;
+                    o.vt[((be * o.kv_heads + hv) * 128 + d) * o.ld_vt + se] = static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1)));
+                }
+            }
+        }
+        return;
+    }
+    const bool isq = wave_col0 < H;
+    uint16_t* const base = isq ? o.q : o.k;
+    const int64_t heads = isq ? o.q_heads : o.kv_heads;
+    const int64_t head = isq ? (wave_col0 >> 7) : ((wave_col0 - H) >> 7);
+    const int c8 = lane & 15;  // this lane's 8-column chunk when reading back
+    // (cos, sin) of this lane's 4 pairs for its 8 rows of block i: all 16
+    // table reads of a block are issued one block ahead, so the block never
+    // waits for the table
+    auto table = [&](int i, float4 (&cs)[8][2]) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const int64_t grow = min(wave_row0 + i * 32 + 4 * t + (lane >> 4), re - 1);
+            const int64_t sp = grow - (grow / seq) * seq;
+            const float4* src = reinterpret_cast<const float4*>(o.rope + sp * 64 + c8 * 4);
+            cs[t][0] = src[0];
+            cs[t][1] = src[1];
+        }
+    };
+    float4 cs[2][8][2];
+    table(0, cs[0]);
+#pragma unroll
+    for (int i = 0; i < WM; ++i) {
+        if (i + 1 < WM) table(i + 1, cs[(i + 1) & 1]);
+        // LDS accesses of one wave complete in order: the reads below see
+        // these writes, and the next block's writes follow these reads.
+#pragma unroll
+        for (int j = 0; j < WN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = 8 * (r >> 2) + 4 * khalf + (r & 3);
+                stage[row * 128 + ((j * 32 + l32) ^ ((row & 4) << 3))] = acc[i][j][r];
+            }
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const int row = 4 * t + (lane >> 4);
+            const float* src = stage + row * 128 + ((c8 * 8) ^ ((row & 4) << 3));
+            const float4 v0 = *reinterpret_cast<const float4*>(src);
+            const float4 v1 = *reinterpret_cast<const float4*>(src + 4);
+            const int64_t grow = wave_row0 + i * 32 + row;
+            if (grow >= re) continue;
+            const int64_t b = grow / seq, sp = grow - b * seq;
+            const float4 cs0 = cs[i & 1][t][0], cs1 = cs[i & 1][t][1];  // pairs 4 c8 .. 4 c8 + 3
+            auto rot = [](float e, float od, float c, float sn) {
+                return pack_bf16x2(fmaf(e, c, -(od * sn)), fmaf(od, c, e * sn));
+            };
+            uint4 pk;
+            pk.x = rot(v0.x, v0.y, cs0.x, cs0.y);
+            pk.y = rot(v0.z, v0.w, cs0.z, cs0.w);
+            pk.z = rot(v1.x, v1.y, cs1.x, cs1.y);
+            pk.w = rot(v1.z, v1.w, cs1.z, cs1.w);
+            *reinterpret_cast<uint4*>(base + ((b * heads + head) * seq + sp) * 128 + c8 * 8) = pk;
+        }
+    }
+}
+
+// GLU store epilogue of a wave's 128 x 64 output block in the four-wave
+// 256 x 256 tile (bf16 out), through a 16 KB LDS region of its own: the
+// silu-combined values go to LDS as bf16 [128 rows][64 columns] (column c of
+// row r at c ^ ((r & 4) << 3), so the two row halves of a write hit different
+// banks), then every lane stores 16-byte row chunks, instead of one 2-byte
+// element per lane per store instruction.  The arithmetic is the generic
+// epilogue's, value for value.
+template <int EPI>
+__device__ __forceinline__ void glu_epilogue_staged(const TiledArgs& p, const floatx16 (&acc)[4][4],
+                                                    int64_t wrow0, int64_t wcol0, int64_t re,
+                                                    const float* scales, int lane, uint16_t* stage) {
+    const int l32 = lane & 31, khalf = lane >> 5;
+    // wcol0: the first of this wave's 64 output columns
+    float sc_lo[2], sc_hi[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int64_t cc = min(wcol0 + j * 32 + l32, p.n - 1);
+        sc_lo[j] = scales ? scales[cc] : 1.f;
+        sc_hi[j] = scales ? scales[p.n + cc] : 1.f;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = i * 32 + 8 * (r >> 2) + 4 * khalf + (r & 3);
+                const float v = glu_combine(EPI, acc[i][2 * j][r] * sc_lo[j], acc[i][2 * j + 1][r] * sc_hi[j]);
+                stage[row * 64 + ((j * 32 + l32) ^ ((row & 4) << 3))] = f32_to_bf16(v);
+            }
+    // a wave's LDS accesses complete in order: the reads see the writes
+    uint16_t* const out = static_cast<uint16_t*>(p.c);
+    const int c8 = lane & 7;
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+        const int row = t * 8 + (lane >> 3);
+        const uint4 v = *reinterpret_cast<const uint4*>(stage + row * 64 + ((c8 * 8) ^ ((row & 4) << 3)));
+        const int64_t grow = wrow0 + row, col = wcol0 + c8 * 8;
+        if (grow >= re) continue;
+        uint16_t* const dst = out + grow * p.ldc + col;
+        if (col + 8 <= p.n) {
+            *reinterpret_cast<uint4*>(dst) = v;
+        } else {
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (col + e < p.n) dst[e] = static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1)));
         }
     }
 }
@@ -1455,6 +1628,19 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
     }
     wait_vmem<0>();
 
+    if constexpr (S64 && kGlu) {
+        if (p.c_dtype == SFG_BF16) {
+            // every wave's reads of the last slabs are done before any wave
+            // reuses its array as staging (the DMA drained above)
+            wait_lds();
+            barrier_no_fence();
+            uint16_t* const stage = wave == 0 ? sS0 : wave == 1 ? sS1 : wave == 2 ? sS2 : sS3;
+            glu_epilogue_staged<EPI>(p, acc, row0 + wm * (BM / kWavesM), ncol0 + wn * (BN / 4), re, scales,
+                                     lane, stage);
+            return;
+        }
+    }
+
     // Epilogue: 32x32 D layout, lane holds column (lane & 31) and rows
     // 8 (r / 4) + 4 (lane >> 5) + (r % 4).  The output dtype and the scales are
     // resolved once per tile, a lane's scales (its columns are fixed) are read
@@ -1555,9 +1741,20 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
         if (p.c_dtype == SFG_F32) store_tile(static_cast<float*>(p.c));
         else store_tile(static_cast<uint16_t*>(p.c));
     }
-    if constexpr (EPI == kEpiQkvRope) qkv_rope_epilogue<WM, WN>(p.qkv, acc, row0 + wm * (BM / kWavesM),
-                                                               ncol0 + wn * (BN / kWavesN), re, p.n,
-                                                               l32, khalf);
+    if constexpr (EPI == kEpiQkvRope) {
+        if constexpr (S64) {
+            // every wave's reads of the last slabs are done before any wave
+            // reuses its array as staging (the DMA drained above)
+            wait_lds();
+            barrier_no_fence();
+            float* const stage = reinterpret_cast<float*>(wave == 0 ? sS0 : wave == 1 ? sS1 : wave == 2 ? sS2 : sS3);
+            qkv_rope_epilogue_staged<WM, WN>(p.qkv, acc, row0 + wm * (BM / kWavesM), ncol0 + wn * (BN / kWavesN),
+                                             re, p.n, lane, stage);
+        } else {
+            qkv_rope_epilogue<WM, WN>(p.qkv, acc, row0 + wm * (BM / kWavesM), ncol0 + wn * (BN / kWavesN), re,
+                                      p.n, l32, khalf);
+        }
+    }
 }
 
 // ===========================================================================

@@ -147,9 +147,13 @@ def test_layer_every_plan_policy_is_bit_identical():
     policies = [(0, 0)] + [(t, 0) for t in range(1, _abi.TILE_COUNT)] + [(0, 8), (_abi.TILE_128x128, 8)]
     dense = CONFIGS["c4"].replace(sequence=1024, hidden=1024, intermediate=2048, query_heads=8,
                                   kv_heads=2)
+    # two sequences of 600: batch boundaries and the last row tile fall inside
+    # a wave's rows, for the fused QKV+RoPE epilogues of every tile
+    ragged = dense.replace(batch=2, sequence=600)
     moe = CONFIGS["c3"].replace(batch=2, sequence=512, hidden=1024, intermediate=512,
                                 query_heads=8, kv_heads=2)
-    for cfg, seed, trace in ((dense, CONFIG_SEEDS["c4"] + 31, False), (moe, CONFIG_SEEDS["c3"] + 31, True)):
+    for cfg, seed, trace in ((dense, CONFIG_SEEDS["c4"] + 31, False), (ragged, CONFIG_SEEDS["c4"] + 32, False),
+                             (moe, CONFIG_SEEDS["c3"] + 31, True)):
         outs, ref = _outputs_by_policy(cfg, seed, policies, trace=trace)
         err = oracle.rel_error(outs[0], ref)
         print(f"{'moe' if cfg.moe else 'dense'} policies: rel_err {err:.3e}")
