@@ -28,7 +28,11 @@ Each measured block carries:
                 reference path) on this host's cores, on a bounded sample of the
                 same workload: prefill as the layer at sampled query rows
                 (K / V for every row, the rest for rows spread over the whole
-                causal range), decode as whole layer steps.
+                causal range), decode as whole layer steps;
+  cold          decode configurations whose layer fits twice in the 256 MB
+                Infinity Cache (C2): the same steps rotating over independent
+                copies of the weights and KV pool, together over twice its
+                size, so no step is served from the previous step's cache.
 Synthetic data: activations N(0,1), weights N(0,0.02), cached K/V N(0,1), drawn
 on the device; norm gains 1; random page table.
 """
@@ -337,11 +341,12 @@ def measure(name, args, device="cuda:0"):
         e.close()
     del plan, x, out
     torch.cuda.empty_cache()
+    work = algorithmic_work(cfg)
+    cold = cold_decode(name, cfg, work, args, device) if cfg.decode else None
 
     def avg(key):
         return sum(s[key] for s in stages) / len(stages)
 
-    work = algorithmic_work(cfg)
     traffic = measured_traffic(name)
     kern_ms = sum(kern_times) / len(kern_times)
     if cfg.decode:
@@ -388,9 +393,54 @@ def measure(name, args, device="cuda:0"):
                    "stage_tflops": stage_tflops(cfg, work, avg)},
         "roofline": roofline,
     }
+    if cold is not None:
+        block["cold"] = cold
     if not args.no_cpu_baseline:
         block["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds)
     return block
+
+
+# Infinity Cache (MALL) of one MI355X: a decode step whose weights and KV fit
+# in it is served from it when steps repeat.
+MALL_BYTES = 256 << 20
+
+
+def cold_decode(name, cfg, work, args, device):
+    """Decode steps whose working set is not cache-resident: when one layer's
+    bytes (weights + KV + activations) fit twice in the MALL, build enough
+    independent copies (own weights, KV pool, page table and workspace) that
+    together they exceed twice its size, and time args.steps steps that rotate
+    over them, so no step finds its data in the MALL or L2 from the step
+    before.  Returns None when one layer already exceeds twice the MALL."""
+    import math
+    import torch
+    from schedforge_amd import CONFIG_SEEDS
+    from schedforge_amd.layer import compile_decoder, run_layer
+
+    per_layer = work["bytes"]
+    if per_layer >= 2 * MALL_BYTES:
+        return None
+    copies = max(2, math.ceil(2 * MALL_BYTES / per_layer) + 1)
+    plans, xs = [], []
+    for c in range(copies):
+        data, perm = make_device_data(cfg, CONFIG_SEEDS[name] + 1000 + c, device)
+        plans.append(compile_decoder(cfg, data, device, page_permutation=perm))
+        xs.append(data.input.contiguous())
+        del data
+    out = torch.empty((cfg.rows, cfg.hidden), dtype=torch.float32, device=device)
+    for i in range(max(args.warmup, copies)):
+        run_layer(plans[i % copies], xs[i % copies], out)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        run_layer(plans[i % copies], xs[i % copies], out)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    del plans, xs, out
+    torch.cuda.empty_cache()
+    return {"value": round(cfg.rows * 1000.0 / ms, 2), "ms_per_step": round(ms, 5), "copies": copies,
+            "rotated_mb": round(copies * per_layer / 1e6, 1),
+            "note": "steps rotate over independent weight sets and KV pools larger than the MALL"}
 
 
 def main():
@@ -431,6 +481,8 @@ def main():
         "config": head["config"],
         "roofline": head["roofline"],
     }
+    if "cold" in head:
+        line["cold"] = head["cold"]
     if "cpu_baseline" in head:
         line["cpu_baseline"] = head["cpu_baseline"]
     if not CONFIGS[args.config].decode and args.decode_config != "none":

@@ -72,8 +72,8 @@ enum sfg_layout { SFG_LAYOUT_NK = 0, SFG_LAYOUT_TILED = 1 };
  * optimiser (ExecutablePlanOptimizer, decoder_compiler.cpp:750-861) searches it. */
 enum sfg_gemm_tile {
     SFG_TILE_AUTO = 0,       /* the largest tile that still gives >= 512 workgroups
-                                (256 x 256 as V); grouped GLU products take V from
-                                128 workgroups up                                   */
+                                (256 x 256 as V); grouped products take V from 128
+                                workgroups up                                       */
     SFG_TILE_256x256_PP = 1, /* eight waves as two ping-pong groups of four          */
     SFG_TILE_256x256_W8 = 2, /* eight waves (2 x 4), 128 x 64 per wave               */
     SFG_TILE_256x256_W4 = 3, /* four waves (2 x 2), 128 x 128 per wave               */

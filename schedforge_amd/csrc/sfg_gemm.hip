@@ -1952,10 +1952,10 @@ DmaShape dma_shape_of(int tile) {
 }
 DmaShape pick_dma_shape(int64_t m, int64_t n_out, bool glu, int groups, int tile) {
     if (tile > SFG_TILE_AUTO && tile < SFG_TILE_COUNT) return dma_shape_of(tile);
-    // Grouped GLU (expert W1|W3): the 256 x 256 tile once it has work for half
-    // the CUs -- measured faster than 256 x 128 on the MoE prefill shape
-    // although its tile count stays under 512.
-    if (groups > 1 && glu && ((m + 255) / 256 + groups) * ((n_out + 127) / 128) >= 128)
+    // Grouped products (expert W1|W3 and W2): the 256 x 256 tile once it has
+    // work for half the CUs -- measured faster than 256 x 128 and 128 x 128 on
+    // the MoE prefill shape although its tile count stays under 512.
+    if (groups > 1 && ((m + 255) / 256 + groups) * ((n_out + (glu ? 127 : 255)) / (glu ? 128 : 256)) >= 128)
         return dma_shape_of(SFG_TILE_256x256_V);
     for (const int t : {SFG_TILE_256x256_V, SFG_TILE_256x128, SFG_TILE_128x128}) {
         const DmaShape sh = dma_shape_of(t);

@@ -48,10 +48,10 @@ TileShape tile_shape(int tile) {
 }
 
 // SFG_TILE_AUTO as the launcher resolves it: the largest tile with >= 512
-// workgroups (256 x 256 on the 64-k slab loop), and that tile for
-// grouped GLU products from 128 workgroups up.
+// workgroups (256 x 256 on the 64-k slab loop), and that tile for grouped
+// products from 128 workgroups up.
 int auto_tile(std::int64_t m, std::int64_t n_out, bool glu, int groups) {
-    if (groups > 1 && glu && (ceil_div(m, 256) + groups) * ceil_div(n_out, 128) >= 128)
+    if (groups > 1 && (ceil_div(m, 256) + groups) * ceil_div(n_out, glu ? 128 : 256) >= 128)
         return SFG_TILE_256x256_V;
     for (const int t : {SFG_TILE_256x256_V, SFG_TILE_256x128, SFG_TILE_128x128}) {
         const TileShape s = tile_shape(t);
