@@ -64,7 +64,11 @@ __device__ __forceinline__ uint4 f32x8_to_bf16x8(const float* v) {
     return r;
 }
 
-__device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }
+// silu(v) = v / (1 + e^-v), the division as a multiply by the hardware
+// reciprocal (1 ulp): the IEEE division's refinement sequence cost the GEMM
+// epilogues a third of their VALU time.  Large negative v: e^-v = inf,
+// reciprocal 0, result -0 (the division's limit).
+__device__ __forceinline__ float silu(float v) { return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v)); }
 
 template <typename T>
 __device__ __forceinline__ T wave_sum(T v) {
