@@ -37,20 +37,22 @@ __device__ __forceinline__ bf16x8 as_bf16x8(const uint4& v) {
     return __builtin_bit_cast(bf16x8, v);
 }
 
-// 8 int8 (two dwords) -> 8 bf16.  |q| <= 127 has at most 7 significant bits,
-// so the fp32 value's low 16 bits are zero and truncation is exact.
+// 8 int8 (two dwords) -> 8 bf16.  |q| <= 128 has at most 8 significant bits,
+// so the fp32 value's low 16 bits are zero and truncation is exact: each
+// byte converts in one instruction (sign-extending byte select), and one byte
+// permute packs the high halves of two such floats (bytes 2, 3 of the first
+// and 2, 3 of the second) into a bf16 pair.
+__device__ __forceinline__ uint32_t hi16_pair(float a, float b) {
+    return __builtin_amdgcn_perm(__float_as_uint(b), __float_as_uint(a), 0x07060302u);
+}
 __device__ __forceinline__ uint4 i8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
     uint4 r;
     const int8_t* p0 = reinterpret_cast<const int8_t*>(&lo);
     const int8_t* p1 = reinterpret_cast<const int8_t*>(&hi);
-    r.x = (__float_as_uint(static_cast<float>(p0[0])) >> 16) |
-          (__float_as_uint(static_cast<float>(p0[1])) & 0xFFFF0000u);
-    r.y = (__float_as_uint(static_cast<float>(p0[2])) >> 16) |
-          (__float_as_uint(static_cast<float>(p0[3])) & 0xFFFF0000u);
-    r.z = (__float_as_uint(static_cast<float>(p1[0])) >> 16) |
-          (__float_as_uint(static_cast<float>(p1[1])) & 0xFFFF0000u);
-    r.w = (__float_as_uint(static_cast<float>(p1[2])) >> 16) |
-          (__float_as_uint(static_cast<float>(p1[3])) & 0xFFFF0000u);
+    r.x = hi16_pair(static_cast<float>(p0[0]), static_cast<float>(p0[1]));
+    r.y = hi16_pair(static_cast<float>(p0[2]), static_cast<float>(p0[3]));
+    r.z = hi16_pair(static_cast<float>(p1[0]), static_cast<float>(p1[1]));
+    r.w = hi16_pair(static_cast<float>(p1[2]), static_cast<float>(p1[3]));
     return r;
 }
 

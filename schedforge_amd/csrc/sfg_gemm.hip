@@ -146,14 +146,16 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny_kernel(SkinnyArgs p) {
 #pragma unroll
             for (int j = 0; j < NBT; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
+        // Activation rows past the group or with a source index outside A
+        // read row 0 instead (no branch around the loads): an MFMA output row
+        // depends only on its own A row, and the epilogue stores nothing for
+        // the former and the zero product for the latter.
         const uint16_t* arow[MT];
-        bool avalid[MT];
 #pragma unroll
         for (int i = 0; i < MT; ++i) {
             const int64_t r = pass + i * 16 + lr;
-            avalid[i] = r < re;
-            int64_t src = avalid[i] ? (p.a_rows ? p.a_rows[r] : r) : 0;
-            if (src < 0 || src >= p.a_rows_limit) { avalid[i] = false; src = 0; }
+            int64_t src = r < re ? (p.a_rows ? p.a_rows[r] : r) : 0;
+            if (src < 0 || src >= p.a_rows_limit) src = 0;
             arow[i] = p.a + src * p.lda + lg * kLaneK;
         }
 
@@ -185,8 +187,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny_kernel(SkinnyArgs p) {
                     const uint16_t* ap = arow[i] + kofs;
 #pragma unroll
                     for (int s = 0; s < 4; ++s)
-                        aq[c][i][s] = avalid[i] ? *reinterpret_cast<const uint4*>(ap + kStepK * s)
-                                                : make_uint4(0, 0, 0, 0);
+                        aq[c][i][s] = *reinterpret_cast<const uint4*>(ap + kStepK * s);
                 }
             }
 #pragma unroll
@@ -238,6 +239,14 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny_kernel(SkinnyArgs p) {
                 for (int r = 0; r < 4; ++r) {
                     const int64_t row = pass + i * 16 + lg * 4 + r;
                     if (row >= re) continue;
+                    // a gathered row whose source index is outside A multiplied zeros
+                    if (p.a_rows) {
+                        const int64_t src = p.a_rows[row];
+                        if (src < 0 || src >= p.a_rows_limit) {
+#pragma unroll
+                            for (int j = 0; j < NBT; ++j) acc[i][j][r] = 0.f;
+                        }
+                    }
                     if (kGlu) {
 #pragma unroll
                         for (int h = 0; h < kGluTiles; ++h) {
