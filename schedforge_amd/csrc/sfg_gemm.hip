@@ -1047,16 +1047,32 @@ __device__ __forceinline__ void glu_epilogue_staged(const TiledArgs& p, const fl
         sc_lo[j] = scales ? scales[cc] : 1.f;
         sc_hi[j] = scales ? scales[p.n + cc] : 1.f;
     }
+    // Two rows at a time through the hardware RNE converter (the same bits as
+    // f32_to_bf16 for finite values); unscaled weights skip the multiplies.
+    auto combine_rows = [&](auto scaled_c) __attribute__((always_inline)) {
+        constexpr bool kScaled = decltype(scaled_c)::value;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = i * 32 + 8 * (r >> 2) + 4 * khalf + (r & 3);
-                const float v = glu_combine(EPI, acc[i][2 * j][r] * sc_lo[j], acc[i][2 * j + 1][r] * sc_hi[j]);
-                stage[row * 64 + ((j * 32 + l32) ^ ((row & 4) << 3))] = f32_to_bf16(v);
-            }
+                for (int r = 0; r < 16; r += 2) {
+                    float v[2];
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        const float g = kScaled ? acc[i][2 * j][r + e] * sc_lo[j] : acc[i][2 * j][r + e];
+                        const float u = kScaled ? acc[i][2 * j + 1][r + e] * sc_hi[j] : acc[i][2 * j + 1][r + e];
+                        v[e] = glu_combine(EPI, g, u);
+                    }
+                    const uint32_t pk = cvt_pk_bf16(v[0], v[1]);
+                    const int row = i * 32 + 8 * (r >> 2) + 4 * khalf + (r & 3);  // rows row, row + 1
+                    const int col = j * 32 + l32;
+                    stage[row * 64 + (col ^ ((row & 4) << 3))] = static_cast<uint16_t>(pk);
+                    stage[(row + 1) * 64 + (col ^ (((row + 1) & 4) << 3))] = static_cast<uint16_t>(pk >> 16);
+                }
+    };
+    if (scales) combine_rows(std::true_type{});
+    else combine_rows(std::false_type{});
     // a wave's LDS accesses complete in order: the reads see the writes
     uint16_t* const out = static_cast<uint16_t*>(p.c);
     const int c8 = lane & 7;
