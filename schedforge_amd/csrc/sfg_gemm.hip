@@ -942,8 +942,8 @@ __device__ __forceinline__ void qkv_rope_epilogue_staged(const QkvRopeOut& o, co
                     const int d = j * 32 + l32;
                     const int g = i * 8 + 2 * rq + khalf;  // positions 4 g .. 4 g + 3
                     uint2 pk;
-                    pk.x = pack_bf16x2(acc[i][j][4 * rq + 0], acc[i][j][4 * rq + 1]);
-                    pk.y = pack_bf16x2(acc[i][j][4 * rq + 2], acc[i][j][4 * rq + 3]);
+                    pk.x = cvt_pk_bf16(acc[i][j][4 * rq + 0], acc[i][j][4 * rq + 1]);
+                    pk.y = cvt_pk_bf16(acc[i][j][4 * rq + 2], acc[i][j][4 * rq + 3]);
                     *reinterpret_cast<uint2*>(st + d * 128 + (g ^ (d & 31)) * 4) = pk;
                 }
         const int64_t hv = (wave_col0 - H - kvd) >> 7;
@@ -1014,8 +1014,9 @@ __device__ __forceinline__ void qkv_rope_epilogue_staged(const QkvRopeOut& o, co
             if (grow >= re) continue;
             const int64_t b = grow / seq, sp = grow - b * seq;
             const float4 cs0 = cs[i & 1][t][0], cs1 = cs[i & 1][t][1];  // pairs 4 c8 .. 4 c8 + 3
+            // hardware RNE pair conversion: the same bits as pack_bf16x2 for finite values
             auto rot = [](float e, float od, float c, float sn) {
-                return pack_bf16x2(fmaf(e, c, -(od * sn)), fmaf(od, c, e * sn));
+                return cvt_pk_bf16(fmaf(e, c, -(od * sn)), fmaf(od, c, e * sn));
             };
             uint4 pk;
             pk.x = rot(v0.x, v0.y, cs0.x, cs0.y);
