@@ -1653,6 +1653,10 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
     }
     }
     wait_vmem<0>();
+    // The epilogues take the lane index again from the lane mask, so no
+    // lane-derived value of the prologue has to live through the main loop.
+    const int elane = static_cast<int>(__lane_id());
+    const int el32 = elane & 31, ekhalf = elane >> 5;
 
     if constexpr (S64 && kGlu) {
         if (p.c_dtype == SFG_BF16) {
@@ -1662,7 +1666,7 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
             barrier_no_fence();
             uint16_t* const stage = wave == 0 ? sS0 : wave == 1 ? sS1 : wave == 2 ? sS2 : sS3;
             glu_epilogue_staged<EPI>(p, acc, row0 + wm * (BM / kWavesM), ncol0 + wn * (BN / 4), re, scales,
-                                     lane, stage);
+                                     elane, stage);
             return;
         }
     }
@@ -1680,7 +1684,7 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
         float sc_lo[kCols], sc_hi[kCols];
 #pragma unroll
         for (int j = 0; j < kCols; ++j) {
-            cols[j] = kGlu ? ncol0 + (wn * WN / 2 + j) * 32 + l32 : ncol0 + wn * (BN / kWavesN) + j * 32 + l32;
+            cols[j] = kGlu ? ncol0 + (wn * WN / 2 + j) * 32 + el32 : ncol0 + wn * (BN / kWavesN) + j * 32 + el32;
             const int64_t cc = min(cols[j], p.n - 1);
             sc_lo[j] = scales ? scales[cc] : 1.f;
             sc_hi[j] = (kGlu && scales) ? scales[p.n + cc] : 1.f;
@@ -1710,7 +1714,7 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
 #pragma unroll
                         for (int h = 0; h < kGroup; ++h) {
                             const int ih = g0 + h, i = ih >> 1, r0 = (ih & 1) * 8;
-                            const int64_t rbase = row0 + wm * (BM / kWavesM) + i * 32 + 4 * khalf;
+                            const int64_t rbase = row0 + wm * (BM / kWavesM) + i * 32 + 4 * ekhalf;
 #pragma unroll
                             for (int rr = 0; rr < 8; ++rr) {
                                 const int r = r0 + rr;
@@ -1726,7 +1730,7 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
 #pragma unroll
                         for (int h = 0; h < kGroup; ++h) {
                             const int ih = g0 + h, i = ih >> 1, r0 = (ih & 1) * 8;
-                            const int64_t rbase = row0 + wm * (BM / kWavesM) + i * 32 + 4 * khalf;
+                            const int64_t rbase = row0 + wm * (BM / kWavesM) + i * 32 + 4 * ekhalf;
 #pragma unroll
                             for (int rr = 0; rr < 8; ++rr)
 #pragma unroll
@@ -1741,7 +1745,7 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
 #pragma unroll
                 for (int h = 0; h < kGroup; ++h) {  // half 32-row blocks: 8 accumulator rows each
                     const int ih = g0 + h, i = ih >> 1, r0 = (ih & 1) * 8;
-                    const int64_t rbase = row0 + wm * (BM / kWavesM) + i * 32 + 4 * khalf;
+                    const int64_t rbase = row0 + wm * (BM / kWavesM) + i * 32 + 4 * ekhalf;
 #pragma unroll
                     for (int rr = 0; rr < 8; ++rr) {
                         const int r = r0 + rr;
@@ -1775,10 +1779,10 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
             barrier_no_fence();
             float* const stage = reinterpret_cast<float*>(wave == 0 ? sS0 : wave == 1 ? sS1 : wave == 2 ? sS2 : sS3);
             qkv_rope_epilogue_staged<WM, WN>(p.qkv, acc, row0 + wm * (BM / kWavesM), ncol0 + wn * (BN / kWavesN),
-                                             re, p.n, lane, stage);
+                                             re, p.n, elane, stage);
         } else {
             qkv_rope_epilogue<WM, WN>(p.qkv, acc, row0 + wm * (BM / kWavesM), ncol0 + wn * (BN / kWavesN), re,
-                                      p.n, l32, khalf);
+                                      p.n, el32, ekhalf);
         }
     }
 }
