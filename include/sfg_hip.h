@@ -310,6 +310,10 @@ int sfg_hip_moe_dispatch_trace_v1(const int32_t* ids, const float* weights, int6
  *          x bf16 [T][H], act bf16 [T*k][I];
  * stage 2: y[r] = act[r] W2[e], w2 [E][H][I], y fp32 [T*k][H].
  * w dtype SFG_BF16 or SFG_I8 (+ scales [E][2I] / [E][H]). */
+/* Workspace bytes sfg_hip_moe_experts_v1 needs for these sizes.  It is 0 for
+ * every shape this build lowers (both stages write only act and y); the query
+ * keeps the workspace convention of the other entries, so a caller that sizes
+ * and passes what it returns stays correct if a later kernel needs scratch. */
 size_t sfg_hip_moe_expert_workspace_v1(int64_t tokens, int64_t hidden, int64_t inter,
                                        int64_t experts, int64_t top_k);
 int sfg_hip_moe_experts_v1(const uint16_t* x, const int32_t* offsets, const int32_t* token_ids,
