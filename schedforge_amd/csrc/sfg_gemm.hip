@@ -947,16 +947,18 @@ __device__ __forceinline__ void qkv_rope_epilogue_staged(const QkvRopeOut& o, co
                     *reinterpret_cast<uint2*>(st + d * 128 + (g ^ (d & 31)) * 4) = pk;
                 }
         const int64_t hv = (wave_col0 - H - kvd) >> 7;
-        const int c = lane & 15;  // positions 8 c .. 8 c + 7 of a d row
+        const int c = lane & 15;                    // positions 8 c .. 8 c + 7 of a d row
+        const int64_t grow = wave_row0 + 8 * c;     // first of the 8 rows
+        const int64_t b = static_cast<uint32_t>(grow) / static_cast<uint32_t>(seq);
+        const int64_t sp = grow - b * seq;
+        uint16_t* const dst0 = o.vt + (b * o.kv_heads + hv) * 128 * o.ld_vt + sp;
 #pragma unroll
         for (int t = 0; t < 32; ++t) {
             const int d = 4 * t + (lane >> 4);
             const int x = d & 31;
             uint4 v = *reinterpret_cast<const uint4*>(st + d * 128 + ((2 * c) ^ (x & ~1)) * 4);
             if (x & 1) v = make_uint4(v.z, v.w, v.x, v.y);  // the two granules of the run swapped
-            const int64_t grow = wave_row0 + 8 * c;         // first of the 8 rows
-            const int64_t b = grow / seq, sp = grow - b * seq;
-            uint16_t* const dst = o.vt + ((b * o.kv_heads + hv) * 128 + d) * o.ld_vt + sp;
+            uint16_t* const dst = dst0 + d * o.ld_vt;
             if (grow + 8 <= re && sp + 8 <= seq) {
                 *reinterpret_cast<uint4*>(dst) = v;
             } else {
@@ -977,14 +979,28 @@ __device__ __forceinline__ void qkv_rope_epilogue_staged(const QkvRopeOut& o, co
     const int64_t heads = isq ? o.q_heads : o.kv_heads;
     const int64_t head = isq ? (wave_col0 >> 7) : ((wave_col0 - H) >> 7);
     const int c8 = lane & 15;  // this lane's 8-column chunk when reading back
+    // (sequence, position) of this lane's first row in block i.  Its rows are
+    // 4 t + (lane >> 4), t = 0..7, so later ones advance the position by 4,
+    // wrapping into the next sequence: one division per block (rows and the
+    // sequence length fit 32 bits on this path) instead of one per row.
+    auto block_pos = [&](int i, int64_t& b, int64_t& sp) {
+        const uint32_t g = static_cast<uint32_t>(wave_row0 + i * 32 + (lane >> 4));
+        b = g / static_cast<uint32_t>(seq);
+        sp = g - b * seq;
+    };
+    auto next_pos = [&](int64_t& b, int64_t& sp) {
+        sp += 4;
+        while (sp >= seq) { sp -= seq; ++b; }
+    };
     // (cos, sin) of this lane's 4 pairs for its 8 rows of block i: all 16
     // table reads of a block are issued one block ahead, so the block never
-    // waits for the table
+    // waits for the table.  (Rows past the end read a valid row, unused.)
     auto table = [&](int i, float4 (&cs)[8][2]) {
+        int64_t bt, sp;
+        block_pos(i, bt, sp);
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
-            const int64_t grow = min(wave_row0 + i * 32 + 4 * t + (lane >> 4), re - 1);
-            const int64_t sp = grow - (grow / seq) * seq;
+            if (t) next_pos(bt, sp);
             const float4* src = reinterpret_cast<const float4*>(o.rope + sp * 64 + c8 * 4);
             cs[t][0] = src[0];
             cs[t][1] = src[1];
@@ -1004,15 +1020,17 @@ __device__ __forceinline__ void qkv_rope_epilogue_staged(const QkvRopeOut& o, co
                 const int row = 8 * (r >> 2) + 4 * khalf + (r & 3);
                 stage[row * 128 + ((j * 32 + l32) ^ ((row & 4) << 3))] = acc[i][j][r];
             }
+        int64_t b, sp;
+        block_pos(i, b, sp);
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
+            if (t) next_pos(b, sp);
             const int row = 4 * t + (lane >> 4);
             const float* src = stage + row * 128 + ((c8 * 8) ^ ((row & 4) << 3));
             const float4 v0 = *reinterpret_cast<const float4*>(src);
             const float4 v1 = *reinterpret_cast<const float4*>(src + 4);
             const int64_t grow = wave_row0 + i * 32 + row;
             if (grow >= re) continue;
-            const int64_t b = grow / seq, sp = grow - b * seq;
             const float4 cs0 = cs[i & 1][t][0], cs1 = cs[i & 1][t][1];  // pairs 4 c8 .. 4 c8 + 3
             // hardware RNE pair conversion: the same bits as pack_bf16x2 for finite values
             auto rot = [](float e, float od, float c, float sn) {
