@@ -983,25 +983,30 @@ __device__ __forceinline__ void qkv_rope_epilogue_staged(const QkvRopeOut& o, co
     // 4 t + (lane >> 4), t = 0..7, so later ones advance the position by 4,
     // wrapping into the next sequence: one division per block (rows and the
     // sequence length fit 32 bits on this path) instead of one per row.
-    auto block_pos = [&](int i, int64_t& b, int64_t& sp) {
+    const uint32_t useq = static_cast<uint32_t>(seq);
+    auto block_pos = [&](int i, uint32_t& b, uint32_t& sp) {
         const uint32_t g = static_cast<uint32_t>(wave_row0 + i * 32 + (lane >> 4));
-        b = g / static_cast<uint32_t>(seq);
-        sp = g - b * seq;
+        b = g / useq;
+        sp = g - b * useq;
     };
-    auto next_pos = [&](int64_t& b, int64_t& sp) {
+    auto next_pos = [&](uint32_t& b, uint32_t& sp) {
         sp += 4;
-        while (sp >= seq) { sp -= seq; ++b; }
+        if (sp >= useq) {  // a sequence boundary (several when seq < 4)
+            const uint32_t q = sp / useq;
+            b += q;
+            sp -= q * useq;
+        }
     };
     // (cos, sin) of this lane's 4 pairs for its 8 rows of block i: all 16
     // table reads of a block are issued one block ahead, so the block never
     // waits for the table.  (Rows past the end read a valid row, unused.)
     auto table = [&](int i, float4 (&cs)[8][2]) {
-        int64_t bt, sp;
+        uint32_t bt, sp;
         block_pos(i, bt, sp);
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
             if (t) next_pos(bt, sp);
-            const float4* src = reinterpret_cast<const float4*>(o.rope + sp * 64 + c8 * 4);
+            const float4* src = reinterpret_cast<const float4*>(o.rope + static_cast<int64_t>(sp) * 64 + c8 * 4);
             cs[t][0] = src[0];
             cs[t][1] = src[1];
         }
@@ -1020,7 +1025,7 @@ __device__ __forceinline__ void qkv_rope_epilogue_staged(const QkvRopeOut& o, co
                 const int row = 8 * (r >> 2) + 4 * khalf + (r & 3);
                 stage[row * 128 + ((j * 32 + l32) ^ ((row & 4) << 3))] = acc[i][j][r];
             }
-        int64_t b, sp;
+        uint32_t b, sp;
         block_pos(i, b, sp);
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
@@ -1041,7 +1046,7 @@ __device__ __forceinline__ void qkv_rope_epilogue_staged(const QkvRopeOut& o, co
             pk.y = rot(v0.z, v0.w, cs0.z, cs0.w);
             pk.z = rot(v1.x, v1.y, cs1.x, cs1.y);
             pk.w = rot(v1.z, v1.w, cs1.z, cs1.w);
-            *reinterpret_cast<uint4*>(base + ((b * heads + head) * seq + sp) * 128 + c8 * 8) = pk;
+            *reinterpret_cast<uint4*>(base + ((static_cast<int64_t>(b) * heads + head) * seq + sp) * 128 + c8 * 8) = pk;
         }
     }
 }
