@@ -906,32 +906,39 @@ __device__ __forceinline__ void qkv_rope_epilogue(const QkvRopeOut& o, const flo
     }
 }
 
-// The same epilogue for a wave's 128 x 128 block of the four-wave 256 x 256
-// tile, through a 16 KB LDS region of its own: for each 32-row block the
-// accumulators go to LDS as fp32 [32][128] (column c of row r at c ^ ((r & 4)
-// << 3), so the two row halves of a write use different banks), then every
-// lane reads 8 consecutive columns of one row, rotates its 4 pairs with a
-// 32-byte read of the (cos, sin) table (issued one row block ahead) and writes
-// 16 bytes of Q or K.  A V^T block is staged transposed and leaves as 16-byte
-// runs of positions; a block that is not a whole head, or V^T when the
-// sequence length is not a multiple of 8, takes the per-lane path.
+// The same epilogue for a wave's block of a four-wave tile (128 x 128 of a
+// 256 x 256 tile, or 64 x 64 of a 128 x 128 one), through the wave's own LDS
+// stage array: for each 32-row block the accumulators go to LDS as fp32
+// [32][kCols] (column c of row r at c ^ ((r & 4) << 3), so the two row halves
+// of a write use different banks), then every lane reads 8 consecutive
+// columns of one row, rotates its 4 pairs with a 32-byte read of the
+// (cos, sin) table (issued one row block ahead) and writes 16 bytes of Q or K.
+// A V^T block is staged transposed and leaves as 16-byte runs of positions; a
+// block past the last column, or V^T when the sequence length is not a
+// multiple of 8, takes the per-lane path.
 template <int WM, int WN>
 __device__ __forceinline__ void qkv_rope_epilogue_staged(const QkvRopeOut& o, const floatx16 (&acc)[WM][WN],
                                                          int64_t wave_row0, int64_t wave_col0, int64_t re,
                                                          int64_t n, int lane, float* stage) {
-    static_assert(WM == 4 && WN == 4, "a 128 x 128 block per wave");
+    static_assert((WM == 4 && WN == 4) || (WM == 2 && WN == 2), "128 x 128 or 64 x 64 per wave");
+    constexpr int kCols = 32 * WN;          // columns of the wave block (within one head)
+    constexpr int kPos = 32 * WM;           // rows (positions) of the wave block
     const int l32 = lane & 31, khalf = lane >> 5;
     const int64_t H = static_cast<int64_t>(o.q_heads) * 128;
     const int64_t kvd = static_cast<int64_t>(o.kv_heads) * 128;
     const int64_t seq = o.seq;
-    if (wave_col0 + 128 > n || (wave_col0 >= H + kvd && seq % 8 != 0)) {
+    if (wave_col0 + kCols > n || (wave_col0 >= H + kvd && seq % 8 != 0)) {
         qkv_rope_epilogue<WM, WN>(o, acc, wave_row0, wave_col0, re, n, l32, khalf);
         return;
     }
+    const int col_in_head = static_cast<int>(wave_col0 & 127);  // 0, or 64 for 64-column blocks
     if (wave_col0 >= H + kvd) {
-        // V^T block: bf16 [128 d][128 s] in LDS, 8-byte granule g of row d at
-        // g ^ (d & 31) (the 32 rows of a write hit 32 distinct granules), then
-        // 16-byte runs of 8 positions of one d row go out whole.
+        // V^T block: bf16 [kCols d][kPos s] in LDS; 8-byte granule g of row d
+        // sits at g ^ x(d), which spreads the 32 rows of a write over distinct
+        // bank pairs (rows are 256 B apart for kPos 128, 128 B for 64).
+        // Then 16-byte runs of 8 positions of one d row go out whole.
+        constexpr int kGran = kPos / 4;
+        auto swz = [](int d) { return kGran == 32 ? (d & 31) : ((d >> 1) & (kGran - 1)); };
         uint16_t* const st = reinterpret_cast<uint16_t*>(stage);
 #pragma unroll
         for (int i = 0; i < WM; ++i)
@@ -944,19 +951,21 @@ __device__ __forceinline__ void qkv_rope_epilogue_staged(const QkvRopeOut& o, co
                     uint2 pk;
                     pk.x = cvt_pk_bf16(acc[i][j][4 * rq + 0], acc[i][j][4 * rq + 1]);
                     pk.y = cvt_pk_bf16(acc[i][j][4 * rq + 2], acc[i][j][4 * rq + 3]);
-                    *reinterpret_cast<uint2*>(st + d * 128 + (g ^ (d & 31)) * 4) = pk;
+                    *reinterpret_cast<uint2*>(st + d * kPos + (g ^ swz(d)) * 4) = pk;
                 }
+        constexpr int kRunLanes = kPos / 8;         // lanes per d row (8 positions each)
+        constexpr int kRowsPer = 64 / kRunLanes;    // d rows per instruction
         const int64_t hv = (wave_col0 - H - kvd) >> 7;
-        const int c = lane & 15;                    // positions 8 c .. 8 c + 7 of a d row
+        const int c = lane % kRunLanes;             // positions 8 c .. 8 c + 7 of a d row
         const int64_t grow = wave_row0 + 8 * c;     // first of the 8 rows
         const int64_t b = static_cast<uint32_t>(grow) / static_cast<uint32_t>(seq);
         const int64_t sp = grow - b * seq;
-        uint16_t* const dst0 = o.vt + (b * o.kv_heads + hv) * 128 * o.ld_vt + sp;
+        uint16_t* const dst0 = o.vt + ((b * o.kv_heads + hv) * 128 + col_in_head) * o.ld_vt + sp;
 #pragma unroll
-        for (int t = 0; t < 32; ++t) {
-            const int d = 4 * t + (lane >> 4);
-            const int x = d & 31;
-            uint4 v = *reinterpret_cast<const uint4*>(st + d * 128 + ((2 * c) ^ (x & ~1)) * 4);
+        for (int t = 0; t < kCols / kRowsPer; ++t) {
+            const int d = kRowsPer * t + lane / kRunLanes;
+            const int x = swz(d);
+            uint4 v = *reinterpret_cast<const uint4*>(st + d * kPos + ((2 * c) ^ (x & ~1)) * 4);
             if (x & 1) v = make_uint4(v.z, v.w, v.x, v.y);  // the two granules of the run swapped
             uint16_t* const dst = dst0 + d * o.ld_vt;
             if (grow + 8 <= re && sp + 8 <= seq) {
@@ -968,7 +977,8 @@ __device__ __forceinline__ void qkv_rope_epilogue_staged(const QkvRopeOut& o, co
                     const int64_t r = grow + e;
                     if (r >= re) break;
                     const int64_t be = r / seq, se = r - be * seq;
-                    o.vt[((be * o.kv_heads + hv) * 128 + d) * o.ld_vt + se] = static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1)));
+                    o.vt[((be * o.kv_heads + hv) * 128 + col_in_head + d) * o.ld_vt + se] =
+                        static_cast<uint16_t>(w[e >> 1] >> (16 * (e & 1)));
                 }
             }
         }
@@ -978,40 +988,45 @@ __device__ __forceinline__ void qkv_rope_epilogue_staged(const QkvRopeOut& o, co
     uint16_t* const base = isq ? o.q : o.k;
     const int64_t heads = isq ? o.q_heads : o.kv_heads;
     const int64_t head = isq ? (wave_col0 >> 7) : ((wave_col0 - H) >> 7);
-    const int c8 = lane & 15;  // this lane's 8-column chunk when reading back
+    constexpr int kChunkLanes = kCols / 8;        // lanes per row when reading back
+    constexpr int kRowsPer = 64 / kChunkLanes;    // rows per read-back step
+    constexpr int kSteps = 32 / kRowsPer;         // steps per 32-row block
+    const int c8 = lane % kChunkLanes;            // this lane's 8-column chunk
+    const int lrow = lane / kChunkLanes;
     // (sequence, position) of this lane's first row in block i.  Its rows are
-    // 4 t + (lane >> 4), t = 0..7, so later ones advance the position by 4,
+    // kRowsPer t + lrow, so later ones advance the position by kRowsPer,
     // wrapping into the next sequence: one division per block (rows and the
     // sequence length fit 32 bits on this path) instead of one per row.
     const uint32_t useq = static_cast<uint32_t>(seq);
     auto block_pos = [&](int i, uint32_t& b, uint32_t& sp) {
-        const uint32_t g = static_cast<uint32_t>(wave_row0 + i * 32 + (lane >> 4));
+        const uint32_t g = static_cast<uint32_t>(wave_row0 + i * 32 + lrow);
         b = g / useq;
         sp = g - b * useq;
     };
     auto next_pos = [&](uint32_t& b, uint32_t& sp) {
-        sp += 4;
-        if (sp >= useq) {  // a sequence boundary (several when seq < 4)
+        sp += kRowsPer;
+        if (sp >= useq) {  // a sequence boundary (several when seq < kRowsPer)
             const uint32_t q = sp / useq;
             b += q;
             sp -= q * useq;
         }
     };
-    // (cos, sin) of this lane's 4 pairs for its 8 rows of block i: all 16
-    // table reads of a block are issued one block ahead, so the block never
-    // waits for the table.  (Rows past the end read a valid row, unused.)
-    auto table = [&](int i, float4 (&cs)[8][2]) {
+    // (cos, sin) of this lane's 4 pairs for its rows of block i: all table
+    // reads of a block are issued one block ahead, so the block never waits
+    // for the table.  (Rows past the end read a valid row, unused.)
+    const int pair0 = col_in_head / 2 + c8 * 4;
+    auto table = [&](int i, float4 (&cs)[kSteps][2]) {
         uint32_t bt, sp;
         block_pos(i, bt, sp);
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
+        for (int t = 0; t < kSteps; ++t) {
             if (t) next_pos(bt, sp);
-            const float4* src = reinterpret_cast<const float4*>(o.rope + static_cast<int64_t>(sp) * 64 + c8 * 4);
+            const float4* src = reinterpret_cast<const float4*>(o.rope + static_cast<int64_t>(sp) * 64 + pair0);
             cs[t][0] = src[0];
             cs[t][1] = src[1];
         }
     };
-    float4 cs[2][8][2];
+    float4 cs[2][kSteps][2];
     table(0, cs[0]);
 #pragma unroll
     for (int i = 0; i < WM; ++i) {
@@ -1023,20 +1038,20 @@ __device__ __forceinline__ void qkv_rope_epilogue_staged(const QkvRopeOut& o, co
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int row = 8 * (r >> 2) + 4 * khalf + (r & 3);
-                stage[row * 128 + ((j * 32 + l32) ^ ((row & 4) << 3))] = acc[i][j][r];
+                stage[row * kCols + ((j * 32 + l32) ^ ((row & 4) << 3))] = acc[i][j][r];
             }
         uint32_t b, sp;
         block_pos(i, b, sp);
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
+        for (int t = 0; t < kSteps; ++t) {
             if (t) next_pos(b, sp);
-            const int row = 4 * t + (lane >> 4);
-            const float* src = stage + row * 128 + ((c8 * 8) ^ ((row & 4) << 3));
+            const int row = kRowsPer * t + lrow;
+            const float* src = stage + row * kCols + ((c8 * 8) ^ ((row & 4) << 3));
             const float4 v0 = *reinterpret_cast<const float4*>(src);
             const float4 v1 = *reinterpret_cast<const float4*>(src + 4);
             const int64_t grow = wave_row0 + i * 32 + row;
             if (grow >= re) continue;
-            const float4 cs0 = cs[i & 1][t][0], cs1 = cs[i & 1][t][1];  // pairs 4 c8 .. 4 c8 + 3
+            const float4 cs0 = cs[i & 1][t][0], cs1 = cs[i & 1][t][1];  // this lane's 4 pairs
             // hardware RNE pair conversion: the same bits as pack_bf16x2 for finite values
             auto rot = [](float e, float od, float c, float sn) {
                 return cvt_pk_bf16(fmaf(e, c, -(od * sn)), fmaf(od, c, e * sn));
@@ -1046,7 +1061,8 @@ __device__ __forceinline__ void qkv_rope_epilogue_staged(const QkvRopeOut& o, co
             pk.y = rot(v0.z, v0.w, cs0.z, cs0.w);
             pk.z = rot(v1.x, v1.y, cs1.x, cs1.y);
             pk.w = rot(v1.z, v1.w, cs1.z, cs1.w);
-            *reinterpret_cast<uint4*>(base + ((static_cast<int64_t>(b) * heads + head) * seq + sp) * 128 + c8 * 8) = pk;
+            *reinterpret_cast<uint4*>(base + ((static_cast<int64_t>(b) * heads + head) * seq + sp) * 128 +
+                                      col_in_head + c8 * 8) = pk;
         }
     }
 }
@@ -1795,7 +1811,10 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
         else store_tile(static_cast<uint16_t*>(p.c));
     }
     if constexpr (EPI == kEpiQkvRope) {
-        if constexpr (S64) {
+        // four-wave tiles with square wave blocks stage through LDS (a wave's
+        // own stage array holds its fp32 32-row block and its V^T block)
+        constexpr bool kStaged = NW == 4 && !PP && ((WM == 4 && WN == 4) || (WM == 2 && WN == 2));
+        if constexpr (kStaged) {
             // every wave's reads of the last slabs are done before any wave
             // reuses its array as staging (the DMA drained above)
             wait_lds();
