@@ -1210,6 +1210,189 @@ struct DmaShapeTraits {
     static constexpr int dma_bytes = 16;  // per lane per LDS DMA instruction (dwordx4)
 };
 
+// Tile of this workgroup in a direct-to-LDS launch.  Grouped (p.offsets):
+// blockIdx.x is the column tile, blockIdx.y walks the row tiles of the groups
+// in order (group g: ceil(rows_g / BM) tiles; false past the last).  Dense: a
+// 1-D grid of tiles_m x tiles_n tiles in the XCD-aware order.  Sets the group
+// g, its row range [rb, re) and the tile (tm, tn).
+template <int BM>
+__device__ __forceinline__ bool dma_tile_coords(const TiledArgs& p, int tiles_m, int tiles_n, int& g,
+                                                int64_t& rb, int64_t& re, int64_t& tm, int64_t& tn) {
+    g = 0;
+    rb = 0;
+    re = p.m;
+    if (p.offsets) {
+        tn = blockIdx.x;
+        int64_t t = blockIdx.y;
+        auto bound = [&](int e) {
+            return min(max(static_cast<int64_t>(p.offsets[e]), int64_t(0)), p.m);
+        };
+        g = -1;
+        for (int e = 0; e < p.groups; ++e) {
+            const int64_t rows = max(bound(e + 1) - bound(e), int64_t(0));
+            const int64_t tiles = (rows + BM - 1) / BM;
+            if (t < tiles) { g = e; break; }
+            t -= tiles;
+        }
+        if (g < 0) return false;
+        rb = bound(g);
+        re = max(bound(g + 1), rb);
+        tm = t;
+    } else {
+        // XCD-aware order: the dispatcher deals consecutive workgroup ids to
+        // the XCDs in turn, so hand each XCD a contiguous run of tiles and
+        // walk them in groups of 8 M-tiles (A and B tiles shared in one L2).
+        const int64_t total = static_cast<int64_t>(tiles_m) * tiles_n;
+        const int64_t i = blockIdx.x;
+        const int64_t x = p.xcds;
+        const int64_t full = total - total % x;
+        int64_t L = i;
+        if (i < full) L = (i % x) * (full / x) + i / x;
+        constexpr int64_t kGroupM = 8;
+        const int64_t group = L / (kGroupM * tiles_n);
+        const int64_t first_m = group * kGroupM;
+        const int64_t gsize = min(static_cast<int64_t>(tiles_m) - first_m, kGroupM);
+        const int64_t in_group = L % (kGroupM * tiles_n);
+        tm = first_m + in_group % gsize;
+        tn = in_group / gsize;
+    }
+    return true;
+}
+
+// Store epilogue of one wave's (BM / 2) x (BN / (NW / 2)) block of a
+// direct-to-LDS tile (wave (wm, wn) of the 2 x (NW / 2) wave grid), for every
+// epilogue but the staged GLU one of the 64-k slab tile.  qkv_stage: this
+// wave's own LDS region for the staged QKV epilogue (every wave calls this
+// function: the staged path meets the others at a barrier first).
+template <int BM, int BN, int NW, int EPI, bool PP, int WM, int WN>
+__device__ __forceinline__ void dma_tile_epilogue(const TiledArgs& p, const floatx16 (&acc)[WM][WN], int wm,
+                                                  int wn, int64_t row0, int64_t ncol0, int64_t re,
+                                                  const float* scales, float* qkv_stage) {
+    constexpr bool kGlu = EpiTraits<EPI>::glu;
+    constexpr int kWavesM = 2, kWavesN = NW / 2;
+    static_assert(WM == BM / (32 * kWavesM) && WN == BN / (32 * kWavesN), "wave block shape");
+    // The epilogues take the lane index again from the lane mask, so no
+    // lane-derived value of the prologue has to live through the main loop.
+    const int elane = static_cast<int>(__lane_id());
+    const int el32 = elane & 31, ekhalf = elane >> 5;
+    // Epilogue: 32x32 D layout, lane holds column (lane & 31) and rows
+    // 8 (r / 4) + 4 (lane >> 5) + (r % 4).  The output dtype and the scales are
+    // resolved once per tile, a lane's scales (its columns are fixed) are read
+    // once, and the residual loads of a group of half blocks (at clamped,
+    // always valid addresses) all precede the group's first store, so the
+    // group waits for memory once instead of once per element; only the
+    // stores are guarded.
+    if constexpr (EPI != kEpiQkvRope) {
+        constexpr int kCols = kGlu ? WN / 2 : WN;  // output columns per lane
+        int64_t cols[kCols];
+        float sc_lo[kCols], sc_hi[kCols];
+#pragma unroll
+        for (int j = 0; j < kCols; ++j) {
+            cols[j] = kGlu ? ncol0 + (wn * WN / 2 + j) * 32 + el32 : ncol0 + wn * (BN / kWavesN) + j * 32 + el32;
+            const int64_t cc = min(cols[j], p.n - 1);
+            sc_lo[j] = scales ? scales[cc] : 1.f;
+            sc_hi[j] = (kGlu && scales) ? scales[p.n + cc] : 1.f;
+        }
+        // Residual rows [0, m) addressable with 32-bit byte offsets: loads go
+        // through a buffer resource (reads past its end return 0, and every
+        // load of a column >= n feeds only an output that is not stored).
+        const bool res_rsrc_ok = EPI == SFG_EPI_RESIDUAL && p.residual &&
+                                 static_cast<uint64_t>(p.m) * p.ldr * 4 <= 0xFFFFFFFFull;
+        const buf_rsrc res_rsrc = make_rsrc(p.residual, res_rsrc_ok ? static_cast<uint32_t>(p.m * p.ldr * 4) : 0u);
+        auto store_tile = [&](auto* out) {
+            using OutT = std::remove_pointer_t<decltype(out)>;
+            // Residual epilogues load the residual of kGroup half blocks before
+            // the first of their stores (each element is still read before it
+            // is written, so an in-place residual stays correct): the tile
+            // waits for memory 2 WM / kGroup times instead of 2 WM.
+            // (four-wave 256 x 256 tiles only: the others have no registers for it).
+            constexpr int kGroup = (EPI == SFG_EPI_RESIDUAL && NW == 4 && BM == 256 && BN == 256) ? 4 : 1;
+#pragma unroll
+            for (int g0 = 0; g0 < 2 * WM; g0 += kGroup) {
+                float res[kGroup][8][kCols];
+                if constexpr (EPI == SFG_EPI_RESIDUAL) {
+                    if (kGroup > 1 && res_rsrc_ok) {
+                        // 32-bit offsets through a buffer resource over the
+                        // residual rows [0, m): one offset per row, the column
+                        // blocks 128 B apart as immediate offsets
+#pragma unroll
+                        for (int h = 0; h < kGroup; ++h) {
+                            const int ih = g0 + h, i = ih >> 1, r0 = (ih & 1) * 8;
+                            const int64_t rbase = row0 + wm * (BM / kWavesM) + i * 32 + 4 * ekhalf;
+#pragma unroll
+                            for (int rr = 0; rr < 8; ++rr) {
+                                const int r = r0 + rr;
+                                const int64_t row = min(rbase + 8 * (r >> 2) + (r & 3), re - 1);
+                                const uint32_t off = static_cast<uint32_t>((row * p.ldr + cols[0]) * 4);
+#pragma unroll
+                                for (int j = 0; j < kCols; ++j)
+                                    res[h][rr][j] = __builtin_bit_cast(
+                                        float, __builtin_amdgcn_raw_buffer_load_b32(res_rsrc, off + j * 128, 0, 0));
+                            }
+                        }
+                    } else {
+#pragma unroll
+                        for (int h = 0; h < kGroup; ++h) {
+                            const int ih = g0 + h, i = ih >> 1, r0 = (ih & 1) * 8;
+                            const int64_t rbase = row0 + wm * (BM / kWavesM) + i * 32 + 4 * ekhalf;
+#pragma unroll
+                            for (int rr = 0; rr < 8; ++rr)
+#pragma unroll
+                                for (int j = 0; j < kCols; ++j) {
+                                    const int r = r0 + rr;
+                                    const int64_t row = min(rbase + 8 * (r >> 2) + (r & 3), re - 1);
+                                    res[h][rr][j] = p.residual[row * p.ldr + min(cols[j], p.n - 1)];
+                                }
+                        }
+                    }
+                }
+#pragma unroll
+                for (int h = 0; h < kGroup; ++h) {  // half 32-row blocks: 8 accumulator rows each
+                    const int ih = g0 + h, i = ih >> 1, r0 = (ih & 1) * 8;
+                    const int64_t rbase = row0 + wm * (BM / kWavesM) + i * 32 + 4 * ekhalf;
+#pragma unroll
+                    for (int rr = 0; rr < 8; ++rr) {
+                        const int r = r0 + rr;
+                        const int64_t row = rbase + 8 * (r >> 2) + (r & 3);
+#pragma unroll
+                        for (int j = 0; j < kCols; ++j) {
+                            float v;
+                            if constexpr (kGlu) {
+                                v = glu_combine(EPI, acc[i][2 * j][r] * sc_lo[j], acc[i][2 * j + 1][r] * sc_hi[j]);
+                            } else {
+                                v = acc[i][j][r] * sc_lo[j];
+                                if constexpr (EPI == SFG_EPI_RESIDUAL) v += res[h][rr][j];
+                            }
+                            if (row < re && cols[j] < p.n) {
+                                if constexpr (sizeof(OutT) == 4) out[row * p.ldc + cols[j]] = v;
+                                else out[row * p.ldc + cols[j]] = f32_to_bf16(v);
+                            }
+                        }
+                    }
+                }
+            }
+        };
+        if (p.c_dtype == SFG_F32) store_tile(static_cast<float*>(p.c));
+        else store_tile(static_cast<uint16_t*>(p.c));
+    }
+    if constexpr (EPI == kEpiQkvRope) {
+        // four-wave tiles with square wave blocks stage through LDS (a wave's
+        // own stage array holds its fp32 32-row block and its V^T block)
+        constexpr bool kStaged = NW == 4 && !PP && ((WM == 4 && WN == 4) || (WM == 2 && WN == 2));
+        if constexpr (kStaged) {
+            // every wave's reads of the last slabs are done before any wave
+            // reuses its array as staging (the DMA drained above)
+            wait_lds();
+            barrier_no_fence();
+            qkv_rope_epilogue_staged<WM, WN>(p.qkv, acc, row0 + wm * (BM / kWavesM), ncol0 + wn * (BN / kWavesN),
+                                             re, p.n, elane, qkv_stage);
+        } else {
+            qkv_rope_epilogue<WM, WN>(p.qkv, acc, row0 + wm * (BM / kWavesM), ncol0 + wn * (BN / kWavesN), re,
+                                      p.n, el32, ekhalf);
+        }
+    }
+}
+
 template <int BM, int BN, int NW, int EPI, bool PP = false, bool S64 = false>
 __global__ __launch_bounds__(NW * 64)
 __attribute__((amdgpu_waves_per_eu(DmaShapeTraits<BM, BN, NW>::occupancy,
@@ -1239,44 +1422,9 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
     const int wm = wave / kWavesN, wn = wave % kWavesN;
     constexpr int kOutCols = kGlu ? BN / 2 : BN;
 
-    int g = 0;
-    int64_t rb = 0, re = p.m;
-    int64_t tm, tn;
-    if (p.offsets) {
-        tn = blockIdx.x;
-        int64_t t = blockIdx.y;
-        auto bound = [&](int e) {
-            return min(max(static_cast<int64_t>(p.offsets[e]), int64_t(0)), p.m);
-        };
-        g = -1;
-        for (int e = 0; e < p.groups; ++e) {
-            const int64_t rows = max(bound(e + 1) - bound(e), int64_t(0));
-            const int64_t tiles = (rows + BM - 1) / BM;
-            if (t < tiles) { g = e; break; }
-            t -= tiles;
-        }
-        if (g < 0) return;
-        rb = bound(g);
-        re = max(bound(g + 1), rb);
-        tm = t;
-    } else {
-        // XCD-aware order: the dispatcher deals consecutive workgroup ids to
-        // the XCDs in turn, so hand each XCD a contiguous run of tiles and
-        // walk them in groups of 8 M-tiles (A and B tiles shared in one L2).
-        const int64_t total = static_cast<int64_t>(tiles_m) * tiles_n;
-        const int64_t i = blockIdx.x;
-        const int64_t x = p.xcds;
-        const int64_t full = total - total % x;
-        int64_t L = i;
-        if (i < full) L = (i % x) * (full / x) + i / x;
-        constexpr int64_t kGroupM = 8;
-        const int64_t group = L / (kGroupM * tiles_n);
-        const int64_t first_m = group * kGroupM;
-        const int64_t gsize = min(static_cast<int64_t>(tiles_m) - first_m, kGroupM);
-        const int64_t in_group = L % (kGroupM * tiles_n);
-        tm = first_m + in_group % gsize;
-        tn = in_group / gsize;
-    }
+    int g;
+    int64_t rb, re, tm, tn;
+    if (!dma_tile_coords<BM>(p, tiles_m, tiles_n, g, rb, re, tm, tn)) return;
     const int64_t row0 = rb + tm * BM;
     if (row0 >= re) return;
     const int64_t ncol0 = tn * kOutCols;
@@ -1692,13 +1840,12 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
     }
     }
     wait_vmem<0>();
-    // The epilogues take the lane index again from the lane mask, so no
-    // lane-derived value of the prologue has to live through the main loop.
-    const int elane = static_cast<int>(__lane_id());
-    const int el32 = elane & 31, ekhalf = elane >> 5;
 
     if constexpr (S64 && kGlu) {
         if (p.c_dtype == SFG_BF16) {
+            // the lane index again from the lane mask, so no lane-derived
+            // value of the prologue has to live through the main loop
+            const int elane = static_cast<int>(__lane_id());
             // every wave's reads of the last slabs are done before any wave
             // reuses its array as staging (the DMA drained above)
             wait_lds();
@@ -1710,123 +1857,8 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
         }
     }
 
-    // Epilogue: 32x32 D layout, lane holds column (lane & 31) and rows
-    // 8 (r / 4) + 4 (lane >> 5) + (r % 4).  The output dtype and the scales are
-    // resolved once per tile, a lane's scales (its columns are fixed) are read
-    // once, and the residual loads of a group of half blocks (at clamped,
-    // always valid addresses) all precede the group's first store, so the
-    // group waits for memory once instead of once per element; only the
-    // stores are guarded.
-    if constexpr (EPI != kEpiQkvRope) {
-        constexpr int kCols = kGlu ? WN / 2 : WN;  // output columns per lane
-        int64_t cols[kCols];
-        float sc_lo[kCols], sc_hi[kCols];
-#pragma unroll
-        for (int j = 0; j < kCols; ++j) {
-            cols[j] = kGlu ? ncol0 + (wn * WN / 2 + j) * 32 + el32 : ncol0 + wn * (BN / kWavesN) + j * 32 + el32;
-            const int64_t cc = min(cols[j], p.n - 1);
-            sc_lo[j] = scales ? scales[cc] : 1.f;
-            sc_hi[j] = (kGlu && scales) ? scales[p.n + cc] : 1.f;
-        }
-        // Residual rows [0, m) addressable with 32-bit byte offsets: loads go
-        // through a buffer resource (reads past its end return 0, and every
-        // load of a column >= n feeds only an output that is not stored).
-        const bool res_rsrc_ok = EPI == SFG_EPI_RESIDUAL && p.residual &&
-                                 static_cast<uint64_t>(p.m) * p.ldr * 4 <= 0xFFFFFFFFull;
-        const buf_rsrc res_rsrc = make_rsrc(p.residual, res_rsrc_ok ? static_cast<uint32_t>(p.m * p.ldr * 4) : 0u);
-        auto store_tile = [&](auto* out) {
-            using OutT = std::remove_pointer_t<decltype(out)>;
-            // Residual epilogues load the residual of kGroup half blocks before
-            // the first of their stores (each element is still read before it
-            // is written, so an in-place residual stays correct): the tile
-            // waits for memory 2 WM / kGroup times instead of 2 WM.
-            // (four-wave 256 x 256 tiles only: the others have no registers for it).
-            constexpr int kGroup = (EPI == SFG_EPI_RESIDUAL && NW == 4 && BM == 256 && BN == 256) ? 4 : 1;
-#pragma unroll
-            for (int g0 = 0; g0 < 2 * WM; g0 += kGroup) {
-                float res[kGroup][8][kCols];
-                if constexpr (EPI == SFG_EPI_RESIDUAL) {
-                    if (kGroup > 1 && res_rsrc_ok) {
-                        // 32-bit offsets through a buffer resource over the
-                        // residual rows [0, m): one offset per row, the column
-                        // blocks 128 B apart as immediate offsets
-#pragma unroll
-                        for (int h = 0; h < kGroup; ++h) {
-                            const int ih = g0 + h, i = ih >> 1, r0 = (ih & 1) * 8;
-                            const int64_t rbase = row0 + wm * (BM / kWavesM) + i * 32 + 4 * ekhalf;
-#pragma unroll
-                            for (int rr = 0; rr < 8; ++rr) {
-                                const int r = r0 + rr;
-                                const int64_t row = min(rbase + 8 * (r >> 2) + (r & 3), re - 1);
-                                const uint32_t off = static_cast<uint32_t>((row * p.ldr + cols[0]) * 4);
-#pragma unroll
-                                for (int j = 0; j < kCols; ++j)
-                                    res[h][rr][j] = __builtin_bit_cast(
-                                        float, __builtin_amdgcn_raw_buffer_load_b32(res_rsrc, off + j * 128, 0, 0));
-                            }
-                        }
-                    } else {
-#pragma unroll
-                        for (int h = 0; h < kGroup; ++h) {
-                            const int ih = g0 + h, i = ih >> 1, r0 = (ih & 1) * 8;
-                            const int64_t rbase = row0 + wm * (BM / kWavesM) + i * 32 + 4 * ekhalf;
-#pragma unroll
-                            for (int rr = 0; rr < 8; ++rr)
-#pragma unroll
-                                for (int j = 0; j < kCols; ++j) {
-                                    const int r = r0 + rr;
-                                    const int64_t row = min(rbase + 8 * (r >> 2) + (r & 3), re - 1);
-                                    res[h][rr][j] = p.residual[row * p.ldr + min(cols[j], p.n - 1)];
-                                }
-                        }
-                    }
-                }
-#pragma unroll
-                for (int h = 0; h < kGroup; ++h) {  // half 32-row blocks: 8 accumulator rows each
-                    const int ih = g0 + h, i = ih >> 1, r0 = (ih & 1) * 8;
-                    const int64_t rbase = row0 + wm * (BM / kWavesM) + i * 32 + 4 * ekhalf;
-#pragma unroll
-                    for (int rr = 0; rr < 8; ++rr) {
-                        const int r = r0 + rr;
-                        const int64_t row = rbase + 8 * (r >> 2) + (r & 3);
-#pragma unroll
-                        for (int j = 0; j < kCols; ++j) {
-                            float v;
-                            if constexpr (kGlu) {
-                                v = glu_combine(EPI, acc[i][2 * j][r] * sc_lo[j], acc[i][2 * j + 1][r] * sc_hi[j]);
-                            } else {
-                                v = acc[i][j][r] * sc_lo[j];
-                                if constexpr (EPI == SFG_EPI_RESIDUAL) v += res[h][rr][j];
-                            }
-                            if (row < re && cols[j] < p.n) {
-                                if constexpr (sizeof(OutT) == 4) out[row * p.ldc + cols[j]] = v;
-                                else out[row * p.ldc + cols[j]] = f32_to_bf16(v);
-                            }
-                        }
-                    }
-                }
-            }
-        };
-        if (p.c_dtype == SFG_F32) store_tile(static_cast<float*>(p.c));
-        else store_tile(static_cast<uint16_t*>(p.c));
-    }
-    if constexpr (EPI == kEpiQkvRope) {
-        // four-wave tiles with square wave blocks stage through LDS (a wave's
-        // own stage array holds its fp32 32-row block and its V^T block)
-        constexpr bool kStaged = NW == 4 && !PP && ((WM == 4 && WN == 4) || (WM == 2 && WN == 2));
-        if constexpr (kStaged) {
-            // every wave's reads of the last slabs are done before any wave
-            // reuses its array as staging (the DMA drained above)
-            wait_lds();
-            barrier_no_fence();
-            float* const stage = reinterpret_cast<float*>(wave == 0 ? sS0 : wave == 1 ? sS1 : wave == 2 ? sS2 : sS3);
-            qkv_rope_epilogue_staged<WM, WN>(p.qkv, acc, row0 + wm * (BM / kWavesM), ncol0 + wn * (BN / kWavesN),
-                                             re, p.n, elane, stage);
-        } else {
-            qkv_rope_epilogue<WM, WN>(p.qkv, acc, row0 + wm * (BM / kWavesM), ncol0 + wn * (BN / kWavesN), re,
-                                      p.n, el32, ekhalf);
-        }
-    }
+    float* const qkv_stage = reinterpret_cast<float*>(wave == 0 ? sS0 : wave == 1 ? sS1 : wave == 2 ? sS2 : sS3);
+    dma_tile_epilogue<BM, BN, NW, EPI, PP>(p, acc, wm, wn, row0, ncol0, re, scales, qkv_stage);
 }
 
 // ===========================================================================

@@ -51,7 +51,7 @@ __device__ void route_select(const float* lg, int experts, int top_k, int tok, i
 }
 
 constexpr int kRouteChunk = 512;
-constexpr int kRouteTokens = 4;        // tokens per workgroup
+constexpr int kRouteTokens = 8;        // tokens per workgroup: 64 chains, one full wave (measured 4% faster than 4 on C3 and C5)
 constexpr int kRouteMaxExperts = 8;    // staged path; larger E uses the direct chain
 constexpr int kRouteBlock = 16;        // chain operands per register block
 // Floats of padding per staged row: room for one block read past the chunk,
