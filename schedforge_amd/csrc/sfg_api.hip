@@ -834,11 +834,11 @@ int sfg_hip_decoder_layer_v1(const sfg_layer_desc* d, const sfg_layer_weights* w
 
     const Marks mk{io->stage_events, s};
     auto gemm = [&](const void* a, int64_t lda, const void* bw, const float* bs, void* c, int c_dtype,
-                    const float* res, int64_t m, int64_t n, int64_t k, int epi) -> int {
+                    const float* res, int64_t m, int64_t n, int64_t k, int epi, int64_t ldc = 0) -> int {
         sfg::GemmProblem p{};
         p.a = a; p.a_dtype = act; p.lda = lda;
         p.b = bw; p.b_dtype = wdt; p.ldb = k; p.b_scales = bs;
-        p.c = c; p.c_dtype = c_dtype; p.ldc = n;
+        p.c = c; p.c_dtype = c_dtype; p.ldc = ldc > 0 ? ldc : n;
         p.residual = res; p.ldr = n;
         p.m = m; p.n = n; p.k = k; p.epilogue = epi; p.groups = 1;
         p.b_layout = d->weight_layout;
@@ -876,7 +876,12 @@ int sfg_hip_decoder_layer_v1(const sfg_layer_desc* d, const sfg_layer_weights* w
         if (ld_vt != d->sequence) sfg::launch_fill_zero(b.v, static_cast<size_t>(d->batch) * kvd * ld_vt * 2, s);
         const int r = sfg::launch_gemm(qp, b.gemm_ws, b.gemm_ws_bytes, s);
         if (r != SFG_OK) return fail(r, "decoder layer QKV GEMM with RoPE epilogue not lowered");
-    } else if ((rc = gemm(b.xn, H, w->w_qkv, w->s_qkv, b.qkv, SFG_F32, nullptr, rows, qkvw, H, SFG_EPI_NONE))) {
+    } else if ((rc = gemm(b.xn, H, w->w_qkv, w->s_qkv, b.qkv, SFG_F32, nullptr, rows,
+                          // a reference decode step attends over the cache only and
+                          // discards the step's K / V (decoder_compiler.cpp:238-243):
+                          // only the Q columns are computed (the first H weight rows,
+                          // a prefix in both weight layouts), into the same rows
+                          decode && !d->kv_append ? H : qkvw, H, SFG_EPI_NONE, qkvw))) {
         return rc;
     }
     mk.mark(SFG_MARK_QKV);
