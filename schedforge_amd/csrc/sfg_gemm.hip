@@ -283,7 +283,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny_kernel(SkinnyArgs p) {
 // L2 for every column tile.  Here a workgroup owns 128 B rows (4 waves x two
 // 16-row tiles) and one 512-k slice: it stages the slice's 64 activation rows
 // in LDS once (rows padded by 16 B so the 16 rows of a fragment read fall on
-// distinct banks), issues every weight load of the slice before that, and
+// distinct banks), with every activation load and then every weight load of
+// the slice in flight together (one memory round trip per workgroup), and
 // writes raw fp32 partial sums [slice][m][n_b].  gemm_splitk_reduce_kernel
 // then sums the slices in order 0, 1, ... and applies the per-channel scale
 // and the epilogue, so the result does not depend on scheduling.
@@ -315,7 +316,22 @@ __global__ __launch_bounds__(256) void gemm_splitk_kernel(SplitArgs p) {
     const int64_t k0 = static_cast<int64_t>(blockIdx.y) * kSplitKS;
     const int64_t col0 = static_cast<int64_t>(blockIdx.x) * kSplitCols + wave * 16 * kSplitTiles;
 
-    // 1. every weight load of this wave's two tiles over the slice
+    // 1. the slice's activation rows, issued first:
+    //    loads return in order, so their LDS stores wait on these alone
+    constexpr int kVecsPerRow = kSplitKS / 8;
+    constexpr int kStageVecs = kSplitRows * kVecsPerRow / 256;
+    uint4 av[kStageVecs];
+#pragma unroll
+    for (int i = 0; i < kStageVecs; ++i) {
+        const int q = tid + 256 * i;
+        const int row = q / kVecsPerRow, v = q % kVecsPerRow;
+        // rows past m read row m - 1 (no branch around the load: a
+        // conditional load is waited for before the branches join) and are
+        // zeroed at the store
+        const int64_t src = row < p.m ? row : p.m - 1;
+        av[i] = *reinterpret_cast<const uint4*>(p.a + src * p.lda + k0 + 8 * v);
+    }
+    // 2. every weight load of this wave's two tiles over the slice
     const char* bbase = static_cast<const char*>(p.b);
     const int64_t chunk_count = p.k / kSkinnyChunk;
     constexpr int64_t kTileBytes = 16 * kSkinnyChunk * ((BDT == SFG_I8) ? 1 : 2);
@@ -339,18 +355,18 @@ __global__ __launch_bounds__(256) void gemm_splitk_kernel(SplitArgs p) {
             }
         }
     }
-    // 2. the slice's activation rows -> LDS (rows >= m read as zero)
-    constexpr int kVecsPerRow = kSplitKS / 8;
-#pragma unroll 4
-    for (int q = tid; q < kSplitRows * kVecsPerRow; q += 256) {
+    // 3. activations -> LDS
+#pragma unroll
+    for (int i = 0; i < kStageVecs; ++i) {
+        const int q = tid + 256 * i;
         const int row = q / kVecsPerRow, v = q % kVecsPerRow;
-        uint4 val = make_uint4(0, 0, 0, 0);
-        if (row < p.m) val = *reinterpret_cast<const uint4*>(p.a + row * p.lda + k0 + 8 * v);
-        *reinterpret_cast<uint4*>(&sa[row * kSplitLdA + 8 * v]) = val;
+        *reinterpret_cast<uint4*>(&sa[row * kSplitLdA + 8 * v]) = row < p.m ? av[i] : make_uint4(0, 0, 0, 0);
     }
-    __syncthreads();
+    // LDS stores done, weight loads still in flight across the barrier
+    wait_lds();
+    barrier_no_fence();
 
-    // 3. MFMAs: A fragments from LDS in the k order of the weight fragments
+    // 4. MFMAs: A fragments from LDS in the k order of the weight fragments
     floatx4 acc[4][kSplitTiles];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -383,7 +399,7 @@ __global__ __launch_bounds__(256) void gemm_splitk_kernel(SplitArgs p) {
             }
         }
     }
-    // 4. partial sums: lane holds column lr, rows 4 lg + r of each 16-row tile
+    // 5. partial sums: lane holds column lr, rows 4 lg + r of each 16-row tile
     float* part = p.part + static_cast<int64_t>(blockIdx.y) * p.m * p.nb;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
