@@ -19,6 +19,7 @@
 //    double-buffered in registers, waves merge in LDS, splits merge in a
 //    second small kernel.
 #include <cstdlib>
+#include <type_traits>
 
 #include "sfg_kernels.hpp"
 
@@ -830,7 +831,8 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(
     }
 }
 
-template <typename OutT, int kDecD>
+// NS > 0: at most NS splits, merged from registers; NS = 0: any count.
+template <typename OutT, int kDecD, int NS>
 __global__ __launch_bounds__(kDecD) void attn_decode_combine_kernel(
     const float* __restrict__ part_ml, const float* __restrict__ part_acc, OutT* __restrict__ out,
     int q_heads, int splits) {
@@ -840,23 +842,29 @@ __global__ __launch_bounds__(kDecD) void attn_decode_combine_kernel(
     const float* pa = part_acc + static_cast<int64_t>(bh) * splits * kDecD + d;
     float mm = -INFINITY;
     float ls = 0.f, as = 0.f;
-    constexpr int kRegSplits = 16;
-    if (splits <= kRegSplits) {
-        // every split's (m, l, acc) loaded before the merge: one memory wait
-        float m_s[kRegSplits], l_s[kRegSplits], a_s[kRegSplits];
+    if constexpr (NS > 0) {
+        // every split's (m, l, acc) loaded before the merge: one memory wait.
+        // Slots past the split count re-read the last split (no branch around
+        // a load: a conditional load is waited for before the branches join)
+        // and are left out of the sums.
+        float m_s[NS], l_s[NS], a_s[NS];
 #pragma unroll
-        for (int s = 0; s < kRegSplits; ++s) {
-            if (s < splits) {
-                m_s[s] = ml[2 * s];
-                l_s[s] = ml[2 * s + 1];
-                a_s[s] = pa[s * kDecD];
-            }
+        for (int s = 0; s < NS; ++s) {
+            const int sc = s < splits ? s : splits - 1;
+            m_s[s] = ml[2 * sc];
+            l_s[s] = ml[2 * sc + 1];
+            a_s[s] = pa[sc * kDecD];
         }
+        // the merge below branches on the (uniform) split maxima; an empty use
+        // keeps the compiler from sinking the acc loads into those branches,
+        // where they would be issued and waited for one at a time
 #pragma unroll
-        for (int s = 0; s < kRegSplits; ++s)
+        for (int s = 0; s < NS; ++s) asm volatile("" ::"v"(a_s[s]));
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
             if (s < splits) mm = fmaxf(mm, m_s[s]);
 #pragma unroll
-        for (int s = 0; s < kRegSplits; ++s) {
+        for (int s = 0; s < NS; ++s) {
             if (s < splits) {
                 const float wf = (m_s[s] == -INFINITY) ? 0.f : fast_exp2(m_s[s] - mm);
                 ls += l_s[s] * wf;
@@ -903,6 +911,7 @@ int launch_attn_decode_paged(const float* q, int64_t q_row_stride, const float* 
                              int64_t pages_per_seq, int64_t num_pages, int splits, float scale,
                              void* workspace, hipStream_t stream, hipEvent_t mid_event) {
     if ((head_dim != 128 && head_dim != 64) || page_tokens != kPageTok) return SFG_ERR_UNSUPPORTED;
+    if (splits < 1) return SFG_ERR_SHAPE;
     const int group = static_cast<int>(q_heads / kv_heads);
     const size_t slots = static_cast<size_t>(batch) * q_heads * splits;
     float* part_ml = static_cast<float*>(workspace);
@@ -934,16 +943,21 @@ int launch_attn_decode_paged(const float* q, int64_t q_row_stride, const float* 
     if (mid_event) (void)hipEventRecord(mid_event, stream);
     const dim3 cgrid(static_cast<unsigned>(batch * q_heads));
     const int qh = static_cast<int>(q_heads);
+    auto combine = [&](auto* o, auto dcon) {
+        using OutT = std::remove_pointer_t<decltype(o)>;
+        constexpr int D = decltype(dcon)::value;
+        if (splits <= 2) attn_decode_combine_kernel<OutT, D, 2><<<cgrid, D, 0, stream>>>(part_ml, part_acc, o, qh, splits);
+        else if (splits <= 4) attn_decode_combine_kernel<OutT, D, 4><<<cgrid, D, 0, stream>>>(part_ml, part_acc, o, qh, splits);
+        else if (splits <= 8) attn_decode_combine_kernel<OutT, D, 8><<<cgrid, D, 0, stream>>>(part_ml, part_acc, o, qh, splits);
+        else if (splits <= 16) attn_decode_combine_kernel<OutT, D, 16><<<cgrid, D, 0, stream>>>(part_ml, part_acc, o, qh, splits);
+        else attn_decode_combine_kernel<OutT, D, 0><<<cgrid, D, 0, stream>>>(part_ml, part_acc, o, qh, splits);
+    };
     if (head_dim == 128) {
-        if (out_dtype == SFG_F32)
-            attn_decode_combine_kernel<float, 128><<<cgrid, 128, 0, stream>>>(part_ml, part_acc, static_cast<float*>(out), qh, splits);
-        else
-            attn_decode_combine_kernel<uint16_t, 128><<<cgrid, 128, 0, stream>>>(part_ml, part_acc, static_cast<uint16_t*>(out), qh, splits);
+        if (out_dtype == SFG_F32) combine(static_cast<float*>(out), std::integral_constant<int, 128>{});
+        else combine(static_cast<uint16_t*>(out), std::integral_constant<int, 128>{});
     } else {
-        if (out_dtype == SFG_F32)
-            attn_decode_combine_kernel<float, 64><<<cgrid, 64, 0, stream>>>(part_ml, part_acc, static_cast<float*>(out), qh, splits);
-        else
-            attn_decode_combine_kernel<uint16_t, 64><<<cgrid, 64, 0, stream>>>(part_ml, part_acc, static_cast<uint16_t*>(out), qh, splits);
+        if (out_dtype == SFG_F32) combine(static_cast<float*>(out), std::integral_constant<int, 64>{});
+        else combine(static_cast<uint16_t*>(out), std::integral_constant<int, 64>{});
     }
     return SFG_OK;
 }

@@ -431,6 +431,21 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(SplitReduceArgs
     const float* pr = p.part + row * p.nb + col;
     constexpr int kBatch = 8;  // slices loaded together, then added in order
     constexpr bool kGlu = EpiTraits<EPI>::glu;
+    // The epilogue's scales and residual values are read before any store:
+    // the output may alias them for all the compiler knows, so loads placed
+    // after a store would each wait a full memory round trip.
+    float sg[4], su[4], rv[4];
+    if (p.scales) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            sg[e] = p.scales[col + e];
+            if constexpr (kGlu) su[e] = p.scales[p.n + col + e];
+        }
+    }
+    if constexpr (EPI == SFG_EPI_RESIDUAL) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) rv[e] = p.residual[row * p.ldr + col + e];
+    }
     float gv[4] = {0.f, 0.f, 0.f, 0.f}, uv[4] = {0.f, 0.f, 0.f, 0.f};
     for (int s0 = 0; s0 < p.slices; s0 += kBatch) {
         float4 g[kBatch], u[kGlu ? kBatch : 1];
@@ -455,14 +470,14 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(SplitReduceArgs
         if (kGlu) {
             float gg = gv[e], uu = uv[e];
             if (p.scales) {
-                gg *= p.scales[cc];
-                uu *= p.scales[p.n + cc];
+                gg *= sg[e];
+                uu *= su[e];
             }
             store_out(p.c, p.c_dtype, row * p.ldc + cc, glu_combine(EPI, gg, uu));
         } else {
             float v = gv[e];
-            if (p.scales) v *= p.scales[cc];
-            if (EPI == SFG_EPI_RESIDUAL) v += p.residual[row * p.ldr + cc];
+            if (p.scales) v *= sg[e];
+            if (EPI == SFG_EPI_RESIDUAL) v += rv[e];
             store_out(p.c, p.c_dtype, row * p.ldc + cc, v);
         }
     }
