@@ -232,6 +232,41 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny_kernel(SkinnyArgs p) {
                 for (int i = 0; i < MT; ++i)
 #pragma unroll
                     for (int j = 0; j < NBT; ++j) acc[i][j] += red[w][i][j][lane];
+            // Everything the epilogue reads is loaded before its first store:
+            // the output may alias these arrays for all the compiler knows,
+            // so a load placed after a store would wait a full memory round
+            // trip.  Rows past the group read its last row and store nothing.
+            // Scale of B row brow[j] + lr (gate or up for GLU tiles).
+            float sv[NBT];
+            if (scales) {
+#pragma unroll
+                for (int j = 0; j < NBT; ++j) sv[j] = scales[brow[j] + lr];
+            }
+            float rv[MT][4][NBT];
+            if constexpr (EPI == SFG_EPI_RESIDUAL && !kGlu) {
+#pragma unroll
+                for (int i = 0; i < MT; ++i)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int64_t row = min(pass + i * 16 + lg * 4 + r, re - 1);
+#pragma unroll
+                        for (int j = 0; j < NBT; ++j) rv[i][r][j] = p.residual[row * p.ldr + out_col + j * 16 + lr];
+                    }
+            }
+            // gathered source indices: all loaded in one branch, compared after
+            int32_t src_row[MT][4];
+            if (p.a_rows) {
+#pragma unroll
+                for (int i = 0; i < MT; ++i)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) src_row[i][r] = p.a_rows[min(pass + i * 16 + lg * 4 + r, re - 1)];
+            }
+            bool zero_row[MT][4];
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    zero_row[i][r] = p.a_rows && (src_row[i][r] < 0 || src_row[i][r] >= p.a_rows_limit);
             // D layout: lane holds column (lane & 15), rows 4*(lane >> 4) + r.
 #pragma unroll
             for (int i = 0; i < MT; ++i) {
@@ -240,12 +275,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny_kernel(SkinnyArgs p) {
                     const int64_t row = pass + i * 16 + lg * 4 + r;
                     if (row >= re) continue;
                     // a gathered row whose source index is outside A multiplied zeros
-                    if (p.a_rows) {
-                        const int64_t src = p.a_rows[row];
-                        if (src < 0 || src >= p.a_rows_limit) {
+                    if (zero_row[i][r]) {
 #pragma unroll
-                            for (int j = 0; j < NBT; ++j) acc[i][j][r] = 0.f;
-                        }
+                        for (int j = 0; j < NBT; ++j) acc[i][j][r] = 0.f;
                     }
                     if (kGlu) {
 #pragma unroll
@@ -253,8 +285,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny_kernel(SkinnyArgs p) {
                             const int64_t col = out_col + 16 * h + lr;
                             float gv = acc[i][h][r], uv = acc[i][kGluTiles + h][r];
                             if (scales) {
-                                gv *= scales[col];
-                                uv *= scales[p.n + col];
+                                gv *= sv[h];
+                                uv *= sv[kGluTiles + h];
                             }
                             store_out(p.c, p.c_dtype, row * p.ldc + col, glu_combine(EPI, gv, uv));
                         }
@@ -263,8 +295,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny_kernel(SkinnyArgs p) {
                         for (int j = 0; j < NBT; ++j) {
                             const int64_t col = out_col + j * 16 + lr;
                             float v = acc[i][j][r];
-                            if (scales) v *= scales[col];
-                            if (EPI == SFG_EPI_RESIDUAL) v += p.residual[row * p.ldr + col];
+                            if (scales) v *= sv[j];
+                            if constexpr (EPI == SFG_EPI_RESIDUAL) v += rv[i][r][j];
                             store_out(p.c, p.c_dtype, row * p.ldc + col, v);
                         }
                     }
