@@ -430,12 +430,55 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(
     }
 }
 
+// top_k <= KMAX: the token's (position, weight) pairs are read once, and each
+// feature block issues every assignment's row load together with the residual
+// before the first wait.  Slots past top_k and invalid positions read row 0 and
+// are left out of the sum, which runs over the slots in order as above.
+template <int KMAX>
+__global__ __launch_bounds__(256) void moe_combine_reg_kernel(
+    const float* __restrict__ y, const int32_t* __restrict__ position,
+    const float* __restrict__ weights, const float* __restrict__ residual,
+    float* __restrict__ out, int hidden, int top_k, int64_t total) {
+    const int t = blockIdx.x;
+    int64_t pos[KMAX];
+    float w[KMAX];
+    bool ok[KMAX];
+#pragma unroll
+    for (int s = 0; s < KMAX; ++s) {
+        const int sc = s < top_k ? s : top_k - 1;
+        const int64_t ps = position[static_cast<int64_t>(t) * top_k + sc];
+        w[s] = weights[static_cast<int64_t>(t) * top_k + sc];
+        ok[s] = s < top_k && ps >= 0 && ps < total;  // corrupt index: contributes nothing
+        pos[s] = ok[s] ? ps : 0;
+    }
+    for (int f = threadIdx.x * 4; f < hidden; f += 256 * 4) {
+        float4 v[KMAX];
+#pragma unroll
+        for (int s = 0; s < KMAX; ++s) v[s] = *reinterpret_cast<const float4*>(y + pos[s] * hidden + f);
+        const float4 r = *reinterpret_cast<const float4*>(residual + static_cast<int64_t>(t) * hidden + f);
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int s = 0; s < KMAX; ++s) {
+            if (!ok[s]) continue;
+            acc.x = fmaf(w[s], v[s].x, acc.x);
+            acc.y = fmaf(w[s], v[s].y, acc.y);
+            acc.z = fmaf(w[s], v[s].z, acc.z);
+            acc.w = fmaf(w[s], v[s].w, acc.w);
+        }
+        *reinterpret_cast<float4*>(out + static_cast<int64_t>(t) * hidden + f) =
+            make_float4(r.x + acc.x, r.y + acc.y, r.z + acc.z, r.w + acc.w);
+    }
+}
+
 void launch_moe_combine(const float* y, const int32_t* position, const float* weights,
                         const float* residual, float* out, int64_t tokens, int64_t hidden,
                         int64_t top_k, hipStream_t stream) {
-    moe_combine_kernel<<<dim3(static_cast<unsigned>(tokens)), 256, 0, stream>>>(
-        y, position, weights, residual, out, static_cast<int>(hidden), static_cast<int>(top_k),
-        tokens * top_k);
+    const dim3 grid(static_cast<unsigned>(tokens));
+    const int h = static_cast<int>(hidden), k = static_cast<int>(top_k);
+    if (top_k <= 2) moe_combine_reg_kernel<2><<<grid, 256, 0, stream>>>(y, position, weights, residual, out, h, k, tokens * top_k);
+    else if (top_k <= 4) moe_combine_reg_kernel<4><<<grid, 256, 0, stream>>>(y, position, weights, residual, out, h, k, tokens * top_k);
+    else if (top_k <= 8) moe_combine_reg_kernel<8><<<grid, 256, 0, stream>>>(y, position, weights, residual, out, h, k, tokens * top_k);
+    else moe_combine_kernel<<<grid, 256, 0, stream>>>(y, position, weights, residual, out, h, k, tokens * top_k);
 }
 
 }  // namespace sfg
