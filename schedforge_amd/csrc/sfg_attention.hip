@@ -678,20 +678,34 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(
         const bool has = lr < G;
         const float* qr = q + static_cast<int64_t>(b) * q_row_stride +
                           static_cast<int64_t>(kvh * G + (has ? lr : 0)) * kDecD;
+        // every Q vector and rotation pair is loaded before the first use (one
+        // memory round trip instead of one per k-step)
+        float4 qa[kKs], qc[kKs];
+        float2 rot[kKs][4];
 #pragma unroll
         for (int s = 0; s < kKs; ++s) {
-            const int d0 = 32 * s + 8 * lg;
+            qa[s] = *reinterpret_cast<const float4*>(qr + 32 * s + 8 * lg);
+            qc[s] = *reinterpret_cast<const float4*>(qr + 32 * s + 8 * lg + 4);
+        }
+        if (rope) {
+            const float2* t = reinterpret_cast<const float2*>(rope) +
+                              static_cast<int64_t>(q_pos) * (kDecD / 2) + 4 * lg;
+#pragma unroll
+            for (int s = 0; s < kKs; ++s)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) rot[s][e] = t[16 * s + e];
+        }
+#pragma unroll
+        for (int s = 0; s < kKs; ++s) {
             float v[8];
-            const float4 a = *reinterpret_cast<const float4*>(qr + d0);
-            const float4 c = *reinterpret_cast<const float4*>(qr + d0 + 4);
+            const float4 a = qa[s];
+            const float4 c = qc[s];
             v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
             v[4] = c.x; v[5] = c.y; v[6] = c.z; v[7] = c.w;
             if (rope) {
-                const float2* t = reinterpret_cast<const float2*>(rope) +
-                                  static_cast<int64_t>(q_pos) * (kDecD / 2) + d0 / 2;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const float2 cs = t[e];
+                    const float2 cs = rot[s][e];
                     const float ev = v[2 * e], od = v[2 * e + 1];
                     v[2 * e] = ev * cs.x - od * cs.y;
                     v[2 * e + 1] = ev * cs.y + od * cs.x;
