@@ -15,6 +15,7 @@
 #include "sfg_oracle.h"
 
 #include <float.h>
+#include <immintrin.h>
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -131,18 +132,92 @@ void sfgo_rms_norm(const float* x, const float* w, float* y, int64_t rows, int64
 
 /* scalar_matmul (decoder_compiler.cpp:64-75) and the register kernels of
  * execute(LoopIR) (runtime.cpp:278-438): every output is a sequential fp32 FMA
- * chain over k starting from 0.  The i-k-j order keeps that chain per output
- * while vectorising across j. */
-void sfgo_matmul(const float* a, const float* b, float* c, int64_t m, int64_t n, int64_t k) {
-#pragma omp parallel for schedule(dynamic, 1)
-    for (int64_t i = 0; i < m; ++i) {
+ * chain over k starting from 0.
+ *
+ * Blocking keeps that chain.  Work is cut into tiles of MM_TM rows x MM_TN
+ * columns (the OpenMP tasks), each walked in k blocks of MM_TK.  Inside a
+ * block a 4 x 32 register kernel holds sixteen 8-lane accumulators, one lane
+ * per output, and adds one rounded fused product per k in increasing order;
+ * the accumulators go back to c between k blocks and resume from there.
+ * Storing and reloading an fp32 value is exact, and _mm256_fmadd_ps is the
+ * lane-wise fmaf, so every output gets the same rounding sequence as the
+ * plain i-k-j loop -- which is what the remainder rows and columns run. */
+#define MM_TM 64
+#define MM_TN 256
+#define MM_TK 256
+
+/* c[0:4][0:32] (row stride ldc) over kn steps: row r of a (stride lda) and a
+ * packed B panel bp [kn][32], both starting at the block's first k; first:
+ * start the chains from 0. */
+static void mm_kernel_4x32(const float* a, int64_t lda, const float* bp, float* c, int64_t ldc,
+                           int64_t kn, int first) {
+    __m256 acc[4][4];
+    for (int r = 0; r < 4; ++r)
+        for (int v = 0; v < 4; ++v)
+            acc[r][v] = first ? _mm256_setzero_ps() : _mm256_loadu_ps(c + r * ldc + 8 * v);
+    for (int64_t t = 0; t < kn; ++t) {
+        const float* br = bp + t * 32;
+        const __m256 b0 = _mm256_loadu_ps(br), b1 = _mm256_loadu_ps(br + 8);
+        const __m256 b2 = _mm256_loadu_ps(br + 16), b3 = _mm256_loadu_ps(br + 24);
+        for (int r = 0; r < 4; ++r) {
+            const __m256 ar = _mm256_broadcast_ss(a + r * lda + t);
+            acc[r][0] = _mm256_fmadd_ps(ar, b0, acc[r][0]);
+            acc[r][1] = _mm256_fmadd_ps(ar, b1, acc[r][1]);
+            acc[r][2] = _mm256_fmadd_ps(ar, b2, acc[r][2]);
+            acc[r][3] = _mm256_fmadd_ps(ar, b3, acc[r][3]);
+        }
+    }
+    for (int r = 0; r < 4; ++r)
+        for (int v = 0; v < 4; ++v) _mm256_storeu_ps(c + r * ldc + 8 * v, acc[r][v]);
+}
+
+/* The plain chain for outputs [i0,i1) x [j0,j1) over k in [k0, k1). */
+static void mm_edge(const float* a, const float* b, float* c, int64_t n, int64_t k, int64_t i0,
+                    int64_t i1, int64_t j0, int64_t j1, int64_t k0, int64_t k1) {
+    for (int64_t i = i0; i < i1; ++i) {
         float* crow = c + i * n;
-        for (int64_t j = 0; j < n; ++j) crow[j] = 0.0f;
-        for (int64_t kk = 0; kk < k; ++kk) {
+        if (k0 == 0)
+            for (int64_t j = j0; j < j1; ++j) crow[j] = 0.0f;
+        for (int64_t kk = k0; kk < k1; ++kk) {
             const float aik = a[i * k + kk];
             const float* brow = b + kk * n;
-            for (int64_t j = 0; j < n; ++j) crow[j] = fmaf(aik, brow[j], crow[j]);
+            for (int64_t j = j0; j < j1; ++j) crow[j] = fmaf(aik, brow[j], crow[j]);
         }
+    }
+}
+
+void sfgo_matmul(const float* a, const float* b, float* c, int64_t m, int64_t n, int64_t k) {
+    const int64_t tiles_m = (m + MM_TM - 1) / MM_TM, tiles_n = (n + MM_TN - 1) / MM_TN;
+    if (k <= 0) {
+        for (int64_t i = 0; i < m * n; ++i) c[i] = 0.0f;
+        return;
+    }
+#pragma omp parallel
+    {
+        /* this thread's packed copy of one B block: MM_TN / 32 panels [MM_TK][32] */
+        float* bp = (float*)malloc(sizeof(float) * MM_TK * MM_TN);
+#pragma omp for schedule(dynamic, 1)
+        for (int64_t t = 0; t < tiles_m * tiles_n; ++t) {
+            /* column tiles outermost: neighbouring tasks share a B panel */
+            const int64_t i0 = (t % tiles_m) * MM_TM, j0 = (t / tiles_m) * MM_TN;
+            const int64_t i1 = i0 + MM_TM < m ? i0 + MM_TM : m;
+            const int64_t j1 = j0 + MM_TN < n ? j0 + MM_TN : n;
+            const int64_t i4 = i0 + (i1 - i0) / 4 * 4, j32 = j0 + (j1 - j0) / 32 * 32;
+            for (int64_t k0 = 0; k0 < k; k0 += MM_TK) {
+                const int64_t k1 = k0 + MM_TK < k ? k0 + MM_TK : k, kn = k1 - k0;
+                if (i4 > i0)
+                    for (int64_t j = j0; j < j32; j += 32) {
+                        float* panel = bp + (j - j0) * MM_TK;
+                        for (int64_t kk = k0; kk < k1; ++kk)
+                            memcpy(panel + (kk - k0) * 32, b + kk * n + j, 32 * sizeof(float));
+                        for (int64_t i = i0; i < i4; i += 4)
+                            mm_kernel_4x32(a + i * k + k0, k, panel, c + i * n + j, n, kn, k0 == 0);
+                    }
+                if (j32 < j1) mm_edge(a, b, c, n, k, i0, i4, j32, j1, k0, k1);
+                if (i4 < i1) mm_edge(a, b, c, n, k, i4, i1, j0, j1, k0, k1);
+            }
+        }
+        free(bp);
     }
 }
 
@@ -250,7 +325,23 @@ static void attention_row(const float* qr, const float* kb, const float* vb, int
                           int64_t limit, int64_t D, int64_t Dv, float scale, float* scores,
                           float* orow) {
     float maximum = -INFINITY;
-    for (int64_t j = 0; j <= limit && j < seq_kv; ++j) {
+    const int64_t count = limit + 1 < seq_kv ? limit + 1 : seq_kv;
+    int64_t j = 0;
+    /* eight keys at a time: eight independent dot chains, each still summed
+     * over d in order (the same bits as one key at a time) */
+    for (; j + 8 <= count; j += 8) {
+        float dot[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+        const float* kr = kb + j * D;
+        for (int64_t d = 0; d < D; ++d) {
+            const float qd = qr[d];
+            for (int t = 0; t < 8; ++t) dot[t] = fmaf(qd, kr[t * D + d], dot[t]);
+        }
+        for (int t = 0; t < 8; ++t) {
+            scores[j + t] = dot[t] * scale;
+            if (scores[j + t] > maximum) maximum = scores[j + t];
+        }
+    }
+    for (; j < count; ++j) {
         const float* kr = kb + j * D;
         float dot = 0.0f;
         for (int64_t d = 0; d < D; ++d) dot = fmaf(qr[d], kr[d], dot);
@@ -492,20 +583,79 @@ void sfgo_quantize_nk(const float* w_nk, int64_t n, int64_t k, int8_t* q, float*
  * into the accumulator with one fused step: acc = fma(x * q, s, acc).  That
  * is what each output does here; q is laid out [K][N] as exact floats so the
  * chain vectorises across n. */
+/* Blocked as sfgo_matmul (same tiles, same per-output chain): the 4 x 32
+ * kernel rounds x * q with _mm256_mul_ps and adds it scaled with one fused
+ * step, lane by lane what the plain loop does.  q is widened (exactly) into
+ * panels of 32 output channels, [n / 32][k][32], read contiguously. */
+static void qmm_kernel_4x32(const float* x, int64_t ldx, const float* qp, const float* s,
+                            float* c, int64_t ldc, int64_t kn, int first) {
+    __m256 acc[4][4];
+    const __m256 s0 = _mm256_loadu_ps(s), s1 = _mm256_loadu_ps(s + 8);
+    const __m256 s2 = _mm256_loadu_ps(s + 16), s3 = _mm256_loadu_ps(s + 24);
+    for (int r = 0; r < 4; ++r)
+        for (int v = 0; v < 4; ++v)
+            acc[r][v] = first ? _mm256_setzero_ps() : _mm256_loadu_ps(c + r * ldc + 8 * v);
+    for (int64_t t = 0; t < kn; ++t) {
+        const float* qr = qp + t * 32;
+        const __m256 q0 = _mm256_loadu_ps(qr), q1 = _mm256_loadu_ps(qr + 8);
+        const __m256 q2 = _mm256_loadu_ps(qr + 16), q3 = _mm256_loadu_ps(qr + 24);
+        for (int r = 0; r < 4; ++r) {
+            const __m256 xr = _mm256_broadcast_ss(x + r * ldx + t);
+            acc[r][0] = _mm256_fmadd_ps(_mm256_mul_ps(xr, q0), s0, acc[r][0]);
+            acc[r][1] = _mm256_fmadd_ps(_mm256_mul_ps(xr, q1), s1, acc[r][1]);
+            acc[r][2] = _mm256_fmadd_ps(_mm256_mul_ps(xr, q2), s2, acc[r][2]);
+            acc[r][3] = _mm256_fmadd_ps(_mm256_mul_ps(xr, q3), s3, acc[r][3]);
+        }
+    }
+    for (int r = 0; r < 4; ++r)
+        for (int v = 0; v < 4; ++v) _mm256_storeu_ps(c + r * ldc + 8 * v, acc[r][v]);
+}
+
+/* The plain chain, q read as float(q[n][k]) straight from the int8 matrix. */
+static void qmm_edge(const float* x, const int8_t* q_nk, const float* scales, float* out,
+                     int64_t n, int64_t k, int64_t i0, int64_t i1, int64_t j0, int64_t j1,
+                     int64_t k0, int64_t k1) {
+    for (int64_t i = i0; i < i1; ++i) {
+        float* crow = out + i * n;
+        if (k0 == 0)
+            for (int64_t j = j0; j < j1; ++j) crow[j] = 0.0f;
+        for (int64_t kk = k0; kk < k1; ++kk) {
+            const float xik = x[i * k + kk];
+            for (int64_t j = j0; j < j1; ++j)
+                crow[j] = fmaf(xik * (float)q_nk[j * k + kk], scales[j], crow[j]);
+        }
+    }
+}
+
 void sfgo_quantized_matmul(const float* x, const int8_t* q_nk, const float* scales,
                            int64_t m, int64_t n, int64_t k, float* out) {
-    float* qf = (float*)malloc(sizeof(float) * (size_t)(n * k));
+    if (k <= 0) {
+        for (int64_t i = 0; i < m * n; ++i) out[i] = 0.0f;
+        return;
+    }
+    const int64_t panels = n / 32;
+    float* qf = (float*)malloc(sizeof(float) * (size_t)(panels > 0 ? panels * 32 * k : 1));
 #pragma omp parallel for schedule(static)
-    for (int64_t c = 0; c < n; ++c)
-        for (int64_t d = 0; d < k; ++d) qf[d * n + c] = (float)q_nk[c * k + d];
+    for (int64_t pk = 0; pk < panels * k; ++pk) {
+        const int64_t p = pk / k, kk = pk % k;
+        float* dst = qf + pk * 32;
+        for (int c = 0; c < 32; ++c) dst[c] = (float)q_nk[(p * 32 + c) * k + kk];
+    }
+    const int64_t tiles_m = (m + MM_TM - 1) / MM_TM, tiles_n = (n + MM_TN - 1) / MM_TN;
 #pragma omp parallel for schedule(dynamic, 1)
-    for (int64_t i = 0; i < m; ++i) {
-        float* crow = out + i * n;
-        for (int64_t j = 0; j < n; ++j) crow[j] = 0.0f;
-        for (int64_t kk = 0; kk < k; ++kk) {
-            const float xik = x[i * k + kk];
-            const float* qrow = qf + kk * n;
-            for (int64_t j = 0; j < n; ++j) crow[j] = fmaf(xik * qrow[j], scales[j], crow[j]);
+    for (int64_t t = 0; t < tiles_m * tiles_n; ++t) {
+        const int64_t i0 = (t % tiles_m) * MM_TM, j0 = (t / tiles_m) * MM_TN;
+        const int64_t i1 = i0 + MM_TM < m ? i0 + MM_TM : m;
+        const int64_t j1 = j0 + MM_TN < n ? j0 + MM_TN : n;
+        const int64_t i4 = i0 + (i1 - i0) / 4 * 4, j32 = j0 + (j1 - j0) / 32 * 32;
+        for (int64_t k0 = 0; k0 < k; k0 += MM_TK) {
+            const int64_t k1 = k0 + MM_TK < k ? k0 + MM_TK : k;
+            for (int64_t j = j0; j < j32; j += 32)
+                for (int64_t i = i0; i < i4; i += 4)
+                    qmm_kernel_4x32(x + i * k + k0, k, qf + ((j / 32) * k + k0) * 32, scales + j,
+                                    out + i * n + j, n, k1 - k0, k0 == 0);
+            if (j32 < j1) qmm_edge(x, q_nk, scales, out, n, k, i0, i4, j32, j1, k0, k1);
+            if (i4 < i1) qmm_edge(x, q_nk, scales, out, n, k, i4, i1, j0, j1, k0, k1);
         }
     }
     free(qf);

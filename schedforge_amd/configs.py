@@ -121,13 +121,21 @@ def algorithmic_work(cfg: DecoderConfig, expert_rows: int | None = None) -> dict
     proj = 2 rows H (H + 2 kvD) + 2 rows H^2; dense FFN = 6 rows H I;
     MoE = 6 T k H I + 2 T H E; attention = 2 (D + Dv) x allowed pairs x B x Hq.
     Bytes: every weight byte once, KV once (decode), activations in and out.
+
+    A decode step with the reference's semantics attends over the cache only
+    and discards the step's own K / V (decoder_compiler.cpp:238-243), so the
+    layer computes only the Q columns of the QKV product: that step counts
+    2 rows H H for it and reads only Wq's bytes.  "reference_proj_flops" keeps
+    the reference's full 2 rows H (H + 2 kvD).
     """
     rows, H, I = cfg.rows, cfg.hidden, cfg.intermediate
     D, kvd = cfg.head_dim, cfg.kv_width
     wbytes = {"f32": 4, "bf16": 2, "w8": 1}[cfg.dtype]
     abytes = 4 if cfg.dtype == "f32" else 2
-    proj_flops = 2 * rows * H * (H + 2 * kvd) + 2 * rows * H * H
-    proj_w = (H * (H + 2 * kvd) + H * H) * wbytes
+    qkv_cols = H if cfg.decode and not cfg.kv_append else H + 2 * kvd
+    reference_proj_flops = 2 * rows * H * (H + 2 * kvd) + 2 * rows * H * H
+    proj_flops = 2 * rows * H * qkv_cols + 2 * rows * H * H
+    proj_w = (H * qkv_cols + H * H) * wbytes
     skv = cfg.context_sequence if cfg.decode else cfg.sequence
     pairs = (causal_pairs(cfg.sequence, skv) if cfg.causal else cfg.sequence * skv)
     attn_flops = 2 * (D + D) * pairs * cfg.batch * cfg.query_heads
@@ -143,6 +151,7 @@ def algorithmic_work(cfg: DecoderConfig, expert_rows: int | None = None) -> dict
     return {
         "flops": proj_flops + attn_flops + ffn_flops,
         "proj_flops": proj_flops, "attn_flops": attn_flops, "ffn_flops": ffn_flops,
+        "reference_proj_flops": reference_proj_flops,
         "weight_bytes": proj_w + ffn_w, "kv_bytes": kv_bytes, "act_bytes": act_bytes,
         "bytes": proj_w + ffn_w + kv_bytes + act_bytes,
         "act_elem_bytes": abytes,
