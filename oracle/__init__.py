@@ -286,4 +286,4 @@ def rel_error(got, ref):
     return float(np.max(np.abs(got - ref)) / max(float(np.max(np.abs(ref))), 1e-6))
 
 
-from .data import make_layer_data, quantize_layer, decoder_layer, decoder_layer_rows  # noqa: E402,F401
+from .data import make_layer_data, quantize_layer, decoder_layer, decoder_layer_rows, prepared_layer  # noqa: E402,F401

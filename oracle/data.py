@@ -173,6 +173,25 @@ def decoder_layer(cfg, d, quant=None, taps: bool = False, threads: int = 0,
     return (out, t) if taps else out
 
 
+def prepared_layer(cfg, d, quant=None, threads: int = 0):
+    """The whole layer as a callable over inputs marshalled once: returns
+    run() -> out [rows, H], each call one sfgo_decoder_layer step on the same
+    prepared structs (for timing the step itself, without re-stacking the
+    expert matrices on every call)."""
+    rows = cfg.batch * cfg.sequence
+    c, ld, keep = _layer_structs(cfg, d, quant, threads, None)
+    out = np.empty((rows, cfg.hidden), np.float32)
+
+    def run():
+        rc = lib().sfgo_decoder_layer(ctypes.byref(c), ctypes.byref(ld), _f(out), None)
+        if rc != 0:
+            raise ValueError("invalid decoder configuration")
+        return out
+
+    run.keep = keep  # the arrays the structs point into live as long as run
+    return run
+
+
 def decoder_layer_rows(cfg, d, sample, quant=None, taps: bool = False, threads: int = 0,
                        trace=None):
     """The prefill layer at rows `sample` only (row = b * S + s): K / V of every

@@ -585,8 +585,9 @@ void sfgo_quantize_nk(const float* w_nk, int64_t n, int64_t k, int8_t* q, float*
  * chain vectorises across n. */
 /* Blocked as sfgo_matmul (same tiles, same per-output chain): the 4 x 32
  * kernel rounds x * q with _mm256_mul_ps and adds it scaled with one fused
- * step, lane by lane what the plain loop does.  q is widened (exactly) into
- * panels of 32 output channels, [n / 32][k][32], read contiguously. */
+ * step, lane by lane what the plain loop does.  Each tile widens its q block
+ * (exactly) into panels of 32 output channels, [k block][32], read
+ * contiguously; the int8 matrix itself is read once per tile row. */
 static void qmm_kernel_4x32(const float* x, int64_t ldx, const float* qp, const float* s,
                             float* c, int64_t ldc, int64_t kn, int first) {
     __m256 acc[4][4];
@@ -633,32 +634,36 @@ void sfgo_quantized_matmul(const float* x, const int8_t* q_nk, const float* scal
         for (int64_t i = 0; i < m * n; ++i) out[i] = 0.0f;
         return;
     }
-    const int64_t panels = n / 32;
-    float* qf = (float*)malloc(sizeof(float) * (size_t)(panels > 0 ? panels * 32 * k : 1));
-#pragma omp parallel for schedule(static)
-    for (int64_t pk = 0; pk < panels * k; ++pk) {
-        const int64_t p = pk / k, kk = pk % k;
-        float* dst = qf + pk * 32;
-        for (int c = 0; c < 32; ++c) dst[c] = (float)q_nk[(p * 32 + c) * k + kk];
-    }
     const int64_t tiles_m = (m + MM_TM - 1) / MM_TM, tiles_n = (n + MM_TN - 1) / MM_TN;
-#pragma omp parallel for schedule(dynamic, 1)
-    for (int64_t t = 0; t < tiles_m * tiles_n; ++t) {
-        const int64_t i0 = (t % tiles_m) * MM_TM, j0 = (t / tiles_m) * MM_TN;
-        const int64_t i1 = i0 + MM_TM < m ? i0 + MM_TM : m;
-        const int64_t j1 = j0 + MM_TN < n ? j0 + MM_TN : n;
-        const int64_t i4 = i0 + (i1 - i0) / 4 * 4, j32 = j0 + (j1 - j0) / 32 * 32;
-        for (int64_t k0 = 0; k0 < k; k0 += MM_TK) {
-            const int64_t k1 = k0 + MM_TK < k ? k0 + MM_TK : k;
-            for (int64_t j = j0; j < j32; j += 32)
-                for (int64_t i = i0; i < i4; i += 4)
-                    qmm_kernel_4x32(x + i * k + k0, k, qf + ((j / 32) * k + k0) * 32, scales + j,
-                                    out + i * n + j, n, k1 - k0, k0 == 0);
-            if (j32 < j1) qmm_edge(x, q_nk, scales, out, n, k, i0, i4, j32, j1, k0, k1);
-            if (i4 < i1) qmm_edge(x, q_nk, scales, out, n, k, i4, i1, j0, j1, k0, k1);
+#pragma omp parallel
+    {
+        /* this thread's widened copy of one q block: MM_TN / 32 panels [MM_TK][32] */
+        float* qp = (float*)malloc(sizeof(float) * MM_TK * MM_TN);
+#pragma omp for schedule(dynamic, 1)
+        for (int64_t t = 0; t < tiles_m * tiles_n; ++t) {
+            const int64_t i0 = (t % tiles_m) * MM_TM, j0 = (t / tiles_m) * MM_TN;
+            const int64_t i1 = i0 + MM_TM < m ? i0 + MM_TM : m;
+            const int64_t j1 = j0 + MM_TN < n ? j0 + MM_TN : n;
+            const int64_t i4 = i0 + (i1 - i0) / 4 * 4, j32 = j0 + (j1 - j0) / 32 * 32;
+            for (int64_t k0 = 0; k0 < k; k0 += MM_TK) {
+                const int64_t k1 = k0 + MM_TK < k ? k0 + MM_TK : k, kn = k1 - k0;
+                if (i4 > i0)
+                    for (int64_t j = j0; j < j32; j += 32) {
+                        float* panel = qp + (j - j0) * MM_TK;
+                        for (int c = 0; c < 32; ++c) {
+                            const int8_t* row = q_nk + (j + c) * k + k0;
+                            for (int64_t kk = 0; kk < kn; ++kk) panel[kk * 32 + c] = (float)row[kk];
+                        }
+                        for (int64_t i = i0; i < i4; i += 4)
+                            qmm_kernel_4x32(x + i * k + k0, k, panel, scales + j, out + i * n + j, n, kn,
+                                            k0 == 0);
+                    }
+                if (j32 < j1) qmm_edge(x, q_nk, scales, out, n, k, i0, i4, j32, j1, k0, k1);
+                if (i4 < i1) qmm_edge(x, q_nk, scales, out, n, k, i4, i1, j0, j1, k0, k1);
+            }
         }
+        free(qp);
     }
-    free(qf);
 }
 
 /* execute_quantized_moe_once (next_milestones.cpp:418-460): per token and slot,
