@@ -31,11 +31,12 @@
  *                 for fragment s; int8: 2 x [64 lanes][16 values] with k =
  *                 32 g + 16 t + [0,16) -- so every load a wave issues reads 1 KB
  *                 contiguous.  Same bytes as [N][K].
- *   paged KV      K pool [page][Hkv][page_tokens][D] bf16, V pool
- *                 [page][Hkv][D][page_tokens] bf16 (token-minor inside a page:
- *                 the decode kernel reads V^T operands as 8-byte runs); each
- *                 (page, kv_head) is one contiguous 4 KB run at D=128, 16-token
- *                 pages.  One page-table row per sequence [B][pages_per_seq].
+ *   paged KV      K pool [page][Hkv][page_tokens][D], V pool
+ *                 [page][Hkv][D][page_tokens] (token-minor inside a page:
+ *                 the decode kernel reads V^T operands as 8-byte runs), bf16
+ *                 (fp32 on the fp32 path); each (page, kv_head) is one
+ *                 contiguous 4 KB run at D=128, 16-token bf16 pages.  One
+ *                 page-table row per sequence [B][pages_per_seq].
  */
 #ifndef SFG_HIP_H
 #define SFG_HIP_H
@@ -96,6 +97,12 @@ enum sfg_epilogue {
 
 /* ---------------- library identity ---------------- */
 int sfg_hip_abi_version(void);
+/* key=value;... invariants of this build (after schedforge_aot_metadata_v1,
+ * llvm_backend.cpp:622-643): abi, arch, dtypes, the activation dtypes and the
+ * weight dtypes each takes, layouts, the lowered envelope (head_dim 1..256,
+ * any page size, any new-token count per decode step, dense and MoE FFNs) and
+ * the shapes the MFMA kernels take (mfma_decode, mfma_prefill, mfma_gemm);
+ * the other shapes run the row-per-wave attention and VALU GEMM kernels. */
 const char* sfg_hip_metadata_v1(void);
 const char* sfg_hip_last_error(void);
 /* CUs, XCDs (hipDeviceAttributeNumberOfXccs) and HBM bytes of a device. */
@@ -144,7 +151,8 @@ int sfg_hip_preferred_weight_layout_v1(int64_t rows, int64_t k, int grouped);
 int sfg_hip_to_bf16_v1(const float* src, uint16_t* dst, int64_t count, void* stream);
 /* RoPE table [seq][head_dim/2][2] = (cos, sin) of float(pos) * powf(theta, -(2i)/D),
  * computed on the HOST with the reference's float expressions
- * (decoder_compiler.cpp:101-106).  Plain host memory. */
+ * (decoder_compiler.cpp:101-106).  Plain host memory.  An odd head_dim has
+ * (head_dim - 1) / 2 pairs; its last dimension is never rotated. */
 int sfg_hip_rope_table_host_v1(float* table, int64_t seq, int64_t head_dim, float theta);
 
 /* ---------------- per-op kernels ---------------- */
@@ -180,6 +188,18 @@ typedef struct {
 size_t sfg_hip_gemm_workspace_v1(int64_t m, int64_t n, int64_t k);
 int sfg_hip_gemm_v1(const sfg_gemm_args* args, void* workspace, size_t workspace_bytes,
                     void* stream);
+/* The grouped product of execute_moe's expert tasks (compute_task +
+ * execute_loop_kernel, moe_compiler.cpp:64-155) in general form: arguments as
+ * sfg_hip_gemm_v1 with m the total rows; group g computes output rows
+ * [offsets[g], offsets[g + 1]) (device int32, groups + 1 entries, clamped to
+ * [0, m]) from A rows a_rows[r] (device int32; NULL: row r; ids outside
+ * [0, a_rows_limit) read as zero rows) with the B matrix and scales of group g
+ * at b + g * b_group_stride elements and b_scales + g * s_group_stride.
+ * Epilogue none, SwiGLU or the MoE GLU (no residual). */
+int sfg_hip_gemm_grouped_v1(const sfg_gemm_args* args, const int32_t* a_rows, int64_t a_rows_limit,
+                            const int32_t* offsets, int groups, int64_t b_group_stride,
+                            int64_t s_group_stride, void* workspace, size_t workspace_bytes,
+                            void* stream);
 
 /* split_qkv + apply_rope (decoder_compiler.cpp:96-148).  qkv fp32
  * [B*S][H + 2 Hkv D]; rope_table [S][D/2][2] device copy of
@@ -219,8 +239,10 @@ int sfg_hip_attn_prefill_vt_v1(const uint16_t* q, const uint16_t* k, const uint1
  * sequence), pools bf16: K [num_pages][Hkv][page_tokens][D], V
  * [num_pages][Hkv][D][page_tokens]; page_table
  * [B][pages_per_seq], seq_lens[B] (each <= pages_per_seq*page_tokens).  out
- * merged [B][Hq*D] in out_dtype.  head_dim 128 or 64, page_tokens 16, GQA group
- * Hq/Hkv in {1, 2, 4, 8, 16}.  kv_splits <= 0 picks a split count.  Page ids
+ * merged [B][Hq*D] in out_dtype.  Any head_dim up to 256 and any page size:
+ * head_dim 128 / 64 with 16-token pages and a GQA group Hq/Hkv in
+ * {1, 2, 4, 8, 16} run the MFMA split kernel, everything else the row kernel
+ * of sfg_hip_attn_paged_v1.  kv_splits <= 0 picks a split count.  Page ids
  * are validated on the host against num_pages only when validate_pages != 0
  * (this reads the table back and synchronises the stream). */
 size_t sfg_hip_attn_decode_workspace_v1(int64_t batch, int64_t q_heads, int64_t head_dim,
@@ -248,7 +270,12 @@ int sfg_hip_attn_decode_paged_v1(const float* q, const uint16_t* k_pool,
  * Nothing in the array needs clearing: each call writes every partial before
  * reading it.  Page ids outside [0, num_pages) are skipped on the device (no
  * host-side table validation: it would synchronise the stream).  Results are
- * bit-identical to sfg_hip_attn_decode_paged_v1 with the same split count. */
+ * bit-identical to sfg_hip_attn_decode_paged_v1 with the same split count.
+ * Under graph capture: make the first call on each device outside the
+ * capture (it looks the array's address up with hipGetSymbolAddress, which
+ * may load the code object); a captured call records only kernel launches,
+ * no memset or copy.  Every replay of every captured call on one device uses
+ * the same array, so replays on different streams race like eager calls. */
 #define SFG_DECODE_SCRATCH_BYTES ((size_t)16 << 20)
 int sfg_hip_attn_decode_paged_noalloc_v1(const float* q, const uint16_t* k_pool,
                                          const uint16_t* v_pool, const int32_t* page_table,
@@ -259,16 +286,55 @@ int sfg_hip_attn_decode_paged_noalloc_v1(const float* q, const uint16_t* k_pool,
                                          int64_t max_context, int32_t kv_splits, float scale,
                                          void* stream);
 
+/* Paged attention in general: execute_paged_decode_attention /
+ * execute_decode_attention (next_milestones.cpp:583-609, attention_compiler.cpp:
+ * 923-1007) for seq_q >= 1 new query rows per sequence, any head_dim up to 256,
+ * any page size, pools of kv_dtype SFG_F32 or SFG_BF16 (layouts as above).
+ * q fp32 and out (out_dtype) are head-major [B][Hq][seq_q][D], the reference's
+ * AttentionData layout.  Sequence b attends over its first L_b keys, L_b =
+ * seq_lens[b] (device) or max_context when seq_lens is NULL; with causal != 0
+ * query row i sees key j iff j <= L_b - seq_q + i (attention_compiler.cpp:68-72),
+ * so seq_q = 1 sees all of them.  A row with no visible key comes out NaN, as
+ * the reference's 0 / 0.  The MFMA split kernel takes the shapes it lowers
+ * (bf16, head_dim 64 / 128, 16-token pages, one row, GQA group up to 16);
+ * the rest run one wave per (sequence, row, head, split) with fp32 dot
+ * products over the head dimension and an fp32 online softmax.  Errors:
+ * SFG_ERR_INVALID_CONFIG for causal with seq_q > max_context (validate_config,
+ * attention_compiler.cpp:23-29), SFG_ERR_UNSUPPORTED for head_dim > 256. */
+size_t sfg_hip_attn_paged_workspace_v1(int64_t batch, int64_t q_heads, int64_t kv_heads,
+                                       int64_t seq_q, int64_t head_dim, int kv_dtype,
+                                       int64_t max_context, int64_t page_tokens,
+                                       int32_t kv_splits);
+int sfg_hip_attn_paged_v1(const float* q, const void* k_pool, const void* v_pool, int kv_dtype,
+                          const int32_t* page_table, const int32_t* seq_lens, void* out,
+                          int out_dtype, int64_t batch, int64_t q_heads, int64_t kv_heads,
+                          int64_t seq_q, int64_t head_dim, int64_t page_tokens,
+                          int64_t pages_per_seq, int64_t num_pages, int64_t max_context,
+                          int causal, int32_t kv_splits, float scale, int validate_pages,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
 /* append_paged_kv (next_milestones.cpp:486-524) on the device pools: keys / values
- * [B][Hkv][tokens][D] (SFG_F32 or SFG_BF16) are stored as bf16 at token positions
- * start_b + t, start_b = seq_lens[b] (device) when seq_lens != NULL, else `start`,
- * through page_table [B][pages_per_seq] into K [num_pages][Hkv][page_tokens][D] /
- * V [num_pages][Hkv][D][page_tokens].  Pages are assigned by the caller (the host
- * allocator, as the reference's free list); positions past the table's capacity and
- * page ids outside [0, num_pages) are not written.  advance != 0 adds `tokens` to
- * seq_lens afterwards.  head_dim 128, page_tokens 16.
+ * [B][Hkv][tokens][D] (dtype SFG_F32 or SFG_BF16) are stored in the pools' dtype
+ * (pool_dtype SFG_F32 or SFG_BF16; the _paged_v1 form takes bf16 pools) at token
+ * positions start_b + t, start_b = seq_lens[b] (device) when seq_lens != NULL,
+ * else `start`, through page_table [B][pages_per_seq] into
+ * K [num_pages][Hkv][page_tokens][D] / V [num_pages][Hkv][D][page_tokens].  Pages
+ * are assigned by the caller (the host allocator, as the reference's free list);
+ * positions past the table's capacity and page ids outside [0, num_pages) are
+ * not written.  advance != 0 adds `tokens` to seq_lens afterwards.  Any
+ * head_dim and page size.
  * gather_paged_kv (next_milestones.cpp:554-581): the first `length` tokens of every
  * sequence back to keys / values [B][Hkv][length][D] fp32. */
+int sfg_hip_kv_append_pool_v1(const void* keys, const void* values, int dtype, void* k_pool,
+                              void* v_pool, int pool_dtype, const int32_t* page_table,
+                              int32_t* seq_lens, int64_t start, int advance, int64_t batch,
+                              int64_t kv_heads, int64_t tokens, int64_t head_dim, int64_t page_tokens,
+                              int64_t pages_per_seq, int64_t num_pages, void* stream);
+int sfg_hip_kv_gather_pool_v1(const void* k_pool, const void* v_pool, int pool_dtype,
+                              const int32_t* page_table, int64_t batch, int64_t kv_heads,
+                              int64_t length, int64_t head_dim, int64_t page_tokens,
+                              int64_t pages_per_seq, int64_t num_pages, float* keys, float* values,
+                              void* stream);
 int sfg_hip_kv_append_paged_v1(const void* keys, const void* values, int dtype, uint16_t* k_pool,
                                uint16_t* v_pool, const int32_t* page_table, int32_t* seq_lens,
                                int64_t start, int advance, int64_t batch, int64_t kv_heads,
@@ -336,7 +402,9 @@ typedef struct {
     int32_t causal;
     int32_t ffn;        /* 0 dense SwiGLU, 1 MoE */
     int32_t experts, top_k;
-    int32_t context;    /* 0: prefill; > 0: decode step over this many cached tokens */
+    int32_t context;    /* 0: prefill; > 0: decode step of `sequence` new tokens per
+                         * sequence over this many cached tokens (causal: new token i
+                         * sees cached key j iff j <= context - sequence + i) */
     int32_t page_tokens, pages_per_seq, num_pages;
     int32_t act_dtype;  /* SFG_F32 (all-fp32 path) or SFG_BF16 */
     int32_t weight_dtype; /* SFG_F32, SFG_BF16 or SFG_I8 */
@@ -372,14 +440,18 @@ typedef struct {
     const float* router; const float* router_bias; /* MoE: [H][E], [E] or NULL */
     const void* w13; const float* s13;           /* MoE: [E][2I][H] */
     const void* w2; const float* s2;             /* MoE: [E][H][I] */
-    uint16_t* k_pool; uint16_t* v_pool;          /* decode: paged bf16 pools (written when kv_append) */
+    void* k_pool; void* v_pool;                  /* decode: paged pools in the activation dtype
+                                                  * (bf16, or fp32 on the fp32 path); written
+                                                  * when kv_append */
     const int32_t* page_table;                   /* decode: [B][pages_per_seq] */
     const float* rope_table;                     /* [rows][D/2][2] device copy of
                                                   * sfg_hip_rope_table_host_v1 with rows =
-                                                  * S (prefill), 1 (decode: position 0), or
-                                                  * pages_per_seq * page_tokens when
-                                                  * kv_append: the new token rotates at its
-                                                  * length, clamped to capacity - 1 */
+                                                  * S (prefill, and decode: positions 0..S-1
+                                                  * within the step), or pages_per_seq *
+                                                  * page_tokens when kv_append: the new
+                                                  * tokens rotate at their true positions,
+                                                  * clamped to capacity - 1.  May be NULL
+                                                  * when head_dim < 2 (nothing rotates) */
 } sfg_layer_weights;
 
 /* Stage marks recorded into caller-created events when io->stage_events != NULL. */

@@ -50,7 +50,8 @@ class LayerCfg(ctypes.Structure):
                                                "query_heads", "kv_heads", "head_dim")] + \
                [("rms_epsilon", ctypes.c_float), ("rope_theta", ctypes.c_float)] + \
                [(n, ctypes.c_int32) for n in ("causal", "moe", "experts", "top_k", "context",
-                                               "int8_weights", "threads", "kv_append")]
+                                               "int8_weights", "threads", "kv_append",
+                                               "kv_pool_f32")]
 
 
 class LayerData(ctypes.Structure):

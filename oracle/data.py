@@ -96,7 +96,8 @@ def _layer_structs(cfg, d, quant, threads, trace):
     c = LayerCfg(cfg.batch, cfg.sequence, cfg.hidden, cfg.intermediate, cfg.query_heads,
                  cfg.kv_heads, cfg.head_dim, cfg.rms_epsilon, cfg.rope_theta, int(cfg.causal),
                  int(cfg.ffn == "moe"), cfg.experts, cfg.top_k, cfg.context_sequence,
-                 int(cfg.dtype == "w8"), threads, int(getattr(cfg, "kv_append", False)))
+                 int(cfg.dtype == "w8"), threads, int(getattr(cfg, "kv_append", False)),
+                 int(cfg.dtype == "f32"))
     ld = LayerData()
     keep = []
 

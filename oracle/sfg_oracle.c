@@ -783,8 +783,9 @@ int sfgo_decoder_layer(const sfgo_layer_cfg* c, const sfgo_layer_data* d, float*
     const int append = c->context > 0 && c->kv_append;
     if (append) {
         /* Append mode (the build's non-reference option): the step's tokens are
-         * rotated at their true positions context + s, stored as bf16 (the pool
-         * dtype) after the cached tokens, and attended over with the cache. */
+         * rotated at their true positions context + s, stored in the pool dtype
+         * (bf16, or fp32 on the fp32 path) after the cached tokens, and
+         * attended over with the cache. */
         sfgo_split_qkv_rope(qkv, c->batch, c->sequence, H, c->query_heads, c->kv_heads, D,
                             c->rope_theta, q, k, v);
         /* Q and K again from the unrotated rows, rotated at the new positions */
@@ -800,8 +801,10 @@ int sfgo_decoder_layer(const sfgo_layer_cfg* c, const sfgo_layer_data* d, float*
             }
         sfgo_rope_at(q, c->batch, c->query_heads, c->sequence, D, c->rope_theta, c->context);
         sfgo_rope_at(k, c->batch, c->kv_heads, c->sequence, D, c->rope_theta, c->context);
-        sfgo_round_bf16(k, kn);
-        sfgo_round_bf16(v, kn);
+        if (!c->kv_pool_f32) {
+            sfgo_round_bf16(k, kn);
+            sfgo_round_bf16(v, kn);
+        }
     } else {
         sfgo_split_qkv_rope(qkv, c->batch, c->sequence, H, c->query_heads, c->kv_heads, D,
                             c->rope_theta, q, k, v);

@@ -105,7 +105,9 @@ typedef struct {
     int32_t int8_weights; /* 1: projections and FFN weights are weight-only int8 */
     int32_t threads;      /* OpenMP threads for the oracle (<=0: default) */
     int32_t kv_append;    /* decode: 1 = the build's append mode (true-position RoPE, the
-                             step's bf16 K/V appended to the cache and attended over) */
+                             step's K/V appended to the cache and attended over) */
+    int32_t kv_pool_f32;  /* append mode: the pools hold fp32 (the fp32 path), so the
+                             appended K/V keep fp32; 0: bf16 pools, rounded to bf16 */
 } sfgo_layer_cfg;
 
 typedef struct {

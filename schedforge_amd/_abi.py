@@ -141,6 +141,18 @@ _SIGNATURES = {
     "sfg_hip_attn_decode_paged_noalloc_v1": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, ctypes.c_int,
                                                      c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,
                                                      c_i64, c_i32, c_f32, c_vp]),
+    "sfg_hip_gemm_grouped_v1": (c_i32, [ctypes.POINTER(GemmArgs), c_vp, c_i64, c_vp, ctypes.c_int, c_i64, c_i64, c_vp, c_sz,
+                                        c_vp]),
+    "sfg_hip_attn_paged_workspace_v1": (c_sz, [c_i64, c_i64, c_i64, c_i64, c_i64, ctypes.c_int, c_i64,
+                                               c_i64, c_i32]),
+    "sfg_hip_attn_paged_v1": (c_i32, [c_vp, c_vp, c_vp, ctypes.c_int, c_vp, c_vp, c_vp, ctypes.c_int,
+                                      c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,
+                                      ctypes.c_int, c_i32, c_f32, ctypes.c_int, c_vp, c_sz, c_vp]),
+    "sfg_hip_kv_append_pool_v1": (c_i32, [c_vp, c_vp, ctypes.c_int, c_vp, c_vp, ctypes.c_int, c_vp, c_vp,
+                                          c_i64, ctypes.c_int, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,
+                                          c_i64, c_vp]),
+    "sfg_hip_kv_gather_pool_v1": (c_i32, [c_vp, c_vp, ctypes.c_int, c_vp, c_i64, c_i64, c_i64, c_i64,
+                                          c_i64, c_i64, c_i64, c_vp, c_vp, c_vp]),
     "sfg_hip_kv_append_paged_v1": (c_i32, [c_vp, c_vp, ctypes.c_int, c_vp, c_vp, c_vp, c_vp, c_i64,
                                            ctypes.c_int, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64,
                                            c_i64, c_vp]),

@@ -11,6 +11,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -54,7 +55,7 @@ float default_scale(int64_t head_dim, float scale) {
 }
 
 // Argument checks shared by the two paged-decode entry points.
-int check_decode_args(const float* q, const uint16_t* k_pool, const uint16_t* v_pool,
+int check_decode_args(const float* q, const void* k_pool, const void* v_pool,
                       const int32_t* page_table, const void* out, int64_t batch, int64_t q_heads,
                       int64_t kv_heads, int64_t head_dim, int64_t page_tokens, int64_t pages_per_seq,
                       int64_t num_pages, int64_t max_context) {
@@ -65,23 +66,84 @@ int check_decode_args(const float* q, const uint16_t* k_pool, const uint16_t* v_
     if (max_context > pages_per_seq * page_tokens)
         return fail(SFG_ERR_GUARD, "paged KV length violates compiled guard (%lld > %lld)",
                     (long long)max_context, (long long)(pages_per_seq * page_tokens));
+    if (head_dim > 256) return fail(SFG_ERR_UNSUPPORTED, "paged attention: head_dim %lld > 256", (long long)head_dim);
     return SFG_OK;
 }
 
-// The split kernel + merge of both paged-decode entry points, partials in ws.
-int launch_decode(const float* q, const uint16_t* k_pool, const uint16_t* v_pool,
-                  const int32_t* page_table, const int32_t* seq_lens, void* out, int out_dtype,
-                  int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
-                  int64_t page_tokens, int64_t pages_per_seq, int64_t num_pages, int64_t max_context,
-                  int splits, float scale, void* ws, void* stream) {
-    const int rc = sfg::launch_attn_decode_paged(
-        q, q_heads * head_dim, nullptr, 0, k_pool, v_pool, page_table, seq_lens, max_context, 0, out,
-        out_dtype, batch, q_heads, kv_heads, head_dim, page_tokens, pages_per_seq, num_pages, splits,
-        default_scale(head_dim, scale), ws, as_stream(stream), nullptr);
+// Which decode kernel a paged-attention call runs and its split count: the
+// MFMA split-KV kernel where it lowers the shape, else the row kernel (any
+// head_dim <= 256, page size, new-token count and pool dtype).  `bytes` is
+// the partials' workspace.
+struct DecodePlan {
+    bool mfma;
+    int splits;
+    size_t bytes;
+};
+
+DecodePlan plan_decode(int kv_dtype, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq_q,
+                       int64_t head_dim, int64_t page_tokens, int64_t max_context, int32_t kv_splits) {
+    if (sfg::decode_mfma_supported(kv_dtype, head_dim, page_tokens, q_heads / kv_heads, seq_q)) {
+        const int s = sfg::decode_split_count(batch, kv_heads, max_context, page_tokens, kv_splits);
+        return {true, s, sfg::decode_workspace_bytes(batch, q_heads, head_dim, s)};
+    }
+    const int64_t rows = batch * seq_q * q_heads;
+    const int s = sfg::paged_rows_split_count(rows, max_context, kv_splits);
+    return {false, s, sfg::paged_rows_workspace_bytes(rows, head_dim, s)};
+}
+
+// The paged attention of the standalone entry points: Q and the output
+// head-major [B][Hq][Sq][D] (one row per (b, h) when Sq = 1, which is also the
+// MFMA kernel's [B][Hq * D]), partials in ws.
+int launch_paged(const DecodePlan& plan, const float* q, const void* k_pool, const void* v_pool,
+                 int kv_dtype, const int32_t* page_table, const int32_t* seq_lens, void* out,
+                 int out_dtype, int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq_q,
+                 int64_t head_dim, int64_t page_tokens, int64_t pages_per_seq, int64_t num_pages,
+                 int64_t max_context, int causal, float scale, void* ws, void* stream) {
+    const float sc = default_scale(head_dim, scale);
+    int rc;
+    if (plan.mfma) {
+        rc = sfg::launch_attn_decode_paged(
+            q, q_heads * head_dim, nullptr, 0, static_cast<const uint16_t*>(k_pool),
+            static_cast<const uint16_t*>(v_pool), page_table, seq_lens, max_context, 0, out, out_dtype,
+            batch, q_heads, kv_heads, head_dim, page_tokens, pages_per_seq, num_pages, plan.splits, sc,
+            ws, as_stream(stream), nullptr);
+    } else {
+        sfg::PagedRowsLaunch a{};
+        a.q = q;
+        a.q_stride_b = q_heads * seq_q * head_dim; a.q_stride_i = head_dim; a.q_stride_h = seq_q * head_dim;
+        a.k_pool = k_pool; a.v_pool = v_pool; a.kv_dtype = kv_dtype;
+        a.page_table = page_table; a.seq_lens = seq_lens; a.max_context = max_context;
+        a.out = out; a.out_dtype = out_dtype;
+        a.out_stride_b = a.q_stride_b; a.out_stride_i = a.q_stride_i; a.out_stride_h = a.q_stride_h;
+        a.batch = batch; a.q_heads = q_heads; a.kv_heads = kv_heads; a.seq_q = seq_q;
+        a.head_dim = head_dim; a.page_tokens = page_tokens; a.pages_per_seq = pages_per_seq;
+        a.num_pages = num_pages; a.splits = plan.splits; a.causal = causal; a.scale = sc;
+        rc = sfg::launch_attn_paged_rows(a, ws, as_stream(stream));
+    }
     if (rc != SFG_OK)
-        return fail(rc, "attn_decode_paged: head_dim %lld / page_tokens %lld / group %lld not lowered",
+        return fail(rc, "paged attention: head_dim %lld / page_tokens %lld / group %lld not lowered",
                     (long long)head_dim, (long long)page_tokens, (long long)(q_heads / kv_heads));
-    return check_launch("attn_decode_paged");
+    return check_launch("paged attention");
+}
+
+// Host-side page-id validation (validate_pages): the table read back and every
+// used entry checked against the pool.
+int validate_page_ids(const int32_t* page_table, int64_t batch, int64_t pages_per_seq, int64_t num_pages,
+                      int64_t max_context, int64_t page_tokens, void* stream) {
+    std::vector<int32_t> table(static_cast<size_t>(batch * pages_per_seq));
+    hipError_t e = hipMemcpyAsync(table.data(), page_table, table.size() * sizeof(int32_t),
+                                  hipMemcpyDeviceToHost, as_stream(stream));
+    if (e == hipSuccess) e = hipStreamSynchronize(as_stream(stream));
+    if (e != hipSuccess) return fail(SFG_ERR_DEVICE, "page table readback: %s", hipGetErrorString(e));
+    const int64_t used = (max_context + page_tokens - 1) / page_tokens;
+    for (int64_t b = 0; b < batch; ++b)
+        for (int64_t p = 0; p < used; ++p) {
+            const int32_t id = table[static_cast<size_t>(b * pages_per_seq + p)];
+            if (id < 0 || id >= num_pages)
+                return fail(SFG_ERR_GUARD, "invalid physical KV page %d (sequence %lld, page %lld)",
+                            id, (long long)b, (long long)p);
+        }
+    return SFG_OK;
 }
 
 // The device address of `scratch` on the current device, looked up once per
@@ -113,18 +175,20 @@ int scratch_on_current_device(void** out) {
 
 namespace sfg {
 
-int device_xcds() {
-    static std::mutex mu;
-    static int cache[kMaxDevices] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 1;
-    std::lock_guard<std::mutex> lock(mu);
-    if (cache[dev] == 0) {
-        int x = 0;
+int device_xcds(hipStream_t stream) {
+    // One query per device, kept in a lock-free table: concurrent first calls
+    // store the same value.  The device is the stream's (the null stream's is
+    // the current device), so a call with another device's stream gets that
+    // device's count.
+    static std::atomic<int> cache[kMaxDevices];
+    hipDevice_t dev = 0;
+    if (hipStreamGetDevice(stream, &dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 1;
+    int x = cache[dev].load(std::memory_order_relaxed);
+    if (x == 0) {
         if (hipDeviceGetAttribute(&x, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess || x <= 0) x = 1;
-        cache[dev] = x;
+        cache[dev].store(x, std::memory_order_relaxed);
     }
-    return cache[dev];
+    return x;
 }
 
 }  // namespace sfg
@@ -149,9 +213,20 @@ extern "C" {
 
 int sfg_hip_abi_version(void) { return SFG_HIP_ABI_VERSION; }
 
+// The lowering envelope, key=value pairs separated by ';' (after the
+// reference's schedforge_aot_metadata_v1 invariants, llvm_backend.cpp:622-643):
+//   act / weights          activation dtypes and the weight dtypes each takes
+//   kv                     paged pools hold the activation dtype
+//   head_dim, page_tokens, decode_tokens   the widest shapes any path lowers
+//   mfma_*                 the shapes the MFMA kernels take (everything else
+//                          runs the row-per-wave attention / VALU GEMM paths)
 const char* sfg_hip_metadata_v1(void) {
-    return "abi=1;arch=gfx950;wavefront=64;dtypes=f32,bf16,i8;weight_layout=NK;"
-           "kv_layout=page,kv_head,page_token,head_dim;page_tokens=16;head_dim=128(bf16 paths);"
+    return "abi=1;arch=gfx950;wavefront=64;dtypes=f32,bf16,i8;act=f32,bf16;"
+           "weights=f32:f32,bf16:bf16|i8;weight_layout=NK,TILED;"
+           "kv_layout=page,kv_head,page_token,head_dim;kv=act_dtype;"
+           "head_dim=1..256;page_tokens=any;decode_tokens=any;ffn=dense,moe;"
+           "mfma_decode=bf16,head_dim=64|128,page_tokens=16,decode_tokens=1,gqa_group=1|2|4|8|16;"
+           "mfma_prefill=bf16,head_dim=64|128;mfma_gemm=bf16|i8,k%32==0;"
            "accumulate=f32;bf16_rounding=rne";
 }
 
@@ -172,9 +247,10 @@ int sfg_hip_target_info_v1(int device, sfg_target_info* info) {
     hipDeviceProp_t prop;
     hipError_t e = hipGetDeviceProperties(&prop, device);
     if (e != hipSuccess) return fail(SFG_ERR_DEVICE, "hipGetDeviceProperties: %s", hipGetErrorString(e));
+    // A runtime that cannot report XCDs gets one, as the kernel launches
+    // assume (device_xcds): the query still describes the device.
     int xcds = 0;
-    e = hipDeviceGetAttribute(&xcds, hipDeviceAttributeNumberOfXccs, device);
-    if (e != hipSuccess) return fail(SFG_ERR_DEVICE, "hipDeviceGetAttribute(XCCs): %s", hipGetErrorString(e));
+    if (hipDeviceGetAttribute(&xcds, hipDeviceAttributeNumberOfXccs, device) != hipSuccess) xcds = 1;
     sfg_target_info t{};
     snprintf(t.architecture, sizeof t.architecture, "%s", prop.gcnArchName);
     t.wavefront = prop.warpSize;
@@ -246,7 +322,9 @@ int sfg_hip_to_bf16_v1(const float* src, uint16_t* dst, int64_t count, void* str
 }
 
 int sfg_hip_rope_table_host_v1(float* table, int64_t seq, int64_t head_dim, float theta) {
-    if (!table || seq <= 0 || head_dim <= 0 || (head_dim & 1))
+    // [seq][head_dim / 2][cos, sin]: an odd head_dim's last dimension is not
+    // rotated (apply_rope's loop stops at dimension + 1 < head_dim)
+    if (seq <= 0 || head_dim <= 0 || (!table && head_dim >= 2))
         return fail(SFG_ERR_SHAPE, "rope_table: invalid arguments");
     // The reference's expressions (decoder_compiler.cpp:101-106), evaluated
     // with the host libm: f = powf(theta, -float(2i)/float(D)); a = float(pos) * f.
@@ -307,6 +385,37 @@ int sfg_hip_gemm_v1(const sfg_gemm_args* a, void* workspace, size_t workspace_by
     return check_launch("gemm");
 }
 
+int sfg_hip_gemm_grouped_v1(const sfg_gemm_args* a, const int32_t* a_rows, int64_t a_rows_limit,
+                            const int32_t* offsets, int groups, int64_t b_group_stride,
+                            int64_t s_group_stride, void* workspace, size_t workspace_bytes,
+                            void* stream) {
+    (void)workspace; (void)workspace_bytes;  // grouped products reduce inside their workgroups
+    if (!a || !a->a || !a->b || !a->c || !offsets || a->m <= 0 || a->n <= 0 || a->k <= 0 || groups <= 0)
+        return fail(SFG_ERR_SHAPE, "gemm_grouped: invalid arguments");
+    if (a->lda < a->k || a->ldb < a->k || a->ldc < a->n)
+        return fail(SFG_ERR_SHAPE, "gemm_grouped: leading dimension too small");
+    if (a_rows && a_rows_limit <= 0) return fail(SFG_ERR_SHAPE, "gemm_grouped: a_rows_limit must be > 0");
+    if (a->epilogue == SFG_EPI_RESIDUAL || a->epilogue < SFG_EPI_NONE || a->epilogue > SFG_EPI_GLU_SILU_UP)
+        return fail(SFG_ERR_SHAPE, "gemm_grouped: epilogue %d (none, SwiGLU or GLU)", a->epilogue);
+    if (a->b_layout != SFG_LAYOUT_NK && a->b_layout != SFG_LAYOUT_TILED)
+        return fail(SFG_ERR_SHAPE, "gemm_grouped: unknown weight layout %d", a->b_layout);
+    if (a->tile < SFG_TILE_AUTO || a->tile >= SFG_TILE_COUNT)
+        return fail(SFG_ERR_SHAPE, "gemm_grouped: unknown tile policy %d", a->tile);
+    sfg::GemmProblem p{};
+    p.a = a->a; p.a_dtype = a->a_dtype; p.lda = a->lda; p.a_rows = a_rows;
+    p.a_rows_limit = a_rows ? a_rows_limit : a->m;
+    p.b = a->b; p.b_dtype = a->b_dtype; p.ldb = a->ldb; p.b_scales = a->b_scales;
+    p.b_group_stride = b_group_stride; p.s_group_stride = s_group_stride;
+    p.c = a->c; p.c_dtype = a->c_dtype; p.ldc = a->ldc;
+    p.m = a->m; p.n = a->n; p.k = a->k; p.epilogue = a->epilogue;
+    p.b_layout = a->b_layout; p.offsets = offsets; p.groups = groups; p.tile = a->tile;
+    const int rc = sfg::launch_gemm(p, nullptr, 0, as_stream(stream));
+    if (rc != SFG_OK)
+        return fail(rc, "gemm_grouped: unsupported combination (a=%d b=%d m=%lld n=%lld k=%lld epi=%d)",
+                    a->a_dtype, a->b_dtype, (long long)a->m, (long long)a->n, (long long)a->k, a->epilogue);
+    return check_launch("gemm_grouped");
+}
+
 int sfg_hip_qkv_split_rope_v1(const float* qkv, const float* rope_table, int64_t batch,
                               int64_t seq, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
                               void* q, void* k, void* v, int out_dtype, void* stream) {
@@ -330,11 +439,11 @@ int sfg_hip_attn_prefill_v1(const void* q, const void* k, const void* v, void* o
         return fail(SFG_ERR_INVALID_CONFIG, "invalid attention configuration");
     const float s = default_scale(head_dim, scale);
     if (dtype == SFG_F32) {
-        if (head_dim > 128) return fail(SFG_ERR_UNSUPPORTED, "attn_prefill f32: head_dim > 128");
-        sfg::launch_attn_prefill_f32(static_cast<const float*>(q), static_cast<const float*>(k),
-                                     static_cast<const float*>(v), out, out_dtype, batch, q_heads,
-                                     kv_heads, seq_q, seq_kv, head_dim, causal, s,
-                                     as_stream(stream));
+        const int rc = sfg::launch_attn_prefill_f32(
+            static_cast<const float*>(q), static_cast<const float*>(k), static_cast<const float*>(v),
+            out, out_dtype, batch, q_heads, kv_heads, seq_q, seq_kv, head_dim, causal, s,
+            as_stream(stream));
+        if (rc != SFG_OK) return fail(rc, "attn_prefill f32: head_dim %lld > 256", (long long)head_dim);
     } else if (dtype == SFG_BF16) {
         const int rc = sfg::launch_attn_prefill_bf16(
             static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
@@ -389,10 +498,16 @@ int sfg_hip_attn_prefill_vt_v1(const uint16_t* q, const uint16_t* k, const uint1
 size_t sfg_hip_attn_decode_workspace_v1(int64_t batch, int64_t q_heads, int64_t head_dim,
                                         int64_t max_context, int64_t page_tokens,
                                         int32_t kv_splits) {
-    // kv_heads only bounds the automatic split choice from below; using q_heads
-    // here gives an upper bound on the split count chosen for any kv_heads.
-    const int splits = sfg::decode_split_count(batch, 1, max_context, page_tokens, kv_splits);
-    return sfg::decode_workspace_bytes(batch, q_heads, head_dim, splits);
+    // kv_heads only bounds the MFMA kernel's automatic split choice from
+    // below; kv_heads = q_heads gives an upper bound on the split count chosen
+    // for any kv_heads.  The row kernel's partials (shapes the MFMA kernel does
+    // not lower) are covered too.
+    if (batch <= 0 || q_heads <= 0 || head_dim <= 0 || max_context <= 0 || page_tokens <= 0) return 0;
+    const int s = sfg::decode_split_count(batch, 1, max_context, page_tokens, kv_splits);
+    const size_t mfma = sfg::decode_workspace_bytes(batch, q_heads, head_dim, s);
+    const int rs = sfg::paged_rows_split_count(batch * q_heads, max_context, kv_splits);
+    const size_t rows = sfg::paged_rows_workspace_bytes(batch * q_heads, head_dim, rs);
+    return mfma > rows ? mfma : rows;
 }
 
 int sfg_hip_attn_decode_paged_v1(const float* q, const uint16_t* k_pool, const uint16_t* v_pool,
@@ -405,28 +520,17 @@ int sfg_hip_attn_decode_paged_v1(const float* q, const uint16_t* k_pool, const u
     int rc = check_decode_args(q, k_pool, v_pool, page_table, out, batch, q_heads, kv_heads, head_dim,
                                page_tokens, pages_per_seq, num_pages, max_context);
     if (rc != SFG_OK) return rc;
-    if (validate_pages) {
-        std::vector<int32_t> table(static_cast<size_t>(batch * pages_per_seq));
-        hipError_t e = hipMemcpyAsync(table.data(), page_table, table.size() * sizeof(int32_t),
-                                      hipMemcpyDeviceToHost, as_stream(stream));
-        if (e == hipSuccess) e = hipStreamSynchronize(as_stream(stream));
-        if (e != hipSuccess) return fail(SFG_ERR_DEVICE, "page table readback: %s", hipGetErrorString(e));
-        const int64_t used = (max_context + page_tokens - 1) / page_tokens;
-        for (int64_t b = 0; b < batch; ++b)
-            for (int64_t p = 0; p < used; ++p) {
-                const int32_t id = table[static_cast<size_t>(b * pages_per_seq + p)];
-                if (id < 0 || id >= num_pages)
-                    return fail(SFG_ERR_GUARD, "invalid physical KV page %d (sequence %lld, page %lld)",
-                                id, (long long)b, (long long)p);
-            }
-    }
-    const int splits = sfg::decode_split_count(batch, kv_heads, max_context, page_tokens, kv_splits);
-    const size_t need = sfg::decode_workspace_bytes(batch, q_heads, head_dim, splits);
-    if (!workspace || workspace_bytes < need)
-        return fail(SFG_ERR_WORKSPACE, "attn_decode_paged: workspace %zu < %zu", workspace_bytes, need);
-    return launch_decode(q, k_pool, v_pool, page_table, seq_lens, out, out_dtype, batch, q_heads,
-                         kv_heads, head_dim, page_tokens, pages_per_seq, num_pages, max_context, splits,
-                         scale, workspace, stream);
+    if (validate_pages &&
+        (rc = validate_page_ids(page_table, batch, pages_per_seq, num_pages, max_context, page_tokens,
+                                stream)) != SFG_OK)
+        return rc;
+    const DecodePlan plan = plan_decode(SFG_BF16, batch, q_heads, kv_heads, 1, head_dim, page_tokens,
+                                        max_context, kv_splits);
+    if (plan.bytes > 0 && (!workspace || workspace_bytes < plan.bytes))
+        return fail(SFG_ERR_WORKSPACE, "attn_decode_paged: workspace %zu < %zu", workspace_bytes, plan.bytes);
+    return launch_paged(plan, q, k_pool, v_pool, SFG_BF16, page_table, seq_lens, out, out_dtype, batch,
+                        q_heads, kv_heads, 1, head_dim, page_tokens, pages_per_seq, num_pages, max_context,
+                        1, scale, workspace, stream);
 }
 
 int sfg_hip_attn_decode_paged_noalloc_v1(const float* q, const uint16_t* k_pool,
@@ -440,19 +544,84 @@ int sfg_hip_attn_decode_paged_noalloc_v1(const float* q, const uint16_t* k_pool,
     int rc = check_decode_args(q, k_pool, v_pool, page_table, out, batch, q_heads, kv_heads, head_dim,
                                page_tokens, pages_per_seq, num_pages, max_context);
     if (rc != SFG_OK) return rc;
-    const int splits = sfg::decode_split_count(batch, kv_heads, max_context, page_tokens, kv_splits);
-    const size_t need = sfg::decode_workspace_bytes(batch, q_heads, head_dim, splits);
-    if (need > SFG_DECODE_SCRATCH_BYTES)
+    const DecodePlan plan = plan_decode(SFG_BF16, batch, q_heads, kv_heads, 1, head_dim, page_tokens,
+                                        max_context, kv_splits);
+    if (plan.bytes > SFG_DECODE_SCRATCH_BYTES)
         return fail(SFG_ERR_WORKSPACE,
                     "attn_decode_paged_noalloc: %zu bytes of split partials (batch %lld x %lld heads x "
                     "%d splits) exceed the library's %zu-byte scratch; use sfg_hip_attn_decode_paged_v1 "
                     "with a workspace",
-                    need, (long long)batch, (long long)q_heads, splits, (size_t)SFG_DECODE_SCRATCH_BYTES);
+                    plan.bytes, (long long)batch, (long long)q_heads, plan.splits,
+                    (size_t)SFG_DECODE_SCRATCH_BYTES);
     void* ws = nullptr;
     if ((rc = scratch_on_current_device(&ws)) != SFG_OK) return rc;
-    return launch_decode(q, k_pool, v_pool, page_table, seq_lens, out, out_dtype, batch, q_heads,
-                         kv_heads, head_dim, page_tokens, pages_per_seq, num_pages, max_context, splits,
-                         scale, ws, stream);
+    return launch_paged(plan, q, k_pool, v_pool, SFG_BF16, page_table, seq_lens, out, out_dtype, batch,
+                        q_heads, kv_heads, 1, head_dim, page_tokens, pages_per_seq, num_pages, max_context,
+                        1, scale, ws, stream);
+}
+
+size_t sfg_hip_attn_paged_workspace_v1(int64_t batch, int64_t q_heads, int64_t kv_heads,
+                                       int64_t seq_q, int64_t head_dim, int kv_dtype,
+                                       int64_t max_context, int64_t page_tokens, int32_t kv_splits) {
+    if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads || seq_q <= 0 ||
+        head_dim <= 0 || max_context <= 0 || page_tokens <= 0)
+        return 0;
+    return plan_decode(kv_dtype, batch, q_heads, kv_heads, seq_q, head_dim, page_tokens, max_context,
+                       kv_splits).bytes;
+}
+
+int sfg_hip_attn_paged_v1(const float* q, const void* k_pool, const void* v_pool, int kv_dtype,
+                          const int32_t* page_table, const int32_t* seq_lens, void* out, int out_dtype,
+                          int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq_q,
+                          int64_t head_dim, int64_t page_tokens, int64_t pages_per_seq,
+                          int64_t num_pages, int64_t max_context, int causal, int32_t kv_splits,
+                          float scale, int validate_pages, void* workspace, size_t workspace_bytes,
+                          void* stream) {
+    int rc = check_decode_args(q, k_pool, v_pool, page_table, out, batch, q_heads, kv_heads, head_dim,
+                               page_tokens, pages_per_seq, num_pages, max_context);
+    if (rc != SFG_OK) return rc;
+    // validate_config (attention_compiler.cpp:23-29): a causal query block no
+    // longer than the keys it attends over
+    if (seq_q <= 0 || (causal && seq_q > max_context))
+        return fail(SFG_ERR_INVALID_CONFIG, "invalid attention configuration");
+    if (kv_dtype != SFG_F32 && kv_dtype != SFG_BF16)
+        return fail(SFG_ERR_UNSUPPORTED, "paged attention: pool dtype %d", kv_dtype);
+    if (out_dtype != SFG_F32 && out_dtype != SFG_BF16)
+        return fail(SFG_ERR_UNSUPPORTED, "paged attention: output dtype %d", out_dtype);
+    if (validate_pages &&
+        (rc = validate_page_ids(page_table, batch, pages_per_seq, num_pages, max_context, page_tokens,
+                                stream)) != SFG_OK)
+        return rc;
+    const DecodePlan plan = plan_decode(kv_dtype, batch, q_heads, kv_heads, seq_q, head_dim, page_tokens,
+                                        max_context, kv_splits);
+    if (plan.bytes > 0 && (!workspace || workspace_bytes < plan.bytes))
+        return fail(SFG_ERR_WORKSPACE, "attn_paged: workspace %zu < %zu", workspace_bytes, plan.bytes);
+    return launch_paged(plan, q, k_pool, v_pool, kv_dtype, page_table, seq_lens, out, out_dtype, batch,
+                        q_heads, kv_heads, seq_q, head_dim, page_tokens, pages_per_seq, num_pages,
+                        max_context, causal, scale, workspace, stream);
+}
+
+int sfg_hip_kv_append_pool_v1(const void* keys, const void* values, int dtype, void* k_pool,
+                              void* v_pool, int pool_dtype, const int32_t* page_table,
+                              int32_t* seq_lens, int64_t start, int advance, int64_t batch,
+                              int64_t kv_heads, int64_t tokens, int64_t head_dim, int64_t page_tokens,
+                              int64_t pages_per_seq, int64_t num_pages, void* stream) {
+    if (!keys || !values || !k_pool || !v_pool || !page_table || batch <= 0 || kv_heads <= 0 ||
+        tokens <= 0 || head_dim <= 0 || page_tokens <= 0 || pages_per_seq <= 0 || num_pages <= 0)
+        return fail(SFG_ERR_SHAPE, "kv_append: invalid arguments");
+    if (dtype != SFG_F32 && dtype != SFG_BF16) return fail(SFG_ERR_UNSUPPORTED, "kv_append: dtype %d", dtype);
+    if (pool_dtype != SFG_F32 && pool_dtype != SFG_BF16)
+        return fail(SFG_ERR_UNSUPPORTED, "kv_append: pool dtype %d", pool_dtype);
+    if (!seq_lens && (start < 0 || start + tokens > pages_per_seq * page_tokens))
+        return fail(SFG_ERR_GUARD, "paged KV capacity exceeded (%lld + %lld > %lld)", (long long)start,
+                    (long long)tokens, (long long)(pages_per_seq * page_tokens));
+    const int rc = sfg::launch_kv_append(keys, values, dtype, kv_heads * tokens * head_dim,
+                                         tokens * head_dim, head_dim, nullptr, k_pool, v_pool, pool_dtype,
+                                         page_table, seq_lens, start, advance, batch, kv_heads, tokens,
+                                         head_dim, page_tokens, pages_per_seq, num_pages, as_stream(stream));
+    if (rc != SFG_OK) return fail(rc, "kv_append: head_dim %lld / page_tokens %lld not lowered",
+                                  (long long)head_dim, (long long)page_tokens);
+    return check_launch("kv_append");
 }
 
 int sfg_hip_kv_append_paged_v1(const void* keys, const void* values, int dtype, uint16_t* k_pool,
@@ -460,21 +629,29 @@ int sfg_hip_kv_append_paged_v1(const void* keys, const void* values, int dtype, 
                                int64_t start, int advance, int64_t batch, int64_t kv_heads,
                                int64_t tokens, int64_t head_dim, int64_t page_tokens,
                                int64_t pages_per_seq, int64_t num_pages, void* stream) {
-    if (!keys || !values || !k_pool || !v_pool || !page_table || batch <= 0 || kv_heads <= 0 ||
-        tokens <= 0 || head_dim <= 0 || page_tokens <= 0 || pages_per_seq <= 0 || num_pages <= 0)
-        return fail(SFG_ERR_SHAPE, "kv_append_paged: invalid arguments");
-    if (dtype != SFG_F32 && dtype != SFG_BF16) return fail(SFG_ERR_UNSUPPORTED, "kv_append_paged: dtype %d", dtype);
-    if (!seq_lens && (start < 0 || start + tokens > pages_per_seq * page_tokens))
-        return fail(SFG_ERR_GUARD, "paged KV capacity exceeded (%lld + %lld > %lld)", (long long)start,
-                    (long long)tokens, (long long)(pages_per_seq * page_tokens));
-    const int rc = sfg::launch_kv_append(keys, values, dtype, kv_heads * tokens * head_dim,
-                                         tokens * head_dim, head_dim, nullptr, k_pool, v_pool, page_table,
-                                         seq_lens, start, advance, batch, kv_heads, tokens, head_dim,
-                                         page_tokens, pages_per_seq, num_pages, as_stream(stream));
-    if (rc != SFG_OK)
-        return fail(rc, "kv_append_paged: head_dim %lld / page_tokens %lld not lowered", (long long)head_dim,
-                    (long long)page_tokens);
-    return check_launch("kv_append_paged");
+    return sfg_hip_kv_append_pool_v1(keys, values, dtype, k_pool, v_pool, SFG_BF16, page_table, seq_lens,
+                                     start, advance, batch, kv_heads, tokens, head_dim, page_tokens,
+                                     pages_per_seq, num_pages, stream);
+}
+
+int sfg_hip_kv_gather_pool_v1(const void* k_pool, const void* v_pool, int pool_dtype,
+                              const int32_t* page_table, int64_t batch, int64_t kv_heads,
+                              int64_t length, int64_t head_dim, int64_t page_tokens,
+                              int64_t pages_per_seq, int64_t num_pages, float* keys, float* values,
+                              void* stream) {
+    if (!k_pool || !v_pool || !page_table || !keys || !values || batch <= 0 || kv_heads <= 0 ||
+        head_dim <= 0 || page_tokens <= 0 || pages_per_seq <= 0 || num_pages <= 0)
+        return fail(SFG_ERR_SHAPE, "kv_gather: invalid arguments");
+    if (length <= 0) return fail(SFG_ERR_INVALID_CONFIG, "cannot gather empty paged KV cache");
+    if (length > pages_per_seq * page_tokens)
+        return fail(SFG_ERR_GUARD, "kv_gather: length %lld beyond the page table", (long long)length);
+    if (pool_dtype != SFG_F32 && pool_dtype != SFG_BF16)
+        return fail(SFG_ERR_UNSUPPORTED, "kv_gather: pool dtype %d", pool_dtype);
+    const int rc = sfg::launch_kv_gather(k_pool, v_pool, pool_dtype, page_table, batch, kv_heads, length,
+                                         head_dim, page_tokens, pages_per_seq, num_pages, keys, values,
+                                         as_stream(stream));
+    if (rc != SFG_OK) return fail(rc, "kv_gather: head_dim %lld not lowered", (long long)head_dim);
+    return check_launch("kv_gather");
 }
 
 int sfg_hip_kv_gather_paged_v1(const uint16_t* k_pool, const uint16_t* v_pool,
@@ -482,17 +659,9 @@ int sfg_hip_kv_gather_paged_v1(const uint16_t* k_pool, const uint16_t* v_pool,
                                int64_t length, int64_t head_dim, int64_t page_tokens,
                                int64_t pages_per_seq, int64_t num_pages, float* keys, float* values,
                                void* stream) {
-    if (!k_pool || !v_pool || !page_table || !keys || !values || batch <= 0 || kv_heads <= 0 ||
-        head_dim <= 0 || page_tokens <= 0 || pages_per_seq <= 0 || num_pages <= 0)
-        return fail(SFG_ERR_SHAPE, "kv_gather_paged: invalid arguments");
-    if (length <= 0) return fail(SFG_ERR_INVALID_CONFIG, "cannot gather empty paged KV cache");
-    if (length > pages_per_seq * page_tokens)
-        return fail(SFG_ERR_GUARD, "kv_gather_paged: length %lld beyond the page table", (long long)length);
-    const int rc = sfg::launch_kv_gather(k_pool, v_pool, page_table, batch, kv_heads, length, head_dim,
-                                         page_tokens, pages_per_seq, num_pages, keys, values,
-                                         as_stream(stream));
-    if (rc != SFG_OK) return fail(rc, "kv_gather_paged: head_dim %lld not lowered", (long long)head_dim);
-    return check_launch("kv_gather_paged");
+    return sfg_hip_kv_gather_pool_v1(k_pool, v_pool, SFG_BF16, page_table, batch, kv_heads, length,
+                                     head_dim, page_tokens, pages_per_seq, num_pages, keys, values,
+                                     stream);
 }
 
 size_t sfg_hip_moe_route_workspace_v1(int64_t tokens, int64_t experts, int64_t top_k) {
@@ -541,15 +710,17 @@ size_t sfg_hip_moe_expert_workspace_v1(int64_t tokens, int64_t hidden, int64_t i
     return 0;
 }
 
-static int moe_experts(const uint16_t* x, const int32_t* offsets, const int32_t* token_ids,
+// The grouped expert products of execute_moe (moe_compiler.cpp:64-155): x and
+// act in the activation dtype (bf16, or fp32 with fp32 weights).
+static int moe_experts(const void* x, int act_dtype, const int32_t* offsets, const int32_t* token_ids,
                        const void* w13, const float* s13, const void* w2, const float* s2,
-                       int w_dtype, int w_layout, uint16_t* act, float* y, int64_t tokens, int64_t hidden,
+                       int w_dtype, int w_layout, void* act, float* y, int64_t tokens, int64_t hidden,
                        int64_t inter, int64_t experts, int64_t top_k, int tile, hipStream_t stream) {
     sfg::GemmProblem p{};
-    p.a = x; p.a_dtype = SFG_BF16; p.lda = hidden; p.a_rows = token_ids; p.a_rows_limit = tokens;
+    p.a = x; p.a_dtype = act_dtype; p.lda = hidden; p.a_rows = token_ids; p.a_rows_limit = tokens;
     p.b = w13; p.b_dtype = w_dtype; p.ldb = hidden; p.b_scales = s13;
     p.b_group_stride = 2 * inter * hidden; p.s_group_stride = 2 * inter;
-    p.c = act; p.c_dtype = SFG_BF16; p.ldc = inter;
+    p.c = act; p.c_dtype = act_dtype; p.ldc = inter;
     p.m = tokens * top_k; p.n = inter; p.k = hidden; p.epilogue = SFG_EPI_GLU_SILU_UP;
     p.b_layout = w_layout;
     p.offsets = offsets; p.groups = static_cast<int>(experts);
@@ -558,7 +729,7 @@ static int moe_experts(const uint16_t* x, const int32_t* offsets, const int32_t*
     if (rc != SFG_OK) return fail(rc, "moe experts W1/W3: shape not lowered (H=%lld I=%lld)",
                                   (long long)hidden, (long long)inter);
     sfg::GemmProblem q{};
-    q.a = act; q.a_dtype = SFG_BF16; q.lda = inter; q.a_rows = nullptr;
+    q.a = act; q.a_dtype = act_dtype; q.lda = inter; q.a_rows = nullptr;
     q.b = w2; q.b_dtype = w_dtype; q.ldb = inter; q.b_scales = s2;
     q.b_group_stride = hidden * inter; q.s_group_stride = hidden;
     q.c = y; q.c_dtype = SFG_F32; q.ldc = hidden;
@@ -584,15 +755,14 @@ int sfg_hip_moe_experts_v1(const uint16_t* x, const int32_t* offsets, const int3
     if (w_dtype != SFG_BF16 && w_dtype != SFG_I8) return fail(SFG_ERR_UNSUPPORTED, "expert dtype %d", w_dtype);
     if (w_layout != SFG_LAYOUT_NK && w_layout != SFG_LAYOUT_TILED)
         return fail(SFG_ERR_SHAPE, "moe experts: unknown weight layout %d", w_layout);
-    return moe_experts(x, offsets, token_ids, w13, s13, w2, s2, w_dtype, w_layout, act, y, tokens,
-                       hidden, inter, experts, top_k, SFG_TILE_AUTO, as_stream(stream));
+    return moe_experts(x, SFG_BF16, offsets, token_ids, w13, s13, w2, s2, w_dtype, w_layout, act, y,
+                       tokens, hidden, inter, experts, top_k, SFG_TILE_AUTO, as_stream(stream));
 }
 
 int sfg_hip_moe_combine_v1(const float* y, const int32_t* position, const float* weights,
                            const float* residual, float* out, int64_t tokens, int64_t hidden,
                            int64_t top_k, void* stream) {
-    if (!y || !position || !weights || !residual || !out || tokens <= 0 || hidden <= 0 ||
-        top_k <= 0 || (hidden & 3))
+    if (!y || !position || !weights || !residual || !out || tokens <= 0 || hidden <= 0 || top_k <= 0)
         return fail(SFG_ERR_SHAPE, "moe_combine: invalid arguments");
     sfg::launch_moe_combine(y, position, weights, residual, out, tokens, hidden, top_k,
                             as_stream(stream));
@@ -645,26 +815,23 @@ int validate_desc(const sfg_layer_desc* d) {
         return fail(SFG_ERR_UNSUPPORTED, "fp32 activations need fp32 weights");
     if (d->act_dtype == SFG_BF16 && d->weight_dtype != SFG_BF16 && d->weight_dtype != SFG_I8)
         return fail(SFG_ERR_UNSUPPORTED, "bf16 activations need bf16 or int8 weights");
+    if (d->head_dim > 256)
+        return fail(SFG_ERR_UNSUPPORTED, "head_dim %d: attention lowers head dims up to 256", d->head_dim);
     if (d->context > 0) {
-        if (d->act_dtype != SFG_BF16)
-            return fail(SFG_ERR_UNSUPPORTED, "decode runs on a bf16 paged KV cache");
+        // the paged pools hold the activation dtype: fp32 for the fp32 path, bf16 otherwise
         if (d->page_tokens <= 0 || d->pages_per_seq <= 0 || d->num_pages <= 0)
             return fail(SFG_ERR_INVALID_CONFIG, "invalid paged KV configuration");
         if (d->context > d->pages_per_seq * d->page_tokens)
             return fail(SFG_ERR_GUARD, "KV cache length violates compiled guard");
-        if (d->kv_append) {
-            if (d->head_dim != 128 || d->page_tokens != 16 || d->sequence != 1)
-                return fail(SFG_ERR_UNSUPPORTED, "kv append lowers head_dim 128, 16-token pages, one token");
-            if (d->context + 1 > d->pages_per_seq * d->page_tokens)
-                return fail(SFG_ERR_GUARD, "paged KV capacity exceeded by the appended token");
-        }
+        // validate_config (attention_compiler.cpp:23-29): the step's causal
+        // query block attends over the cached keys
+        if (d->causal && !d->kv_append && d->sequence > d->context)
+            return fail(SFG_ERR_INVALID_CONFIG, "invalid attention configuration");
+        if (d->kv_append && d->context + d->sequence > d->pages_per_seq * d->page_tokens)
+            return fail(SFG_ERR_GUARD, "paged KV capacity exceeded by the appended tokens");
     } else if (d->kv_append) {
         return fail(SFG_ERR_INVALID_CONFIG, "kv append needs a decode step (context > 0)");
-    } else if (d->causal && d->sequence <= 0) {
-        return fail(SFG_ERR_INVALID_CONFIG, "invalid attention configuration");
     }
-    if (d->ffn == 1 && d->act_dtype != SFG_BF16)
-        return fail(SFG_ERR_UNSUPPORTED, "MoE layers run with bf16 activations");
     if (d->weight_layout != SFG_LAYOUT_NK && d->weight_layout != SFG_LAYOUT_TILED)
         return fail(SFG_ERR_SHAPE, "unknown weight layout %d", d->weight_layout);
     if (d->gemm_tile < SFG_TILE_AUTO || d->gemm_tile >= SFG_TILE_COUNT)
@@ -674,6 +841,14 @@ int validate_desc(const sfg_layer_desc* d) {
     if (d->weight_layout == SFG_LAYOUT_TILED && d->act_dtype != SFG_BF16)
         return fail(SFG_ERR_UNSUPPORTED, "tiled weights are bf16 / int8");
     return SFG_OK;
+}
+
+// The decode attention of a layer step: the keys it may reach (the cache,
+// plus the step's own tokens when they are appended) and the kernel choice.
+DecodePlan layer_decode_plan(const sfg_layer_desc* d) {
+    const int64_t keys = static_cast<int64_t>(d->context) + (d->kv_append ? d->sequence : 0);
+    return plan_decode(d->act_dtype, d->batch, d->query_heads, d->kv_heads, d->sequence, d->head_dim,
+                       d->page_tokens, keys, d->kv_splits);
 }
 
 // The flash prefill over V^T serves bf16 activations at head_dim 128.
@@ -705,7 +880,7 @@ LayerBuffers plan_buffers(const sfg_layer_desc* d, void* ws) {
     b.r1 = static_cast<float*>(c.take(rows * H * 4));
     if (moe) {
         const int64_t assign = rows * d->top_k;
-        b.act = c.take(assign * I * 2);
+        b.act = c.take(assign * I * ae);
         b.y = static_cast<float*>(c.take(assign * H * 4));
         b.ids = static_cast<int32_t*>(c.take(assign * 4));
         b.wts = static_cast<float*>(c.take(assign * 4));
@@ -718,11 +893,7 @@ LayerBuffers plan_buffers(const sfg_layer_desc* d, void* ws) {
     } else {
         b.act = c.take(rows * I * ae);
     }
-    if (d->context > 0) {
-        const int splits = sfg::decode_split_count(d->batch, d->kv_heads, d->context + (d->kv_append ? 1 : 0),
-                                                   d->page_tokens, d->kv_splits);
-        b.attn_ws = c.take(sfg::decode_workspace_bytes(d->batch, d->query_heads, D, splits));
-    }
+    if (d->context > 0) b.attn_ws = c.take(layer_decode_plan(d).bytes);
     // Split-K scratch sized for the widest projection.
     size_t g = 0;
     const int64_t ns[4] = {qkvw, H, 2 * I, H};
@@ -817,7 +988,7 @@ int sfg_hip_decoder_layer_v1(const sfg_layer_desc* d, const sfg_layer_weights* w
     const int64_t qkvw = H + 2 * kvd;
     const int act = d->act_dtype;
     const int wdt = d->weight_dtype;
-    if (!w->rms1 || !w->rms2 || !w->w_qkv || !w->w_o || !w->rope_table)
+    if (!w->rms1 || !w->rms2 || !w->w_qkv || !w->w_o || (!w->rope_table && D >= 2))
         return fail(SFG_ERR_SHAPE, "decoder layer: missing attention weights");
     if (wdt == SFG_I8 && (!w->s_qkv || !w->s_o)) return fail(SFG_ERR_SHAPE, "int8 weights need scales");
     if (moe) {
@@ -897,41 +1068,59 @@ int sfg_hip_decoder_layer_v1(const sfg_layer_desc* d, const sfg_layer_weights* w
     mk.mark(SFG_MARK_ROPE);
     // 4. attention -> merged [rows][H]
     if (decode) {
-        if (d->sequence != 1) return fail(SFG_ERR_UNSUPPORTED, "decode lowers one new token per sequence");
         const bool append = d->kv_append != 0;
-        const int splits = sfg::decode_split_count(d->batch, d->kv_heads, d->context + (append ? 1 : 0),
-                                                   d->page_tokens, d->kv_splits);
+        const int64_t S = d->sequence;
+        const int64_t capacity = static_cast<int64_t>(d->pages_per_seq) * d->page_tokens;
+        const DecodePlan plan = layer_decode_plan(d);
         if (append) {
-            // Append mode: the step's K (rotated at its true position, the
-            // sequence's length) and V go into the pools at that position,
-            // as append_paged_kv does (next_milestones.cpp:486-524).
-            rc = sfg::launch_kv_append(b.qkv + H, b.qkv + H + kvd, SFG_F32, qkvw, D, 0, w->rope_table,
-                                       w->k_pool, w->v_pool, w->page_table, io->seq_lens, d->context,
-                                       0, d->batch, d->kv_heads, 1, D, d->page_tokens, d->pages_per_seq,
-                                       d->num_pages, s);
+            // Append mode: the step's K (rotated at its true positions, the
+            // sequence's length onwards) and V go into the pools there, as
+            // append_paged_kv does (next_milestones.cpp:486-524).  Row (b, t)
+            // of the QKV product is b S + t.
+            rc = sfg::launch_kv_append(b.qkv + H, b.qkv + H + kvd, SFG_F32, S * qkvw, D, qkvw,
+                                       w->rope_table, w->k_pool, w->v_pool, act, w->page_table,
+                                       io->seq_lens, d->context, 0, d->batch, d->kv_heads, S, D,
+                                       d->page_tokens, d->pages_per_seq, d->num_pages, s);
             if (rc != SFG_OK) return fail(rc, "kv append not lowered (head_dim %lld)", (long long)D);
         }
-        // RoPE of the new token's query is applied while the kernel loads Q
-        // straight from the QKV rows: at position 0 within the step, as the
+        // RoPE of the step's queries is applied while the kernel loads Q
+        // straight from the QKV rows: at the index within the step, as the
         // reference rotates it (decoder_compiler.cpp:96-104), or in append mode
-        // at the sequence's length, over the cache including the new token.
-        rc = sfg::launch_attn_decode_paged(
-            b.qkv, qkvw, w->rope_table, append ? -1 : 0, w->k_pool, w->v_pool, w->page_table,
-            append ? io->seq_lens : nullptr, d->context, append ? 1 : 0,
-            b.attn, act, d->batch, d->query_heads, d->kv_heads, D, d->page_tokens, d->pages_per_seq,
-            d->num_pages, splits, scale, b.attn_ws, s,
-            io->stage_events ? static_cast<hipEvent_t>(io->stage_events[SFG_MARK_ATTN_MAIN]) : nullptr);
+        // at the true positions, over the cache including the new tokens.
+        hipEvent_t mid = io->stage_events ? static_cast<hipEvent_t>(io->stage_events[SFG_MARK_ATTN_MAIN]) : nullptr;
+        if (plan.mfma) {
+            rc = sfg::launch_attn_decode_paged(
+                b.qkv, qkvw, w->rope_table, append ? -1 : 0, static_cast<const uint16_t*>(w->k_pool),
+                static_cast<const uint16_t*>(w->v_pool), w->page_table, append ? io->seq_lens : nullptr,
+                d->context, append ? 1 : 0, b.attn, act, d->batch, d->query_heads, d->kv_heads, D,
+                d->page_tokens, d->pages_per_seq, d->num_pages, plan.splits, scale, b.attn_ws, s, mid);
+        } else {
+            // any head_dim / page size / step length / pool dtype: query row i
+            // of a sequence sees key j <= keys - S + i (attention_compiler.cpp:68-72)
+            sfg::PagedRowsLaunch a{};
+            a.q = b.qkv; a.q_stride_b = S * qkvw; a.q_stride_i = qkvw; a.q_stride_h = D;
+            a.rope = w->rope_table; a.rope_rows = static_cast<int>(append ? capacity : S);
+            a.rope_pos = append ? -1 : 0;
+            a.k_pool = w->k_pool; a.v_pool = w->v_pool; a.kv_dtype = act;
+            a.page_table = w->page_table; a.seq_lens = append ? io->seq_lens : nullptr;
+            a.max_context = d->context; a.len_extra = append ? static_cast<int>(S) : 0;
+            a.out = b.attn; a.out_dtype = act;
+            a.out_stride_b = S * H; a.out_stride_i = H; a.out_stride_h = D;
+            a.batch = d->batch; a.q_heads = d->query_heads; a.kv_heads = d->kv_heads; a.seq_q = S;
+            a.head_dim = D; a.page_tokens = d->page_tokens; a.pages_per_seq = d->pages_per_seq;
+            a.num_pages = d->num_pages; a.splits = plan.splits; a.causal = d->causal; a.scale = scale;
+            a.mid_event = mid;
+            rc = sfg::launch_attn_paged_rows(a, b.attn_ws, s);
+        }
         if (rc != SFG_OK) return fail(rc, "decode attention not lowered (head_dim %lld)", (long long)D);
-        if (append && io->seq_lens)
-            sfg::launch_kv_advance(io->seq_lens, d->batch, 1,
-                                   static_cast<int64_t>(d->pages_per_seq) * d->page_tokens, s);
+        if (append && io->seq_lens) sfg::launch_kv_advance(io->seq_lens, d->batch, S, capacity, s);
     } else {
         if (act == SFG_F32) {
-            if (D > 128) return fail(SFG_ERR_UNSUPPORTED, "fp32 attention head_dim > 128");
-            sfg::launch_attn_prefill_f32(static_cast<const float*>(b.q), static_cast<const float*>(b.k),
-                                         static_cast<const float*>(b.v), b.attn, act, d->batch,
-                                         d->query_heads, d->kv_heads, d->sequence, d->sequence, D,
-                                         d->causal, scale, s);
+            rc = sfg::launch_attn_prefill_f32(static_cast<const float*>(b.q), static_cast<const float*>(b.k),
+                                              static_cast<const float*>(b.v), b.attn, act, d->batch,
+                                              d->query_heads, d->kv_heads, d->sequence, d->sequence, D,
+                                              d->causal, scale, s);
+            if (rc != SFG_OK) return fail(rc, "fp32 attention head_dim %lld not lowered", (long long)D);
         } else if (vt) {
             rc = sfg::launch_attn_prefill_vt(static_cast<const uint16_t*>(b.q),
                                              static_cast<const uint16_t*>(b.k),
@@ -982,9 +1171,8 @@ int sfg_hip_decoder_layer_v1(const sfg_layer_desc* d, const sfg_layer_weights* w
         if (rc != SFG_OK) return fail(rc, "MoE dispatch not lowered");
         mk.mark(SFG_MARK_ROUTE);
         const float* route_w = d->use_routing_trace ? io->trace_weights : b.wts;
-        rc = moe_experts(static_cast<const uint16_t*>(b.xn), b.offsets, b.token_ids, w->w13, w->s13,
-                         w->w2, w->s2, wdt, d->weight_layout, static_cast<uint16_t*>(b.act), b.y, rows,
-                         H, I, E, K, d->gemm_tile, s);
+        rc = moe_experts(b.xn, act, b.offsets, b.token_ids, w->w13, w->s13, w->w2, w->s2, wdt,
+                         d->weight_layout, b.act, b.y, rows, H, I, E, K, d->gemm_tile, s);
         if (rc != SFG_OK) return rc;
         mk.mark(SFG_MARK_FFN_UP);
         sfg::launch_moe_combine(b.y, b.position, route_w, b.r1, io->out, rows, H, K, s);

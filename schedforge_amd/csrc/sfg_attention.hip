@@ -1,8 +1,9 @@
 // sfg_attention.hip -- GQA attention for gfx950.
 //
-//  * attn_prefill_f32_kernel: fp32 online softmax (attention_compiler.cpp:286-377),
+//  * attn_prefill_rows_kernel: online softmax (attention_compiler.cpp:286-377),
 //    one wave per query row, 64 keys per step (one per lane), values
-//    accumulated with the wave owning the head dimension.
+//    accumulated with the wave owning the head dimension (up to 256): the
+//    fp32 path, and bf16 head dims the MFMA kernels do not lower.
 //  * attn_prefill_bf16_kernel: IO-aware flash prefill on v_mfma_f32_32x32x16_bf16.
 //    A workgroup owns 128 query rows of one (batch, head); each wave 32 rows.
 //    Scores are formed transposed, S^T = K Q^T, so lane l owns query row
@@ -26,35 +27,44 @@
 namespace sfg {
 
 // ===========================================================================
-// fp32 prefill
+// Row-per-wave prefill, any head_dim up to kRowMaxD: the fp32 path, and bf16
+// shapes the MFMA kernels do not lower (head_dim other than 64 / 128).
 // ===========================================================================
-template <typename OutT>
-__global__ __launch_bounds__(256) void attn_prefill_f32_kernel(
-    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+constexpr int kRowMaxD = 256;
+
+template <typename InT>
+__device__ __forceinline__ float in_f32(const InT* p, int64_t i) {
+    if constexpr (sizeof(InT) == 4) return p[i];
+    else return bf16_to_f32(p[i]);
+}
+
+template <typename InT, typename OutT>
+__global__ __launch_bounds__(256) void attn_prefill_rows_kernel(
+    const InT* __restrict__ q, const InT* __restrict__ k, const InT* __restrict__ v,
     OutT* __restrict__ out, int q_heads, int kv_heads, int seq_q, int seq_kv, int head_dim,
     int causal, float scale) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int qi = blockIdx.x * 4 + wave;
     const int h = blockIdx.y, b = blockIdx.z;
-    __shared__ float sq[4][128];
+    __shared__ float sq[4][kRowMaxD];
     if (qi >= seq_q) return;
     const int kvh = h * kv_heads / q_heads;
-    const float* qr = q + ((static_cast<int64_t>(b) * q_heads + h) * seq_q + qi) * head_dim;
-    for (int d = lane; d < head_dim; d += 64) sq[wave][d] = qr[d];
+    const InT* qr = q + ((static_cast<int64_t>(b) * q_heads + h) * seq_q + qi) * head_dim;
+    for (int d = lane; d < head_dim; d += 64) sq[wave][d] = in_f32(qr, d);
     __builtin_amdgcn_wave_barrier();
-    const float* kb = k + (static_cast<int64_t>(b) * kv_heads + kvh) * seq_kv * head_dim;
-    const float* vb = v + (static_cast<int64_t>(b) * kv_heads + kvh) * seq_kv * head_dim;
+    const InT* kb = k + (static_cast<int64_t>(b) * kv_heads + kvh) * seq_kv * head_dim;
+    const InT* vb = v + (static_cast<int64_t>(b) * kv_heads + kvh) * seq_kv * head_dim;
     const int limit = causal ? (seq_kv - seq_q + qi) : (seq_kv - 1);
     float m = -INFINITY, l = 0.f;
-    float acc0 = 0.f, acc1 = 0.f;  // dims lane, lane + 64
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};  // dims lane + 64 r
     for (int base = 0; base <= limit && base < seq_kv; base += 64) {
         const int j = base + lane;
         float s = -INFINITY;
         if (j <= limit && j < seq_kv) {
-            const float* kr = kb + static_cast<int64_t>(j) * head_dim;
+            const InT* kr = kb + static_cast<int64_t>(j) * head_dim;
             float dot = 0.f;
-            for (int d = 0; d < head_dim; ++d) dot = fmaf(sq[wave][d], kr[d], dot);
+            for (int d = 0; d < head_dim; ++d) dot = fmaf(sq[wave][d], in_f32(kr, d), dot);
             s = dot * scale;
         }
         const float mx = wave_max(s);
@@ -62,43 +72,55 @@ __global__ __launch_bounds__(256) void attn_prefill_f32_kernel(
         const float alpha = (m == -INFINITY) ? 0.f : expf(m - m_new);
         const float p = (s == -INFINITY) ? 0.f : expf(s - m_new);
         l = l * alpha + wave_sum(p);
-        acc0 *= alpha;
-        acc1 *= alpha;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] *= alpha;
         const int count = min(64, min(limit, seq_kv - 1) - base + 1);
         for (int t = 0; t < count; ++t) {
             const float pt = __shfl(p, t, 64);
-            const float* vr = vb + static_cast<int64_t>(base + t) * head_dim;
-            if (lane < head_dim) acc0 = fmaf(pt, vr[lane], acc0);
-            if (lane + 64 < head_dim) acc1 = fmaf(pt, vr[lane + 64], acc1);
+            const InT* vr = vb + static_cast<int64_t>(base + t) * head_dim;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                if (lane + 64 * r < head_dim) acc[r] = fmaf(pt, in_f32(vr, lane + 64 * r), acc[r]);
         }
         m = m_new;
     }
     const int64_t row = static_cast<int64_t>(b) * seq_q + qi;
     OutT* orow = out + row * (static_cast<int64_t>(q_heads) * head_dim) + h * head_dim;
-    if (lane < head_dim) {
-        const float o = acc0 / l;
-        if constexpr (sizeof(OutT) == 4) orow[lane] = o; else orow[lane] = f32_to_bf16(o);
-    }
-    if (lane + 64 < head_dim) {
-        const float o = acc1 / l;
-        if constexpr (sizeof(OutT) == 4) orow[lane + 64] = o; else orow[lane + 64] = f32_to_bf16(o);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int d = lane + 64 * r;
+        if (d < head_dim) {
+            const float o = acc[r] / l;
+            if constexpr (sizeof(OutT) == 4) orow[d] = o; else orow[d] = f32_to_bf16(o);
+        }
     }
 }
 
-void launch_attn_prefill_f32(const float* q, const float* k, const float* v, void* out,
-                             int out_dtype, int64_t batch, int64_t q_heads, int64_t kv_heads,
-                             int64_t seq_q, int64_t seq_kv, int64_t head_dim, int causal,
-                             float scale, hipStream_t stream) {
+template <typename InT>
+static void launch_prefill_rows(const InT* q, const InT* k, const InT* v, void* out, int out_dtype,
+                                int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t seq_q,
+                                int64_t seq_kv, int64_t head_dim, int causal, float scale,
+                                hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>((seq_q + 3) / 4), static_cast<unsigned>(q_heads),
                     static_cast<unsigned>(batch));
     if (out_dtype == SFG_F32)
-        attn_prefill_f32_kernel<float><<<grid, 256, 0, stream>>>(
+        attn_prefill_rows_kernel<InT, float><<<grid, 256, 0, stream>>>(
             q, k, v, static_cast<float*>(out), q_heads, kv_heads, seq_q, seq_kv, head_dim, causal,
             scale);
     else
-        attn_prefill_f32_kernel<uint16_t><<<grid, 256, 0, stream>>>(
+        attn_prefill_rows_kernel<InT, uint16_t><<<grid, 256, 0, stream>>>(
             q, k, v, static_cast<uint16_t*>(out), q_heads, kv_heads, seq_q, seq_kv, head_dim,
             causal, scale);
+}
+
+int launch_attn_prefill_f32(const float* q, const float* k, const float* v, void* out,
+                            int out_dtype, int64_t batch, int64_t q_heads, int64_t kv_heads,
+                            int64_t seq_q, int64_t seq_kv, int64_t head_dim, int causal,
+                            float scale, hipStream_t stream) {
+    if (head_dim > kRowMaxD) return SFG_ERR_UNSUPPORTED;
+    launch_prefill_rows(q, k, v, out, out_dtype, batch, q_heads, kv_heads, seq_q, seq_kv, head_dim,
+                        causal, scale, stream);
+    return SFG_OK;
 }
 
 // ===========================================================================
@@ -281,7 +303,13 @@ int launch_attn_prefill_bf16(const uint16_t* q, const uint16_t* k, const uint16_
                              int out_dtype, int64_t batch, int64_t q_heads, int64_t kv_heads,
                              int64_t seq_q, int64_t seq_kv, int64_t head_dim, int causal,
                              float scale, hipStream_t stream) {
-    if (head_dim != 128 && head_dim != 64) return SFG_ERR_UNSUPPORTED;
+    if (head_dim != 128 && head_dim != 64) {
+        // other head dims: the row-per-wave kernel on the bf16 operands
+        if (head_dim > kRowMaxD) return SFG_ERR_UNSUPPORTED;
+        launch_prefill_rows(q, k, v, out, out_dtype, batch, q_heads, kv_heads, seq_q, seq_kv,
+                            head_dim, causal, scale, stream);
+        return SFG_OK;
+    }
     const float scale_log2 = scale * kLog2e;
     const dim3 grid(static_cast<unsigned>((seq_q + kFaBM - 1) / kFaBM),
                     static_cast<unsigned>(q_heads), static_cast<unsigned>(batch));
@@ -608,7 +636,7 @@ int launch_attn_prefill_vt(const uint16_t* q, const uint16_t* k, const uint16_t*
     a.ld_vt = static_cast<int>(ld_vt); a.causal = causal;
     a.nqb = static_cast<int>((seq_q + bm - 1) / bm);
     a.scale_log2 = scale * kLog2e;
-    a.xcds = device_xcds();
+    a.xcds = device_xcds(stream);
     const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.nqb) * q_heads * batch));
     if (waves == 8) attn_prefill_fa2_kernel<8><<<grid, 512, 0, stream>>>(a);
     else attn_prefill_fa2_kernel<4><<<grid, 256, 0, stream>>>(a);
@@ -630,7 +658,6 @@ int launch_attn_prefill_vt(const uint16_t* q, const uint16_t* k, const uint16_t*
 // query per lane: the online softmax needs only a 4-lane max per page and a
 // per-lane rescale.
 // ===========================================================================
-constexpr int kKvD = 128;  // head_dim of the append / gather kernels
 constexpr int kPageTok = 16;
 
 typedef short short4v __attribute__((ext_vector_type(4)));
@@ -917,6 +944,12 @@ size_t decode_workspace_bytes(int64_t batch, int64_t q_heads, int64_t head_dim, 
     return ml + acc;
 }
 
+bool decode_mfma_supported(int kv_dtype, int64_t head_dim, int64_t page_tokens, int64_t group,
+                           int64_t seq_q) {
+    return kv_dtype == SFG_BF16 && (head_dim == 128 || head_dim == 64) && page_tokens == kPageTok &&
+           seq_q == 1 && (group == 1 || group == 2 || group == 4 || group == 8 || group == 16);
+}
+
 int launch_attn_decode_paged(const float* q, int64_t q_row_stride, const float* rope, int rope_pos,
                              const uint16_t* k_pool, const uint16_t* v_pool,
                              const int32_t* page_table, const int32_t* seq_lens, int64_t max_context,
@@ -977,48 +1010,290 @@ int launch_attn_decode_paged(const float* q, int64_t q_row_stride, const float* 
 }
 
 // ===========================================================================
+// Generic paged attention: any head_dim up to kRowMaxD, any page size, seq_q
+// >= 1 new query rows per sequence under the causal offset j <= len - seq_q +
+// i (attention_compiler.cpp:68-72), fp32 or bf16 pools; the decode path for
+// the shapes the MFMA split kernel does not lower (fp32 caches, head dims
+// other than 64 / 128, pages other than 16 tokens, more than one new token,
+// GQA groups above 16).  One wave per (sequence, query row, query head,
+// split): lane j scores key j of each 64-key chunk against the query held in
+// LDS (one sequential fp32 FMA chain over the head dimension), then the wave
+// accumulates p V with lane d owning dims d, d + 64, ... (online softmax,
+// attention_compiler.cpp:102-112).  With more than one split each wave leaves
+// its (m, l, acc) partial and attn_combine_rows_kernel merges them
+// (merge_online, attention_compiler.cpp:132-145).  Q and the output are
+// addressed by (batch, row, head) element strides: head-major [B][Hq][Sq][D]
+// (the reference's attention layout) or merged rows [B][Sq][Hq][D]
+// (merge_attention's, decoder_compiler.cpp:150-174).
+// ===========================================================================
+struct RowStrides {
+    int64_t b, i, h;  // element strides of batch, query row and head; dims contiguous
+    __device__ int64_t at(int bb, int ii, int hh) const {
+        return bb * b + ii * i + static_cast<int64_t>(hh) * h;
+    }
+};
+
+struct PagedRowsArgs {
+    const float* q; RowStrides qs;
+    const float2* rope; int rope_rows;      // optional [rope_rows][D/2] (cos, sin)
+    int rope_pos;                           // >= 0: row i rotates at rope_pos + i; < 0: at seq_lens[b] + i
+    const void* k_pool; const void* v_pool; // K [page][Hkv][pt][D], V [page][Hkv][D][pt]
+    const int32_t* page_table; const int32_t* seq_lens;
+    int uniform_len, len_extra;             // keys: (seq_lens ? seq_lens[b] : uniform_len) + len_extra
+    void* out; int out_f32; RowStrides os;
+    float* part_ml; float* part_acc;
+    int q_heads, kv_heads, seq_q, head_dim, page_tokens, pages_per_seq, num_pages, splits, causal;
+    float scale;
+};
+
+template <typename KvT>
+__device__ __forceinline__ float kv_f32(const KvT* p, int64_t i) {
+    if constexpr (sizeof(KvT) == 4) return p[i];
+    else return bf16_to_f32(p[i]);
+}
+
+template <typename KvT>
+__global__ __launch_bounds__(64) void attn_paged_rows_kernel(PagedRowsArgs p) {
+    const int lane = threadIdx.x;
+    const int slot = blockIdx.x;  // (b seq_q + i) q_heads + h
+    const int split = blockIdx.y;
+    const int h = slot % p.q_heads;
+    const int bi = slot / p.q_heads;
+    const int i = bi % p.seq_q, b = bi / p.seq_q;
+    const int kvh = h * p.kv_heads / p.q_heads;
+    const int D = p.head_dim, pt = p.page_tokens;
+    const int capacity = p.pages_per_seq * pt;
+    const int len0 = p.seq_lens ? p.seq_lens[b] : p.uniform_len;
+    const int len = min(len0 + p.len_extra, capacity);
+    const int kend = max(p.causal ? min(len, len - p.seq_q + i + 1) : len, 0);
+    const int k0 = static_cast<int>(static_cast<int64_t>(kend) * split / p.splits);
+    const int k1 = static_cast<int>(static_cast<int64_t>(kend) * (split + 1) / p.splits);
+
+    __shared__ float sq[kRowMaxD];
+    const float* qr = p.q + p.qs.at(b, i, h);
+    for (int d = lane; d < D; d += 64) sq[d] = qr[d];
+    __syncthreads();
+    if (p.rope && p.rope_rows > 0) {
+        const int pos = min(max((p.rope_pos >= 0 ? p.rope_pos : len0) + i, 0), p.rope_rows - 1);
+        for (int t = lane; t < D / 2; t += 64) {
+            const float2 cs = p.rope[static_cast<int64_t>(pos) * (D / 2) + t];
+            const float e = sq[2 * t], o = sq[2 * t + 1];
+            sq[2 * t] = e * cs.x - o * cs.y;
+            sq[2 * t + 1] = e * cs.y + o * cs.x;
+        }
+        __syncthreads();
+    }
+    const KvT* kpool = static_cast<const KvT*>(p.k_pool);
+    const KvT* vpool = static_cast<const KvT*>(p.v_pool);
+    const int32_t* table = p.page_table + static_cast<int64_t>(b) * p.pages_per_seq;
+    float m = -INFINITY, l = 0.f;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int base = k0; base < k1; base += 64) {
+        const int j = base + lane;
+        float s = -INFINITY;
+        int page = -1;
+        if (j < k1) {
+            const int id = table[j / pt];
+            if (id >= 0 && id < p.num_pages) {
+                page = id;
+                const KvT* kr = kpool + ((static_cast<int64_t>(id) * p.kv_heads + kvh) * pt + j % pt) * D;
+                float dot = 0.f;
+                for (int d = 0; d < D; ++d) dot = fmaf(sq[d], kv_f32(kr, d), dot);
+                s = dot * p.scale;
+            }
+        }
+        const float m_new = fmaxf(m, wave_max(s));
+        if (m_new == -INFINITY) continue;  // wave-uniform: nothing visible in this chunk yet
+        const float alpha = m == -INFINITY ? 0.f : expf(m - m_new);
+        const float pr = s == -INFINITY ? 0.f : expf(s - m_new);
+        l = l * alpha + wave_sum(pr);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] *= alpha;
+        const int count = min(64, k1 - base);
+        for (int t = 0; t < count; ++t) {
+            const float pt_t = __shfl(pr, t, 64);
+            const int pg = __shfl(page, t, 64);
+            if (pg < 0) continue;  // wave-uniform
+            const int jt = base + t;
+            const KvT* vb = vpool + (static_cast<int64_t>(pg) * p.kv_heads + kvh) * D * pt + jt % pt;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int d = lane + 64 * r;
+                if (d < D) acc[r] = fmaf(pt_t, kv_f32(vb, static_cast<int64_t>(d) * pt), acc[r]);
+            }
+        }
+        m = m_new;
+    }
+    if (p.splits == 1) {
+        const int64_t o0 = p.os.at(b, i, h);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int d = lane + 64 * r;
+            if (d >= D) continue;
+            const float o = acc[r] / l;  // no visible key: 0 / 0, as the reference's softmax gives
+            if (p.out_f32) static_cast<float*>(p.out)[o0 + d] = o;
+            else static_cast<uint16_t*>(p.out)[o0 + d] = f32_to_bf16(o);
+        }
+        return;
+    }
+    const int64_t part = static_cast<int64_t>(slot) * p.splits + split;
+    if (lane == 0) {
+        p.part_ml[2 * part] = m;
+        p.part_ml[2 * part + 1] = l;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int d = lane + 64 * r;
+        if (d < D) p.part_acc[part * D + d] = acc[r];
+    }
+}
+
+// merge_online over a row's splits: weights e^(m_s - M), output sum / L.
+__global__ __launch_bounds__(64) void attn_combine_rows_kernel(const float* __restrict__ part_ml,
+                                                              const float* __restrict__ part_acc,
+                                                              void* out, int out_f32, RowStrides os,
+                                                              int q_heads, int seq_q, int head_dim,
+                                                              int splits) {
+    const int lane = threadIdx.x;
+    const int64_t slot = blockIdx.x;  // (b seq_q + i) q_heads + h
+    const int h = static_cast<int>(slot % q_heads);
+    const int bi = static_cast<int>(slot / q_heads);
+    const int64_t o0 = os.at(bi / seq_q, bi % seq_q, h);
+    const int D = head_dim;
+    float M = -INFINITY;
+    for (int s = 0; s < splits; ++s) M = fmaxf(M, part_ml[2 * (slot * splits + s)]);
+    float L = 0.f;
+    float o[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < splits; ++s) {
+        const int64_t part = slot * splits + s;
+        const float ms = part_ml[2 * part];
+        if (ms == -INFINITY) continue;
+        const float w = expf(ms - M);
+        L = fmaf(part_ml[2 * part + 1], w, L);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int d = lane + 64 * r;
+            if (d < D) o[r] = fmaf(w, part_acc[part * D + d], o[r]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int d = lane + 64 * r;
+        if (d >= D) continue;
+        const float v = o[r] / L;
+        if (out_f32) static_cast<float*>(out)[o0 + d] = v;
+        else static_cast<uint16_t*>(out)[o0 + d] = f32_to_bf16(v);
+    }
+}
+
+int paged_rows_split_count(int64_t rows, int64_t max_keys, int32_t requested) {
+    if (requested > 0) return static_cast<int>(requested < max_keys ? requested : (max_keys > 0 ? max_keys : 1));
+    // >= 1024 waves while every split keeps >= 256 keys
+    int s = 1;
+    while (rows * s < 1024 && max_keys / (s * 2) >= 256) s *= 2;
+    return s;
+}
+
+size_t paged_rows_workspace_bytes(int64_t rows, int64_t head_dim, int splits) {
+    if (splits <= 1) return 0;
+    const size_t parts = static_cast<size_t>(rows) * splits;
+    return ((parts * 2 * sizeof(float) + 255) / 256) * 256 + ((parts * head_dim * sizeof(float) + 255) / 256) * 256;
+}
+
+int launch_attn_paged_rows(const PagedRowsLaunch& a, void* workspace, hipStream_t stream) {
+    if (a.head_dim < 1 || a.head_dim > kRowMaxD || a.page_tokens < 1 || a.splits < 1 || a.seq_q < 1)
+        return SFG_ERR_UNSUPPORTED;
+    if (a.kv_dtype != SFG_F32 && a.kv_dtype != SFG_BF16) return SFG_ERR_UNSUPPORTED;
+    PagedRowsArgs p{};
+    p.q = a.q; p.qs = RowStrides{a.q_stride_b, a.q_stride_i, a.q_stride_h};
+    p.os = RowStrides{a.out_stride_b, a.out_stride_i, a.out_stride_h};
+    p.rope = reinterpret_cast<const float2*>(a.rope); p.rope_rows = a.rope_rows; p.rope_pos = a.rope_pos;
+    p.k_pool = a.k_pool; p.v_pool = a.v_pool;
+    p.page_table = a.page_table; p.seq_lens = a.seq_lens;
+    p.uniform_len = static_cast<int>(a.max_context); p.len_extra = a.len_extra;
+    p.out = a.out; p.out_f32 = a.out_dtype == SFG_F32;
+    const int64_t rows = a.batch * a.seq_q * a.q_heads;
+    if (a.splits > 1) {
+        const size_t parts = static_cast<size_t>(rows) * a.splits;
+        p.part_ml = static_cast<float*>(workspace);
+        p.part_acc = reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                              ((parts * 2 * sizeof(float) + 255) / 256) * 256);
+    }
+    p.q_heads = static_cast<int>(a.q_heads); p.kv_heads = static_cast<int>(a.kv_heads);
+    p.seq_q = static_cast<int>(a.seq_q); p.head_dim = static_cast<int>(a.head_dim);
+    p.page_tokens = static_cast<int>(a.page_tokens); p.pages_per_seq = static_cast<int>(a.pages_per_seq);
+    p.num_pages = static_cast<int>(a.num_pages); p.splits = a.splits; p.causal = a.causal;
+    p.scale = a.scale;
+    const dim3 grid(static_cast<unsigned>(rows), static_cast<unsigned>(a.splits));
+    if (a.kv_dtype == SFG_F32) attn_paged_rows_kernel<float><<<grid, 64, 0, stream>>>(p);
+    else attn_paged_rows_kernel<uint16_t><<<grid, 64, 0, stream>>>(p);
+    if (a.mid_event) (void)hipEventRecord(a.mid_event, stream);
+    if (a.splits > 1)
+        attn_combine_rows_kernel<<<dim3(static_cast<unsigned>(rows)), 64, 0, stream>>>(
+            p.part_ml, p.part_acc, a.out, p.out_f32, p.os, p.q_heads, p.seq_q, p.head_dim, a.splits);
+    return SFG_OK;
+}
+
+// ===========================================================================
 // Paged KV cache maintenance: append_paged_kv / gather_paged_kv
 // (next_milestones.cpp:486-524, 554-581) on the device pools
-// K [page][Hkv][16][128], V [page][Hkv][128][16] (bf16) through per-sequence
-// page tables [B][pages_per_seq].  Pages are assigned by the host (the plan's
-// allocator, as the reference's free list); the kernels only move data and
-// skip any position past the table's capacity or any page id outside the pool.
+// K [page][Hkv][page_tokens][D], V [page][Hkv][D][page_tokens] (fp32 or bf16)
+// through per-sequence page tables [B][pages_per_seq].  Pages are assigned by
+// the host (the plan's allocator, as the reference's free list); the kernels
+// only move data and skip any position past the table's capacity or any page
+// id outside the pool.  Any head_dim, any page size.
 // ===========================================================================
 struct KvAppendArgs {
     const void* keys; const void* values; int src_f32;
     int64_t sb, sh, st;           // source element strides: batch, kv head, token (dims contiguous)
-    const float2* rope;           // [positions][64] (cos, sin) or null: keys rotated at their position
-    uint16_t* k_pool; uint16_t* v_pool;
+    const float2* rope;           // [positions][D/2] (cos, sin) or null: keys rotated at their position
+    void* k_pool; void* v_pool;
     const int32_t* page_table; const int32_t* seq_lens; int start;
-    int kv_heads, pages_per_seq, num_pages;
+    int kv_heads, head_dim, page_tokens, pages_per_seq, num_pages;
 };
 
-__device__ __forceinline__ float2 load_pair(const void* base, int f32, int64_t idx) {
-    if (f32) return *reinterpret_cast<const float2*>(static_cast<const float*>(base) + idx);
-    const uint32_t w = *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(base) + idx);
-    return make_float2(bf16_to_f32(static_cast<uint16_t>(w & 0xFFFFu)), bf16_to_f32(static_cast<uint16_t>(w >> 16)));
+__device__ __forceinline__ float load_src(const void* base, int f32, int64_t idx) {
+    if (f32) return static_cast<const float*>(base)[idx];
+    return bf16_to_f32(static_cast<const uint16_t*>(base)[idx]);
 }
 
-// One wave per (token, kv_head, sequence); lane = dim pair (2 lane, 2 lane + 1).
+template <typename KvT>
+__device__ __forceinline__ KvT to_pool(float v) {
+    if constexpr (sizeof(KvT) == 4) return v;
+    else return f32_to_bf16(v);
+}
+
+// One wave per (token, kv_head, sequence); lane d owns dims d, d + 64, ...
+// (with RoPE: pairs (2t, 2t + 1) for t = lane, lane + 64, ...).
+template <typename KvT>
 __global__ __launch_bounds__(64) void kv_append_kernel(KvAppendArgs a) {
     const int t = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-    const int pair = threadIdx.x;
+    const int lane = threadIdx.x;
+    const int D = a.head_dim, pt = a.page_tokens;
     const int pos = (a.seq_lens ? a.seq_lens[b] : a.start) + t;
-    if (pos < 0 || pos >= a.pages_per_seq * kPageTok) return;
-    const int phys = a.page_table[static_cast<int64_t>(b) * a.pages_per_seq + pos / kPageTok];
+    if (pos < 0 || pos >= a.pages_per_seq * pt) return;
+    const int phys = a.page_table[static_cast<int64_t>(b) * a.pages_per_seq + pos / pt];
     if (phys < 0 || phys >= a.num_pages) return;
-    const int slot = pos % kPageTok;
-    const int64_t src = b * a.sb + h * a.sh + t * a.st + 2 * pair;
-    float2 kv = load_pair(a.keys, a.src_f32, src);
-    if (a.rope) {
-        const float2 cs = a.rope[static_cast<int64_t>(pos) * (kKvD / 2) + pair];
-        kv = make_float2(kv.x * cs.x - kv.y * cs.y, kv.x * cs.y + kv.y * cs.x);
-    }
+    const int slot = pos % pt;
+    const int64_t src = b * a.sb + h * a.sh + t * a.st;
     const int64_t blk = static_cast<int64_t>(phys) * a.kv_heads + h;
-    *reinterpret_cast<uint32_t*>(a.k_pool + (blk * kPageTok + slot) * kKvD + 2 * pair) = pack_bf16x2(kv.x, kv.y);
-    const float2 vv = load_pair(a.values, a.src_f32, src);
-    a.v_pool[(blk * kKvD + 2 * pair) * kPageTok + slot] = f32_to_bf16(vv.x);
-    a.v_pool[(blk * kKvD + 2 * pair + 1) * kPageTok + slot] = f32_to_bf16(vv.y);
+    KvT* kdst = static_cast<KvT*>(a.k_pool) + (blk * pt + slot) * D;
+    KvT* vdst = static_cast<KvT*>(a.v_pool) + blk * D * pt + slot;
+    if (a.rope) {
+        for (int q = lane; q < D / 2; q += 64) {
+            const float e = load_src(a.keys, a.src_f32, src + 2 * q);
+            const float o = load_src(a.keys, a.src_f32, src + 2 * q + 1);
+            const float2 cs = a.rope[static_cast<int64_t>(pos) * (D / 2) + q];
+            kdst[2 * q] = to_pool<KvT>(e * cs.x - o * cs.y);
+            kdst[2 * q + 1] = to_pool<KvT>(e * cs.y + o * cs.x);
+        }
+        // an odd head_dim's last dimension is not rotated (apply_rope stops at d + 1 < D)
+        if ((D & 1) && lane == 0) kdst[D - 1] = to_pool<KvT>(load_src(a.keys, a.src_f32, src + D - 1));
+    } else {
+        for (int d = lane; d < D; d += 64) kdst[d] = to_pool<KvT>(load_src(a.keys, a.src_f32, src + d));
+    }
+    for (int d = lane; d < D; d += 64)
+        vdst[static_cast<int64_t>(d) * pt] = to_pool<KvT>(load_src(a.values, a.src_f32, src + d));
 }
 
 // Lengths advance by the appended tokens and saturate at the capacity: tokens
@@ -1030,47 +1305,49 @@ __global__ __launch_bounds__(256) void kv_advance_kernel(int32_t* seq_lens, int 
     if (b < batch) seq_lens[b] = min(seq_lens[b] + tokens, capacity);
 }
 
-// gather_paged_kv: pools -> keys / values [B][Hkv][length][128] fp32 (bf16 widened exactly).
-__global__ __launch_bounds__(64) void kv_gather_kernel(const uint16_t* __restrict__ k_pool,
-                                                       const uint16_t* __restrict__ v_pool,
+// gather_paged_kv: pools -> keys / values [B][Hkv][length][D] fp32 (bf16 widened exactly).
+template <typename KvT>
+__global__ __launch_bounds__(64) void kv_gather_kernel(const KvT* __restrict__ k_pool,
+                                                       const KvT* __restrict__ v_pool,
                                                        const int32_t* __restrict__ page_table,
-                                                       int kv_heads, int pages_per_seq, int num_pages,
-                                                       int length, float* __restrict__ keys,
+                                                       int kv_heads, int head_dim, int page_tokens,
+                                                       int pages_per_seq, int num_pages, int length,
+                                                       float* __restrict__ keys,
                                                        float* __restrict__ values) {
     const int t = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-    const int pair = threadIdx.x;
-    const int phys = page_table[static_cast<int64_t>(b) * pages_per_seq + t / kPageTok];
-    const int64_t dst = ((static_cast<int64_t>(b) * kv_heads + h) * length + t) * kKvD + 2 * pair;
-    float2 kk = make_float2(0.f, 0.f), vv = make_float2(0.f, 0.f);
-    if (phys >= 0 && phys < num_pages) {
-        const int slot = t % kPageTok;
-        const int64_t blk = static_cast<int64_t>(phys) * kv_heads + h;
-        const uint32_t kw = *reinterpret_cast<const uint32_t*>(k_pool + (blk * kPageTok + slot) * kKvD + 2 * pair);
-        kk = make_float2(bf16_to_f32(static_cast<uint16_t>(kw & 0xFFFFu)), bf16_to_f32(static_cast<uint16_t>(kw >> 16)));
-        vv = make_float2(bf16_to_f32(v_pool[(blk * kKvD + 2 * pair) * kPageTok + slot]),
-                         bf16_to_f32(v_pool[(blk * kKvD + 2 * pair + 1) * kPageTok + slot]));
+    const int lane = threadIdx.x;
+    const int D = head_dim, pt = page_tokens;
+    const int phys = page_table[static_cast<int64_t>(b) * pages_per_seq + t / pt];
+    const bool ok = phys >= 0 && phys < num_pages;
+    const int slot = t % pt;
+    const int64_t blk = static_cast<int64_t>(ok ? phys : 0) * kv_heads + h;
+    const int64_t dst = ((static_cast<int64_t>(b) * kv_heads + h) * length + t) * D;
+    for (int d = lane; d < D; d += 64) {
+        keys[dst + d] = ok ? kv_f32(k_pool, (blk * pt + slot) * D + d) : 0.f;
+        values[dst + d] = ok ? kv_f32(v_pool, (blk * D + d) * pt + slot) : 0.f;
     }
-    *reinterpret_cast<float2*>(keys + dst) = kk;
-    *reinterpret_cast<float2*>(values + dst) = vv;
 }
 
 int launch_kv_append(const void* keys, const void* values, int src_dtype, int64_t sb, int64_t sh,
-                     int64_t st, const float* rope, uint16_t* k_pool, uint16_t* v_pool,
+                     int64_t st, const float* rope, void* k_pool, void* v_pool, int pool_dtype,
                      const int32_t* page_table, int32_t* seq_lens, int64_t start, int advance,
                      int64_t batch, int64_t kv_heads, int64_t tokens, int64_t head_dim,
                      int64_t page_tokens, int64_t pages_per_seq, int64_t num_pages,
                      hipStream_t stream) {
-    if (head_dim != kKvD || page_tokens != kPageTok) return SFG_ERR_UNSUPPORTED;
+    if (head_dim < 1 || page_tokens < 1) return SFG_ERR_UNSUPPORTED;
+    if (pool_dtype != SFG_F32 && pool_dtype != SFG_BF16) return SFG_ERR_UNSUPPORTED;
     KvAppendArgs a{};
     a.keys = keys; a.values = values; a.src_f32 = src_dtype == SFG_F32;
     a.sb = sb; a.sh = sh; a.st = st;
     a.rope = reinterpret_cast<const float2*>(rope);
     a.k_pool = k_pool; a.v_pool = v_pool; a.page_table = page_table; a.seq_lens = seq_lens;
     a.start = static_cast<int>(start);
-    a.kv_heads = static_cast<int>(kv_heads); a.pages_per_seq = static_cast<int>(pages_per_seq);
+    a.kv_heads = static_cast<int>(kv_heads); a.head_dim = static_cast<int>(head_dim);
+    a.page_tokens = static_cast<int>(page_tokens); a.pages_per_seq = static_cast<int>(pages_per_seq);
     a.num_pages = static_cast<int>(num_pages);
-    kv_append_kernel<<<dim3(static_cast<unsigned>(tokens), static_cast<unsigned>(kv_heads),
-                            static_cast<unsigned>(batch)), 64, 0, stream>>>(a);
+    const dim3 grid(static_cast<unsigned>(tokens), static_cast<unsigned>(kv_heads), static_cast<unsigned>(batch));
+    if (pool_dtype == SFG_F32) kv_append_kernel<float><<<grid, 64, 0, stream>>>(a);
+    else kv_append_kernel<uint16_t><<<grid, 64, 0, stream>>>(a);
     if (advance && seq_lens)
         kv_advance_kernel<<<dim3(static_cast<unsigned>((batch + 255) / 256)), 256, 0, stream>>>(
             seq_lens, static_cast<int>(batch), static_cast<int>(tokens),
@@ -1084,15 +1361,23 @@ void launch_kv_advance(int32_t* seq_lens, int64_t batch, int64_t tokens, int64_t
         seq_lens, static_cast<int>(batch), static_cast<int>(tokens), static_cast<int>(capacity));
 }
 
-int launch_kv_gather(const uint16_t* k_pool, const uint16_t* v_pool, const int32_t* page_table,
+int launch_kv_gather(const void* k_pool, const void* v_pool, int pool_dtype, const int32_t* page_table,
                      int64_t batch, int64_t kv_heads, int64_t length, int64_t head_dim,
                      int64_t page_tokens, int64_t pages_per_seq, int64_t num_pages, float* keys,
                      float* values, hipStream_t stream) {
-    if (head_dim != kKvD || page_tokens != kPageTok) return SFG_ERR_UNSUPPORTED;
-    kv_gather_kernel<<<dim3(static_cast<unsigned>(length), static_cast<unsigned>(kv_heads),
-                            static_cast<unsigned>(batch)), 64, 0, stream>>>(
-        k_pool, v_pool, page_table, static_cast<int>(kv_heads), static_cast<int>(pages_per_seq),
-        static_cast<int>(num_pages), static_cast<int>(length), keys, values);
+    if (head_dim < 1 || page_tokens < 1) return SFG_ERR_UNSUPPORTED;
+    if (pool_dtype != SFG_F32 && pool_dtype != SFG_BF16) return SFG_ERR_UNSUPPORTED;
+    const dim3 grid(static_cast<unsigned>(length), static_cast<unsigned>(kv_heads), static_cast<unsigned>(batch));
+    const int kvh = static_cast<int>(kv_heads), d = static_cast<int>(head_dim), pt = static_cast<int>(page_tokens);
+    const int pps = static_cast<int>(pages_per_seq), np = static_cast<int>(num_pages), len = static_cast<int>(length);
+    if (pool_dtype == SFG_F32)
+        kv_gather_kernel<float><<<grid, 64, 0, stream>>>(static_cast<const float*>(k_pool),
+                                                         static_cast<const float*>(v_pool), page_table,
+                                                         kvh, d, pt, pps, np, len, keys, values);
+    else
+        kv_gather_kernel<uint16_t><<<grid, 64, 0, stream>>>(static_cast<const uint16_t*>(k_pool),
+                                                            static_cast<const uint16_t*>(v_pool), page_table,
+                                                            kvh, d, pt, pps, np, len, keys, values);
     return SFG_OK;
 }
 

@@ -156,30 +156,38 @@ void launch_rmsnorm(const float* x, const float* w, void* y, int y_dtype, int64_
 
 // ---------------------------------------------------------------------------
 // split_qkv + apply_rope (decoder_compiler.cpp:96-148).  One thread per
-// (row, head-slot, pair): Q heads, then K heads, then V heads of one row.  The
-// rotation uses the host-built table (cos, sin per position and pair), whose
-// float expressions are the reference's, so no device libm enters the angle.
+// (row, head-slot, unit): Q heads, then K heads, then V heads of one row; a
+// unit is the pair (2u, 2u + 1), and for an odd head_dim the last dimension,
+// which apply_rope leaves unrotated (its loop stops at dimension + 1 <
+// head_dim).  The rotation uses the host-built table (cos, sin per position
+// and pair), whose float expressions are the reference's, so no device libm
+// enters the angle.
 // ---------------------------------------------------------------------------
+template <typename OutT>
+__device__ __forceinline__ void store_act(OutT* dst, float v) {
+    if constexpr (sizeof(OutT) == 4) *dst = v;
+    else *dst = f32_to_bf16(v);
+}
+
 template <typename OutT>
 __global__ __launch_bounds__(256) void split_rope_kernel(
     const float* __restrict__ qkv, const float2* __restrict__ table, int batch, int seq,
     int q_heads, int kv_heads, int head_dim, OutT* __restrict__ q, OutT* __restrict__ k,
     OutT* __restrict__ v) {
     const int half = head_dim >> 1;
+    const int units = (head_dim + 1) >> 1;
     const int heads_total = q_heads + 2 * kv_heads;
-    const int64_t total = static_cast<int64_t>(batch) * seq * heads_total * half;
+    const int64_t total = static_cast<int64_t>(batch) * seq * heads_total * units;
     const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (idx >= total) return;
-    const int pair = static_cast<int>(idx % half);
-    const int64_t rest = idx / half;
+    const int unit = static_cast<int>(idx % units);
+    const int64_t rest = idx / units;
     const int slot = static_cast<int>(rest % heads_total);
     const int64_t row = rest / heads_total;
     const int b = static_cast<int>(row / seq);
     const int s = static_cast<int>(row % seq);
-    const int width = heads_total * head_dim;
-    const float2 ev = *reinterpret_cast<const float2*>(qkv + row * width + slot * head_dim +
-                                                       2 * pair);
-    float o0 = ev.x, o1 = ev.y;
+    const int64_t width = static_cast<int64_t>(heads_total) * head_dim;
+    const float* src = qkv + row * width + static_cast<int64_t>(slot) * head_dim + 2 * unit;
     OutT* dst;
     if (slot < q_heads) {
         dst = q + ((static_cast<int64_t>(b) * q_heads + slot) * seq + s) * head_dim;
@@ -191,22 +199,26 @@ __global__ __launch_bounds__(256) void split_rope_kernel(
         dst = v + ((static_cast<int64_t>(b) * kv_heads + (slot - q_heads - kv_heads)) * seq + s) *
                       head_dim;
     }
+    dst += 2 * unit;
+    if (unit == half) {  // odd head_dim: the last dimension is copied as is
+        store_act(dst, src[0]);
+        return;
+    }
+    const float e = src[0], o = src[1];
+    float o0 = e, o1 = o;
     if (slot < q_heads + kv_heads) {
-        const float2 cs = table[static_cast<int64_t>(s) * half + pair];
-        o0 = ev.x * cs.x - ev.y * cs.y;
-        o1 = ev.x * cs.y + ev.y * cs.x;
+        const float2 cs = table[static_cast<int64_t>(s) * half + unit];
+        o0 = e * cs.x - o * cs.y;
+        o1 = e * cs.y + o * cs.x;
     }
-    if constexpr (sizeof(OutT) == 4) {
-        *reinterpret_cast<float2*>(dst + 2 * pair) = make_float2(o0, o1);
-    } else {
-        *reinterpret_cast<uint32_t*>(dst + 2 * pair) = pack_bf16x2(o0, o1);
-    }
+    store_act(dst, o0);
+    store_act(dst + 1, o1);
 }
 
 void launch_split_rope(const float* qkv, const float* table, int64_t batch, int64_t seq,
                        int64_t q_heads, int64_t kv_heads, int64_t head_dim, void* q, void* k,
                        void* v, int out_dtype, hipStream_t stream) {
-    const int64_t total = batch * seq * (q_heads + 2 * kv_heads) * (head_dim / 2);
+    const int64_t total = batch * seq * (q_heads + 2 * kv_heads) * ((head_dim + 1) / 2);
     const dim3 grid(static_cast<unsigned>((total + 255) / 256));
     const float2* t = reinterpret_cast<const float2*>(table);
     if (out_dtype == SFG_F32)

@@ -1925,33 +1925,73 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
 }
 
 // ===========================================================================
-// fp32 GEMM (VALU): 64x64 tile, BK 16, 256 threads x (4 rows x 4 cols).
+// VALU GEMM: 64x64 tile, BK 16, 256 threads x (4 rows x 4 cols), one fp32
+// FMA chain per output in k order.  The fp32 path (AT = BT = float), and the
+// fallback for bf16 / int8 products the MFMA kernels do not lower (K not a
+// multiple of their k step, rows not 16-byte aligned): A fp32 or bf16, B fp32,
+// bf16 or int8 with per-channel scales applied after the sum; grouped
+// problems and the dispatch gather as in the tiled kernels.
 // For GLU epilogues the tile covers 32 outputs: thread columns {2t, 2t+1}
 // of the gate block and the same two of the up block.
 // ===========================================================================
-struct F32Args {
-    const float* a; int64_t lda;
-    const float* b; int64_t ldb;
+struct VecArgs {
+    const void* a; int64_t lda; const int32_t* a_rows; int64_t a_rows_limit;
+    const void* b; int64_t ldb; const float* scales;
+    int64_t b_group_stride, s_group_stride;
     void* c; int c_dtype; int64_t ldc;
     const float* residual; int64_t ldr;
     int64_t m, n, k;
+    const int32_t* offsets; int groups;
 };
 
-template <int EPI>
-__global__ __launch_bounds__(256) void gemm_f32_kernel(F32Args p) {
+template <typename T>
+__device__ __forceinline__ float elem_f32(const T* p, int64_t i) {
+    if constexpr (std::is_same_v<T, float>) return p[i];
+    else if constexpr (std::is_same_v<T, int8_t>) return static_cast<float>(p[i]);
+    else return bf16_to_f32(p[i]);
+}
+
+constexpr int kVecTM = 64;
+
+template <typename AT, typename BT, int EPI>
+__global__ __launch_bounds__(256) void gemm_vec_kernel(VecArgs p) {
     constexpr bool kGlu = EpiTraits<EPI>::glu;
     __shared__ float sA[16][64 + 4];
     __shared__ float sB[16][64 + 4];
     const int tid = threadIdx.x;
     const int tx = tid & 15, ty = tid >> 4;
-    const int64_t m0 = static_cast<int64_t>(blockIdx.y) * 64;
+    // Map blockIdx.y to (group, row tile).
+    int g = 0;
+    int64_t rb = 0, re = p.m, mtile = blockIdx.y;
+    if (p.offsets) {
+        int64_t t = blockIdx.y;
+        g = -1;
+        auto bound = [&](int e) { return min(max(static_cast<int64_t>(p.offsets[e]), int64_t(0)), p.m); };
+        for (int e = 0; e < p.groups; ++e) {
+            const int64_t lo = bound(e);
+            const int64_t tiles = (max(bound(e + 1) - lo, int64_t(0)) + kVecTM - 1) / kVecTM;
+            if (t < tiles) { g = e; break; }
+            t -= tiles;
+        }
+        if (g < 0) return;
+        rb = bound(g);
+        re = max(bound(g + 1), rb);
+        mtile = t;
+    }
+    const int64_t m0 = rb + mtile * kVecTM;
+    if (m0 >= re) return;
+    const AT* A = static_cast<const AT*>(p.a);
+    const BT* B = static_cast<const BT*>(p.b) + static_cast<int64_t>(g) * p.b_group_stride;
+    const float* scales = p.scales ? p.scales + static_cast<int64_t>(g) * p.s_group_stride : nullptr;
     const int64_t n0 = static_cast<int64_t>(blockIdx.x) * (kGlu ? 32 : 64);
-    // B tile row -> B matrix row.
+    // B tile row -> B matrix row; valid when its output column is below n.
     auto brow_of = [&](int local) -> int64_t {
         if (kGlu) return local < 32 ? n0 + local : p.n + n0 + local - 32;
         return n0 + local;
     };
-    const int64_t bmax = kGlu ? 2 * p.n : p.n;
+    auto bcol_ok = [&](int local) -> bool {
+        return kGlu ? (local < 32 ? n0 + local : n0 + local - 32) < p.n : n0 + local < p.n;
+    };
     float acc[4][4] = {};
     // thread's 4 B-tile columns
     int bc[4];
@@ -1962,10 +2002,13 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(F32Args p) {
         for (int e = tid; e < 64 * 16; e += 256) {
             const int r = e >> 4, kk = e & 15;
             const int64_t gr = m0 + r, gk = k0 + kk;
-            sA[kk][r] = (gr < p.m && gk < p.k) ? p.a[gr * p.lda + gk] : 0.f;
-            const int64_t br = brow_of(r);
-            const bool bok = (kGlu ? (r < 32 ? n0 + r < p.n : n0 + r - 32 < p.n) : br < bmax) && gk < p.k;
-            sB[kk][r] = bok ? p.b[br * p.ldb + gk] : 0.f;
+            float av = 0.f;
+            if (gr < re && gk < p.k) {
+                const int64_t src = p.a_rows ? p.a_rows[gr] : gr;
+                if (src >= 0 && src < p.a_rows_limit) av = elem_f32(A, src * p.lda + gk);
+            }
+            sA[kk][r] = av;
+            sB[kk][r] = (bcol_ok(r) && gk < p.k) ? elem_f32(B, brow_of(r) * p.ldb + gk) : 0.f;
         }
         __syncthreads();
 #pragma unroll
@@ -1982,27 +2025,67 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(F32Args p) {
         }
         __syncthreads();
     }
+    // per-channel scales of int8 weights (quantized_invoke, next_milestones.cpp:50-69)
+    float sc[4] = {1.f, 1.f, 1.f, 1.f};
+    if (scales) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sc[j] = bcol_ok(bc[j]) ? scales[brow_of(bc[j])] : 1.f;
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int64_t row = m0 + ty * 4 + i;
-        if (row >= p.m) continue;
+        if (row >= re) continue;
         if (kGlu) {
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 const int64_t col = n0 + bc[j];
-                if (col < p.n) store_out(p.c, p.c_dtype, row * p.ldc + col, glu_combine(EPI, acc[i][j], acc[i][j + 2]));
+                if (col < p.n)
+                    store_out(p.c, p.c_dtype, row * p.ldc + col,
+                              glu_combine(EPI, acc[i][j] * sc[j], acc[i][j + 2] * sc[j + 2]));
             }
         } else {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int64_t col = n0 + bc[j];
                 if (col >= p.n) continue;
-                float v = acc[i][j];
+                float v = acc[i][j] * sc[j];
                 if (EPI == SFG_EPI_RESIDUAL) v += p.residual[row * p.ldr + col];
                 store_out(p.c, p.c_dtype, row * p.ldc + col, v);
             }
         }
     }
+}
+
+template <typename AT, typename BT>
+void launch_vec_t(const VecArgs& a, int epi, hipStream_t stream) {
+    const bool glu = epi == SFG_EPI_SWIGLU || epi == SFG_EPI_GLU_SILU_UP;
+    const int64_t row_tiles = a.offsets ? (a.m + kVecTM - 1) / kVecTM + a.groups : (a.m + kVecTM - 1) / kVecTM;
+    const dim3 grid(static_cast<unsigned>((a.n + (glu ? 31 : 63)) / (glu ? 32 : 64)), static_cast<unsigned>(row_tiles));
+    switch (epi) {
+        case SFG_EPI_NONE: gemm_vec_kernel<AT, BT, SFG_EPI_NONE><<<grid, 256, 0, stream>>>(a); break;
+        case SFG_EPI_RESIDUAL: gemm_vec_kernel<AT, BT, SFG_EPI_RESIDUAL><<<grid, 256, 0, stream>>>(a); break;
+        case SFG_EPI_SWIGLU: gemm_vec_kernel<AT, BT, SFG_EPI_SWIGLU><<<grid, 256, 0, stream>>>(a); break;
+        default: gemm_vec_kernel<AT, BT, SFG_EPI_GLU_SILU_UP><<<grid, 256, 0, stream>>>(a); break;
+    }
+}
+
+// The VALU kernel for any NK-layout problem it can read; SFG_ERR_UNSUPPORTED
+// for the QKV-RoPE epilogue and tiled weights.
+int launch_vec(const GemmProblem& p, hipStream_t stream) {
+    if (p.epilogue == kEpiQkvRope || p.b_layout != SFG_LAYOUT_NK) return SFG_ERR_UNSUPPORTED;
+    VecArgs a{};
+    a.a = p.a; a.lda = p.lda; a.a_rows = p.a_rows; a.a_rows_limit = p.a_rows ? p.a_rows_limit : p.m;
+    a.b = p.b; a.ldb = p.ldb; a.scales = p.b_dtype == SFG_I8 ? p.b_scales : nullptr;
+    a.b_group_stride = p.offsets ? p.b_group_stride : 0;
+    a.s_group_stride = p.offsets ? p.s_group_stride : 0;
+    a.c = p.c; a.c_dtype = p.c_dtype; a.ldc = p.ldc;
+    a.residual = p.residual; a.ldr = p.ldr;
+    a.m = p.m; a.n = p.n; a.k = p.k; a.offsets = p.offsets; a.groups = p.offsets ? p.groups : 1;
+    if (p.a_dtype == SFG_F32 && p.b_dtype == SFG_F32) launch_vec_t<float, float>(a, p.epilogue, stream);
+    else if (p.a_dtype == SFG_BF16 && p.b_dtype == SFG_BF16) launch_vec_t<uint16_t, uint16_t>(a, p.epilogue, stream);
+    else if (p.a_dtype == SFG_BF16 && p.b_dtype == SFG_I8) launch_vec_t<uint16_t, int8_t>(a, p.epilogue, stream);
+    else return SFG_ERR_UNSUPPORTED;
+    return SFG_OK;
 }
 
 // ===========================================================================
@@ -2192,32 +2275,22 @@ size_t gemm_workspace_bytes(int64_t m, int64_t n, int64_t k) {
 int launch_gemm(const GemmProblem& problem, void* workspace, size_t workspace_bytes,
                 hipStream_t stream) {
     GemmProblem p = problem;
-    p.xcds = device_xcds();
+    p.xcds = device_xcds(stream);
     const bool glu = is_glu(p.epilogue);
     if (p.epilogue == kEpiQkvRope && !gemm_qkv_rope_supported(p)) return SFG_ERR_UNSUPPORTED;
     if (p.a_dtype == SFG_F32) {
-        if (p.b_dtype != SFG_F32 || p.offsets || p.a_rows || p.b_layout != SFG_LAYOUT_NK)
-            return SFG_ERR_UNSUPPORTED;
-        F32Args a{static_cast<const float*>(p.a), p.lda, static_cast<const float*>(p.b), p.ldb,
-                  p.c, p.c_dtype, p.ldc, p.residual, p.ldr, p.m, p.n, p.k};
-        const dim3 grid(static_cast<unsigned>((p.n + (glu ? 31 : 63)) / (glu ? 32 : 64)),
-                        static_cast<unsigned>((p.m + 63) / 64));
-        switch (p.epilogue) {
-            case SFG_EPI_NONE: gemm_f32_kernel<SFG_EPI_NONE><<<grid, 256, 0, stream>>>(a); break;
-            case SFG_EPI_RESIDUAL: gemm_f32_kernel<SFG_EPI_RESIDUAL><<<grid, 256, 0, stream>>>(a); break;
-            case SFG_EPI_SWIGLU: gemm_f32_kernel<SFG_EPI_SWIGLU><<<grid, 256, 0, stream>>>(a); break;
-            default: gemm_f32_kernel<SFG_EPI_GLU_SILU_UP><<<grid, 256, 0, stream>>>(a); break;
-        }
-        return SFG_OK;
+        if (p.b_dtype != SFG_F32) return SFG_ERR_UNSUPPORTED;
+        return launch_vec(p, stream);
     }
     if (p.a_dtype != SFG_BF16 || (p.b_dtype != SFG_BF16 && p.b_dtype != SFG_I8))
         return SFG_ERR_UNSUPPORTED;
     if (p.b_dtype == SFG_I8 && p.b_scales == nullptr) return SFG_ERR_SHAPE;
-    // every bf16 / int8 kernel reads A and B rows as 16-byte vectors
+    // every bf16 / int8 MFMA kernel reads A and B rows as 16-byte vectors and
+    // steps k by 32: other rows and depths run on the VALU kernel
     const int64_t b_elem = p.b_dtype == SFG_I8 ? 1 : 2;
     if ((reinterpret_cast<uintptr_t>(p.a) & 15) || (reinterpret_cast<uintptr_t>(p.b) & 15) ||
-        (p.lda * 2) % 16 != 0 || (p.ldb * b_elem) % 16 != 0)
-        return SFG_ERR_UNSUPPORTED;
+        (p.lda * 2) % 16 != 0 || (p.ldb * b_elem) % 16 != 0 || p.k % kTK != 0)
+        return launch_vec(p, stream);
     const int groups = p.offsets ? p.groups : 1;
     // 33..64 dense rows: split-K slices when the caller's workspace holds the
     // partial sums (sized by gemm_workspace_bytes).
@@ -2281,7 +2354,6 @@ int launch_gemm(const GemmProblem& problem, void* workspace, size_t workspace_by
         return SFG_OK;
     }
     if (p.b_layout == SFG_LAYOUT_TILED) return SFG_ERR_UNSUPPORTED;  // tiled weights feed the skinny kernel only
-    if (p.k % kTK != 0) return SFG_ERR_UNSUPPORTED;
     // The direct-to-LDS and 128 x 128 kernels mask a ragged last column tile;
     // the 256 x 128 register-staged kernel needs whole tiles.
     const bool whole_n = p.n % (glu ? 64 : 128) == 0;

@@ -59,10 +59,10 @@ struct GemmProblem {
     int xcds;                   // XCDs workgroups are dealt over (launch_gemm fills it)
 };
 
-// XCDs of the current device (hipDeviceAttributeNumberOfXccs), queried once per
-// device: the dispatcher deals consecutive workgroup ids over them in turn,
-// which the XCD-aware tile orders undo.
-int device_xcds();
+// XCDs of the device that owns `stream` (hipDeviceAttributeNumberOfXccs),
+// queried once per device: the dispatcher deals consecutive workgroup ids over
+// them in turn, which the XCD-aware tile orders undo.
+int device_xcds(hipStream_t stream);
 
 bool gemm_qkv_rope_supported(const GemmProblem& p);
 size_t gemm_workspace_bytes(int64_t m, int64_t n, int64_t k);
@@ -73,10 +73,13 @@ int launch_gemm(const GemmProblem& p, void* workspace, size_t workspace_bytes,
                 hipStream_t stream);
 
 // attention
-void launch_attn_prefill_f32(const float* q, const float* k, const float* v, void* out,
+// Row-per-wave online softmax, head_dim <= 256 (SFG_ERR_UNSUPPORTED beyond).
+int launch_attn_prefill_f32(const float* q, const float* k, const float* v, void* out,
                              int out_dtype, int64_t batch, int64_t q_heads, int64_t kv_heads,
                              int64_t seq_q, int64_t seq_kv, int64_t head_dim, int causal,
                              float scale, hipStream_t stream);
+// MFMA flash prefill at head_dim 64 / 128; other head dims up to 256 run the
+// row-per-wave kernel on the bf16 operands.
 int launch_attn_prefill_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v, void* out,
                              int out_dtype, int64_t batch, int64_t q_heads, int64_t kv_heads,
                              int64_t seq_q, int64_t seq_kv, int64_t head_dim, int causal,
@@ -94,6 +97,11 @@ void launch_v_transpose(const float* qkv, int64_t batch, int64_t seq, int64_t q_
 int decode_split_count(int64_t batch, int64_t kv_heads, int64_t max_context,
                        int64_t page_tokens, int32_t requested);
 size_t decode_workspace_bytes(int64_t batch, int64_t q_heads, int64_t head_dim, int splits);
+// The MFMA split-KV decode: bf16 pools, head_dim 64 / 128, 16-token pages, one
+// new token per sequence, GQA group 1 / 2 / 4 / 8 / 16 (decode_mfma_supported);
+// SFG_ERR_UNSUPPORTED otherwise (launch_attn_paged_rows takes those).
+bool decode_mfma_supported(int kv_dtype, int64_t head_dim, int64_t page_tokens, int64_t group,
+                           int64_t seq_q);
 int launch_attn_decode_paged(const float* q, int64_t q_row_stride, const float* rope, int rope_pos,
                              const uint16_t* k_pool, const uint16_t* v_pool,
                              const int32_t* page_table, const int32_t* seq_lens, int64_t max_context,
@@ -102,18 +110,39 @@ int launch_attn_decode_paged(const float* q, int64_t q_row_stride, const float* 
                              int64_t pages_per_seq, int64_t num_pages, int splits, float scale,
                              void* workspace, hipStream_t stream, hipEvent_t mid_event);
 
-// Paged KV append / gather (pages pre-assigned in the tables).  Sources are
-// [b][h][t][128] with element strides sb / sh / st; rope (optional) rotates the
-// keys at their positions; advance != 0 adds `tokens` to seq_lens afterwards.
+// Generic paged attention (any head_dim <= 256, any page size, seq_q >= 1 rows
+// per sequence under the causal offset, fp32 or bf16 pools).  Q (fp32) and the
+// output are addressed by element strides of (batch, row, head), dims
+// contiguous.  Partials of splits > 1 go to the workspace
+// (paged_rows_workspace_bytes(B seq_q Hq, D, splits)).
+struct PagedRowsLaunch {
+    const float* q; int64_t q_stride_b, q_stride_i, q_stride_h;
+    const float* rope; int rope_rows; int rope_pos;  // optional RoPE of Q (rope_pos < 0: at seq_lens[b] + i)
+    const void* k_pool; const void* v_pool; int kv_dtype;
+    const int32_t* page_table; const int32_t* seq_lens;
+    int64_t max_context; int len_extra;     // keys per sequence: (seq_lens[b] or max_context) + len_extra
+    void* out; int out_dtype; int64_t out_stride_b, out_stride_i, out_stride_h;
+    int64_t batch, q_heads, kv_heads, seq_q, head_dim, page_tokens, pages_per_seq, num_pages;
+    int splits, causal; float scale;
+    hipEvent_t mid_event;                   // recorded between the split and combine kernels
+};
+int paged_rows_split_count(int64_t rows, int64_t max_keys, int32_t requested);
+size_t paged_rows_workspace_bytes(int64_t rows, int64_t head_dim, int splits);
+int launch_attn_paged_rows(const PagedRowsLaunch& a, void* workspace, hipStream_t stream);
+
+// Paged KV append / gather (pages pre-assigned in the tables), any head_dim and
+// page size, pools fp32 or bf16.  Sources are [b][h][t][D] with element
+// strides sb / sh / st; rope (optional) rotates the keys at their positions;
+// advance != 0 adds `tokens` to seq_lens afterwards.
 int launch_kv_append(const void* keys, const void* values, int src_dtype, int64_t sb, int64_t sh,
-                     int64_t st, const float* rope, uint16_t* k_pool, uint16_t* v_pool,
+                     int64_t st, const float* rope, void* k_pool, void* v_pool, int pool_dtype,
                      const int32_t* page_table, int32_t* seq_lens, int64_t start, int advance,
                      int64_t batch, int64_t kv_heads, int64_t tokens, int64_t head_dim,
                      int64_t page_tokens, int64_t pages_per_seq, int64_t num_pages,
                      hipStream_t stream);
 void launch_kv_advance(int32_t* seq_lens, int64_t batch, int64_t tokens, int64_t capacity,
                        hipStream_t stream);
-int launch_kv_gather(const uint16_t* k_pool, const uint16_t* v_pool, const int32_t* page_table,
+int launch_kv_gather(const void* k_pool, const void* v_pool, int pool_dtype, const int32_t* page_table,
                      int64_t batch, int64_t kv_heads, int64_t length, int64_t head_dim,
                      int64_t page_tokens, int64_t pages_per_seq, int64_t num_pages, float* keys,
                      float* values, hipStream_t stream);

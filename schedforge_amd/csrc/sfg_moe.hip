@@ -470,12 +470,31 @@ __global__ __launch_bounds__(256) void moe_combine_reg_kernel(
     }
 }
 
+// Hidden sizes that are not a multiple of 4: one feature per thread, the same
+// slot-ordered sum.
+__global__ __launch_bounds__(256) void moe_combine_scalar_kernel(
+    const float* __restrict__ y, const int32_t* __restrict__ position,
+    const float* __restrict__ weights, const float* __restrict__ residual,
+    float* __restrict__ out, int hidden, int top_k, int64_t total) {
+    const int t = blockIdx.x;
+    for (int f = threadIdx.x; f < hidden; f += 256) {
+        float acc = 0.f;
+        for (int s = 0; s < top_k; ++s) {
+            const int64_t pos = position[static_cast<int64_t>(t) * top_k + s];
+            if (pos < 0 || pos >= total) continue;  // corrupt index: contributes nothing
+            acc = fmaf(weights[static_cast<int64_t>(t) * top_k + s], y[pos * hidden + f], acc);
+        }
+        out[static_cast<int64_t>(t) * hidden + f] = residual[static_cast<int64_t>(t) * hidden + f] + acc;
+    }
+}
+
 void launch_moe_combine(const float* y, const int32_t* position, const float* weights,
                         const float* residual, float* out, int64_t tokens, int64_t hidden,
                         int64_t top_k, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(tokens));
     const int h = static_cast<int>(hidden), k = static_cast<int>(top_k);
-    if (top_k <= 2) moe_combine_reg_kernel<2><<<grid, 256, 0, stream>>>(y, position, weights, residual, out, h, k, tokens * top_k);
+    if (hidden & 3) moe_combine_scalar_kernel<<<grid, 256, 0, stream>>>(y, position, weights, residual, out, h, k, tokens * top_k);
+    else if (top_k <= 2) moe_combine_reg_kernel<2><<<grid, 256, 0, stream>>>(y, position, weights, residual, out, h, k, tokens * top_k);
     else if (top_k <= 4) moe_combine_reg_kernel<4><<<grid, 256, 0, stream>>>(y, position, weights, residual, out, h, k, tokens * top_k);
     else if (top_k <= 8) moe_combine_reg_kernel<8><<<grid, 256, 0, stream>>>(y, position, weights, residual, out, h, k, tokens * top_k);
     else moe_combine_kernel<<<grid, 256, 0, stream>>>(y, position, weights, residual, out, h, k, tokens * top_k);

@@ -6,7 +6,9 @@ Layout differences, by design (the decode kernels stream one 4 KB run per
 (page, kv_head)):
   * one page table per sequence, [B][pages_per_seq], instead of one table
     shared by the batch (the reference's storage is [page][B][Hkv][tok][D]);
-  * K pool [page][Hkv][16][D] and V pool [page][Hkv][D][16], bf16.
+  * K pool [page][Hkv][page_tokens][D] and V pool [page][Hkv][D][page_tokens],
+    bf16 by default or fp32 (PagedKVConfig.pool_dtype, a build extension: the
+    reference stores fp32, so an fp32 pool holds its values exactly).
 Pages come from one free list shared by all sequences, initialised 0..N-1 and
 popped from the back, as make_paged_kv_cache / append_paged_kv do
 (next_milestones.cpp:472-484, 496-501); every guard raises the reference's error
@@ -35,12 +37,15 @@ class PagedKVConfig:
     head_dim_value: int = 1
     page_tokens: int = 16
     capacity: int = 0
+    pool_dtype: str = "bf16"    # build extension: "bf16" or "f32"
 
     def validate(self) -> None:
         """validate_paged_config (next_milestones.cpp:23-27)."""
         if (self.batch <= 0 or self.kv_heads <= 0 or self.head_dim <= 0 or self.head_dim_value <= 0
                 or self.page_tokens <= 0 or self.capacity <= 0):
             raise ValueError("invalid paged KV configuration")
+        if self.pool_dtype not in ("bf16", "f32"):
+            raise ValueError(f"unknown paged KV pool dtype {self.pool_dtype}")
 
     @property
     def pages_per_seq(self) -> int:
@@ -118,8 +123,10 @@ class PagedKVCache:
         self.device = torch.device(device)
         self.lib = _abi.load()
         n, h, pt, d = config.num_pages, config.kv_heads, config.page_tokens, config.head_dim
-        self.k_pool = torch.zeros((n, h, pt, d), dtype=torch.int16, device=self.device)
-        self.v_pool = torch.zeros((n, h, d, pt), dtype=torch.int16, device=self.device)
+        self.pool_dtype = F32 if config.pool_dtype == "f32" else BF16
+        store = torch.float32 if self.pool_dtype == F32 else torch.int16
+        self.k_pool = torch.zeros((n, h, pt, d), dtype=store, device=self.device)
+        self.v_pool = torch.zeros((n, h, d, pt), dtype=store, device=self.device)
         self.table = torch.from_numpy(self.alloc.table_array()).to(self.device)
 
     # reference field names
@@ -153,7 +160,8 @@ def make_paged_kv_cache(config: PagedKVConfig, device="cuda") -> PagedKVCache:
 
 def append_paged_kv(cache: PagedKVCache, keys, values, tokens: int, stream=None) -> None:
     """append_paged_kv (next_milestones.cpp:486-524): keys / values [B][Hkv][T][D]
-    (fp32, or bf16 bits in int16) appended at the cache length, stored bf16."""
+    (fp32, or bf16 bits in int16) appended at the cache length, stored in the
+    pools' dtype."""
     import torch
     c = cache.config
     shape = (c.batch, c.kv_heads, tokens, c.head_dim)
@@ -170,10 +178,10 @@ def append_paged_kv(cache: PagedKVCache, keys, values, tokens: int, stream=None)
     cache.alloc.reserve(tokens)
     cache._sync_table()
     s = torch.cuda.current_stream(cache.device).cuda_stream if stream is None else stream
-    check(cache.lib.sfg_hip_kv_append_paged_v1(
+    check(cache.lib.sfg_hip_kv_append_pool_v1(
         keys.data_ptr(), values.data_ptr(), dtype, cache.k_pool.data_ptr(), cache.v_pool.data_ptr(),
-        cache.table.data_ptr(), None, cache.length, 0, c.batch, c.kv_heads, tokens, c.head_dim,
-        c.page_tokens, c.pages_per_seq, c.num_pages, s))
+        cache.pool_dtype, cache.table.data_ptr(), None, cache.length, 0, c.batch, c.kv_heads, tokens,
+        c.head_dim, c.page_tokens, c.pages_per_seq, c.num_pages, s))
     torch.cuda.current_stream(cache.device).synchronize()
     cache.alloc.length += tokens
 
@@ -200,12 +208,48 @@ def gather_paged_kv(cache: PagedKVCache, stream=None):
                        device=cache.device)
     values = torch.empty_like(keys)
     s = torch.cuda.current_stream(cache.device).cuda_stream if stream is None else stream
-    check(cache.lib.sfg_hip_kv_gather_paged_v1(
-        cache.k_pool.data_ptr(), cache.v_pool.data_ptr(), cache.table.data_ptr(), c.batch, c.kv_heads,
-        cache.length, c.head_dim, c.page_tokens, c.pages_per_seq, c.num_pages, keys.data_ptr(),
-        values.data_ptr(), s))
+    check(cache.lib.sfg_hip_kv_gather_pool_v1(
+        cache.k_pool.data_ptr(), cache.v_pool.data_ptr(), cache.pool_dtype, cache.table.data_ptr(),
+        c.batch, c.kv_heads, cache.length, c.head_dim, c.page_tokens, c.pages_per_seq, c.num_pages,
+        keys.data_ptr(), values.data_ptr(), s))
     torch.cuda.current_stream(cache.device).synchronize()
     return keys.cpu().numpy(), values.cpu().numpy()
+
+
+def paged_decode_attention(cache: PagedKVCache, query, q_heads: int, seq_q: int = 1,
+                           causal: bool = True, scale: float = 0.0, kv_splits: int = 0,
+                           out_dtype=F32, stream=None) -> np.ndarray:
+    """execute_paged_decode_attention (next_milestones.cpp:583-609) over the
+    cache's pools: query [B][Hq][seq_q][D] fp32 attends over each sequence's
+    cached tokens (query row i sees key j <= length - seq_q + i when causal,
+    attention_compiler.cpp:68-72); returns [B][Hq][seq_q][D] fp32 (bf16 values
+    when out_dtype is BF16) as numpy, through sfg_hip_attn_paged_v1."""
+    import torch
+    c = cache.config
+    if cache.length <= 0:
+        raise ValueError("cannot attend over an empty paged KV cache")
+    if q_heads <= 0 or q_heads % c.kv_heads:
+        raise ValueError("invalid attention configuration")
+    q = torch.as_tensor(np.ascontiguousarray(query, np.float32)).to(cache.device)
+    if q.numel() != c.batch * q_heads * seq_q * c.head_dim:
+        raise ValueError("paged attention query shape mismatch")
+    shape = (c.batch, q_heads, seq_q, c.head_dim)
+    out = torch.empty(shape, dtype=torch.float32 if out_dtype == F32 else torch.int16, device=cache.device)
+    ws_bytes = cache.lib.sfg_hip_attn_paged_workspace_v1(c.batch, q_heads, c.kv_heads, seq_q, c.head_dim,
+                                                         cache.pool_dtype, cache.length, c.page_tokens,
+                                                         kv_splits)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=cache.device)
+    s = torch.cuda.current_stream(cache.device).cuda_stream if stream is None else stream
+    check(cache.lib.sfg_hip_attn_paged_v1(
+        q.data_ptr(), cache.k_pool.data_ptr(), cache.v_pool.data_ptr(), cache.pool_dtype,
+        cache.table.data_ptr(), None, out.data_ptr(), out_dtype, c.batch, q_heads, c.kv_heads, seq_q,
+        c.head_dim, c.page_tokens, c.pages_per_seq, c.num_pages, cache.length, int(causal), kv_splits,
+        float(scale), 0, ws.data_ptr(), ws.numel(), s))
+    torch.cuda.current_stream(cache.device).synchronize()
+    res = out.cpu().numpy()
+    if out_dtype != F32:
+        res = (res.view(np.uint16).astype(np.uint32) << 16).view(np.float32)
+    return res
 
 
 def gather_plan_kv(plan, length: int, stream=None):
@@ -216,8 +260,8 @@ def gather_plan_kv(plan, length: int, stream=None):
     keys = torch.empty((d.batch, d.kv_heads, length, d.head_dim), dtype=torch.float32, device=plan.device)
     values = torch.empty_like(keys)
     s = torch.cuda.current_stream(plan.device).cuda_stream if stream is None else stream
-    check(plan.lib.sfg_hip_kv_gather_paged_v1(
-        plan.t["k_pool"].data_ptr(), plan.t["v_pool"].data_ptr(), plan.t["page_table"].data_ptr(),
+    check(plan.lib.sfg_hip_kv_gather_pool_v1(
+        plan.t["k_pool"].data_ptr(), plan.t["v_pool"].data_ptr(), d.act_dtype, plan.t["page_table"].data_ptr(),
         d.batch, d.kv_heads, length, d.head_dim, d.page_tokens, d.pages_per_seq, d.num_pages,
         keys.data_ptr(), values.data_ptr(), s))
     torch.cuda.current_stream(plan.device).synchronize()

@@ -9,8 +9,9 @@ device layouts (constant specialisation, decoder_compiler.cpp:535-552):
   w_qkv [H + 2 kvD][H], w_o [H][H], w_gate_up [2I][H], w_down [H][I],
   w13 [E][2I][H] (W1^T rows then W3^T rows), w2 [E][H][I];
   bf16 (round to nearest even) or int8 + per-channel scales.
-Decode steps read K/V from paged bf16 pools -- K [page][Hkv][16][D], V
-[page][Hkv][D][16] -- addressed by a per-sequence page table.
+Decode steps read K/V from paged pools in the activation dtype (bf16, fp32 on
+the fp32 path) -- K [page][Hkv][page_tokens][D], V [page][Hkv][D][page_tokens]
+-- addressed by a per-sequence page table.
 """
 from __future__ import annotations
 
@@ -144,7 +145,8 @@ class DecoderExecutablePlan:
             dst = torch.empty((experts, rows_per_expert, k_dim), dtype=torch.int8, device=self.device)
             scales = torch.empty((experts, rows_per_expert), dtype=torch.float32, device=self.device)
         else:
-            dst = torch.empty((experts, rows_per_expert, k_dim), dtype=torch.int16, device=self.device)
+            dst = torch.empty((experts, rows_per_expert, k_dim),
+                              dtype=torch.float32 if wdt == F32 else torch.int16, device=self.device)
             scales = None
         esz = dst.element_size()
         for e in range(experts):
@@ -246,12 +248,17 @@ def compile_decoder(config: DecoderConfig, data: DecoderData, device="cuda",
                            .permute(0, 2, 1, 3, 4)
             if name == "v_pool":  # V is token-minor inside a page: [page][Hkv][D][16]
                 blocks = blocks.transpose(-1, -2)
-            blocks = blocks.reshape(num_pages, cfg.kv_heads, *blocks.shape[-2:])
+            # contiguous [page][Hkv][...] memory, whatever strides the view
+            # has (a batch of one reshapes the permuted view without a copy)
+            blocks = blocks.reshape(num_pages, cfg.kv_heads, *blocks.shape[-2:]).contiguous()
             del padded
-            pool32 = torch.empty_like(blocks)
+            pool32 = torch.empty(blocks.shape, dtype=torch.float32, device=plan.device)
             idx = t["page_table"].reshape(-1).long()
             pool32[idx] = blocks
             del blocks
+            if cfg.dtype == "f32":  # the fp32 path keeps fp32 pools
+                t[name] = pool32
+                continue
             pool = torch.empty(pool32.shape, dtype=torch.int16, device=plan.device)
             check(lib.sfg_hip_to_bf16_v1(pool32.data_ptr(), pool.data_ptr(), pool32.numel(), stream))
             torch.cuda.current_stream(plan.device).synchronize()

@@ -448,16 +448,20 @@ struct Packer {
 // Paged pools from [B][Hkv][ctx][D] fp32: K [page][Hkv][pt][D] and V
 // [page][Hkv][D][pt] (token-minor inside a page), bf16, page p of sequence b
 // at physical slot table[b][p]; positions past the context stay zero.
-std::vector<std::uint16_t> build_pool(const DecoderConfig& c, const std::vector<float>& cache,
-                                      const std::vector<std::int32_t>& table, bool token_minor) {
+// One paged pool in the layout the decode kernels read (K token-major, V
+// token-minor inside a page), in the activation dtype: fp32 for the fp32
+// path, bf16 bits otherwise.
+template <typename T>
+std::vector<T> build_pool(const DecoderConfig& c, const std::vector<float>& cache,
+                          const std::vector<std::int32_t>& table, bool token_minor) {
     const std::int64_t pt = c.page_tokens, D = c.head_dim, Hkv = c.kv_heads, ctx = c.context_sequence;
     const std::int64_t pps = c.pages_per_sequence();
     const std::int64_t page_elems = Hkv * pt * D;
-    std::vector<std::uint16_t> pool(static_cast<std::size_t>(table.size()) * page_elems, 0);
+    std::vector<T> pool(static_cast<std::size_t>(table.size()) * page_elems, T{});
     parallel_for(c.batch * pps, [&](std::int64_t begin, std::int64_t end) {
         for (std::int64_t bp = begin; bp < end; ++bp) {
             const std::int64_t b = bp / pps, p = bp % pps;
-            std::uint16_t* page = pool.data() + table[bp] * page_elems;
+            T* page = pool.data() + table[bp] * page_elems;
             for (std::int64_t h = 0; h < Hkv; ++h)
                 for (std::int64_t t = 0; t < pt; ++t) {
                     const std::int64_t token = p * pt + t;
@@ -465,7 +469,8 @@ std::vector<std::uint16_t> build_pool(const DecoderConfig& c, const std::vector<
                     const float* src = cache.data() + ((b * Hkv + h) * ctx + token) * D;
                     for (std::int64_t e = 0; e < D; ++e) {
                         const std::int64_t at = token_minor ? (h * D + e) * pt + t : (h * pt + t) * D + e;
-                        page[at] = bf16_bits(src[e]);
+                        if constexpr (sizeof(T) == 4) page[at] = src[e];
+                        else page[at] = bf16_bits(src[e]);
                     }
                 }
         }
@@ -690,17 +695,25 @@ DecoderExecutablePlan DecoderCompiler::compile(const DecoderConfig& config, cons
         w.page_table = static_cast<const std::int32_t*>(pt);
         plan.constants.push_back({"page_table", {c.batch, pages_per_seq}, {c.batch, pages_per_seq}, "i32",
                                   table.size() * 4});
+        const bool f32_pool = c.precision == DecoderPrecision::F32;
         for (const bool is_value : {false, true}) {
-            const auto pool = build_pool(c, is_value ? data.cached_value : data.cached_key, table, is_value);
             const std::string name = is_value ? "v_pool" : "k_pool";
-            void* p = dev.add(name, pool.size() * 2);
-            dev.upload(p, pool.data(), pool.size() * 2);
-            dev.sync();  // the host pool is released at scope end
-            (is_value ? w.v_pool : w.k_pool) = static_cast<std::uint16_t*>(p);
+            const std::vector<float>& cache = is_value ? data.cached_value : data.cached_key;
+            void* p = nullptr;
+            std::size_t bytes = 0;
+            auto place = [&](const auto& pool) {
+                bytes = pool.size() * sizeof(pool[0]);
+                p = dev.add(name, bytes);
+                dev.upload(p, pool.data(), bytes);
+                dev.sync();  // the host pool is released at scope end
+            };
+            if (f32_pool) place(build_pool<float>(c, cache, table, is_value));
+            else place(build_pool<std::uint16_t>(c, cache, table, is_value));
+            (is_value ? w.v_pool : w.k_pool) = p;
             plan.constants.push_back({name, {c.batch, c.kv_heads, c.context_sequence, static_cast<int>(D)},
                                       is_value ? std::vector<int>{num_pages, c.kv_heads, static_cast<int>(D), c.page_tokens}
                                                : std::vector<int>{num_pages, c.kv_heads, c.page_tokens, static_cast<int>(D)},
-                                      "paged:bf16", pool.size() * 2});
+                                      f32_pool ? "paged:f32" : "paged:bf16", bytes});
         }
     }
 

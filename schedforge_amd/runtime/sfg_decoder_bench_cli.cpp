@@ -10,9 +10,8 @@
 //   optimizer   the reference's optimizer pair (tiny-prefill-s128 and
 //               tiny-decode-kv512) unless --filter picks others; forces --optimize
 //   baseline    the five benchmark configurations c1..c5 at their own precisions
-// Options of this target: --precision=f32|bf16|w8 (default bf16: decode runs
-// on a bf16 paged KV cache and MoE on bf16 activations, so fp32 profiles of
-// those kinds are recorded as skipped), --device=N, --compile-only (every
+// Options of this target: --precision=f32|bf16|w8 (default bf16; f32 runs every
+// profile on the fp32 path, decode over fp32 paged pools), --device=N, --compile-only (every
 // profile analytical, no GPU touched), --expect-dir=DIR (a measured profile P
 // with a file DIR/P.f32 of rows x hidden raw fp32 values gets max_error
 // against it; the others report NaN).  Real-execution budgets default to a

@@ -206,8 +206,8 @@ void bind_buffer(sfg_layer_weights& w, const std::string& name, void* p) {
     else if (name == "expert_w13.scales") w.s13 = f;
     else if (name == "expert_w2") w.w2 = p;
     else if (name == "expert_w2.scales") w.s2 = f;
-    else if (name == "k_pool") w.k_pool = static_cast<std::uint16_t*>(p);
-    else if (name == "v_pool") w.v_pool = static_cast<std::uint16_t*>(p);
+    else if (name == "k_pool") w.k_pool = p;
+    else if (name == "v_pool") w.v_pool = p;
     else if (name == "page_table") w.page_table = static_cast<const std::int32_t*>(p);
     else if (name == "rope_table") w.rope_table = f;
     else throw std::runtime_error("unknown .sfe plan buffer: " + name);

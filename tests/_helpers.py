@@ -2,6 +2,8 @@
 from __future__ import annotations
 
 import ctypes
+import json
+import os
 
 import numpy as np
 
@@ -123,8 +125,16 @@ def branch_errors(x, out, taps, ref_out, ref_taps):
 
 
 def assert_branches(x, out, taps, ref_out, ref_taps, tol, label=""):
+    """Every branch error below tol.  With SFG_PARITY_LOG set to a file path,
+    each check also appends {label, tol, rows, errors} to it as a JSON line
+    (the record of the parity margins)."""
     err = branch_errors(x, out, taps, ref_out, ref_taps)
     print(f"{label} " + " ".join(f"{k} {v:.3e}" for k, v in err.items()))
+    log = os.environ.get("SFG_PARITY_LOG")
+    if log:
+        with open(log, "a") as f:
+            f.write(json.dumps({"label": label, "tol": tol, "rows": int(np.asarray(out).shape[0]),
+                                **{k: float(v) for k, v in err.items()}}) + "\n")
     bad = {k: v for k, v in err.items() if not v < tol}
     assert not bad, f"{label}: over tolerance {tol}: {bad}"
     return err

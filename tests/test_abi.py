@@ -178,3 +178,64 @@ def test_layer_taps_lie_inside_the_workspace(lib):
         assert all(a[1] <= b[0] for a, b in zip(spans, spans[1:])), spans
     assert tap(_desc(), 99)[0] == _abi.ERR_SHAPE
     assert tap(_desc(hidden=250), 0)[0] == _abi.ERR_INVALID_CONFIG
+
+
+def test_widened_layer_domain_validates_on_host(lib):
+    """Decode on fp32 pools, MoE on fp32 activations, several new tokens per
+    decode step and head dims up to 256 are lowered (a workspace size comes
+    back); a causal step longer than its cache (validate_config,
+    attention_compiler.cpp:23-29) and head dims above 256 are refused."""
+    ws = lambda **kw: lib.sfg_hip_decoder_layer_workspace_v1(ctypes.byref(_desc(**kw)))
+    assert ws(act_dtype=_abi.F32, weight_dtype=_abi.F32) > 0                       # fp32 decode
+    assert ws(act_dtype=_abi.F32, weight_dtype=_abi.F32, ffn=1, context=0) > 0      # fp32 MoE
+    assert ws(sequence=3) > 0                                                        # S = 3 decode
+    assert ws(hidden=8, query_heads=2, head_dim=4, page_tokens=4, pages_per_seq=16, num_pages=32) > 0
+    assert ws(sequence=3, kv_append=1, context=61) > 0                               # append 3
+    assert _call_layer(lib, _desc(sequence=65)) == _abi.ERR_INVALID_CONFIG          # S > context
+    assert _call_layer(lib, _desc(sequence=4, kv_append=1, context=61)) == _abi.ERR_GUARD  # past capacity
+    assert _call_layer(lib, _desc(hidden=2 * 320, head_dim=320, context=0)) == _abi.ERR_UNSUPPORTED
+
+
+def test_generic_paged_attention_entry_validates_on_host(lib):
+    """sfg_hip_attn_paged_v1 rejects on the host, before any launch."""
+    call = lambda **kw: lib.sfg_hip_attn_paged_v1(
+        *[kw.get(k, v) for k, v in dict(
+            q=1, k=1, v=1, kv_dtype=_abi.F32, table=1, lens=None, out=1, out_dtype=_abi.F32, batch=1,
+            hq=4, hkv=2, sq=1, d=4, pt=4, pps=3, pages=3, ctx=7, causal=1, splits=0).items()],
+        ctypes.c_float(0.0), 0, None, kw.get("ws_bytes", 0), None)
+    assert call(sq=8) == _abi.ERR_INVALID_CONFIG        # causal, 8 rows over 7 keys
+    assert call(d=257) == _abi.ERR_UNSUPPORTED          # head_dim above 256
+    assert call(kv_dtype=_abi.I8) == _abi.ERR_UNSUPPORTED
+    assert call(ctx=13) == _abi.ERR_GUARD               # beyond 3 pages of 4 tokens
+    assert call(hkv=3) == _abi.ERR_INVALID_CONFIG       # GQA ratio
+    # several splits need a workspace
+    need = lib.sfg_hip_attn_paged_workspace_v1(1, 4, 2, 1, 4, _abi.F32, 7, 4, 3)
+    assert need > 0 and call(splits=3) == _abi.ERR_WORKSPACE
+    # the bf16 decode entry's workspace query bounds the general one from above
+    # (it assumes the worst kv_heads and covers both kernels)
+    for hkv in (1, 4, 16):
+        assert 0 < lib.sfg_hip_attn_paged_workspace_v1(16, 16, hkv, 1, 128, _abi.BF16, 4096, 16, 0) <= \
+            lib.sfg_hip_attn_decode_workspace_v1(16, 16, 128, 4096, 16, 0)
+
+
+def test_grouped_gemm_and_pool_entries_validate_on_host(lib):
+    args = _abi.GemmArgs()
+    args.a = args.b = args.c = 1
+    args.m, args.n, args.k, args.lda, args.ldb, args.ldc = 8, 8, 8, 8, 8, 8
+    args.epilogue = 1  # SFG_EPI_RESIDUAL: no residual in the grouped form
+    assert lib.sfg_hip_gemm_grouped_v1(ctypes.byref(args), None, 0, 1, 2, 0, 0, None, 0, None) == _abi.ERR_SHAPE
+    args.epilogue = 0
+    assert lib.sfg_hip_gemm_grouped_v1(ctypes.byref(args), None, 0, None, 2, 0, 0, None, 0, None) == _abi.ERR_SHAPE
+    assert lib.sfg_hip_kv_append_pool_v1(1, 1, _abi.F32, 1, 1, 7, 1, None, 0, 0, 1, 1, 1, 4, 4, 3, 3,
+                                         None) == _abi.ERR_UNSUPPORTED
+    assert lib.sfg_hip_kv_gather_pool_v1(1, 1, _abi.F32, 1, 1, 1, 13, 4, 4, 3, 3, 1, 1, None) == _abi.ERR_GUARD
+
+
+def test_metadata_states_the_lowering_envelope(lib):
+    """The metadata string names what the library lowers, as key=value pairs."""
+    meta = dict(kv.split("=", 1) for kv in lib.sfg_hip_metadata_v1().decode().split(";")
+                if "=" in kv and kv.count("=") == 1)
+    assert meta["abi"] == "1" and meta["arch"] == "gfx950"
+    assert meta["act"] == "f32,bf16" and meta["head_dim"] == "1..256"
+    assert meta["page_tokens"] == "any" and meta["decode_tokens"] == "any"
+    assert meta["ffn"] == "dense,moe" and meta["kv"] == "act_dtype"

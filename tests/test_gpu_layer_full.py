@@ -5,10 +5,9 @@ The reference checks execute_once against reference_decoder_layer at any shape
   C3  MoE prefill, 2048 tokens: the whole oracle layer (a few seconds), once
       with routing on the device (rows routed differently must be near ties of
       the oracle's logits) and once under the oracle's own routing trace;
-  C4  Llama-3-8B-shaped prefill, S 8192: the GPU runs the whole layer; the
-      oracle runs sfgo_decoder_layer_rows (K / V of every row, the rest for a
-      sample of 272 query rows spread over the whole causal range, first and
-      last included), pinned bit-exact against the full oracle on the CPU;
+  C4  Llama-3-8B-shaped prefill, S 8192: the whole layer on both sides, every
+      row compared (the oracle's register-blocked products take a few tens of
+      seconds for it);
   C5  Mixtral-shaped int8 decode, 64 sequences over 8192 cached tokens, every
       row on both sides, routed on the device and under the oracle's trace.
 Every check compares the output and, on their own scales, the attention
@@ -74,21 +73,15 @@ def test_c3_full_size_matches_oracle():
     assert_branches(d.input, res2.output, taps2, ref, rt, TOL["bf16"], "c3 full, routing trace")
 
 
-def test_c4_full_size_matches_row_sampled_oracle():
+def test_c4_full_size_matches_oracle():
     cfg = CONFIGS["c4"]
     d = oracle.make_layer_data(cfg, CONFIG_SEEDS["c4"])
     plan, res, taps = _compile_and_run(cfg, d)
-    print(f"c4 full: {res.milliseconds:.4f} ms/layer")
-    S = cfg.sequence
-    edges = [0, 1, 2, 31, 32, 63, 64, 127, 128, 255, 256, 1023, 1024, 4095, 4096, S - 129, S - 128,
-             S - 65, S - 64, S - 2, S - 1]
-    rng = np.random.default_rng(CONFIG_SEEDS["c4"])
-    sample = np.unique(np.r_[edges, rng.choice(S, 256, replace=False)])
+    print(f"c4 full: {res.milliseconds:.4f} ms/layer", flush=True)
     del plan
     torch.cuda.empty_cache()
-    ref, rt = oracle.decoder_layer_rows(cfg, d, sample, taps=True)
-    assert_branches(d.input[sample], res.output[sample], _rows(taps, sample), ref, rt, TOL["bf16"],
-                    f"c4 full, {sample.size} sampled rows")
+    ref, rt = oracle.decoder_layer(cfg, d, taps=True)
+    assert_branches(d.input, res.output, taps, ref, rt, TOL["bf16"], "c4 full, every row")
 
 
 def test_c5_full_size_matches_oracle():

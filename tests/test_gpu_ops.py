@@ -291,21 +291,27 @@ def test_gemm_rejects_bad_shapes(lib):
         _abi.check(lib.sfg_hip_gemm_v1(ctypes.byref(args), None, 0, stream()))
 
 
-def test_gemm_rejects_misaligned_operands(lib):
-    """bf16 / int8 rows are read as 16-byte vectors: a row pitch that is not a
-    multiple of 16 bytes, or an operand not 16-byte aligned, is refused."""
+def test_gemm_misaligned_operands_run_on_the_valu_kernel(lib):
+    """bf16 / int8 MFMA kernels read rows as 16-byte vectors: a row pitch that
+    is not a multiple of 16 bytes, or an operand not 16-byte aligned, runs on
+    the VALU kernel instead (exact here: small integers)."""
     m, n, k = 16, 256, 256
-    a = bf16_dev(np.ones((m, k + 8), np.float32))
-    b = bf16_dev(np.ones((n, k), np.float32))
+    rng = np.random.default_rng(5)
+    a32 = rng.integers(-2, 3, (m, k + 8)).astype(np.float32)
+    b32 = rng.integers(-2, 3, (n, k)).astype(np.float32)
+    a, b = bf16_dev(a32), bf16_dev(b32)
     c = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    flat = a32.reshape(-1)
     for lda, a_off in ((k + 1, 0), (k, 1)):  # odd pitch; base 2 bytes in
         args = _abi.GemmArgs()
         args.a, args.a_dtype, args.lda = a.data_ptr() + 2 * a_off, BF16, lda
         args.b, args.b_dtype, args.ldb, args.b_scales = b.data_ptr(), BF16, k, None
         args.c, args.c_dtype, args.ldc = c.data_ptr(), F32, n
         args.m, args.n, args.k, args.epilogue = m, n, k, EPI_NONE
-        with pytest.raises(ValueError):
-            _abi.check(lib.sfg_hip_gemm_v1(ctypes.byref(args), None, 0, stream()))
+        _abi.check(lib.sfg_hip_gemm_v1(ctypes.byref(args), None, 0, stream()))
+        _sync()
+        rows = np.stack([flat[a_off + r * lda: a_off + r * lda + k] for r in range(m)])
+        np.testing.assert_array_equal(host(c), (rows.astype(np.float64) @ b32.T.astype(np.float64)))
 
 
 # ------------------------------------------------------------------ packing
