@@ -1956,8 +1956,8 @@ constexpr int kVecTM = 64;
 template <typename AT, typename BT, int EPI>
 __global__ __launch_bounds__(256) void gemm_vec_kernel(VecArgs p) {
     constexpr bool kGlu = EpiTraits<EPI>::glu;
-    __shared__ float sA[16][64 + 4];
-    __shared__ float sB[16][64 + 4];
+    __shared__ float sA[2][16][64 + 4];
+    __shared__ float sB[2][16][64 + 4];
     const int tid = threadIdx.x;
     const int tx = tid & 15, ty = tid >> 4;
     // Map blockIdx.y to (group, row tile).
@@ -1997,32 +1997,64 @@ __global__ __launch_bounds__(256) void gemm_vec_kernel(VecArgs p) {
     int bc[4];
     if (kGlu) { bc[0] = 2 * tx; bc[1] = 2 * tx + 1; bc[2] = 32 + 2 * tx; bc[3] = 33 + 2 * tx; }
     else { bc[0] = 4 * tx; bc[1] = 4 * tx + 1; bc[2] = 4 * tx + 2; bc[3] = 4 * tx + 3; }
-    for (int64_t k0 = 0; k0 < p.k; k0 += 16) {
-        // load 64x16 of A and B (transposed into [k][row])
-        for (int e = tid; e < 64 * 16; e += 256) {
-            const int r = e >> 4, kk = e & 15;
-            const int64_t gr = m0 + r, gk = k0 + kk;
-            float av = 0.f;
-            if (gr < re && gk < p.k) {
-                const int64_t src = p.a_rows ? p.a_rows[gr] : gr;
-                if (src >= 0 && src < p.a_rows_limit) av = elem_f32(A, src * p.lda + gk);
-            }
-            sA[kk][r] = av;
-            sB[kk][r] = (bcol_ok(r) && gk < p.k) ? elem_f32(B, brow_of(r) * p.ldb + gk) : 0.f;
+    // This thread moves elements e = tid + 256 i (i < 4) of each 64 x 16 slab
+    // of A and of B: row e >> 4, k e & 15.  Sources are resolved once (the
+    // dispatch gather included); -1 marks a row past the tile, which loads 0.
+    const int lk = tid & 15;
+    int64_t a_src[4], b_src[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = (tid + 256 * i) >> 4;
+        const int64_t gr = m0 + r;
+        int64_t src = -1;
+        if (gr < re) {
+            src = p.a_rows ? p.a_rows[gr] : gr;
+            if (src < 0 || src >= p.a_rows_limit) src = -1;
         }
-        __syncthreads();
+        a_src[i] = src < 0 ? -1 : src * p.lda;
+        b_src[i] = bcol_ok(r) ? brow_of(r) * p.ldb : -1;
+    }
+    // Two LDS stages: slab s + 1 is loaded into registers while slab s is
+    // multiplied, then stored into the other stage (one barrier per slab).
+    float va[4], vb[4];
+    auto fetch = [&](int64_t k0) {
+        const int64_t gk = k0 + lk;
+        const bool kin = gk < p.k;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            va[i] = (kin && a_src[i] >= 0) ? elem_f32(A, a_src[i] + gk) : 0.f;
+            vb[i] = (kin && b_src[i] >= 0) ? elem_f32(B, b_src[i] + gk) : 0.f;
+        }
+    };
+    auto stash = [&](int st) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = (tid + 256 * i) >> 4;
+            sA[st][lk][r] = va[i];
+            sB[st][lk][r] = vb[i];
+        }
+    };
+    fetch(0);
+    stash(0);
+    __syncthreads();
+    int st = 0;
+    for (int64_t k0 = 0; k0 < p.k; k0 += 16, st ^= 1) {
+        const bool more = k0 + 16 < p.k;
+        if (more) fetch(k0 + 16);
 #pragma unroll
         for (int kk = 0; kk < 16; ++kk) {
             float av[4], bv[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) av[i] = sA[kk][ty * 4 + i];
+            for (int i = 0; i < 4; ++i) av[i] = sA[st][kk][ty * 4 + i];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) bv[j] = sB[kk][bc[j]];
+            for (int j = 0; j < 4; ++j) bv[j] = sB[st][kk][bc[j]];
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(av[i], bv[j], acc[i][j]);
         }
+        // the other stage was last read before the previous barrier
+        if (more) stash(st ^ 1);
         __syncthreads();
     }
     // per-channel scales of int8 weights (quantized_invoke, next_milestones.cpp:50-69)
