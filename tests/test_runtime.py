@@ -230,6 +230,49 @@ def test_cli_moe_layer_matches_oracle(tmp_path, name):
     assert set(bad.tolist()) <= set(ties.tolist()), (bad, ties)
 
 
+# The reference's own decoder-test shape (test_schedforge.cpp:823-825) and
+# decode steps beyond one new token, through the C++ runtime's pools and plan.
+_WIDE = {
+    "f32-decode": SMALL["c2"].replace(dtype="f32"),
+    "f32-decode-s2-pages4": SMALL["c2"].replace(dtype="f32", sequence=2, page_tokens=4),
+    "bf16-decode-s3": SMALL["c2"].replace(sequence=3),
+    "ref-h16d4-decode-f32": SMALL["c2"].replace(batch=1, hidden=16, intermediate=32, query_heads=4,
+                                                  kv_heads=2, head_dim=4, context_sequence=16,
+                                                  dtype="f32", rms_epsilon=1e-5),
+}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", list(_WIDE))
+def test_cli_widened_decode_matches_oracle(tmp_path, name):
+    """fp32 decode over fp32 paged pools, several new tokens per step, any
+    page size and head_dim, through sfg-decoder (the C++ runtime compiles the
+    plan, packs the pools and checks its output against the expected file)."""
+    cfg = _WIDE[name]
+    r, ref, got, _ = _gpu_case(tmp_path, cfg, CONFIG_SEEDS["c2"] + 61)
+    assert r.returncode == 0, r.stderr
+    assert oracle.rel_error(got, ref) < TOL[cfg.dtype]
+
+
+@pytest.mark.gpu
+def test_cli_fp32_moe_layer_matches_oracle(tmp_path):
+    """An fp32 MoE layer (the reference's only MoE arithmetic) through the C++
+    runtime: grouped fp32 expert products on the VALU kernel.  fp32 routing is
+    bit-exact against the oracle's chains given equal router inputs, which agree
+    to fp32 rounding here, so only near ties may route differently."""
+    cfg = SMALL["c3"].replace(dtype="f32", batch=1, sequence=64)
+    seed = CONFIG_SEEDS["c3"] + 61
+    r, ref, got, _ = _gpu_case(tmp_path, cfg, seed)
+    assert got is not None, r.stderr
+    d = oracle.make_layer_data(cfg, seed)
+    _, taps = oracle.decoder_layer(cfg, d, taps=True)
+    ties = near_tie_rows(route_logits(taps["normalized2"], d.router_weight, d.router_bias),
+                         cfg.top_k, 1e-4)
+    rows_err = np.max(np.abs(got - ref), axis=1) / max(np.max(np.abs(ref)), 1e-6)
+    bad = np.nonzero(rows_err >= TOL["f32"])[0]
+    assert set(bad.tolist()) <= set(ties.tolist()), (bad, ties)
+
+
 @pytest.mark.gpu
 def test_cli_gemm_tile_policy_keeps_output(tmp_path):
     """--gemm-tile / --attn-waves change kernel variants only: the output of a

@@ -3,7 +3,9 @@ with its split partials in the library's device scratch array instead of a
 caller workspace, called through the C ABI.  Its output must equal, bit for bit,
 sfg_hip_attn_decode_paged_v1's with the same split count, on two calls in a row
 (the second smaller, so stale partials of the first would show), bf16 and fp32
-outputs; a request whose partials exceed the array is refused before any launch.
+outputs, on the MFMA kernel's shapes and on the row kernel's; captured into a
+HIP graph after an eager first call, every replay matches too; a request whose
+partials exceed the array is refused before any launch.
 """
 from __future__ import annotations
 
@@ -97,3 +99,63 @@ def test_no_alloc_decode_refuses_partials_beyond_the_scratch():
                                                   ctypes.c_float(0.0), stream())
     assert rc == _abi.ERR_WORKSPACE
     assert b"scratch" in lib.sfg_hip_last_error()
+
+
+def test_no_alloc_decode_replays_under_graph_capture():
+    """After a first eager call on the device (which looks the scratch address
+    up, outside any capture), the entry point captures into a HIP graph: it
+    records kernel launches only.  Each of three replays, with new query values
+    copied in eagerly and the stream synchronised between them, equals the
+    workspace entry point on the same inputs bit for bit."""
+    lib = _abi.load()
+    c = _case(8, 16, 4, 1024, 604)
+    _no_alloc(lib, c, _abi.F32, 0)  # warm-up on this device, eager
+    out = torch.empty((c["B"], c["Hq"] * D), dtype=torch.float32, device="cuda")
+    side = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph, stream=side):
+        rc = lib.sfg_hip_attn_decode_paged_noalloc_v1(*_args(c), out.data_ptr(), _abi.F32,
+                                                      *_dims(c, 0), side.cuda_stream)
+    assert rc == 0, lib.sfg_hip_last_error()
+    for rep in range(3):
+        c["q"].copy_(torch.from_numpy(oracle.normal(700 + rep, 0, (c["B"], c["Hq"], 1, D))))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = host(out)
+        want = _with_workspace(lib, c, _abi.F32, 0)
+        print(f"replay {rep}: equal {np.array_equal(got, want)}")
+        np.testing.assert_array_equal(got, want)
+
+
+def test_no_alloc_decode_on_the_row_kernel_matches_workspace_entry():
+    """A shape the MFMA split kernel does not lower (head_dim 96, 8-token
+    pages) runs the row kernel with its partials in the same scratch, bit for
+    bit equal to the workspace entry point, twice in a row with different
+    split counts."""
+    lib = _abi.load()
+    B, Hq, Hkv, d, pt, ctx, seed = 3, 6, 2, 96, 8, 300, 605
+    pps = (ctx + pt - 1) // pt
+    table = oracle.page_permutation(seed, B * pps).reshape(B, pps).astype(np.int32)
+    kp = oracle.round_bf16(oracle.normal(seed, 15, (B * pps, Hkv, pt, d)))
+    vp = oracle.round_bf16(oracle.normal(seed, 16, (B * pps, Hkv, d, pt)))
+    q, k, v = dev(oracle.normal(seed, 0, (B, Hq, 1, d))), bf16_dev(kp), bf16_dev(vp)
+    tab, lens = dev(table), dev(np.array([ctx, 17, 123], np.int32))
+    for splits in (4, 0):
+        outs = []
+        for noalloc in (False, True):
+            out = torch.empty((B, Hq * d), dtype=torch.float32, device="cuda")
+            args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), tab.data_ptr(), lens.data_ptr(),
+                    out.data_ptr(), _abi.F32, B, Hq, Hkv, d, pt, pps, B * pps, ctx, splits,
+                    ctypes.c_float(0.0))
+            if noalloc:
+                _abi.check(lib.sfg_hip_attn_decode_paged_noalloc_v1(*args, stream()))
+            else:
+                wsb = lib.sfg_hip_attn_decode_workspace_v1(B, Hq, d, ctx, pt, splits)
+                ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device="cuda")
+                _abi.check(lib.sfg_hip_attn_decode_paged_v1(*args, 1, ws.data_ptr(), ws.numel(), stream()))
+            torch.cuda.synchronize()
+            outs.append(host(out))
+        np.testing.assert_array_equal(outs[1], outs[0])
+        assert np.isfinite(outs[0]).all()
