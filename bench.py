@@ -231,6 +231,33 @@ def cpu_model() -> str:
     return "unknown"
 
 
+def reference_gemm_check(cfg, threads):
+    """One 64-row slice of the workload's up-projection GEMM (hidden ->
+    2 x intermediate, fp32) through the reference's own CPU GEMM runtime
+    (apply_schedule + execute under decoder_schedule's Latency family, built
+    from the reference sources into oracle/_ref) and through the oracle's
+    sfgo_matmul, same operands, same thread count: both rates, and whether
+    the two results agree bit for bit."""
+    import numpy as np
+    import oracle
+    if oracle.ref_gemm_lib() is None:
+        return "oracle/_ref/libsfg_ref_gemm.so not built"
+    m, n, k = 64, 2 * cfg.intermediate, cfg.hidden
+    a = oracle.normal(7, 0, (m, k))
+    b = oracle.normal(7, 1, (k, n), std=0.02)
+    flops = 2.0 * m * n * k
+    t = time.perf_counter()
+    want = oracle.reference_gemm(a, b, family=0, threads=threads)
+    ref_s = time.perf_counter() - t
+    t = time.perf_counter()
+    got = oracle.matmul(a, b)
+    port_s = time.perf_counter() - t
+    return {"shape_mnk": [m, n, k], "threads": threads,
+            "reference_execute_gflops": round(flops / ref_s / 1e9, 2),
+            "oracle_gflops": round(flops / port_s / 1e9, 2),
+            "bit_identical": bool(np.array_equal(got.view(np.uint32), want.view(np.uint32)))}
+
+
 def cpu_baseline(cfg, budget_s: float):
     """Time the CPU restatement on whole layer steps of the workload.
 
@@ -262,8 +289,11 @@ def cpu_baseline(cfg, budget_s: float):
             "what": "restatement: oracle/sfg_oracle.c, a C restatement of reference_decoder_layer "
                     "(OpenMP over the host's threads)",
             "method": f"measured: median of {len(steps)} whole layer step(s), nothing extrapolated",
-            "reference_cpu_path": "not built: its translation units need LLVM 18 "
-                                  "(llvm_backend.cpp), which this image lacks",
+            "reference_cpu_path": "decoder, attention and MoE compilers not built: they call "
+                                  "the LLVM JIT (LLVMJITBackend), and LLVM 18 is not in this "
+                                  "image; the reference's GEMM runtime is built and timed in "
+                                  "reference_gemm",
+            "reference_gemm": reference_gemm_check(cfg, threads),
             "cpu_model": cpu_model(), "threads": threads,
             "step_s": {"median": round(med, 4), "min": round(min(steps), 4),
                        "max": round(max(steps), 4)},

@@ -39,6 +39,53 @@ def build() -> Path:
     return LIB_PATH
 
 
+# The reference's own CPU GEMM runtime (oracle/ref_gemm.cpp over the reference
+# sources, `make ref`): built in this container only, where the sources are;
+# the built library travels with the tree.
+REF_ROOT = Path("/root/reference")
+REF_LIB_PATH = HERE / "_ref" / "libsfg_ref_gemm.so"
+_ref_lib = None
+
+
+def build_ref() -> Path | None:
+    """Compile the reference GEMM library when the reference sources are
+    present; None (nothing built) where they are not."""
+    if not (REF_ROOT / "src" / "runtime.cpp").is_file():
+        return None
+    subprocess.run(["make", "-s", "-C", str(HERE), "ref", f"REF={REF_ROOT}"], check=True)
+    return REF_LIB_PATH
+
+
+def ref_gemm_lib() -> ctypes.CDLL | None:
+    """The reference GEMM library, built if it can be; None if neither a built
+    library nor the sources are here."""
+    global _ref_lib
+    if _ref_lib is None:
+        if not REF_LIB_PATH.exists() and build_ref() is None:
+            return None
+        _ref_lib = ctypes.CDLL(str(REF_LIB_PATH))
+        _ref_lib.sfgr_decoder_gemm.restype = ctypes.c_int
+        _ref_lib.sfgr_decoder_gemm.argtypes = [fp, fp, fp] + [ctypes.c_int] * 5
+    return _ref_lib
+
+
+def reference_gemm(a, b, family: int = 0, threads: int = 1) -> np.ndarray:
+    """a @ b by the reference's execute() under the schedule its decoder gives
+    the projections (family 0 Latency, 1 Throughput)."""
+    ref = ref_gemm_lib()
+    if ref is None:
+        raise RuntimeError("reference GEMM library not built and reference sources absent")
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    m, k = a.shape
+    k2, n = b.shape
+    assert k == k2
+    c = np.empty((m, n), np.float32)
+    if ref.sfgr_decoder_gemm(_f(a), _f(b), _f(c), m, n, k, family, threads) != 0:
+        raise RuntimeError("reference execute() failed")
+    return c
+
+
 class AttnCfg(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in ("batch", "query_heads", "kv_heads", "seq_q",
                                                "seq_kv", "head_dim", "head_dim_value", "causal")] + \

@@ -7,7 +7,9 @@ known-answer tests, and an independent float64 formulation of the whole layer.
 
   function                 pinned by
   sfgo_rms_norm            golden; closed form x=c -> c w / sqrt(c^2+eps)
-  sfgo_matmul              integer operands (exact) vs NumPy int64
+  sfgo_matmul              integer operands (exact) vs NumPy int64; bit for bit
+                           against the reference's own execute()
+                           (tests/test_oracle_ref.py)
   sfgo_rope / split_qkv    golden; position-0 identity; pair norms; known angle
   sfgo_attention           golden (causal + full); equal keys -> prefix mean;
                            one-hot V -> probability row
