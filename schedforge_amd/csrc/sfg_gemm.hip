@@ -150,6 +150,10 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny_kernel(SkinnyArgs p) {
         // read row 0 instead (no branch around the loads): an MFMA output row
         // depends only on its own A row, and the epilogue stores nothing for
         // the former and the zero product for the latter.
+        // 16-row blocks of this pass that hold rows (wave-uniform): a grouped
+        // pass past its expert's rows skips the activation loads and MFMAs of
+        // the empty blocks (their outputs are never stored)
+        const int mt_live = static_cast<int>(min(static_cast<int64_t>(MT), (re - pass + 15) / 16));
         const uint16_t* arow[MT];
 #pragma unroll
         for (int i = 0; i < MT; ++i) {
@@ -184,6 +188,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny_kernel(SkinnyArgs p) {
                 }
 #pragma unroll
                 for (int i = 0; i < MT; ++i) {
+                    if (i > 0 && i >= mt_live) break;
                     const uint16_t* ap = arow[i] + kofs;
 #pragma unroll
                     for (int s = 0; s < 4; ++s)
@@ -207,7 +212,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny_kernel(SkinnyArgs p) {
                     }
                 }
 #pragma unroll
-                for (int i = 0; i < MT; ++i)
+                for (int i = 0; i < MT; ++i) {
+                    if (i > 0 && i >= mt_live) break;
 #pragma unroll
                     for (int s = 0; s < 4; ++s) {
                         const bf16x8 a = as_bf16x8(aq[c][i][s]);
@@ -215,6 +221,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny_kernel(SkinnyArgs p) {
                         for (int j = 0; j < NBT; ++j)
                             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bf[j][s], acc[i][j], 0, 0, 0);
                     }
+                }
             }
         }
 
