@@ -391,7 +391,7 @@ def measure(name, args, device="cuda:0"):
             kbytes = esz * (T * H + E * 2 * I * H + T * K * I) + esz * (T * K * I + E * H * I) + 4 * T * K * H
         else:
             kflops = 2 * T * H * 2 * I
-            kname = ("gemm_f32_kernel" if cfg.dtype == "f32" else "gemm_dma_kernel") + " (gate|up + SwiGLU)"
+            kname = ("gemm_vec_kernel" if cfg.dtype == "f32" else "gemm_dma_kernel") + " (gate|up + SwiGLU)"
             kbytes = esz * (T * H + 2 * I * H + T * I)
         achieved = kflops / (kern_ms * 1e-3) / 1e12
         layer_tf = work["flops"] / (ms_per_step * 1e-3) / 1e12

@@ -5,21 +5,27 @@
 // (runtime.cpp:581-626), the MoE expert loops (moe_compiler.cpp:64-155) and
 // weight-only int8 quantized_invoke (next_milestones.cpp:50-69).
 //
-// Three kernels, picked by shape:
+// Kernels, picked by shape:
 //  * gemm_skinny_kernel   M <= 64 rows (decode; grouped experts loop over
-//    64-row passes): weight-streaming, HBM bound.  v_mfma_f32_16x16x32_bf16
-//    with the activation rows as the A operand; bf16 or int8 weights (int8 ->
-//    bf16 is exact), 64 B contiguous per lane per 128-k chunk, split-K over up
-//    to 8 waves of one workgroup with a fixed-order LDS reduction.
-//  * gemm_mfma_kernel     large M (prefill, grouped experts): 128x128x32 tiles,
-//    v_mfma_f32_32x32x16_bf16, A/B staged through padded LDS with register
-//    prefetch of the next k-slab, optional A-row gather for dispatched tokens
-//    and per-group (expert) segments read from device offsets.
+//    16- to 64-row passes): weight-streaming, HBM bound.
+//    v_mfma_f32_16x16x32_bf16 with the activation rows as the A operand; bf16
+//    or int8 weights (int8 -> bf16 is exact), 64 B contiguous per lane per
+//    128-k chunk, split-K over up to 8 waves of one workgroup with a
+//    fixed-order LDS reduction.
 //  * gemm_splitk_kernel   33..64 dense rows with a caller workspace: 512-k
 //    slices, activations staged once per workgroup in LDS, fp32 partials
 //    summed in slice order by gemm_splitk_reduce_kernel (scale + epilogue).
-//  * gemm_f32_kernel      fp32 operands (the fp32 parity config): 64x64 LDS
-//    tiles on the VALU.
+//  * gemm_dma_kernel      bf16 prefill and grouped experts, >= 1024 rows:
+//    256x256 (64-k slabs), 256x128, 128x256 or 128x128 tiles, operands global
+//    -> LDS by DMA, v_mfma_f32_32x32x16_bf16, optional A-row gather and
+//    per-group (expert) segments read from device offsets.
+//  * gemm_mfma256_kernel  int8-weight products with >= 1024 rows: 256x128
+//    tiles, k-slabs through padded LDS with register prefetch.
+//  * gemm_mfma_kernel     the other tiled products (fewer rows, ragged N):
+//    128x128x32 tiles through padded LDS with register prefetch.
+//  * gemm_vec_kernel      fp32 operands (the fp32 configurations) and the
+//    bf16 / int8 products the MFMA kernels do not lower: one sequential fp32
+//    FMA chain per output on the VALU.
 #include <type_traits>
 
 #include "sfg_kernels.hpp"
