@@ -38,6 +38,13 @@ __device__ __forceinline__ float in_f32(const InT* p, int64_t i) {
     else return bf16_to_f32(p[i]);
 }
 
+// One wave per query row, the workgroup's four rows (consecutive rows of one
+// head) sharing each 64-key chunk of K and V, which the workgroup stages into
+// LDS with coalesced loads (K rows padded to D + 1 floats, so the 64 lanes
+// reading one key row each touch distinct banks).  Lane j then scores key j
+// of the chunk with one sequential fp32 FMA chain over the head dimension, and
+// the wave accumulates p V with lane d owning dims d, d + 64, ... (online
+// softmax, attention_compiler.cpp:102-112).
 template <typename InT, typename OutT>
 __global__ __launch_bounds__(256) void attn_prefill_rows_kernel(
     const InT* __restrict__ q, const InT* __restrict__ k, const InT* __restrict__ v,
@@ -45,26 +52,72 @@ __global__ __launch_bounds__(256) void attn_prefill_rows_kernel(
     int causal, float scale) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int qi = blockIdx.x * 4 + wave;
+    const int q0 = blockIdx.x * 4;
+    const int qi = q0 + wave;
     const int h = blockIdx.y, b = blockIdx.z;
     __shared__ float sq[4][kRowMaxD];
-    if (qi >= seq_q) return;
+    __shared__ float sK[64 * (kRowMaxD + 1)];
+    __shared__ float sV[64 * kRowMaxD];
+    const bool live = qi < seq_q;
     const int kvh = h * kv_heads / q_heads;
-    const InT* qr = q + ((static_cast<int64_t>(b) * q_heads + h) * seq_q + qi) * head_dim;
-    for (int d = lane; d < head_dim; d += 64) sq[wave][d] = in_f32(qr, d);
-    __builtin_amdgcn_wave_barrier();
+    if (live) {
+        const InT* qr = q + ((static_cast<int64_t>(b) * q_heads + h) * seq_q + qi) * head_dim;
+        for (int d = lane; d < head_dim; d += 64) sq[wave][d] = in_f32(qr, d);
+    }
     const InT* kb = k + (static_cast<int64_t>(b) * kv_heads + kvh) * seq_kv * head_dim;
     const InT* vb = v + (static_cast<int64_t>(b) * kv_heads + kvh) * seq_kv * head_dim;
     const int limit = causal ? (seq_kv - seq_q + qi) : (seq_kv - 1);
+    // keys the workgroup's last live row attends to
+    const int q_last = min(q0 + 3, seq_q - 1);
+    const int block_limit = min(causal ? (seq_kv - seq_q + q_last) : (seq_kv - 1), seq_kv - 1);
+    const int kstride = head_dim + 1;
     float m = -INFINITY, l = 0.f;
     float acc[4] = {0.f, 0.f, 0.f, 0.f};  // dims lane + 64 r
-    for (int base = 0; base <= limit && base < seq_kv; base += 64) {
+    for (int base = 0; base <= block_limit; base += 64) {
+        const int nkeys = min(64, block_limit - base + 1);
+        const int total = nkeys * head_dim;
+        __syncthreads();  // the previous chunk's reads are done
+        // eight loads of each operand in flight per thread: the loads past
+        // the chunk re-read its last element (no branch around a load) and
+        // are not stored
+        for (int e0 = threadIdx.x; e0 < total; e0 += 256 * 8) {
+            float kv[8], vv[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int64_t src = static_cast<int64_t>(base) * head_dim + min(e0 + 256 * i, total - 1);
+                kv[i] = in_f32(kb, src);
+                vv[i] = in_f32(vb, src);
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int e = e0 + 256 * i;
+                if (e < total) {
+                    const int row = e / head_dim, col = e - row * head_dim;
+                    sK[row * kstride + col] = kv[i];
+                    sV[e] = vv[i];
+                }
+            }
+        }
+        __syncthreads();
+        if (!live || base > limit) continue;
         const int j = base + lane;
         float s = -INFINITY;
         if (j <= limit && j < seq_kv) {
-            const InT* kr = kb + static_cast<int64_t>(j) * head_dim;
+            const float* kr = sK + lane * kstride;
             float dot = 0.f;
-            for (int d = 0; d < head_dim; ++d) dot = fmaf(sq[wave][d], in_f32(kr, d), dot);
+            // eight steps' operands read before their FMAs (same chain order)
+            int d = 0;
+            for (; d + 8 <= head_dim; d += 8) {
+                float qv[8], kv[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    qv[i] = sq[wave][d + i];
+                    kv[i] = kr[d + i];
+                }
+#pragma unroll
+                for (int i = 0; i < 8; ++i) dot = fmaf(qv[i], kv[i], dot);
+            }
+            for (; d < head_dim; ++d) dot = fmaf(sq[wave][d], kr[d], dot);
             s = dot * scale;
         }
         const float mx = wave_max(s);
@@ -75,15 +128,32 @@ __global__ __launch_bounds__(256) void attn_prefill_rows_kernel(
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[r] *= alpha;
         const int count = min(64, min(limit, seq_kv - 1) - base + 1);
-        for (int t = 0; t < count; ++t) {
+        int t = 0;
+        for (; t + 8 <= count; t += 8) {
+            float pt[8], vv[8][4];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                pt[i] = __shfl(p, t + i, 64);
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    vv[i][r] = lane + 64 * r < head_dim ? sV[(t + i) * head_dim + lane + 64 * r] : 0.f;
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (lane + 64 * r < head_dim) acc[r] = fmaf(pt[i], vv[i][r], acc[r]);
+        }
+        for (; t < count; ++t) {
             const float pt = __shfl(p, t, 64);
-            const InT* vr = vb + static_cast<int64_t>(base + t) * head_dim;
+            const float* vr = sV + t * head_dim;
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-                if (lane + 64 * r < head_dim) acc[r] = fmaf(pt, in_f32(vr, lane + 64 * r), acc[r]);
+                if (lane + 64 * r < head_dim) acc[r] = fmaf(pt, vr[lane + 64 * r], acc[r]);
         }
         m = m_new;
     }
+    if (!live) return;
     const int64_t row = static_cast<int64_t>(b) * seq_q + qi;
     OutT* orow = out + row * (static_cast<int64_t>(q_heads) * head_dim) + h * head_dim;
 #pragma unroll

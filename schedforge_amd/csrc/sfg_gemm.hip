@@ -1938,14 +1938,14 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
 }
 
 // ===========================================================================
-// VALU GEMM: 64x64 tile, BK 16, 256 threads x (4 rows x 4 cols), one fp32
-// FMA chain per output in k order.  The fp32 path (AT = BT = float), and the
-// fallback for bf16 / int8 products the MFMA kernels do not lower (K not a
+// VALU GEMM: 64x64, 32x32, 16x32 or 16x16 tiles (k slabs of 16 to 128),
+// 256 threads, one fp32 FMA chain per output in k order.  The fp32 path (AT = BT = float), and
+// the fallback for bf16 / int8 products the MFMA kernels do not lower (K not a
 // multiple of their k step, rows not 16-byte aligned): A fp32 or bf16, B fp32,
 // bf16 or int8 with per-channel scales applied after the sum; grouped
 // problems and the dispatch gather as in the tiled kernels.
-// For GLU epilogues the tile covers 32 outputs: thread columns {2t, 2t+1}
-// of the gate block and the same two of the up block.
+// For GLU epilogues a thread's columns are RN / 2 of the gate block and the
+// same RN / 2 of the up block.
 // ===========================================================================
 struct VecArgs {
     const void* a; int64_t lda; const int32_t* a_rows; int64_t a_rows_limit;
@@ -1964,13 +1964,25 @@ __device__ __forceinline__ float elem_f32(const T* p, int64_t i) {
     else return bf16_to_f32(p[i]);
 }
 
-constexpr int kVecTM = 64;
+constexpr int kVecMinTiles = 256;  // VALU GEMM: smallest grid a tile may give
 
-template <typename AT, typename BT, int EPI>
+// TM x TN output tile per workgroup of 16 x 16 threads, RM x RN outputs per
+// thread (TM = 16 RM, TN = 16 RN B rows; GLU tiles hold TN / 2 gate and TN / 2
+// up rows and give TN / 2 output columns).  Every output is one sequential
+// fp32 FMA chain over k whatever the tile, so every tile gives the same bits.
+template <typename AT, typename BT, int EPI, int TM, int TN, int KS>
 __global__ __launch_bounds__(256) void gemm_vec_kernel(VecArgs p) {
     constexpr bool kGlu = EpiTraits<EPI>::glu;
-    __shared__ float sA[2][16][64 + 4];
-    __shared__ float sB[2][16][64 + 4];
+    constexpr int RM = TM / 16, RN = TN / 16;
+    static_assert(TM % 16 == 0 && TN % 16 == 0, "tiles of 16 x 16 threads");
+    static_assert(!kGlu || RN % 2 == 0, "GLU threads pair gate and up columns");
+    // KS: k per LDS slab; each thread moves LA elements of A and LB of B per slab
+    static_assert(KS >= 16 && KS <= 256 && (KS & (KS - 1)) == 0, "slab depth");
+    constexpr int kKsShift = KS == 16 ? 4 : KS == 32 ? 5 : KS == 64 ? 6 : KS == 128 ? 7 : 8;
+    constexpr int LA = TM * KS / 256, LB = TN * KS / 256;
+    static_assert(LA >= 1 && LB >= 1, "every thread moves A and B elements");
+    __shared__ float sA[2][KS][TM + 4];
+    __shared__ float sB[2][KS][TN + 4];
     const int tid = threadIdx.x;
     const int tx = tid & 15, ty = tid >> 4;
     // Map blockIdx.y to (group, row tile).
@@ -1982,7 +1994,7 @@ __global__ __launch_bounds__(256) void gemm_vec_kernel(VecArgs p) {
         auto bound = [&](int e) { return min(max(static_cast<int64_t>(p.offsets[e]), int64_t(0)), p.m); };
         for (int e = 0; e < p.groups; ++e) {
             const int64_t lo = bound(e);
-            const int64_t tiles = (max(bound(e + 1) - lo, int64_t(0)) + kVecTM - 1) / kVecTM;
+            const int64_t tiles = (max(bound(e + 1) - lo, int64_t(0)) + TM - 1) / TM;
             if (t < tiles) { g = e; break; }
             t -= tiles;
         }
@@ -1991,33 +2003,38 @@ __global__ __launch_bounds__(256) void gemm_vec_kernel(VecArgs p) {
         re = max(bound(g + 1), rb);
         mtile = t;
     }
-    const int64_t m0 = rb + mtile * kVecTM;
+    const int64_t m0 = rb + mtile * TM;
     if (m0 >= re) return;
     const AT* A = static_cast<const AT*>(p.a);
     const BT* B = static_cast<const BT*>(p.b) + static_cast<int64_t>(g) * p.b_group_stride;
     const float* scales = p.scales ? p.scales + static_cast<int64_t>(g) * p.s_group_stride : nullptr;
-    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * (kGlu ? 32 : 64);
+    constexpr int kOutCols = kGlu ? TN / 2 : TN;
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kOutCols;
     // B tile row -> B matrix row; valid when its output column is below n.
     auto brow_of = [&](int local) -> int64_t {
-        if (kGlu) return local < 32 ? n0 + local : p.n + n0 + local - 32;
+        if (kGlu) return local < TN / 2 ? n0 + local : p.n + n0 + local - TN / 2;
         return n0 + local;
     };
     auto bcol_ok = [&](int local) -> bool {
-        return kGlu ? (local < 32 ? n0 + local : n0 + local - 32) < p.n : n0 + local < p.n;
+        return kGlu ? (local < TN / 2 ? n0 + local : n0 + local - TN / 2) < p.n : n0 + local < p.n;
     };
-    float acc[4][4] = {};
-    // thread's 4 B-tile columns
-    int bc[4];
-    if (kGlu) { bc[0] = 2 * tx; bc[1] = 2 * tx + 1; bc[2] = 32 + 2 * tx; bc[3] = 33 + 2 * tx; }
-    else { bc[0] = 4 * tx; bc[1] = 4 * tx + 1; bc[2] = 4 * tx + 2; bc[3] = 4 * tx + 3; }
-    // This thread moves elements e = tid + 256 i (i < 4) of each 64 x 16 slab
-    // of A and of B: row e >> 4, k e & 15.  Sources are resolved once (the
-    // dispatch gather included); -1 marks a row past the tile, which loads 0.
-    const int lk = tid & 15;
-    int64_t a_src[4], b_src[4];
+    float acc[RM][RN] = {};
+    // this thread's RN B-tile rows: GLU, RN / 2 gate rows and the matching up rows
+    int bc[RN];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int r = (tid + 256 * i) >> 4;
+    for (int j = 0; j < RN; ++j) {
+        if (kGlu) bc[j] = (j < RN / 2) ? (RN / 2) * tx + j : TN / 2 + (RN / 2) * tx + (j - RN / 2);
+        else bc[j] = RN * tx + j;
+    }
+    // This thread moves elements e = tid + 256 i of each TM x KS slab of A
+    // (i < LA) and TN x KS slab of B (i < LB): row e / KS, k e % KS (the same
+    // k for every i).  Sources are resolved once (the dispatch gather
+    // included); -1 marks a row past the tile, which loads 0.
+    const int lk = tid & (KS - 1);
+    int64_t a_src[LA], b_src[LB];
+#pragma unroll
+    for (int i = 0; i < LA; ++i) {
+        const int r = (tid + 256 * i) >> kKsShift;
         const int64_t gr = m0 + r;
         int64_t src = -1;
         if (gr < re) {
@@ -2025,72 +2042,71 @@ __global__ __launch_bounds__(256) void gemm_vec_kernel(VecArgs p) {
             if (src < 0 || src >= p.a_rows_limit) src = -1;
         }
         a_src[i] = src < 0 ? -1 : src * p.lda;
+    }
+#pragma unroll
+    for (int i = 0; i < LB; ++i) {
+        const int r = (tid + 256 * i) >> kKsShift;
         b_src[i] = bcol_ok(r) ? brow_of(r) * p.ldb : -1;
     }
     // Two LDS stages: slab s + 1 is loaded into registers while slab s is
     // multiplied, then stored into the other stage (one barrier per slab).
-    float va[4], vb[4];
+    float va[LA], vb[LB];
     auto fetch = [&](int64_t k0) {
         const int64_t gk = k0 + lk;
         const bool kin = gk < p.k;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            va[i] = (kin && a_src[i] >= 0) ? elem_f32(A, a_src[i] + gk) : 0.f;
-            vb[i] = (kin && b_src[i] >= 0) ? elem_f32(B, b_src[i] + gk) : 0.f;
-        }
+        for (int i = 0; i < LA; ++i) va[i] = (kin && a_src[i] >= 0) ? elem_f32(A, a_src[i] + gk) : 0.f;
+#pragma unroll
+        for (int i = 0; i < LB; ++i) vb[i] = (kin && b_src[i] >= 0) ? elem_f32(B, b_src[i] + gk) : 0.f;
     };
     auto stash = [&](int st) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = (tid + 256 * i) >> 4;
-            sA[st][lk][r] = va[i];
-            sB[st][lk][r] = vb[i];
-        }
+        for (int i = 0; i < LA; ++i) sA[st][lk][(tid + 256 * i) >> kKsShift] = va[i];
+#pragma unroll
+        for (int i = 0; i < LB; ++i) sB[st][lk][(tid + 256 * i) >> kKsShift] = vb[i];
     };
     fetch(0);
     stash(0);
     __syncthreads();
     int st = 0;
-    for (int64_t k0 = 0; k0 < p.k; k0 += 16, st ^= 1) {
-        const bool more = k0 + 16 < p.k;
-        if (more) fetch(k0 + 16);
+    for (int64_t k0 = 0; k0 < p.k; k0 += KS, st ^= 1) {
+        const bool more = k0 + KS < p.k;
+        if (more) fetch(k0 + KS);
 #pragma unroll
-        for (int kk = 0; kk < 16; ++kk) {
-            float av[4], bv[4];
+        for (int kk = 0; kk < KS; ++kk) {
+            float av[RM], bv[RN];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) av[i] = sA[st][kk][ty * 4 + i];
+            for (int i = 0; i < RM; ++i) av[i] = sA[st][kk][ty * RM + i];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) bv[j] = sB[st][kk][bc[j]];
+            for (int j = 0; j < RN; ++j) bv[j] = sB[st][kk][bc[j]];
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < RM; ++i)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(av[i], bv[j], acc[i][j]);
+                for (int j = 0; j < RN; ++j) acc[i][j] = fmaf(av[i], bv[j], acc[i][j]);
         }
         // the other stage was last read before the previous barrier
         if (more) stash(st ^ 1);
         __syncthreads();
     }
     // per-channel scales of int8 weights (quantized_invoke, next_milestones.cpp:50-69)
-    float sc[4] = {1.f, 1.f, 1.f, 1.f};
-    if (scales) {
+    float sc[RN];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) sc[j] = bcol_ok(bc[j]) ? scales[brow_of(bc[j])] : 1.f;
-    }
+    for (int j = 0; j < RN; ++j) sc[j] = (scales && bcol_ok(bc[j])) ? scales[brow_of(bc[j])] : 1.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int64_t row = m0 + ty * 4 + i;
+    for (int i = 0; i < RM; ++i) {
+        const int64_t row = m0 + ty * RM + i;
         if (row >= re) continue;
         if (kGlu) {
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
+            for (int j = 0; j < RN / 2; ++j) {
                 const int64_t col = n0 + bc[j];
                 if (col < p.n)
                     store_out(p.c, p.c_dtype, row * p.ldc + col,
-                              glu_combine(EPI, acc[i][j] * sc[j], acc[i][j + 2] * sc[j + 2]));
+                              glu_combine(EPI, acc[i][j] * sc[j], acc[i][j + RN / 2] * sc[j + RN / 2]));
             }
         } else {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+            for (int j = 0; j < RN; ++j) {
                 const int64_t col = n0 + bc[j];
                 if (col >= p.n) continue;
                 float v = acc[i][j] * sc[j];
@@ -2101,17 +2117,42 @@ __global__ __launch_bounds__(256) void gemm_vec_kernel(VecArgs p) {
     }
 }
 
+template <typename AT, typename BT, int TM, int TN, int KS>
+void launch_vec_tile(const VecArgs& a, int epi, hipStream_t stream) {
+    const bool glu = epi == SFG_EPI_SWIGLU || epi == SFG_EPI_GLU_SILU_UP;
+    const int64_t cols = glu ? TN / 2 : TN;
+    const int64_t row_tiles = a.offsets ? (a.m + TM - 1) / TM + a.groups : (a.m + TM - 1) / TM;
+    const dim3 grid(static_cast<unsigned>((a.n + cols - 1) / cols), static_cast<unsigned>(row_tiles));
+    switch (epi) {
+        case SFG_EPI_NONE: gemm_vec_kernel<AT, BT, SFG_EPI_NONE, TM, TN, KS><<<grid, 256, 0, stream>>>(a); break;
+        case SFG_EPI_RESIDUAL: gemm_vec_kernel<AT, BT, SFG_EPI_RESIDUAL, TM, TN, KS><<<grid, 256, 0, stream>>>(a); break;
+        default:
+            // GLU tiles pair gate and up rows per thread (the caller never
+            // sends a GLU product to a one-column tile)
+            if constexpr ((TN / 16) % 2 == 0) {
+                if (epi == SFG_EPI_SWIGLU) gemm_vec_kernel<AT, BT, SFG_EPI_SWIGLU, TM, TN, KS><<<grid, 256, 0, stream>>>(a);
+                else gemm_vec_kernel<AT, BT, SFG_EPI_GLU_SILU_UP, TM, TN, KS><<<grid, 256, 0, stream>>>(a);
+            }
+            break;
+    }
+}
+
+// Largest tile that still gives a workgroup to most CUs: each thread's RM x RN
+// chains run the whole K, so on small products (the fp32 parity config's 128
+// rows) a 64 x 64 tile leaves most of the GPU idle with 16 chains per thread.
 template <typename AT, typename BT>
 void launch_vec_t(const VecArgs& a, int epi, hipStream_t stream) {
     const bool glu = epi == SFG_EPI_SWIGLU || epi == SFG_EPI_GLU_SILU_UP;
-    const int64_t row_tiles = a.offsets ? (a.m + kVecTM - 1) / kVecTM + a.groups : (a.m + kVecTM - 1) / kVecTM;
-    const dim3 grid(static_cast<unsigned>((a.n + (glu ? 31 : 63)) / (glu ? 32 : 64)), static_cast<unsigned>(row_tiles));
-    switch (epi) {
-        case SFG_EPI_NONE: gemm_vec_kernel<AT, BT, SFG_EPI_NONE><<<grid, 256, 0, stream>>>(a); break;
-        case SFG_EPI_RESIDUAL: gemm_vec_kernel<AT, BT, SFG_EPI_RESIDUAL><<<grid, 256, 0, stream>>>(a); break;
-        case SFG_EPI_SWIGLU: gemm_vec_kernel<AT, BT, SFG_EPI_SWIGLU><<<grid, 256, 0, stream>>>(a); break;
-        default: gemm_vec_kernel<AT, BT, SFG_EPI_GLU_SILU_UP><<<grid, 256, 0, stream>>>(a); break;
-    }
+    auto tiles = [&](int64_t tm, int64_t tn) {
+        const int64_t cols = glu ? tn / 2 : tn;
+        return ((a.m + tm - 1) / tm + (a.offsets ? a.groups : 0)) * ((a.n + cols - 1) / cols);
+    };
+    // slab depth grows as the tile shrinks: each thread keeps moving 4 - 8
+    // elements per slab, so a slab's loads cover its chain steps' latency
+    if (tiles(64, 64) >= kVecMinTiles) launch_vec_tile<AT, BT, 64, 64, 16>(a, epi, stream);
+    else if (tiles(32, 32) >= kVecMinTiles) launch_vec_tile<AT, BT, 32, 32, 32>(a, epi, stream);
+    else if (glu) launch_vec_tile<AT, BT, 16, 32, 64>(a, epi, stream);
+    else launch_vec_tile<AT, BT, 16, 16, 128>(a, epi, stream);
 }
 
 // The VALU kernel for any NK-layout problem it can read; SFG_ERR_UNSUPPORTED
