@@ -71,6 +71,7 @@ __global__ __launch_bounds__(256) void attn_prefill_rows_kernel(
     const int q_last = min(q0 + 3, seq_q - 1);
     const int block_limit = min(causal ? (seq_kv - seq_q + q_last) : (seq_kv - 1), seq_kv - 1);
     const int kstride = head_dim + 1;
+    const float inv_d = 1.0f / static_cast<float>(head_dim);
     float m = -INFINITY, l = 0.f;
     float acc[4] = {0.f, 0.f, 0.f, 0.f};  // dims lane + 64 r
     for (int base = 0; base <= block_limit; base += 64) {
@@ -92,8 +93,10 @@ __global__ __launch_bounds__(256) void attn_prefill_rows_kernel(
             for (int i = 0; i < 8; ++i) {
                 const int e = e0 + 256 * i;
                 if (e < total) {
-                    const int row = e / head_dim, col = e - row * head_dim;
-                    sK[row * kstride + col] = kv[i];
+                    // row = e / head_dim: (e + 0.5) / D stays at least 0.5 / D
+                    // away from an integer, far beyond float error for e < 2^15
+                    const int row = static_cast<int>((static_cast<float>(e) + 0.5f) * inv_d);
+                    sK[e + row] = kv[i];  // row * (D + 1) + col
                     sV[e] = vv[i];
                 }
             }
