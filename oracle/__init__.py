@@ -52,7 +52,7 @@ def build_ref() -> Path | None:
     present; None (nothing built) where they are not."""
     if not (REF_ROOT / "src" / "runtime.cpp").is_file():
         return None
-    subprocess.run(["make", "-s", "-C", str(HERE), "ref", f"REF={REF_ROOT}"], check=True)
+    subprocess.run(["make", "-s", "-j8", "-C", str(HERE), "ref", f"REF={REF_ROOT}"], check=True)
     return REF_LIB_PATH
 
 
