@@ -221,13 +221,19 @@ def test_row_prefill_other_head_dims(d, dtype):
 
 @pytest.mark.parametrize("m,n,k,bdt,epi,grouped", [
     (7, 20, 16, "bf16", 0, False), (33, 24, 48, "bf16", 1, False), (65, 40, 16, "i8", 0, False),
-    (70, 24, 16, "bf16", 2, False), (50, 12, 40, "f32", 3, True), (40, 16, 24, "i8", 3, True)])
+    (70, 24, 16, "bf16", 2, False), (50, 12, 40, "f32", 3, True), (40, 16, 24, "i8", 3, True),
+    # sizes that select the larger VALU tiles: 64 x 64 (256+ workgroups) and 32 x 32
+    (1024, 1024, 48, "f32", 0, False), (512, 512, 40, "f32", 1, False),
+    (1024, 1024, 24, "f32", 2, False), (512, 512, 24, "bf16", 3, False),
+    (1024, 256, 40, "i8", 0, True)])
 def test_valu_gemm_fallback_is_exact(m, n, k, bdt, epi, grouped):
     """Products the MFMA kernels do not lower (k not a multiple of 32) run on
     the VALU kernel: with small-integer operands every product and partial sum
     is exact in fp32, so the result must equal the fp64 product bit for bit
     (and the SwiGLU / GLU epilogues the fp32 expressions of it); int8 weights
-    carry their per-channel scales, grouped problems their row gather."""
+    carry their per-channel scales, grouped problems their row gather.  The
+    kernel's tile (64 x 64, 32 x 32, 16 x 32 or 16 x 16, by how many
+    workgroups each gives) changes nothing: the shapes cover every one."""
     from schedforge_amd import _abi
     lib = _abi.load()
     rng = np.random.default_rng(m * n + k)
