@@ -949,7 +949,7 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(
 template <typename OutT, int kDecD, int NS>
 __global__ __launch_bounds__(kDecD) void attn_decode_combine_kernel(
     const float* __restrict__ part_ml, const float* __restrict__ part_acc, OutT* __restrict__ out,
-    int q_heads, int splits) {
+    int splits) {
     const int bh = blockIdx.x;  // b * q_heads + h
     const int d = threadIdx.x;
     const float* ml = part_ml + static_cast<int64_t>(bh) * splits * 2;
@@ -1062,15 +1062,14 @@ int launch_attn_decode_paged(const float* q, int64_t q_row_stride, const float* 
 #undef SFG_DECODE
     if (mid_event) (void)hipEventRecord(mid_event, stream);
     const dim3 cgrid(static_cast<unsigned>(batch * q_heads));
-    const int qh = static_cast<int>(q_heads);
     auto combine = [&](auto* o, auto dcon) {
         using OutT = std::remove_pointer_t<decltype(o)>;
         constexpr int D = decltype(dcon)::value;
-        if (splits <= 2) attn_decode_combine_kernel<OutT, D, 2><<<cgrid, D, 0, stream>>>(part_ml, part_acc, o, qh, splits);
-        else if (splits <= 4) attn_decode_combine_kernel<OutT, D, 4><<<cgrid, D, 0, stream>>>(part_ml, part_acc, o, qh, splits);
-        else if (splits <= 8) attn_decode_combine_kernel<OutT, D, 8><<<cgrid, D, 0, stream>>>(part_ml, part_acc, o, qh, splits);
-        else if (splits <= 16) attn_decode_combine_kernel<OutT, D, 16><<<cgrid, D, 0, stream>>>(part_ml, part_acc, o, qh, splits);
-        else attn_decode_combine_kernel<OutT, D, 0><<<cgrid, D, 0, stream>>>(part_ml, part_acc, o, qh, splits);
+        if (splits <= 2) attn_decode_combine_kernel<OutT, D, 2><<<cgrid, D, 0, stream>>>(part_ml, part_acc, o, splits);
+        else if (splits <= 4) attn_decode_combine_kernel<OutT, D, 4><<<cgrid, D, 0, stream>>>(part_ml, part_acc, o, splits);
+        else if (splits <= 8) attn_decode_combine_kernel<OutT, D, 8><<<cgrid, D, 0, stream>>>(part_ml, part_acc, o, splits);
+        else if (splits <= 16) attn_decode_combine_kernel<OutT, D, 16><<<cgrid, D, 0, stream>>>(part_ml, part_acc, o, splits);
+        else attn_decode_combine_kernel<OutT, D, 0><<<cgrid, D, 0, stream>>>(part_ml, part_acc, o, splits);
     };
     if (head_dim == 128) {
         if (out_dtype == SFG_F32) combine(static_cast<float*>(out), std::integral_constant<int, 128>{});

@@ -99,7 +99,7 @@ __global__ __launch_bounds__(256) void rmsnorm_reg_kernel(const float* __restric
     double sum = 0.0;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-        if ((threadIdx.x + 256 * i) * 4 >= width) break;
+        if ((static_cast<int>(threadIdx.x) + 256 * i) * 4 >= width) break;
         sum += static_cast<double>(v[i].x) * v[i].x;
         sum += static_cast<double>(v[i].y) * v[i].y;
         sum += static_cast<double>(v[i].z) * v[i].z;

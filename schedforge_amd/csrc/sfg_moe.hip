@@ -175,7 +175,7 @@ __global__ __launch_bounds__(256) void moe_router_kernel(
         logits[t_local * experts + e] = acc;
     }
     __syncthreads();
-    if (threadIdx.x >= per_block) return;
+    if (static_cast<int>(threadIdx.x) >= per_block) return;
     const int tok = blockIdx.x * per_block + threadIdx.x;
     if (tok >= tokens) return;
     route_select(logits + threadIdx.x * experts, experts, top_k, tok, ids, weights);
