@@ -219,6 +219,39 @@ def test_row_prefill_other_head_dims(d, dtype):
     assert oracle.rel_error(out.cpu().numpy(), ref) < TOL["f32"]
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("sq,skv,causal,hkv", [(9, 9, True, 2), (5, 7, True, 2), (8, 8, False, 2),
+                                               (128, 128, True, 2), (9, 9, True, 1), (3, 11, False, 1)])
+def test_reference_attention_test_shapes(sq, skv, causal, hkv, dtype):
+    """The shapes of the reference's attention test (test_schedforge.cpp:689-757:
+    batch 1, four query heads, head_dim 8; 9 x 9 causal, 5 queries over 7 keys
+    with the causal offset j <= Skv - Sq + i, 8 x 8 non-causal, 128 x 128, and
+    MQA) through sfg_hip_attn_prefill_v1, against reference_attention on the
+    same (for bf16, bf16-rounded) operands."""
+    from schedforge_amd import _abi
+    lib = _abi.load()
+    B, hq, d = 1, 4, 8
+    rng = np.random.default_rng(sq * 100 + skv + 7 * hkv + int(causal))
+    q = rng.standard_normal((B, hq, sq, d)).astype(np.float32)
+    k = rng.standard_normal((B, hkv, skv, d)).astype(np.float32)
+    v = rng.standard_normal((B, hkv, skv, d)).astype(np.float32)
+    if dtype == "bf16":
+        q, k, v = oracle.round_bf16(q), oracle.round_bf16(k), oracle.round_bf16(v)
+        args = [dev(oracle.to_bf16_bits(a).view(np.int16)) for a in (q, k, v)]
+        dt = _abi.BF16
+    else:
+        args, dt = [dev(a) for a in (q, k, v)], _abi.F32
+    out = torch.empty((B, sq, hq, d), dtype=torch.float32, device="cuda")
+    KEEP_ALIVE.append(out)
+    _abi.check(lib.sfg_hip_attn_prefill_v1(args[0].data_ptr(), args[1].data_ptr(), args[2].data_ptr(),
+                                           out.data_ptr(), dt, _abi.F32, B, hq, hkv, sq, skv, d,
+                                           int(causal), ctypes.c_float(0.0), None))
+    ref = oracle.attention(q, k, v, causal=causal).transpose(0, 2, 1, 3)  # merged [B][Sq][Hq][D]
+    err = oracle.rel_error(out.cpu().numpy(), ref)
+    print(f"Sq {sq} Skv {skv} causal {causal} Hkv {hkv} {dtype}: rel err {err:.2e}")
+    assert err < TOL["f32"], err
+
+
 @pytest.mark.parametrize("m,n,k,bdt,epi,grouped", [
     (7, 20, 16, "bf16", 0, False), (33, 24, 48, "bf16", 1, False), (65, 40, 16, "i8", 0, False),
     (70, 24, 16, "bf16", 2, False), (50, 12, 40, "f32", 3, True), (40, 16, 24, "i8", 3, True),
