@@ -662,7 +662,9 @@ def _route(lib, x, router, bias, top_k):
                                               # 1024 assignments; a ragged last chunk
                                               (4096, 128, 16, 2, 1.0), (1537, 256, 8, 2, 0.5),
                                               # chunked dispatch: more experts / assignments
-                                              (300, 256, 32, 2, 1.0), (5000, 128, 8, 2, 0.5)])
+                                              (300, 256, 32, 2, 1.0), (5000, 128, 8, 2, 0.5),
+                                              # the reference's MoE test shape (test_schedforge.cpp:617)
+                                              (7, 8, 4, 2, 0.0)])
 def test_moe_route_bit_exact(lib, T, H, E, k, bias_std):
     x = oracle.normal(101, 0, (T, H))
     router = oracle.normal(101, 10, (H, E), 0.02)
@@ -747,10 +749,15 @@ def test_moe_dispatch_trace_skips_out_of_range_experts(lib, T, E):
 
 # ------------------------------------------------------------------ MoE experts + combine
 @pytest.mark.parametrize("wdt", ["bf16", "w8"])
-@pytest.mark.parametrize("T,layout", [(256, 0), (16, 0), (700, 0), (1500, 0), (16, 1), (256, 1)])
-def test_moe_experts_and_combine_match_oracle(lib, wdt, T, layout):
+@pytest.mark.parametrize("T,layout,H,I,E", [(256, 0, 512, 256, 8), (16, 0, 512, 256, 8),
+                                             (700, 0, 512, 256, 8), (1500, 0, 512, 256, 8),
+                                             (16, 1, 512, 256, 8), (256, 1, 512, 256, 8),
+                                             # the reference's MoE test shape, MoeConfig{7, 8, 12, 4, 2}
+                                             # (test_schedforge.cpp:617): k of 8 and 12 take the VALU kernel
+                                             (7, 0, 8, 12, 4)])
+def test_moe_experts_and_combine_match_oracle(lib, wdt, T, layout, H, I, E):
     """Grouped expert GEMMs + combine; layout 1 = fragment-tiled weights (decode sizes only)."""
-    H, I, E, k = 512, 256, 8, 2
+    k = 2
     x = oracle.round_bf16(oracle.normal(111, 0, (T, H)))
     router = oracle.normal(111, 10, (H, E), 0.02)
     bias = oracle.normal(111, 11, (E,), 1.0)
