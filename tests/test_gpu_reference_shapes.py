@@ -258,7 +258,10 @@ def test_reference_attention_test_shapes(sq, skv, causal, hkv, dtype):
     # sizes that select the larger VALU tiles: 64 x 64 (256+ workgroups) and 32 x 32
     (1024, 1024, 48, "f32", 0, False), (512, 512, 40, "f32", 1, False),
     (1024, 1024, 24, "f32", 2, False), (512, 512, 24, "bf16", 3, False),
-    (1024, 256, 40, "i8", 0, True)])
+    (1024, 256, 40, "i8", 0, True),
+    # the reference's int8 matmul test shape, QuantizedMatMulConfig{7, 9, 5}
+    # (test_schedforge.cpp:411), without its bias / ReLU (not on the decoder path)
+    (7, 9, 5, "i8", 0, False), (7, 9, 5, "i8", 1, False)])
 def test_valu_gemm_fallback_is_exact(m, n, k, bdt, epi, grouped):
     """Products the MFMA kernels do not lower (k not a multiple of 32) run on
     the VALU kernel: with small-integer operands every product and partial sum
