@@ -306,7 +306,7 @@ __global__ __launch_bounds__(256) void attn_prefill_bf16_kernel(
                 s_acc[j][r] = sv;
                 tmax = fmaxf(tmax, sv);
             }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        tmax = xor32_max(tmax);
         const float m_new = fmaxf(m_run, tmax);
         const float alpha = (m_run == -INFINITY) ? 0.f : fast_exp2(m_run - m_new);
         float psum = 0.f;
@@ -578,7 +578,7 @@ void attn_prefill_fa2_kernel(Fa2Args p) {
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, s[j][r]);
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64)) * c;
+        tmax = xor32_max(tmax) * c;
         const bool upd = tmax > m_run + 8.0f;
         if (__builtin_amdgcn_ballot_w64(upd)) {
             const float m_new = upd ? tmax : m_run;
@@ -884,8 +884,8 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(
             sv[r] = (ok && tok < len) ? st[r] * scale_log2 : -INFINITY;
             mx = fmaxf(mx, sv[r]);
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        mx = xor16_max(mx);
+        mx = xor32_max(mx);
         const float m_new = fmaxf(m_run, mx);
         if (m_new != -INFINITY) {
             const float alpha = (m_run == -INFINITY) ? 0.f : fast_exp2(m_run - m_new);
@@ -906,8 +906,8 @@ __global__ __launch_bounds__(256) void attn_decode_split_kernel(
         }
     }
 #undef SFG_LOAD_PAGE
-    l_run += __shfl_xor(l_run, 16, 64);
-    l_run += __shfl_xor(l_run, 32, 64);
+    l_run = xor16_sum(l_run);
+    l_run = xor32_sum(l_run);
 
     // Merge the 4 waves in LDS.  acc[dt][r] = O^T[d = 16 dt + 4 lg + r][query lr].
     __shared__ float s_m[4][G], s_l[4][G];

@@ -85,6 +85,27 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// The value lane l ^ 32 (resp. l ^ 16) holds, combined with this lane's by
+// max or +, from v_permlane32_swap (v_permlane16_swap): one VALU op instead
+// of a ds_bpermute round trip through LDS.  Two-operand max and sum are
+// commutative, so each lane gets the same bits as f(v, shfl_xor(v, 32)).
+__device__ __forceinline__ float xor32_max(float v) {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+}
+__device__ __forceinline__ float xor16_max(float v) {
+    const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+}
+__device__ __forceinline__ float xor16_sum(float v) {
+    const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+}
+
 // v_exp_f32: 2^x.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
