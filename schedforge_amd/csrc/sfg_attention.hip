@@ -136,7 +136,7 @@ __global__ __launch_bounds__(256) void attn_prefill_rows_kernel(
             float pt[8], vv[8][4];
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                pt[i] = __shfl(p, t + i, 64);
+                pt[i] = lane_bcast(p, t + i);
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
                     vv[i][r] = lane + 64 * r < head_dim ? sV[(t + i) * head_dim + lane + 64 * r] : 0.f;
@@ -148,7 +148,7 @@ __global__ __launch_bounds__(256) void attn_prefill_rows_kernel(
                     if (lane + 64 * r < head_dim) acc[r] = fmaf(pt[i], vv[i][r], acc[r]);
         }
         for (; t < count; ++t) {
-            const float pt = __shfl(p, t, 64);
+            const float pt = lane_bcast(p, t);
             const float* vr = sV + t * head_dim;
 #pragma unroll
             for (int r = 0; r < 4; ++r)
@@ -1183,8 +1183,8 @@ __global__ __launch_bounds__(64) void attn_paged_rows_kernel(PagedRowsArgs p) {
         for (int r = 0; r < 4; ++r) acc[r] *= alpha;
         const int count = min(64, k1 - base);
         for (int t = 0; t < count; ++t) {
-            const float pt_t = __shfl(pr, t, 64);
-            const int pg = __shfl(page, t, 64);
+            const float pt_t = lane_bcast(pr, t);
+            const int pg = lane_bcast(page, t);
             if (pg < 0) continue;  // wave-uniform
             const int jt = base + t;
             const KvT* vb = vpool + (static_cast<int64_t>(pg) * p.kv_heads + kvh) * D * pt + jt % pt;

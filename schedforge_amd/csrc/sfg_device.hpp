@@ -72,19 +72,6 @@ __device__ __forceinline__ uint4 f32x8_to_bf16x8(const float* v) {
 // reciprocal 0, result -0 (the division's limit).
 __device__ __forceinline__ float silu(float v) { return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v)); }
 
-template <typename T>
-__device__ __forceinline__ T wave_sum(T v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-    return v;
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
-    return v;
-}
-
 // The value lane l ^ 32 (resp. l ^ 16) holds, combined with this lane's by
 // max or +, from v_permlane32_swap (v_permlane16_swap): one VALU op instead
 // of a ds_bpermute round trip through LDS.  Two-operand max and sum are
@@ -105,6 +92,54 @@ __device__ __forceinline__ float xor16_sum(float v) {
     const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
     return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
 }
+
+// The value of lane l ^ X for X = 1, 2, 4, 8, by DPP inside 16-lane rows:
+// quad_perm for 1 and 2, row_ror:8 for 8, and for 4 two moves under bank
+// masks (banks 0 and 2 take lane l + 4 by row_ror:12, banks 1 and 3 lane
+// l - 4 by row_ror:4).
+template <int CTRL, int BANKS = 0xF>
+__device__ __forceinline__ float dpp_mov(float old, float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, 0xF, BANKS, false));
+}
+__device__ __forceinline__ float lane_xor1(float v) { return dpp_mov<0xB1>(v, v); }
+__device__ __forceinline__ float lane_xor2(float v) { return dpp_mov<0x4E>(v, v); }
+__device__ __forceinline__ float lane_xor4(float v) { return dpp_mov<0x124, 0xA>(dpp_mov<0x12C, 0x5>(v, v), v); }
+__device__ __forceinline__ float lane_xor8(float v) { return dpp_mov<0x128>(v, v); }
+
+// Sum and max over the wave by the xor butterfly 32, 16, 8, 4, 2, 1 (each
+// step v op partner), without LDS: the float sum has the same association,
+// hence the same bits, as the same butterfly over __shfl_xor.
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+template <>
+__device__ __forceinline__ float wave_sum<float>(float v) {
+    v = xor32_sum(v);
+    v = xor16_sum(v);
+    v += lane_xor8(v);
+    v += lane_xor4(v);
+    v += lane_xor2(v);
+    v += lane_xor1(v);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+    v = xor32_max(v);
+    v = xor16_max(v);
+    v = fmaxf(v, lane_xor8(v));
+    v = fmaxf(v, lane_xor4(v));
+    v = fmaxf(v, lane_xor2(v));
+    return fmaxf(v, lane_xor1(v));
+}
+
+// Lane `src`'s value in every lane (v_readlane_b32); src must be the same in
+// every lane of the wave.
+__device__ __forceinline__ float lane_bcast(float v, int src) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
+}
+__device__ __forceinline__ int lane_bcast(int v, int src) { return __builtin_amdgcn_readlane(v, src); }
 
 // v_exp_f32: 2^x.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
