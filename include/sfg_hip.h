@@ -428,7 +428,9 @@ typedef struct {
                          * SFG_TILE_AUTO (0) picks per shape.  Same results for every
                          * tile; a plan-policy knob searched by the plan optimiser. */
     int32_t attn_waves; /* bf16 flash prefill (head_dim 128): 4 or 8 waves, i.e. 128 or
-                         * 256 query rows per workgroup; 0: 4.  Same results either way. */
+                         * 256 query rows per workgroup; 0: 8 when the 256-row grid
+                         * holds at least 4 workgroups per CU, else 4.  Same results
+                         * either way. */
 } sfg_layer_desc;
 
 typedef struct {

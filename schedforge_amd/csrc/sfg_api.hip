@@ -191,6 +191,19 @@ int device_xcds(hipStream_t stream) {
     return x;
 }
 
+int device_cus(hipStream_t stream) {
+    // Compute units of the stream's device, cached like device_xcds.
+    static std::atomic<int> cache[kMaxDevices];
+    hipDevice_t dev = 0;
+    if (hipStreamGetDevice(stream, &dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 1;
+    int x = cache[dev].load(std::memory_order_relaxed);
+    if (x == 0) {
+        if (hipDeviceGetAttribute(&x, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || x <= 0) x = 1;
+        cache[dev].store(x, std::memory_order_relaxed);
+    }
+    return x;
+}
+
 }  // namespace sfg
 
 namespace {

@@ -700,7 +700,15 @@ int launch_attn_prefill_vt(const uint16_t* q, const uint16_t* k, const uint16_t*
                            int causal, float scale, int waves_policy, hipStream_t stream) {
     if (head_dim != kFaD) return SFG_ERR_UNSUPPORTED;
     if (ld_vt % kFa2BN != 0 || ld_vt < seq_kv) return SFG_ERR_SHAPE;
-    const int waves = waves_policy == 8 ? 8 : 4;
+    // Policy 0: eight waves (256 query rows, a three-stage K / V^T ring: two
+    // tiles of load latency hidden instead of one) once that grid holds at
+    // least four workgroups per CU; below that the 128-row blocks balance
+    // the causal work better.  Same results either way.
+    int waves = waves_policy;
+    if (waves != 4 && waves != 8) {
+        const int64_t grid8 = (seq_q + 255) / 256 * q_heads * batch;
+        waves = grid8 >= 4 * static_cast<int64_t>(device_cus(stream)) ? 8 : 4;
+    }
     const int bm = waves * 32;
     Fa2Args a{};
     a.q = q; a.k = k; a.vt = vt; a.out = out; a.out_f32 = out_dtype == SFG_F32;

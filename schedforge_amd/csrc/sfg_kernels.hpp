@@ -63,6 +63,8 @@ struct GemmProblem {
 // queried once per device: the dispatcher deals consecutive workgroup ids over
 // them in turn, which the XCD-aware tile orders undo.
 int device_xcds(hipStream_t stream);
+// Compute units of the stream's device (cached per device).
+int device_cus(hipStream_t stream);
 
 bool gemm_qkv_rope_supported(const GemmProblem& p);
 size_t gemm_workspace_bytes(int64_t m, int64_t n, int64_t k);

@@ -122,7 +122,7 @@ struct DecoderPlanPolicy {
     int weight_layout = -1;         // SFG_LAYOUT_NK / SFG_LAYOUT_TILED; -1: per shape
     int kv_splits = 0;              // decode split-KV count; 0: per shape
     int gemm_tile = SFG_TILE_AUTO;  // sfg_gemm_tile of the bf16 prefill / expert GEMMs
-    int attn_waves = 0;             // bf16 flash prefill: 4 or 8 waves; 0: 4
+    int attn_waves = 0;             // bf16 flash prefill: 4 or 8 waves; 0: by grid size
     std::string dump() const;
     bool operator==(const DecoderPlanPolicy&) const = default;
 };

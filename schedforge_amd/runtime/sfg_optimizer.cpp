@@ -146,7 +146,11 @@ struct Terms {
         const double flops = 2.0 * (2.0 * D) * pairs * c.batch * c.query_heads;
         if (f32) return flops / (m.valu_fp32_flops * 0.2) * 1e6 + m.launch_microseconds;
         if (D != 128) return flops / (m.mfma_bf16_flops * 0.15) * 1e6 + m.launch_microseconds;
-        const int waves = q.attn_waves == 8 ? 8 : 4;
+        // policy 0 resolves as the library does: 8 once 256-row blocks give
+        // at least four workgroups per CU
+        const double groups8 = std::ceil(S / 256.0) * c.batch * c.query_heads;
+        const int waves = q.attn_waves == 4 || q.attn_waves == 8 ? q.attn_waves
+                          : (groups8 >= 4.0 * m.compute_units ? 8 : 4);
         const double block_rows = 32.0 * waves;
         const double groups = std::ceil(S / block_rows) * c.batch * c.query_heads;
         const double slots = m.compute_units * (waves == 4 ? 2.0 : 1.0);
@@ -261,7 +265,7 @@ std::vector<DecoderPlanPolicy> ExecutablePlanOptimizer::policies(const DecoderCo
                 add(p);
             }
     } else if (c.precision == DecoderPrecision::BF16 && c.rows() >= kBigMinRows) {
-        const std::vector<int> waves = c.head_dim == 128 ? std::vector<int>{0, 8} : std::vector<int>{0};
+        const std::vector<int> waves = c.head_dim == 128 ? std::vector<int>{0, 4, 8} : std::vector<int>{0};
         for (int tile = SFG_TILE_AUTO; tile < SFG_TILE_COUNT; ++tile)
             for (const int w : waves) {
                 DecoderPlanPolicy p;

@@ -144,7 +144,7 @@ def test_layer_every_plan_policy_is_bit_identical():
     both flash-prefill block heights give the same bits (dense prefill with the
     fused QKV+RoPE epilogue, and the grouped expert GEMMs under a routing trace)."""
     from schedforge_amd import _abi
-    policies = [(0, 0)] + [(t, 0) for t in range(1, _abi.TILE_COUNT)] + [(0, 8), (_abi.TILE_128x128, 8)]
+    policies = [(0, 0)] + [(t, 0) for t in range(1, _abi.TILE_COUNT)] + [(0, 4), (0, 8), (_abi.TILE_128x128, 8)]
     dense = CONFIGS["c4"].replace(sequence=1024, hidden=1024, intermediate=2048, query_heads=8,
                                   kv_heads=2)
     # two sequences of 600: batch boundaries and the last row tile fall inside
