@@ -100,3 +100,36 @@ def test_c5_full_size_matches_oracle():
                     TOL["w8"], "c5 full, device routing (rows routed alike)")
     res2, taps2 = _rerun(plan, d.input, (rt["ids"], rt["weights"]))
     assert_branches(d.input, res2.output, taps2, ref, rt, TOL["w8"], "c5 full, routing trace")
+
+
+@pytest.mark.parametrize("name", ["c5", "c2"])
+def test_full_size_decode_is_exact_under_page_layout_and_batch_order(name):
+    """Two exact properties of a full-size decode step, every stage of which
+    works per row or per sequence (attention per sequence over its own pages,
+    projections, norms, routing and expert products per row):
+      - where the pages sit in the pool does not matter: a second physical
+        layout of the same logical caches gives the same bits;
+      - reversing the order of the sequences (inputs and their caches)
+        reverses the output rows, bit for bit."""
+    import copy
+    from schedforge_amd.layer import compile_decoder, execute_decoder_layer
+    cfg = CONFIGS[name]
+    d = oracle.make_layer_data(cfg, CONFIG_SEEDS[name] + 41)
+
+    def run(dd, perm):
+        plan = compile_decoder(cfg, decoder_data(dd), "cuda", page_permutation=perm)
+        out = execute_decoder_layer(plan, dd.input, warmup=0, repetitions=1).output
+        del plan
+        torch.cuda.empty_cache()
+        return out
+
+    base = run(d, d.page_permutation)
+    assert np.isfinite(base).all()
+    moved = np.roll(d.page_permutation, 12345)  # same logical pages, other physical slots
+    assert not np.array_equal(moved, d.page_permutation)
+    assert np.array_equal(run(d, moved), base), "output depends on the physical page layout"
+    rev = copy.copy(d)
+    rev.input = np.ascontiguousarray(d.input[::-1])
+    rev.cached_key = np.ascontiguousarray(d.cached_key[::-1])
+    rev.cached_value = np.ascontiguousarray(d.cached_value[::-1])
+    assert np.array_equal(run(rev, d.page_permutation), base[::-1]), "batch order changes a row's bits"
