@@ -157,3 +157,32 @@ def test_c3_full_size_prefill_is_exact_under_batch_order():
     rev_in = np.ascontiguousarray(d.input.reshape(B, S, H)[::-1].reshape(B * S, H))
     rev_out = run(rev_in).reshape(B, S, H)[::-1].reshape(B * S, H)
     assert np.array_equal(rev_out, base), "sequence order changes a row's bits"
+
+
+def test_c4_full_size_prefill_is_causal_and_prefix_consistent():
+    """Two exact properties of the full C4 prefill (one sequence of 8192):
+      - causality: changing the second half of the input leaves the first
+        half's output bits as they were (masked keys add exact zeros);
+      - prefix consistency: the first 4096 rows run as a sequence of their own
+        give the same bits as in the full sequence, though the two shapes
+        take other GEMM tiles and flash block heights (every such policy
+        computes the same arithmetic)."""
+    from schedforge_amd.layer import compile_decoder, execute_decoder_layer
+    cfg = CONFIGS["c4"]
+    d = oracle.make_layer_data(cfg, CONFIG_SEEDS["c4"] + 41)
+    half = cfg.sequence // 2
+
+    def run(c, x):
+        plan = compile_decoder(c, decoder_data(d), "cuda", page_permutation=None)
+        out = execute_decoder_layer(plan, x, warmup=0, repetitions=1).output
+        del plan
+        torch.cuda.empty_cache()
+        return out
+
+    base = run(cfg, d.input)
+    assert np.isfinite(base).all()
+    changed = d.input.copy()
+    changed[half:] = changed[half:][::-1] * np.float32(1.5)
+    assert np.array_equal(run(cfg, changed)[:half], base[:half]), "a later row changed an earlier output"
+    prefix = run(cfg.replace(sequence=half), np.ascontiguousarray(d.input[:half]))
+    assert np.array_equal(prefix, base[:half]), "the prefix as its own sequence differs"
