@@ -159,8 +159,10 @@ def test_c3_full_size_prefill_is_exact_under_batch_order():
     assert np.array_equal(rev_out, base), "sequence order changes a row's bits"
 
 
-def test_c4_full_size_prefill_is_causal_and_prefix_consistent():
-    """Two exact properties of the full C4 prefill (one sequence of 8192):
+@pytest.mark.parametrize("name", ["c4", "c1"])
+def test_full_size_prefill_is_causal_and_prefix_consistent(name):
+    """Two exact properties of the full C4 prefill (one sequence of 8192) and
+    of C1's fp32 one (one sequence of 128):
       - causality: changing the second half of the input leaves the first
         half's output bits as they were (masked keys add exact zeros);
       - prefix consistency: the first 4096 rows run as a sequence of their own
@@ -168,8 +170,8 @@ def test_c4_full_size_prefill_is_causal_and_prefix_consistent():
         take other GEMM tiles and flash block heights (every such policy
         computes the same arithmetic)."""
     from schedforge_amd.layer import compile_decoder, execute_decoder_layer
-    cfg = CONFIGS["c4"]
-    d = oracle.make_layer_data(cfg, CONFIG_SEEDS["c4"] + 41)
+    cfg = CONFIGS[name]
+    d = oracle.make_layer_data(cfg, CONFIG_SEEDS[name] + 41)
     half = cfg.sequence // 2
 
     def run(c, x):
