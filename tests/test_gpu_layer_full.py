@@ -13,6 +13,10 @@ The reference checks execute_once against reference_decoder_layer at any shape
 Every check compares the output and, on their own scales, the attention
 output and both residual branches (tests/_helpers.py branch_errors).
 Tolerances: bf16 2e-2, int8 weights 1e-2 (max|got - ref| / max|ref|).
+Exact properties at full size, bit for bit and without the oracle: decode
+(C5, C2) under another physical page layout and under reversed batch order,
+the MoE prefill (C3) under reversed sequence order, and the causal prefills
+(C4, C1) under a changed suffix and with a prefix run as its own sequence.
 """
 from __future__ import annotations
 
