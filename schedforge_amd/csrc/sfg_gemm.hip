@@ -2401,19 +2401,23 @@ int launch_gemm(const GemmProblem& problem, void* workspace, size_t workspace_by
         }
         return SFG_OK;
     }
-    // The skinny kernel streams K in 128-element chunks; other K go tiled.
-    const bool skinny = p.k % kSkinnyChunk == 0 &&
-                        (p.offsets ? (p.m <= kSkinnyGroupedMaxTotal) : (p.m <= kSkinnyMaxRows));
+    // The skinny kernel streams K in 128-element chunks and writes whole
+    // 16-column tiles; other K, and an N its tiles do not divide, go to the
+    // tiled or VALU kernels (which mask a ragged last column tile) when B is
+    // [N][K].  Fragment-tiled B is read by the skinny kernel only.
+    const bool skinny_rows = p.k % kSkinnyChunk == 0 &&
+                             (p.offsets ? (p.m <= kSkinnyGroupedMaxTotal) : (p.m <= kSkinnyMaxRows));
+    // grouped problems: 32 rows per pass covers the typical decode expert
+    const int64_t rows_hint = p.offsets ? 32 : p.m;
+    // grouped: four B tiles per workgroup (GLU: two gate + two up) halve
+    // the activation re-reads per weight byte
+    const bool g4 = p.offsets && p.n % (glu ? 32 : 64) == 0;
+    const int nbt = g4 ? 4 : (glu ? 2 : (rows_hint <= 16 ? 1 : 2));
+    const int64_t tile_cols = glu ? 16 * nbt / 2 : 16 * nbt;
+    const bool skinny = skinny_rows && p.n % tile_cols == 0;
+    if (skinny_rows && !skinny && p.b_layout == SFG_LAYOUT_TILED) return SFG_ERR_UNSUPPORTED;
     if (skinny) {
-        // grouped problems: 32 rows per pass covers the typical decode expert
-        const int64_t rows_hint = p.offsets ? 32 : p.m;
         const int mt = rows_hint <= 16 ? 1 : (rows_hint <= 32 ? 2 : 4);
-        // grouped: four B tiles per workgroup (GLU: two gate + two up) halve
-        // the activation re-reads per weight byte
-        const bool g4 = p.offsets && p.n % (glu ? 32 : 64) == 0;
-        const int nbt = g4 ? 4 : (glu ? 2 : (rows_hint <= 16 ? 1 : 2));
-        const int64_t tile_cols = glu ? 16 * nbt / 2 : 16 * nbt;
-        if (p.n % tile_cols != 0) return SFG_ERR_UNSUPPORTED;
         // A grouped launch already has groups x N/16 workgroups, several per
         // CU: two waves each keeps the K split (and its LDS reduction) short.
         // So does a 16-row GLU product up to K = 2048 (two load batches per

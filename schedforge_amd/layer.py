@@ -191,12 +191,14 @@ def compile_decoder(config: DecoderConfig, data: DecoderData, device="cuda",
     t["rms1"] = _dev(data.rms1_weight, plan.device)
     t["rms2"] = _dev(data.rms2_weight, plan.device)
     # One weight layout for the whole plan: fragment-tiled when every product
-    # runs on the decode (skinny) kernel, [N][K] otherwise.
+    # runs on the decode (skinny) kernel -- every depth takes it and every
+    # width is a multiple of 64, which its 16-, 32- and 64-column tiles
+    # divide -- [N][K] otherwise.
     layout = _abi.LAYOUT_NK
     if wdt != F32:
         ks = [H, I]
         tiled = all(lib.sfg_hip_preferred_weight_layout_v1(cfg.rows, k, 0) == _abi.LAYOUT_TILED
-                    for k in ks)
+                    for k in ks) and all(n % 64 == 0 for n in (cfg.qkv_width, H, I))
         if cfg.moe:
             tiled = tiled and all(lib.sfg_hip_preferred_weight_layout_v1(
                 cfg.rows * cfg.top_k, k, 1) == _abi.LAYOUT_TILED for k in ks)

@@ -600,8 +600,12 @@ DecoderExecutablePlan DecoderCompiler::compile(const DecoderConfig& config, cons
     // runs on the decode GEMV kernels, [N][K] otherwise.
     int layout = SFG_LAYOUT_NK;
     if (c.precision != DecoderPrecision::F32) {
+        // (and every product's width a multiple of 64, which each of the
+        // GEMV kernels' 16-, 32- and 64-column tiles divides)
+        const int64_t qkv_n = H + 2 * static_cast<int64_t>(c.kv_heads) * c.head_dim;
         bool tiled = dev.lib->preferred_layout(rows, H, 0) == SFG_LAYOUT_TILED &&
-                     dev.lib->preferred_layout(rows, I, 0) == SFG_LAYOUT_TILED;
+                     dev.lib->preferred_layout(rows, I, 0) == SFG_LAYOUT_TILED &&
+                     qkv_n % 64 == 0 && H % 64 == 0 && I % 64 == 0;
         if (moe)
             tiled = tiled && dev.lib->preferred_layout(rows * c.top_k, H, 1) == SFG_LAYOUT_TILED &&
                     dev.lib->preferred_layout(rows * c.top_k, I, 1) == SFG_LAYOUT_TILED;
