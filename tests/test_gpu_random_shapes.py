@@ -8,6 +8,13 @@ decoder accepts them (decoder_compiler.cpp:26-39 validate) -- 24 layers:
   of 1..300 tokens, pages of 4, 8 or 16 tokens), dense or MoE (2..8 experts,
   top-1 or top-2), f32 / bf16 / int8 weights, head_dim 4..128, GQA groups
   1..4, ragged sequence lengths and FFN widths.
+A second generator draws 12 layers onto the bf16 / int8 MFMA paths, at sizes
+where the oracle still takes about a second: prefill of 512..2100 rows in 1..4
+ragged sequences at head_dim 64 or 128 (the fused QKV + RoPE epilogue from
+1024 rows, the flash kernels), and decode of one or two new tokens for 1..64
+sequences over up to 3000 cached tokens in 16-token pages (the MFMA split-KV
+kernel and the decode GEMVs), GQA groups 1..16, FFN widths that are and are
+not multiples of the GEMM tiles.
 Each layer is checked like the reduced configurations: the output, the
 attention output and both residual branches against the oracle (MoE under
 the oracle's routing trace, and routed on the device with rows whose oracle
@@ -62,7 +69,44 @@ def random_configs(n=24, seed=SEED):
     return out
 
 
+def mfma_path_configs(n=12, seed=SEED + 1):
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        head_dim = int(rng.choice([64, 128]))
+        kv_heads = int(rng.choice([1, 2, 4]))
+        group = int(rng.choice([1, 2, 3, 4, 8, 16]))
+        while kv_heads * group * head_dim > 2048:
+            if group > 1:
+                group //= 2
+            else:
+                kv_heads //= 2
+        moe = bool(rng.random() < 0.5)
+        experts = int(rng.choice([2, 4, 8, 16]))
+        decode = bool(rng.random() < 0.5)
+        width = (int(rng.choice([64, 128, 256, 512, 1024, 1408, 2048])) if rng.random() < 0.7
+                 else int(8 * rng.integers(8, 257)))
+        kw = dict(hidden=kv_heads * group * head_dim, query_heads=kv_heads * group,
+                  kv_heads=kv_heads, head_dim=head_dim, intermediate=width,
+                  dtype=str(rng.choice(["bf16", "w8"])) if decode else "bf16",
+                  ffn="moe" if moe else "dense", experts=experts,
+                  top_k=int(min(experts, rng.integers(1, 5))))
+        if decode:
+            new_tokens = int(rng.choice([1, 1, 1, 1, 2]))
+            kw.update(batch=int(rng.integers(1, 65)), sequence=new_tokens,
+                      context_sequence=int(rng.integers(new_tokens, 3001)), page_tokens=16)
+        else:
+            batch = int(rng.integers(1, 5))
+            kw.update(batch=batch, sequence=int(rng.integers(max(1, 512 // batch), 2100 // batch + 1)),
+                      context_sequence=0)
+        cfg = CONFIGS["c1"].replace(**kw)
+        cfg.validate()
+        out.append(cfg)
+    return out
+
+
 CASES = random_configs()
+MFMA_CASES = mfma_path_configs()
 
 
 def _label(cfg):
@@ -73,13 +117,11 @@ def _label(cfg):
             f"D{cfg.head_dim} I{cfg.intermediate} {ffn}")
 
 
-@pytest.mark.parametrize("idx", range(len(CASES)), ids=[f"case{i}" for i in range(len(CASES))])
-def test_random_layer_matches_oracle(idx):
+def _check_layer(cfg, seed):
     from schedforge_amd.layer import compile_decoder, execute_decoder_layer, layer_taps
-    cfg = CASES[idx]
     label = _label(cfg)
     print(label, flush=True)
-    d = oracle.make_layer_data(cfg, SEED + idx)
+    d = oracle.make_layer_data(cfg, seed)
     ref, rt = oracle.decoder_layer(cfg, d, taps=True)
     plan = compile_decoder(cfg, decoder_data(d), "cuda", page_permutation=d.page_permutation)
     res = execute_decoder_layer(plan, d.input, warmup=0, repetitions=1)
@@ -99,6 +141,17 @@ def test_random_layer_matches_oracle(idx):
     plan.desc.use_routing_trace = 1
     res2 = execute_decoder_layer(plan, d.input, warmup=0, repetitions=1)
     assert_branches(d.input, res2.output, layer_taps(plan), ref, rt, tol, label + ", routing trace")
+
+
+@pytest.mark.parametrize("idx", range(len(CASES)), ids=[f"case{i}" for i in range(len(CASES))])
+def test_random_layer_matches_oracle(idx):
+    _check_layer(CASES[idx], SEED + idx)
+
+
+@pytest.mark.parametrize("idx", range(len(MFMA_CASES)),
+                         ids=[f"mfma{i}" for i in range(len(MFMA_CASES))])
+def test_random_mfma_path_layer_matches_oracle(idx):
+    _check_layer(MFMA_CASES[idx], SEED + 200 + idx)
 
 
 def test_append_decode_with_a_qkv_width_the_gemv_tiles_do_not_divide():
