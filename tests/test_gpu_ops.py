@@ -761,12 +761,55 @@ def test_moe_experts_and_combine_match_oracle(lib, wdt, T, layout, H, I, E):
     x = oracle.round_bf16(oracle.normal(111, 0, (T, H)))
     router = oracle.normal(111, 10, (H, E), 0.02)
     bias = oracle.normal(111, 11, (E,), 1.0)
-    w1 = oracle.normal(111, 12, (E, H, I), 0.02)
-    w3 = oracle.normal(111, 13, (E, H, I), 0.02)
-    w2 = oracle.normal(111, 14, (E, I, H), 0.02)
-    if wdt == "bf16":
-        w1, w3, w2 = (oracle.round_bf16(w) for w in (w1, w3, w2))
     ids, w, counts, offsets, tok, slots, rw, pos = _route(lib, x, router, bias, k)
+    _check_experts_and_combine(lib, wdt, layout, x, ids, w, offsets, tok, pos, H, I, E, k)
+
+
+def _dispatch_trace(lib, ids, w, E):
+    T, k = ids.shape
+    counts = torch.empty(E, dtype=torch.int32, device="cuda")
+    offsets = torch.empty(E + 1, dtype=torch.int32, device="cuda")
+    tok = torch.empty(T * k, dtype=torch.int32, device="cuda")
+    slots = torch.empty(T * k, dtype=torch.int32, device="cuda")
+    rw = torch.empty(T * k, dtype=torch.float32, device="cuda")
+    pos = torch.empty(T * k, dtype=torch.int32, device="cuda")
+    _abi.check(lib.sfg_hip_moe_dispatch_trace_v1(dev(ids).data_ptr(), dev(w).data_ptr(), T, E, k,
+                                                 counts.data_ptr(), offsets.data_ptr(),
+                                                 tok.data_ptr(), slots.data_ptr(), rw.data_ptr(),
+                                                 pos.data_ptr(), stream()))
+    _sync()
+    return host(counts), host(offsets), host(tok), host(pos)
+
+
+@pytest.mark.parametrize("wdt", ["bf16", "w8"])
+@pytest.mark.parametrize("T,layout", [(16, 1), (256, 1), (256, 0), (1500, 0)])
+def test_moe_experts_with_every_token_on_two_experts(lib, wdt, T, layout):
+    """The most skewed routing a top-2 trace can give: every token on experts
+    0 and E - 1, the six experts between them empty.  One group then holds T
+    rows -- 16 and 256 rows take the grouped decode GEMV (256 x 2 = 512
+    assignments is its largest grouped problem, 16 passes of 32 rows over one
+    expert), 1500 rows the grouped MFMA tiles -- while the empty groups launch
+    workgroups that must store nothing."""
+    H, I, E, k = 512, 256, 8, 2
+    x = oracle.round_bf16(oracle.normal(113, 0, (T, H)))
+    rng = np.random.default_rng(113)
+    ids = np.where(rng.random((T, 1)) < 0.5, [[0, E - 1]], [[E - 1, 0]]).astype(np.int32)
+    w = rng.random((T, k)).astype(np.float32)
+    w /= w.sum(axis=1, keepdims=True)
+    counts, offsets, tok, pos = _dispatch_trace(lib, ids, w, E)
+    assert counts[0] == T and counts[E - 1] == T and counts[1:E - 1].sum() == 0
+    _check_experts_and_combine(lib, wdt, layout, x, ids, w, offsets, tok, pos, H, I, E, k, seed=113)
+
+
+def _check_experts_and_combine(lib, wdt, layout, x, ids, w, offsets, tok, pos, H, I, E, k, seed=111):
+    """Grouped expert GEMMs (sfg_hip_moe_experts_v1) and the weighted combine
+    for a routing (ids, w) already dispatched, against the oracle's MoE."""
+    T = x.shape[0]
+    w1 = oracle.normal(seed, 12, (E, H, I), 0.02)
+    w3 = oracle.normal(seed, 13, (E, H, I), 0.02)
+    w2 = oracle.normal(seed, 14, (E, I, H), 0.02)
+    if wdt == "bf16":
+        w1, w3, w2 = (oracle.round_bf16(m) for m in (w1, w3, w2))
     # device weights in [E][2I][H] / [E][H][I]
     if wdt == "bf16":
         w13 = np.concatenate([w1.transpose(0, 2, 1), w3.transpose(0, 2, 1)], axis=1)
@@ -796,7 +839,7 @@ def test_moe_experts_and_combine_match_oracle(lib, wdt, T, layout, H, I, E):
                                           w2d.data_ptr(), s2d.data_ptr() if s2d is not None else None,
                                           dt, layout, act.data_ptr(), y.data_ptr(), T, H, I, E, k, None, 0,
                                           stream()))
-    resid = oracle.normal(111, 5, (T, H))
+    resid = oracle.normal(seed, 5, (T, H))
     out = torch.empty((T, H), dtype=torch.float32, device="cuda")
     _abi.check(lib.sfg_hip_moe_combine_v1(y.data_ptr(), dev(pos).data_ptr(), dev(w).data_ptr(),
                                           dev(resid).data_ptr(), out.data_ptr(), T, H, k, stream()))
