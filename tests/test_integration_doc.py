@@ -1,7 +1,7 @@
-"""INTEGRATION.md's reference-side C++ binding compiles against include/sfg_hip.h
-(CPU only): every ```cpp block of the file, in order, as one translation unit,
-checked with g++ -std=c++20 -fsyntax-only -- so a stub call with the wrong
-number or type of arguments fails here."""
+"""The integration guide's reference-side C++ binding compiles against
+include/sfg_hip.h (CPU only): every ```cpp block of the guide, in order, as one
+translation unit, checked with g++ -std=c++20 -fsyntax-only -- so a stub call
+with the wrong number or type of arguments fails here."""
 from __future__ import annotations
 
 import re
