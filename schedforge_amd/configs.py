@@ -146,7 +146,8 @@ def algorithmic_work(cfg: DecoderConfig, expert_rows: int | None = None) -> dict
     else:
         ffn_flops = 6 * rows * H * I
         ffn_w = 3 * H * I * wbytes
-    kv_bytes = 2 * cfg.batch * cfg.kv_heads * cfg.context_sequence * D * 2 if cfg.decode else 0
+    # the paged pools hold the activation dtype: fp32 on the fp32 path, bf16 otherwise
+    kv_bytes = 2 * cfg.batch * cfg.kv_heads * cfg.context_sequence * D * abytes if cfg.decode else 0
     act_bytes = rows * H * 4 * 2  # x in, out
     return {
         "flops": proj_flops + attn_flops + ffn_flops,
