@@ -14,7 +14,9 @@ ragged sequences at head_dim 64 or 128 (the fused QKV + RoPE epilogue from
 1024 rows, the flash kernels), and decode of one or two new tokens for 1..64
 sequences over up to 3000 cached tokens in 16-token pages (the MFMA split-KV
 kernel and the decode GEMVs), GQA groups 1..16, FFN widths that are and are
-not multiples of the GEMM tiles.
+not multiples of the GEMM tiles.  A third draws 8 append-mode decode steps
+(the step's K / V stored into the pools first, 1..5 new tokens over 1..300
+cached ones, pages of 1..32 tokens).
 Each layer is checked like the reduced configurations: the output, the
 attention output and both residual branches against the oracle (MoE under
 the oracle's routing trace, and routed on the device with rows whose oracle
@@ -105,12 +107,42 @@ def mfma_path_configs(n=12, seed=SEED + 1):
     return out
 
 
+def append_configs(n=8, seed=SEED + 2):
+    """Append-mode decode steps (the step's K / V go into the paged pools at
+    their true positions first, then the step attends over them): 1..5 new
+    tokens over 1..300 cached ones -- more new tokens than cached ones too --
+    in pages of 1..32 tokens, with room left in the page tables."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        head_dim = int(rng.choice([4, 12, 32, 64, 80, 128]))
+        kv_heads = int(rng.choice([1, 2, 4]))
+        group = int(rng.choice([1, 2, 4]))
+        moe = bool(rng.random() < 0.5)
+        experts = int(rng.choice([2, 4, 8]))
+        new_tokens = int(rng.choice([1, 2, 3, 5]))
+        context = int(rng.integers(1, 301))
+        cfg = CONFIGS["c1"].replace(
+            batch=int(rng.integers(1, 9)), sequence=new_tokens, context_sequence=context,
+            page_tokens=int(rng.choice([1, 4, 16, 32])), kv_append=True,
+            kv_capacity=context + new_tokens + int(rng.integers(0, 40)),
+            hidden=kv_heads * group * head_dim, query_heads=kv_heads * group, kv_heads=kv_heads,
+            head_dim=head_dim, intermediate=int(8 * rng.integers(2, 65)),
+            dtype=str(rng.choice(["f32", "bf16", "w8"])), ffn="moe" if moe else "dense",
+            experts=experts, top_k=int(min(experts, rng.choice([1, 2]))))
+        cfg.validate()
+        out.append(cfg)
+    return out
+
+
 CASES = random_configs()
 MFMA_CASES = mfma_path_configs()
+APPEND_CASES = append_configs()
 
 
 def _label(cfg):
-    mode = f"decode S{cfg.sequence} ctx{cfg.context_sequence} p{cfg.page_tokens}" if cfg.decode \
+    mode = (f"decode{' append' if cfg.kv_append else ''} S{cfg.sequence} "
+            f"ctx{cfg.context_sequence} p{cfg.page_tokens}") if cfg.decode \
         else f"prefill B{cfg.batch} S{cfg.sequence}"
     ffn = f"moe E{cfg.experts} k{cfg.top_k}" if cfg.moe else "dense"
     return (f"{mode} {cfg.dtype} H{cfg.hidden} Hq{cfg.query_heads} Hkv{cfg.kv_heads} "
@@ -123,7 +155,9 @@ def _check_layer(cfg, seed):
     print(label, flush=True)
     d = oracle.make_layer_data(cfg, seed)
     ref, rt = oracle.decoder_layer(cfg, d, taps=True)
-    plan = compile_decoder(cfg, decoder_data(d), "cuda", page_permutation=d.page_permutation)
+    # an append plan sizes its page tables for the capacity: identity pages
+    perm = None if cfg.kv_append else d.page_permutation
+    plan = compile_decoder(cfg, decoder_data(d), "cuda", page_permutation=perm)
     res = execute_decoder_layer(plan, d.input, warmup=0, repetitions=1)
     taps = layer_taps(plan)
     assert np.isfinite(res.output).all(), label
@@ -133,12 +167,21 @@ def _check_layer(cfg, seed):
         return
     differ = check_device_routing(taps, rt, d.router_weight, d.router_bias, cfg.top_k)
     same = np.setdiff1d(np.arange(cfg.rows), differ)
-    sel = lambda t: {k: v[same] for k, v in t.items() if k != "counts"}
+    # row-indexed taps only (an append step's oracle taps also hold the new
+    # K / V per sequence)
+    sel = lambda t: {k: v[same] for k, v in t.items()
+                     if k != "counts" and np.ndim(v) == 2 and len(v) == cfg.rows}
     assert_branches(d.input[same], res.output[same], sel(taps), ref[same], sel(rt), tol,
                     label + ", device routing")
-    plan.t["trace_ids"] = torch.from_numpy(np.ascontiguousarray(rt["ids"], np.int32)).cuda()
-    plan.t["trace_weights"] = torch.from_numpy(np.ascontiguousarray(rt["weights"], np.float32)).cuda()
-    plan.desc.use_routing_trace = 1
+    if cfg.kv_append:
+        # an append step advances the plan's cached lengths: the trace run
+        # starts again from the same cache in a plan of its own
+        d.routing_trace = (rt["ids"], rt["weights"])
+        plan = compile_decoder(cfg, decoder_data(d), "cuda", page_permutation=perm)
+    else:
+        plan.t["trace_ids"] = torch.from_numpy(np.ascontiguousarray(rt["ids"], np.int32)).cuda()
+        plan.t["trace_weights"] = torch.from_numpy(np.ascontiguousarray(rt["weights"], np.float32)).cuda()
+        plan.desc.use_routing_trace = 1
     res2 = execute_decoder_layer(plan, d.input, warmup=0, repetitions=1)
     assert_branches(d.input, res2.output, layer_taps(plan), ref, rt, tol, label + ", routing trace")
 
@@ -152,6 +195,12 @@ def test_random_layer_matches_oracle(idx):
                          ids=[f"mfma{i}" for i in range(len(MFMA_CASES))])
 def test_random_mfma_path_layer_matches_oracle(idx):
     _check_layer(MFMA_CASES[idx], SEED + 200 + idx)
+
+
+@pytest.mark.parametrize("idx", range(len(APPEND_CASES)),
+                         ids=[f"append{i}" for i in range(len(APPEND_CASES))])
+def test_random_append_step_matches_oracle(idx):
+    _check_layer(APPEND_CASES[idx], SEED + 300 + idx)
 
 
 def test_append_decode_with_a_qkv_width_the_gemv_tiles_do_not_divide():
