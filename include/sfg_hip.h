@@ -174,7 +174,10 @@ int sfg_hip_rmsnorm_v1(const float* x, const float* w, void* y, int y_dtype, int
  * rows with k a multiple of 512 (>= 1024) and N (2N for GLU) a multiple of
  * 128: those run split-K over 512-k slices with fp32 partial sums in the
  * workspace, summed in slice order.  With a smaller workspace (or NULL) the
- * same shapes run the single-pass decode kernel instead. */
+ * same shapes run the single-pass decode kernel instead.
+ * b_layout SFG_LAYOUT_TILED is read by the decode GEMV only: bf16 / int8 B,
+ * at most 64 rows (grouped: 512 in all), K % 128 == 0 and N % 16 == 0;
+ * other shapes with tiled B return SFG_ERR_UNSUPPORTED. */
 typedef struct {
     const void* a; int32_t a_dtype; int64_t lda;
     const void* b; int32_t b_dtype; int64_t ldb; const float* b_scales;

@@ -1522,7 +1522,12 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
     const int slot16 = piece * kDmaBytes / 16;
     const int sub = (piece % (16 / kDmaBytes)) * (kDmaBytes / 2);  // bf16 offset inside the 16-byte slot
     auto chunk_of = [&](int local_row) { return ((slot16 ^ ((local_row >> 2) & 3)) * 8) + sub; };
-    const buf_rsrc ra = make_rsrc(p.a, static_cast<uint32_t>(p.a_rows_limit * p.lda * 2));
+    // A gathered id outside [0, a_rows_limit) is a zero row: its loads start
+    // at the end of A's resource, so every slab of it reads the zeros an
+    // out-of-range buffer load returns (the host keeps that offset plus any
+    // k offset inside 32 bits).
+    const uint32_t a_bytes = static_cast<uint32_t>(p.a_rows_limit * p.lda * 2);
+    const buf_rsrc ra = make_rsrc(p.a, a_bytes);
     uint32_t a_off[kLoadsA];
 #pragma unroll
     for (int i = 0; i < kLoadsA; ++i) {
@@ -1530,8 +1535,8 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
         const int64_t r = row0 + local;
         int64_t src = r < re ? r : row0;
         if (p.a_rows) src = p.a_rows[src];
-        if (src < 0 || src >= p.a_rows_limit) src = 0;
-        a_off[i] = static_cast<uint32_t>((src * p.lda + chunk_of(local)) * 2);
+        a_off[i] = (src < 0 || src >= p.a_rows_limit) ? a_bytes
+                                                      : static_cast<uint32_t>((src * p.lda + chunk_of(local)) * 2);
     }
     const uint16_t* bbase = static_cast<const uint16_t*>(p.b) + bgroup;
     const buf_rsrc rb_ = make_rsrc(bbase, static_cast<uint32_t>((kGlu ? 2 : 1) * p.n * p.ldb * 2));
@@ -1681,8 +1686,8 @@ void gemm_dma_kernel(TiledArgs p, int tiles_m, int tiles_n) {
             const int64_t r = row0 + local;
             int64_t src = r < re ? r : row0;
             if (p.a_rows) src = p.a_rows[src];
-            if (src < 0 || src >= p.a_rows_limit) src = 0;
-            dma_a[i] = static_cast<uint32_t>((src * p.lda + chunk * 8) * 2);
+            dma_a[i] = (src < 0 || src >= p.a_rows_limit) ? a_bytes  // zero row, as above
+                                                          : static_cast<uint32_t>((src * p.lda + chunk * 8) * 2);
             int64_t brow;
             if (kGlu) {
                 const int block = local >> 5;
@@ -2412,7 +2417,8 @@ int launch_gemm(const GemmProblem& problem, void* workspace, size_t workspace_by
     // grouped: four B tiles per workgroup (GLU: two gate + two up) halve
     // the activation re-reads per weight byte
     const bool g4 = p.offsets && p.n % (glu ? 32 : 64) == 0;
-    const int nbt = g4 ? 4 : (glu ? 2 : (rows_hint <= 16 ? 1 : 2));
+    int nbt = g4 ? 4 : (glu ? 2 : (rows_hint <= 16 ? 1 : 2));
+    if (!glu && !g4 && p.n % (16 * nbt) != 0) nbt = 1;  // widths of an odd number of 16-column tiles
     const int64_t tile_cols = glu ? 16 * nbt / 2 : 16 * nbt;
     const bool skinny = skinny_rows && p.n % tile_cols == 0;
     if (skinny_rows && !skinny && p.b_layout == SFG_LAYOUT_TILED) return SFG_ERR_UNSUPPORTED;
@@ -2458,8 +2464,10 @@ int launch_gemm(const GemmProblem& problem, void* workspace, size_t workspace_by
     a.m = p.m; a.n = p.n; a.k = p.k; a.offsets = p.offsets; a.groups = groups;
     a.qkv = p.qkv;
     a.xcds = p.xcds;
-    // the direct-to-LDS kernel addresses each operand with 32-bit byte offsets
-    const bool fits32 = static_cast<uint64_t>(a.a_rows_limit) * p.lda * 2 <= 0xFFFFFFFFull &&
+    // the direct-to-LDS kernel addresses each operand with 32-bit byte offsets;
+    // a gathered zero row's loads sit at A's end plus the k offset
+    const bool fits32 = static_cast<uint64_t>(a.a_rows_limit) * p.lda * 2 +
+                                (p.a_rows ? static_cast<uint64_t>(p.k) * 2 + 64 : 0) <= 0xFFFFFFFFull &&
                         static_cast<uint64_t>(glu ? 2 : 1) * p.n * p.ldb * 2 <= 0xFFFFFFFFull;
     if (big && fits32 && p.b_dtype == SFG_BF16) {
         const DmaShape sh = pick_dma_shape(p.m, p.n, glu, groups, p.tile);

@@ -291,6 +291,92 @@ def test_gemm_rejects_bad_shapes(lib):
         _abi.check(lib.sfg_hip_gemm_v1(ctypes.byref(args), None, 0, stream()))
 
 
+@pytest.mark.parametrize("wdt", ["bf16", "i8"])
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("m,epi", [(20, EPI_NONE), (48, EPI_RESIDUAL), (64, EPI_NONE)])
+def test_gemm_decode_gemv_widths_of_an_odd_number_of_16_column_tiles(lib, wdt, layout, m, epi):
+    """17..64 decode rows take the decode GEMV on 32-column tiles; a width of
+    624 = 39 x 16 columns runs it on 16-column tiles instead (with [N][K] and
+    fragment-tiled weights alike), exact on small-integer operands."""
+    n, k = 624, 2304
+    rng = np.random.default_rng(m + layout)
+    a = rng.integers(-3, 4, size=(m, k)).astype(np.float32)
+    res = rng.integers(-5, 6, size=(m, n)).astype(np.float32)
+    if wdt == "bf16":
+        b = rng.integers(-3, 4, size=(n, k)).astype(np.float32)
+        bd = dev(tile_nk(oracle.to_bf16_bits(b), "bf16").view(np.int16)) if layout else bf16_dev(b)
+        bdt, sc = BF16, None
+    else:
+        q = rng.integers(-127, 128, size=(n, k)).astype(np.int8)
+        b = q.astype(np.float32)
+        bd = dev(tile_nk(q, "int8")) if layout else dev(q)
+        bdt, sc = I8, dev(np.ones(n, np.float32))
+    c = _gemm(lib, bf16_dev(a), BF16, bd, bdt, m, n, k, epi, scales=sc, layout=layout,
+              residual=dev(res) if epi == EPI_RESIDUAL else None, workspace=False)
+    acc = a.astype(np.float64) @ b.T.astype(np.float64)
+    np.testing.assert_array_equal(host(c), _ref_epilogue(acc, epi, n, res).astype(np.float32))
+
+
+@pytest.mark.parametrize("tile", list(range(_abi.TILE_COUNT)))
+@pytest.mark.parametrize("wdt,epi", [("bf16", EPI_NONE), ("bf16", EPI_SWIGLU), ("i8", EPI_GLU_SILU_UP)])
+def test_gemm_grouped_gather_ids_outside_a_are_zero_rows(lib, tile, wdt, epi):
+    """sfg_hip_gemm_grouped_v1 with a gather list holding ids outside
+    [0, a_rows_limit) (-1 and past the end): those output rows are the
+    product of a zero row (zero; the GLU epilogues of zeros are zero too),
+    every other row the product of its gathered A row -- on the grouped
+    MFMA kernels (3000 rows over five groups, one of them empty) under every
+    tile policy.  Small-integer operands and power-of-two scales keep every
+    value exact."""
+    rng = np.random.default_rng(401 + tile)
+    counts = [700, 0, 1100, 33, 1167]
+    G, m, n, k, T = len(counts), sum(counts), 320, 256, 900
+    glu = epi != EPI_NONE
+    nb = 2 * n if glu else n
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    a = rng.integers(-3, 4, size=(T, k)).astype(np.float32)
+    rows = rng.integers(0, T, size=m).astype(np.int32)
+    rows[rng.random(m) < 0.05] = -1
+    rows[rng.random(m) < 0.05] = T + 7
+    rows[[0, 700, m - 1]] = [-1, T, T - 1]           # group edges
+    if wdt == "i8":
+        q = rng.integers(-127, 128, size=(G, nb, k)).astype(np.int8)
+        s = rng.choice(np.array([0.5, 1.0, 2.0], np.float32), size=(G, nb)).astype(np.float32)
+        bd, bdt, sd, s_stride = dev(q), I8, dev(s), nb
+        bm = q.astype(np.float64) * s[..., None].astype(np.float64)
+    else:
+        b = rng.integers(-3, 4, size=(G, nb, k)).astype(np.float32)
+        bd, bdt, sd, s_stride = bf16_dev(b), BF16, None, 0
+        bm = b.astype(np.float64)
+    ad, rd, od = bf16_dev(a), dev(rows), dev(offsets)
+    c = torch.full((m, n), 7.0, dtype=torch.float32, device="cuda")   # stale contents
+    args = _abi.GemmArgs()
+    args.a, args.a_dtype, args.lda = ad.data_ptr(), BF16, k
+    args.b, args.b_dtype, args.ldb = bd.data_ptr(), bdt, k
+    args.b_scales = sd.data_ptr() if sd is not None else None
+    args.c, args.c_dtype, args.ldc = c.data_ptr(), F32, n
+    args.residual, args.ldr = None, n
+    args.m, args.n, args.k, args.epilogue = m, n, k, epi
+    args.b_layout, args.tile = 0, tile
+    ws = torch.zeros(max(lib.sfg_hip_gemm_workspace_v1(m, n, k), 256), dtype=torch.uint8, device="cuda")
+    _abi.check(lib.sfg_hip_gemm_grouped_v1(ctypes.byref(args), rd.data_ptr(), T, od.data_ptr(), G,
+                                           nb * k, s_stride, ws.data_ptr(), ws.numel(), stream()))
+    _sync()
+    acc = np.zeros((m, nb))
+    for g in range(G):
+        src = rows[offsets[g]:offsets[g + 1]]
+        valid = (src >= 0) & (src < T)
+        arow = np.zeros((len(src), k))
+        arow[valid] = a[src[valid]]
+        acc[offsets[g]:offsets[g + 1]] = arow @ bm[g].T
+    ref = _ref_epilogue(acc, epi, n)
+    zero = (rows < 0) | (rows >= T)
+    assert np.all(host(c)[zero] == 0.0)
+    if glu:
+        np.testing.assert_allclose(host(c), ref, rtol=1e-5, atol=1e-5)
+    else:
+        np.testing.assert_array_equal(host(c), ref.astype(np.float32))
+
+
 def test_gemm_misaligned_operands_run_on_the_valu_kernel(lib):
     """bf16 / int8 MFMA kernels read rows as 16-byte vectors: a row pitch that
     is not a multiple of 16 bytes, or an operand not 16-byte aligned, runs on
