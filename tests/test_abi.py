@@ -180,6 +180,43 @@ def test_layer_taps_lie_inside_the_workspace(lib):
     assert tap(_desc(hidden=250), 0)[0] == _abi.ERR_INVALID_CONFIG
 
 
+def test_random_descriptors_get_a_code_and_a_sane_workspace(lib):
+    """3000 seeded descriptors with fields drawn from edge values (0, -1,
+    2^31 - 1, mismatched head counts, unknown dtypes, layouts, tile and wave
+    policies): the workspace query and the layer entry (null weights / io)
+    return an ABI code, never crash; every descriptor the query accepts reports
+    at least the bf16 bytes of its activation rows (no 32-bit wrap)."""
+    rng = np.random.default_rng(20261205)
+    i32 = 2**31 - 1
+    edge = [0, 1, -1, 2, 3, 7, 16, 64, 128, 1000, 4096, 65536, 1 << 20, i32, -i32 - 1]
+    codes = {_abi.ERR_INVALID_CONFIG, _abi.ERR_SHAPE, _abi.ERR_UNSUPPORTED, _abi.ERR_GUARD}
+    pick = lambda xs: int(rng.choice(xs))
+    for _ in range(3000):
+        d = _abi.LayerDesc()
+        d.abi = _abi.ABI_VERSION
+        d.head_dim = pick([1, 4, 64, 128, 256, 257, 0, -4, 1 << 16])
+        d.query_heads = pick([1, 2, 8, 32, 128, 0, -1, 1 << 12])
+        d.kv_heads = pick([1, 2, 4, 8, 3, 0])
+        d.hidden = d.query_heads * d.head_dim if rng.random() < 0.8 else pick(edge)
+        d.batch, d.sequence, d.intermediate, d.context = (pick(edge) for _ in range(4))
+        d.pages_per_seq, d.num_pages = pick(edge), pick(edge)
+        d.page_tokens = pick([0, 1, 16, -16, 1 << 20])
+        d.rms_epsilon = float(rng.choice([1e-6, 0.0, -1.0, float("nan")]))
+        d.rope_theta, d.causal, d.ffn = 1e4, pick([0, 1]), pick([0, 1, 2])
+        d.experts, d.top_k = pick([0, 1, 8, 64, -1, 4096]), pick([0, 1, 2, 8, 9])
+        d.act_dtype = pick([_abi.F32, _abi.BF16, 7])
+        d.weight_dtype = pick([_abi.F32, _abi.BF16, _abi.I8, 9])
+        d.kv_splits, d.use_routing_trace = pick([0, 1, 64, -3, i32]), pick([0, 1])
+        d.weight_layout, d.kv_append = pick([0, 1, 5]), pick([0, 1])
+        d.gemm_tile, d.attn_waves = pick([0, 3, 8, -1]), pick([0, 4, 8, 5])
+        ws = lib.sfg_hip_decoder_layer_workspace_v1(ctypes.byref(d))
+        rc = lib.sfg_hip_decoder_layer_v1(ctypes.byref(d), ctypes.byref(_abi.LayerWeights()),
+                                          ctypes.byref(_abi.LayerIO()), None, 0, None)
+        assert rc in codes, rc
+        if ws:
+            assert ws >= d.batch * d.sequence * d.hidden * 2
+
+
 def test_widened_layer_domain_validates_on_host(lib):
     """Decode on fp32 pools, MoE on fp32 activations, several new tokens per
     decode step and head dims up to 256 are lowered (a workspace size comes
