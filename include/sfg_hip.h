@@ -207,7 +207,9 @@ int sfg_hip_gemm_grouped_v1(const sfg_gemm_args* args, const int32_t* a_rows, in
 /* split_qkv + apply_rope (decoder_compiler.cpp:96-148).  qkv fp32
  * [B*S][H + 2 Hkv D]; rope_table [S][D/2][2] device copy of
  * sfg_hip_rope_table_host_v1.  q [B][Hq][S][D], k/v [B][Hkv][S][D] in out_dtype
- * (k and v may be NULL: a decode step discards them, decoder_compiler.cpp:238-243). */
+ * (k and v may be NULL: a decode step discards them, decoder_compiler.cpp:238-243).
+ * Any head_dim: an odd one's last dimension is copied unrotated (apply_rope's
+ * pair loop stops at d + 1 < D); rope_table may be NULL when head_dim is 1. */
 int sfg_hip_qkv_split_rope_v1(const float* qkv, const float* rope_table, int64_t batch,
                               int64_t seq, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
                               void* q, void* k, void* v, int out_dtype, void* stream);

@@ -432,8 +432,11 @@ int sfg_hip_gemm_grouped_v1(const sfg_gemm_args* a, const int32_t* a_rows, int64
 int sfg_hip_qkv_split_rope_v1(const float* qkv, const float* rope_table, int64_t batch,
                               int64_t seq, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
                               void* q, void* k, void* v, int out_dtype, void* stream) {
-    if (!qkv || !rope_table || !q || batch <= 0 || seq <= 0 || q_heads <= 0 || kv_heads <= 0 ||
-        head_dim <= 0 || (head_dim & 1) || q_heads % kv_heads)
+    // any head_dim: an odd one's last dimension is copied unrotated, as
+    // apply_rope's pair loop (d + 1 < head_dim) leaves it; head_dim 1 has no
+    // pair and reads no table
+    if (!qkv || (!rope_table && head_dim >= 2) || !q || batch <= 0 || seq <= 0 || q_heads <= 0 ||
+        kv_heads <= 0 || head_dim <= 0 || q_heads % kv_heads)
         return fail(SFG_ERR_SHAPE, "qkv_split_rope: invalid arguments");
     if (out_dtype != SFG_F32 && out_dtype != SFG_BF16)
         return fail(SFG_ERR_UNSUPPORTED, "qkv_split_rope: dtype %d", out_dtype);

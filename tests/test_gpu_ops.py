@@ -445,6 +445,34 @@ def test_split_rope_matches_oracle(lib, dtype):
     np.testing.assert_array_equal(conv(v)[:, :, 0], exact_v[:, :, 0])
 
 
+@pytest.mark.parametrize("dtype", [F32, BF16])
+@pytest.mark.parametrize("D", [1, 5, 33])
+def test_split_rope_odd_head_dims(lib, dtype, D):
+    """An odd head_dim's last dimension is copied unrotated, as apply_rope's
+    pair loop (decoder_compiler.cpp:101-114, d + 1 < D) leaves it; head_dim 1
+    has no pair and needs no table."""
+    B, S, Hq, Hkv, theta = 2, 23, 6, 2, 10000.0
+    H = Hq * D
+    qkv = oracle.normal(62, D, (B * S, H + 2 * Hkv * D))
+    table = np.zeros((S, max(D // 2, 1), 2), np.float32)
+    _abi.check(lib.sfg_hip_rope_table_host_v1(table.ctypes.data, S, D, ctypes.c_float(theta)))
+    tdt = torch.float32 if dtype == F32 else torch.int16
+    q = torch.empty((B, Hq, S, D), dtype=tdt, device="cuda")
+    k = torch.empty((B, Hkv, S, D), dtype=tdt, device="cuda")
+    v = torch.empty((B, Hkv, S, D), dtype=tdt, device="cuda")
+    _abi.check(lib.sfg_hip_qkv_split_rope_v1(dev(qkv).data_ptr(), dev(table).data_ptr() if D > 1 else None,
+                                             B, S, Hq, Hkv, D, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                             dtype, stream()))
+    _sync()
+    rq, rk, rv = oracle.split_qkv_rope(qkv, B, S, H, Hq, Hkv, D, theta)
+    conv = host if dtype == F32 else bf16_host
+    exact = (lambda a: a) if dtype == F32 else oracle.round_bf16
+    for got, ref in ((q, rq), (k, rk), (v, rv)):
+        assert oracle.rel_error(conv(got), ref) < (1e-6 if dtype == F32 else 8e-3)
+        # the last (unpaired) dimension is the input's, exactly
+        np.testing.assert_array_equal(conv(got)[..., D - 1], exact(ref)[..., D - 1])
+
+
 # ------------------------------------------------------------------ attention
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("shape", [(1, 4, 2, 128, 128, 64), (2, 4, 1, 33, 70, 64),

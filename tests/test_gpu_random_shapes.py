@@ -203,6 +203,24 @@ def test_random_append_step_matches_oracle(idx):
     _check_layer(APPEND_CASES[idx], SEED + 300 + idx)
 
 
+@pytest.mark.parametrize("kind", ["prefill f32 D5", "decode bf16 D33", "append w8 D7", "prefill bf16 D1"])
+def test_odd_head_dim_layer_matches_oracle(kind):
+    """Odd head dims: RoPE rotates the pairs (2i, 2i + 1) and leaves the last
+    dimension as it is (apply_rope's loop, decoder_compiler.cpp:101-114), in the
+    split kernel (prefill), in the decode attention's Q rotation and in the
+    append path's K rotation."""
+    base = CONFIGS["c1"].replace(query_heads=6, kv_heads=2, intermediate=200)
+    cfg = {
+        "prefill f32 D5": base.replace(head_dim=5, hidden=30, batch=2, sequence=37),
+        "decode bf16 D33": base.replace(head_dim=33, hidden=198, batch=3, sequence=1, dtype="bf16",
+                                        context_sequence=70, page_tokens=8, ffn="moe", experts=4, top_k=2),
+        "append w8 D7": base.replace(head_dim=7, hidden=42, batch=2, sequence=3, dtype="w8",
+                                     context_sequence=20, page_tokens=4, kv_append=True, kv_capacity=30),
+        "prefill bf16 D1": base.replace(head_dim=1, hidden=6, batch=1, sequence=50, dtype="bf16"),
+    }[kind]
+    _check_layer(cfg, SEED + 400 + len(kind))
+
+
 def test_append_decode_with_a_qkv_width_the_gemv_tiles_do_not_divide():
     """An append-mode decode step computes the whole QKV product (the new
     tokens' K and V are stored): 32 heads of 4 over one K/V head give a QKV
