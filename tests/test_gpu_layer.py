@@ -88,6 +88,30 @@ def test_layer_reduced_moe_device_routing(name):
     _check(res, ref, taps, TOL[cfg.dtype], f"{name}-small (device routing)", rows=same)
 
 
+@pytest.mark.parametrize("name", ["c3", "c5"])
+def test_layer_moe_with_every_token_on_two_experts(name):
+    """A routing trace (decoder_compiler.cpp:281-284) that sends every token to
+    experts 2 and 5 (random order and weights), the other experts empty: the
+    MoE prefill's grouped MFMA GEMMs and the int8 decode's grouped GEMVs see one
+    group holding every row and empty groups around it.  Every row meets the
+    tolerance against the oracle under the same trace."""
+    from schedforge_amd.layer import compile_decoder, execute_decoder_layer, layer_taps
+    cfg = SMALL[name]
+    d = oracle.make_layer_data(cfg, CONFIG_SEEDS[name] + 7)
+    rng = np.random.default_rng(CONFIG_SEEDS[name] + 7)
+    pair = np.array([2, 5], np.int32)
+    ids = np.stack([rng.permutation(pair) for _ in range(cfg.rows)]).astype(np.int32)
+    w = rng.random((cfg.rows, 2)).astype(np.float32)
+    w /= w.sum(axis=1, keepdims=True)
+    tr = (ids, w)
+    d.routing_trace = tr
+    ref, taps = oracle.decoder_layer(cfg, d, taps=True, trace=tr)
+    plan = compile_decoder(cfg, decoder_data(d), "cuda", page_permutation=d.page_permutation)
+    res = execute_decoder_layer(plan, d.input, warmup=0, repetitions=1)
+    assert_branches(d.input, res.output, layer_taps(plan), ref, taps, TOL[cfg.dtype],
+                    f"{name}-small, every token on experts 2 and 5")
+
+
 def test_layer_reduced_w8_dense():
     """Weight-only int8 dense decode layer (execute_quantized_decoder_layer,
     next_milestones.cpp:339-385, 676-697) against the oracle's int8 path."""
