@@ -247,10 +247,13 @@ std::vector<DecoderPlanPolicy> ExecutablePlanOptimizer::policies(const DecoderCo
         const std::int64_t pages = ceil_div(c.context_sequence, c.page_tokens);
         std::vector<int> layouts = {-1};
         if (!f32) {
-            // the tiled layout exists only where every product runs on the GEMV kernels
+            // the tiled layout exists only where every product runs on the GEMV
+            // kernels: depths a multiple of 128 and widths -- the QKV width
+            // included -- a multiple of 64, as the plan compile requires
             const bool moe = c.ffn == DecoderFFNKind::MoE;
+            const std::int64_t qkv_n = c.hidden + 2 * static_cast<std::int64_t>(c.kv_heads) * c.head_dim;
             const bool tiled = c.rows() <= kSkinnyMaxRows && c.hidden % 128 == 0 && c.intermediate % 128 == 0 &&
-                               (!moe || c.rows() * c.top_k <= kSkinnyGroupedMaxTotal);
+                               qkv_n % 64 == 0 && (!moe || c.rows() * c.top_k <= kSkinnyGroupedMaxTotal);
             layouts = {SFG_LAYOUT_NK};
             if (tiled) layouts.push_back(SFG_LAYOUT_TILED);
         }

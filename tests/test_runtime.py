@@ -351,3 +351,37 @@ def test_bench_harness_fills_max_error_from_expected_outputs(tmp_path):
         assert f"max_error=" in next(l for l in r.stdout.splitlines() if f"] {name} " in l)
     measured_others = [n for n, row in rows.items() if n not in refs and row["evidence"] == "measured"]
     assert measured_others and all(np.isnan(float(rows[n]["max_error"])) for n in measured_others)
+
+
+def test_optimizer_offers_tiled_weights_only_where_the_plan_compiles(tmp_path):
+    """ExecutablePlanOptimizer::policies (CPU, no GPU): a fragment-tiled
+    candidate exists only where the plan compile accepts one -- every product
+    on the decode GEMV with depths a multiple of 128 and widths a multiple of
+    64.  H 128 with one K/V head of 4 gives a QKV width of 136, so that decode
+    offers [N][K] weights only; H 2048 with 128-wide heads offers both."""
+    from schedforge_amd import build as B
+    src = tmp_path / "policies.cpp"
+    src.write_text(r'''
+#include "sfg_decoder.hpp"
+#include <cstdio>
+using namespace schedforge::hip;
+static int tiled(int hidden, int q_heads, int kv_heads, int head_dim) {
+    DecoderConfig c;
+    c.batch = 2; c.sequence = 1; c.hidden = hidden; c.intermediate = 256;
+    c.query_heads = q_heads; c.kv_heads = kv_heads; c.head_dim = head_dim;
+    c.context_sequence = 40; c.page_tokens = 16; c.precision = DecoderPrecision::BF16;
+    int n = 0;
+    for (const auto& p : ExecutablePlanOptimizer().policies(c)) n += p.weight_layout == SFG_LAYOUT_TILED;
+    return n;
+}
+int main() { std::printf("%d %d\n", tiled(128, 32, 1, 4), tiled(2048, 16, 4, 128)); }
+''')
+    exe = tmp_path / "policies"
+    r = subprocess.run(["g++", "-std=c++20", "-D__HIP_PLATFORM_AMD__", f"-I{B.RUNTIME}",
+                        f"-I{B.PKG.parent / 'include'}", "-I/opt/rocm/include", str(src), "-o", str(exe),
+                        f"-L{B.LIBDIR}", "-lsfg_decoder", f"-Wl,-rpath,{B.LIBDIR}", *B.HIP_LINK],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-2000:]
+    out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()
+    assert out[0] == "0", out
+    assert int(out[1]) > 0, out
