@@ -235,10 +235,17 @@ def compile_decoder(config: DecoderConfig, data: DecoderData, device="cuda",
             table_pages = np.asarray(data.page_table, dtype=np.int32).reshape(cfg.batch, pages_per_seq)
         else:
             perm = (np.arange(num_pages, dtype=np.int32) if page_permutation is None
-                    else np.asarray(page_permutation, dtype=np.int32))
+                    else np.asarray(page_permutation, dtype=np.int32).reshape(-1))
+            if perm.size != num_pages:
+                raise ValueError(f"page_permutation holds {perm.size} page ids; the plan's tables "
+                                 f"need batch x pages_per_seq = {num_pages}")
             table_pages = perm.reshape(cfg.batch, pages_per_seq)
         if table_pages.min() < 0 or table_pages.max() >= num_pages:
             raise ValueError("invalid physical KV page")
+        # one physical page per logical page: a page named twice would hold two
+        # sequences' keys at once
+        if np.unique(table_pages).size != table_pages.size:
+            raise ValueError("a physical KV page is assigned twice")
         t["page_table"] = torch.from_numpy(np.ascontiguousarray(table_pages)).to(plan.device)
         for name, src in (("k_pool", data.cached_key), ("v_pool", data.cached_value)):
             flat = _dev(src, plan.device).reshape(cfg.batch, cfg.kv_heads, cfg.context_sequence, D)

@@ -112,6 +112,25 @@ def test_layer_moe_with_every_token_on_two_experts(name):
                     f"{name}-small, every token on experts 2 and 5")
 
 
+def test_decode_plan_refuses_a_bad_page_permutation():
+    """compile_decoder's physical page assignment: a permutation of the wrong
+    length, an id outside the pool and a page named twice are refused on the
+    host before any pool is filled."""
+    from schedforge_amd.layer import compile_decoder
+    cfg = SMALL["c2"].replace(batch=2, context_sequence=40)
+    d = oracle.make_layer_data(cfg, CONFIG_SEEDS["c2"] + 9)
+    good = np.asarray(d.page_permutation, np.int32)
+    compile_decoder(cfg, decoder_data(d), "cuda", page_permutation=good)
+    dup = good.copy()
+    dup[1] = dup[0]
+    out_of_range = good.copy()
+    out_of_range[-1] = good.size
+    for perm, msg in ((good[:-1], "page ids"), (out_of_range, "invalid physical KV page"),
+                      (dup, "assigned twice")):
+        with pytest.raises(ValueError, match=msg):
+            compile_decoder(cfg, decoder_data(d), "cuda", page_permutation=perm)
+
+
 def test_layer_reduced_w8_dense():
     """Weight-only int8 dense decode layer (execute_quantized_decoder_layer,
     next_milestones.cpp:339-385, 676-697) against the oracle's int8 path."""
