@@ -112,6 +112,25 @@ def test_layer_moe_with_every_token_on_two_experts(name):
                     f"{name}-small, every token on experts 2 and 5")
 
 
+def test_layer_on_a_created_stream_gives_the_same_bits():
+    """The layer launched on a stream the caller created (default priority)
+    instead of the null stream: the library resolves the device, its CU and
+    XCD counts from that stream, and the output is the same, bit for bit
+    (a prefill whose grouped and dense GEMMs use the XCD-aware tile order, and
+    a decode)."""
+    from schedforge_amd.layer import compile_decoder, execute_decoder_layer
+    for name in ("c3", "c2"):
+        cfg = SMALL[name]
+        d = oracle.make_layer_data(cfg, CONFIG_SEEDS[name] + 13)
+        plan = compile_decoder(cfg, decoder_data(d), "cuda", page_permutation=d.page_permutation)
+        base = execute_decoder_layer(plan, d.input, warmup=0, repetitions=1).output
+        side = torch.cuda.Stream()
+        with torch.cuda.stream(side):
+            other = execute_decoder_layer(plan, d.input, warmup=0, repetitions=1).output
+        torch.cuda.synchronize()
+        assert np.array_equal(base, other), name
+
+
 def test_decode_plan_refuses_a_bad_page_permutation():
     """compile_decoder's physical page assignment: a permutation of the wrong
     length, an id outside the pool and a page named twice are refused on the
